@@ -1,0 +1,190 @@
+"""Benchmark: GEMM TFLOP/s of the 1.6B decoder-block set (fwd + dX + dW, M=8192) on one MI355X.
+
+One step = the 15 GEMMs a decoder block issues at BASELINE config 3 (d_model 2048,
+GQA 16 q / 4 kv heads x 128 -> fused QKV 2048->3072, attention-out 2048->2048,
+SwiGLU gate/up 2048->5632, down 5632->2048; tokens M = 8 x 1024 = 8192):
+forward Y = X W (NN, bf16 out), dX = dY W^T (NT, bf16 out), dW += X^T dY (TN, fp32
+accumulate), bf16 inputs, fp32 accumulation, all operands resident in HBM.
+value = algorithmic FLOPs x steps / timed seconds.
+
+roofline: the kernel with the largest share of GPU time in the timed region,
+timed per launch with HIP events on the launch stream; achieved = its
+algorithmic FLOPs / its summed launch time, against the dense bf16 MFMA peak.
+cpu_baseline: the oracle's fp32 OpenMP SGEMM (oracle/mi_oracle.c, cblas_sgemm
+semantics) on a bounded sample of the same set (token rows M_cpu), rank 0 only.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(ROOT, "large-language-model_amd"))
+
+PEAK_BF16_TFLOPS = 2516.6   # MI355X dense bf16 MFMA
+PEAK_HBM_GBS = 8000.0
+
+# (name, d_in, d_out) of the config-3 decoder block, engine layout W[d_in, d_out]
+BLOCK = [("qkv", 2048, 3072), ("o", 2048, 2048), ("gate", 2048, 5632), ("up", 2048, 5632),
+         ("down", 5632, 2048)]
+M_TOKENS = 8192
+
+
+def block_flops(M: int) -> int:
+    return sum(3 * 2 * M * din * dout for _, din, dout in BLOCK)
+
+
+def parse():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--cpu-rows", type=int, default=2048, help="token rows of the CPU sample")
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="also launch a 1 GiB device copy (for PMC byte-counter scaling)")
+    return ap.parse_args()
+
+
+def cpu_baseline(m_rows: int) -> dict:
+    import numpy as np
+
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import oracle
+
+    flops = 0
+    t_total = 0.0
+    rng = np.random.default_rng(0)
+    for _, din, dout in BLOCK:
+        x = rng.standard_normal((m_rows, din), dtype=np.float32)
+        w = rng.standard_normal((din, dout), dtype=np.float32) * 0.02
+        dy = rng.standard_normal((m_rows, dout), dtype=np.float32) * 1e-2
+        dw = np.zeros((din, dout), np.float32)
+        t0 = time.perf_counter()
+        oracle.sgemm_omp(0, 0, m_rows, dout, din, x, w)                       # fwd
+        oracle.sgemm_omp(0, 1, m_rows, din, dout, dy, w)                      # dX
+        oracle.sgemm_omp(1, 0, din, dout, m_rows, x, dy, C=dw, beta=1.0)      # dW +=
+        t_total += time.perf_counter() - t0
+        flops += 3 * 2 * m_rows * din * dout
+    return {"value": round(flops / t_total / 1e12, 4), "unit": "TFLOP/s",
+            "cores": oracle.num_threads(), "kind": "port",
+            "sample": f"config-3 block set (15 GEMMs) at M={m_rows} token rows instead of "
+                      f"{M_TOKENS}, fp32 (bf16 inputs upcast), {flops / 1e9:.1f} GFLOP, "
+                      f"{t_total:.2f} s"}
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(json.dumps({"error": "this build runs on one GPU only; --gpus must be 1 "
+                                   "(multi-GPU sharding is described in DESIGN.md, not run)"}))
+        sys.exit(2)
+    import torch
+
+    import mi_gemm as mi
+
+    dev = torch.device("cuda:0")
+    mi.init()
+    M = M_TOKENS
+    g = torch.Generator(device=dev)
+    g.manual_seed(1234)
+    ops = []
+    for name, din, dout in BLOCK:
+        X = torch.randn((M, din), generator=g, device=dev).to(torch.bfloat16)
+        W = (torch.randn((din, dout), generator=g, device=dev) * 0.02).to(torch.bfloat16)
+        dY = (torch.randn((M, dout), generator=g, device=dev) * 1e-2).to(torch.bfloat16)
+        Y = torch.empty((M, dout), dtype=torch.bfloat16, device=dev)
+        dX = torch.empty((M, din), dtype=torch.bfloat16, device=dev)
+        dW = torch.zeros((din, dout), dtype=torch.float32, device=dev)
+        ops.append((name, "fwd NN", 2 * M * din * dout,
+                    lambda X=X, W=W, Y=Y, din=din, dout=dout:
+                    mi.gemm(X, W, Y, M, dout, din, sync=False)))
+        ops.append((name, "dX NT", 2 * M * din * dout,
+                    lambda dY=dY, W=W, dX=dX, din=din, dout=dout:
+                    mi.gemm(dY, W, dX, M, din, dout, transB=True, sync=False)))
+        ops.append((name, "dW TN", 2 * M * din * dout,
+                    lambda X=X, dY=dY, dW=dW, din=din, dout=dout:
+                    mi.gemm(X, dY, dW, din, dout, M, transA=True, beta=1.0, sync=False)))
+
+    def step():
+        for _, _, _, fn in ops:
+            fn()
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+
+    # Timed region: K steps; every launch bracketed by events on the launch stream.
+    stream = torch.cuda.current_stream()
+    evs = [[(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+            for _ in ops] for _ in range(args.steps)]
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for s in range(args.steps):
+        for i, (_, _, _, fn) in enumerate(ops):
+            evs[s][i][0].record(stream)
+            fn()
+            evs[s][i][1].record(stream)
+    torch.cuda.synchronize()
+    t1 = time.perf_counter()
+    elapsed = t1 - t0
+    flops = block_flops(M)
+    value = flops * args.steps / elapsed / 1e12
+
+    # Per-kernel (operand layout) totals over the timed region.
+    per_kind = {}
+    per_op = {}
+    for s in range(args.steps):
+        for i, (name, kind, fl, _) in enumerate(ops):
+            ms = evs[s][i][0].elapsed_time(evs[s][i][1])
+            k = kind.split()[1]
+            tot = per_kind.setdefault(k, [0.0, 0, 0])
+            tot[0] += ms
+            tot[1] += fl
+            tot[2] += 1
+            per_op.setdefault(f"{name} {kind}", [0.0, fl])[0] += ms
+    dom = max(per_kind, key=lambda k: per_kind[k][0])
+    ms_dom, fl_dom, n_dom = per_kind[dom]
+    achieved = fl_dom / (ms_dom / 1e3) / 1e12
+    breakdown = {k: round(v[1] / (v[0] / args.steps / 1e3) / 1e12, 1) for k, v in per_op.items()}
+
+    if args.copy_calibration:
+        a = torch.empty(1 << 28, dtype=torch.float32, device=dev)
+        b = torch.empty_like(a)
+        b.copy_(a)
+        torch.cuda.synchronize()
+
+    out = {
+        "metric": "GEMM TFLOP/s (fwd+bwd, 1.6B block, M=8192) and % of MI355X MFMA peak",
+        "value": round(value, 2),
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(elapsed / args.steps * 1e3, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (torch.randn on device; X~N(0,1), W~N(0,0.02), dY~N(0,1e-2))",
+        "config": {"workload": "1.6B decoder-block GEMM set: fwd NN + dX NT + dW TN (beta=1, fp32) "
+                               "for QKV 2048->3072, O 2048->2048, gate/up 2048->5632, down "
+                               "5632->2048; M=8192 tokens; bf16 in / fp32 acc",
+                   "M": M, "d_model": 2048, "gemms_per_step": len(ops),
+                   "flops_per_step": flops, "pct_of_peak": round(100 * value / PEAK_BF16_TFLOPS, 2),
+                   "per_gemm_tflops": breakdown},
+        "roofline": {"bound": "mfma", "achieved": round(achieved, 2), "peak": PEAK_BF16_TFLOPS,
+                     "unit": "TFLOP/s", "frac": round(achieved / PEAK_BF16_TFLOPS, 4),
+                     "traffic": None, "kernel": f"gemm_kernel bf16 {dom} (256x256 tile)",
+                     "launches": n_dom, "avg_launch_ms": round(ms_dom / n_dom, 4)},
+    }
+    if not args.no_cpu:
+        out["cpu_baseline"] = cpu_baseline(args.cpu_rows)
+    print(json.dumps(out))
+
+
+if __name__ == "__main__":
+    main()

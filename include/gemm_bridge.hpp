@@ -1,0 +1,107 @@
+// gemm_bridge.hpp -- C++ mirror of the reference engine's GEMM operator layer,
+// implemented over the C ABI in mi_gemm.h.
+//
+// Same names, argument meaning and error behaviour as the reference's
+// metal_bridge GEMM entry points (cpp/include/gpu_kernel/MetalBridge.hpp) and
+// Tensor::matmul (cpp/include/Tensor.hpp:230, cpp/src/Tensor.cpp:174-228), so an
+// engine built on them can switch namespaces.  Differences, all deliberate:
+//   * pointers are HIP device pointers (the reference wrapped unified-memory host
+//     pointers, MetalBridge.mm:765-834);
+//   * the reference's float* parameters of gemm_backward / gemm_proj_trans_b /
+//     residual_add carry bf16 storage (buffers sized with sizeof(__bf16),
+//     MetalBridge.mm:1353-1355,1928; residual_add.metal:15-17); the mirror keeps
+//     that interpretation and adds explicit fp32 variants;
+//   * errors print "[mi_bridge] <function>: <reason>" to stderr and return, as the
+//     bridge did (MetalBridge.mm:1360); last_status() exposes the code.
+#pragma once
+#include <cstddef>
+#include <cstdint>
+#include <stdexcept>
+#include <vector>
+
+#include "mi_gemm.h"
+
+namespace mi_bridge {
+
+// MetalBridge.hpp:20-21
+void initialize();
+bool is_available();
+
+// MetalBridge.hpp:29-30.  Inside a scope every call is enqueued on the bridge's
+// stream without waiting; end_scope() waits once.  Outside a scope each call
+// waits for its own completion (MetalBridge.mm:1384-1406).
+void begin_scope();
+void end_scope();
+inline void start_batch() { begin_scope(); }
+inline void commit_batch() { end_scope(); }
+
+// The stream the bridge enqueues on (a hipStream_t), created on first use.
+void* stream();
+
+// Status of the last bridge call on this thread (mi_status).
+int last_status();
+
+// MetalBridge.hpp:39-42: C[M,N] = op(A) op(B), bf16 in / bf16 out, fp32 accumulate.
+// is_forward is accepted and ignored, as in gemm_bf16.metal.
+void gemm_bf16(const void* A, const void* B, void* C, size_t M, size_t N, size_t K,
+               bool transA = false, bool transB = false, bool is_forward = false);
+
+// MetalBridge.hpp:44-46: C = (SiLU(gate) * up) * B, bf16, gate/up [M,K], B [K,N].
+void fused_swiglu_gemm(const void* gate_proj, const void* up_proj, const void* B, void* C,
+                       size_t M, size_t N, size_t K);
+
+// MetalBridge.hpp:119-120: C = SiLU(A*Bg) * (A*Bu), fp32, A [M,K], Bg/Bu [K,N].
+void gemm_ffn(const float* a, const float* b_gate, const float* b_up, float* c, size_t M,
+              size_t N, size_t K);
+
+// MetalBridge.hpp:121: C = A*B, fp32 row-major NN (the cblas_sgemm call of
+// MetalBridge.mm:695-697, here on the GPU).
+void gemm_proj(const float* a, const float* b, float* c, size_t M, size_t N, size_t K);
+
+// MetalBridge.hpp:122-123 / MetalBridge.mm:1925-1930: C[M,N] = A^T B with A
+// stored [K,M], bf16 storage, overwriting C.
+void gemm_backward(const float* a_transposed, const float* b, float* c, size_t M, size_t N,
+                   size_t K);
+
+// The engine's weight-gradient semantics (Transformer.cpp:236,288-289,
+// gemm_backward.metal:104-115): dW[M,N] (fp32) += A^T B, A [K,M] and B [K,N] bf16.
+void gemm_backward_accumulate(const void* a_transposed, const void* b, float* c, size_t M,
+                              size_t N, size_t K);
+
+// MetalBridge.hpp:124-125 / MetalBridge.mm:1932-1936: C = A B^T, B stored [N,K],
+// bf16 storage.
+void gemm_proj_trans_b(const float* a, const float* b_transposed, float* c, size_t M, size_t N,
+                       size_t K);
+
+// MetalBridge.hpp:78: a[i] += b[i] on bf16 storage (residual_add.metal:15-28).
+void residual_add(float* a, const float* b, size_t n);
+// fp32 storage variant.
+void residual_add_f32(float* a, const float* b, size_t n);
+
+// ---- Tensor::matmul mirror ---------------------------------------------------
+
+enum class DType : uint8_t { FP32, BF16 };  // Tensor.hpp:14
+
+// A non-owning view of a row-major device tensor with up to 5 dims (Tensor.hpp:31-76).
+struct DeviceTensor {
+  void* data = nullptr;
+  std::vector<size_t> shape;
+  DType dtype = DType::BF16;
+  size_t numel() const {
+    size_t n = 1;
+    for (size_t d : shape) n *= d;
+    return n;
+  }
+  size_t itemsize() const { return dtype == DType::BF16 ? 2 : 4; }
+};
+
+// Shape of `a.matmul(b)` (Tensor.cpp:174-209), throwing std::invalid_argument with
+// the reference's messages on rank < 2, inner or batch mismatch.
+std::vector<size_t> matmul_shape(const DeviceTensor& a, const DeviceTensor& b);
+
+// out = a.matmul(b): projection (N-D x 2-D) or same-rank batched product, one
+// launch for all batch slices; out.dtype = a.dtype, out.data preallocated with
+// matmul_shape(a, b) elements.  a and b must share a dtype.
+void matmul(const DeviceTensor& a, const DeviceTensor& b, DeviceTensor& out);
+
+}  // namespace mi_bridge

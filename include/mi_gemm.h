@@ -1,0 +1,160 @@
+/*
+ * mi_gemm.h -- C ABI of the MI355X (gfx950) GEMM core.
+ *
+ * Drop-in boundary for the matmul operator layer of the reference C++ engine
+ * (rahul238xaviers/large-language-model, cpp/).  Every entry point below states
+ * the reference interface it replaces.  Plain pointers and sizes only: all
+ * matrix pointers are DEVICE pointers owned by the caller; `stream` is a
+ * hipStream_t (NULL = legacy default stream).  Every call is asynchronous on
+ * `stream` and returns a status code (0 = MI_OK) after validating its
+ * arguments on the host; nothing here allocates device memory.
+ *
+ * Layout conventions (row-major, as in the reference, gemm_bf16.metal:45,63):
+ *   op(A)[m,k] = transA ? A[k*lda + m] : A[m*lda + k]     (op(A) is M x K)
+ *   op(B)[k,n] = transB ? B[n*ldb + k] : B[k*ldb + n]     (op(B) is K x N)
+ *   C[m,n] at C[m*ldc + n]
+ * Engine layout (weights W[in,out], Y = X*W) is transA=0, transB=0 (NN);
+ * nn.Linear layout (W[out,in], Y = X*W^T) is NT; weight gradients dW = X^T*dY
+ * are TN.
+ *
+ * Epilogue, applied in fp32 to the fp32 accumulator acc = sum_k op(A)*op(B):
+ *   t = alpha*acc                         (dual-B: t = SiLU(alpha*acc_g) * (alpha*acc_u))
+ *   t += bias[n]                          if epi->bias
+ *   t += beta * C[m,n]                    if beta != 0 (C read in its own dtype)
+ *   t += R[m*ldr + n]                     if epi->residual
+ *   C[m,n] = t   (fp32, or bf16 rounded to nearest even)
+ * with SiLU(x) = x / (1 + exp(-x)).
+ */
+#ifndef MI_GEMM_H
+#define MI_GEMM_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef enum mi_dtype { MI_F32 = 0, MI_BF16 = 1 } mi_dtype;
+
+typedef enum mi_status {
+  MI_OK = 0,
+  MI_ERR_SHAPE = 1,       /* negative size, inconsistent K segments, bad batch description */
+  MI_ERR_LD = 2,          /* leading dimension smaller than the row it must hold */
+  MI_ERR_NULL = 3,        /* required pointer is NULL */
+  MI_ERR_DTYPE = 4,       /* dtype combination not supported */
+  MI_ERR_UNSUPPORTED = 5, /* feature combination not supported (message says which) */
+  MI_ERR_WORKSPACE = 6,   /* workspace too small for the requested split */
+  MI_ERR_HIP = 7,         /* HIP runtime error (message carries hipGetErrorString) */
+  MI_ERR_NO_DEVICE = 8    /* no gfx950 device visible */
+} mi_status;
+
+/* Causal structure of a batched product (GQA attention forms). */
+typedef enum mi_causal {
+  MI_CAUSAL_NONE = 0,
+  MI_CAUSAL_OUT_LOWER = 1, /* only C[m,n] with n <= m is computed; n > m gets mask_value   */
+  MI_CAUSAL_A_LOWER = 2,   /* op(A)[m,k] == 0 for k > m (within a K segment): skipped     */
+  MI_CAUSAL_A_UPPER = 3    /* op(A)[m,k] == 0 for k < m (within a K segment): skipped     */
+} mi_causal;
+
+/* Optional fused prologue/epilogue operands.  Any field may be NULL / 0. */
+typedef struct mi_epilogue {
+  const void* bias;      /* [N] row-broadcast bias, dtype bias_dtype                       */
+  int32_t bias_dtype;    /* mi_dtype                                                        */
+  const void* residual;  /* R[M, ldr] added after beta*C, dtype residual_dtype              */
+  int32_t residual_dtype;
+  int64_t ldr;
+  const void* B2;        /* dual-B SiLU gate: C = SiLU(A*B) (.) (A*B2), B2 laid out as B     */
+  const void* A2;        /* SiLU-gate prologue: op(A) := SiLU(A) (.) A2, A2 laid out as A    */
+} mi_epilogue;
+
+/*
+ * Strided batch: problem z in [0, batch) is split as zo = z / heads,
+ * zi = z % heads and operand X is offset by  zo*X_outer + (zi / X_group)*X_inner
+ * elements.  X_group > 1 maps several query heads onto one shared KV head
+ * (GQA: kv_h = h / (nH/nKV), Attention.cpp:241).  The reduction dimension is
+ * k_segments segments of K each; segment j of A / B starts seg_a / seg_b
+ * elements after segment 0 (the KV-group reduction of dK/dV, Attention.cpp:332,
+ * 344-345, is one product whose K runs over the nH/nKV query heads).
+ */
+typedef struct mi_batch {
+  int64_t batch, heads;
+  int64_t a_outer, a_inner, a_group;
+  int64_t b_outer, b_inner, b_group;
+  int64_t c_outer, c_inner, c_group;
+  int64_t r_outer, r_inner;  /* residual batch strides (group 1) */
+  int64_t k_segments;        /* >= 1 */
+  int64_t seg_a, seg_b;
+  int32_t causal;            /* mi_causal */
+  float mask_value;          /* written where MI_CAUSAL_OUT_LOWER masks */
+} mi_batch;
+
+/* Initialise the runtime on the current device; idempotent.  Returns
+ * MI_ERR_NO_DEVICE when no gfx950 GPU is visible.  Replaces
+ * metal_bridge::initialize / is_available (MetalBridge.hpp:20-21). */
+int mi_init(void);
+
+/* Text of the last error raised on the calling thread ("" if none). */
+const char* mi_last_error(void);
+
+/* Library version string. */
+const char* mi_version(void);
+
+/* Workspace bytes mi_gemm / mi_gemm_batched would use for split-K on this
+ * problem when given unlimited workspace (0 if it would not split). */
+size_t mi_gemm_workspace_size(int transA, int transB, int64_t M, int64_t N, int64_t K,
+                              int32_t dtype_in, int32_t dtype_c, int64_t batch);
+
+/*
+ * General GEMM with fused epilogue.  A and B share one input dtype (MI_BF16 or
+ * MI_F32); C is MI_BF16 or MI_F32.  workspace may be NULL (then no split-K).
+ * Replaces metal_bridge::gemm_bf16 (MetalBridge.hpp:39-42), gemm_proj (:121),
+ * gemm_backward (:122-123), gemm_proj_trans_b (:124-125), gemm_ffn (:119-120,
+ * via epi->B2) and fused_swiglu_gemm (:44-46, via epi->A2), and the residual
+ * pass residual_add (:78) when fused via epi->residual or beta = 1.
+ */
+int mi_gemm(void* stream, int transA, int transB, int64_t M, int64_t N, int64_t K,
+            float alpha, const void* A, int64_t lda, const void* B, int64_t ldb,
+            int32_t dtype_in, float beta, void* C, int64_t ldc, int32_t dtype_c,
+            const mi_epilogue* epi, void* workspace, size_t workspace_bytes);
+
+/*
+ * Strided-batched GEMM with GQA head mapping, K segments and causal skipping.
+ * Replaces the per-slice gemm_bf16 loop of Tensor::matmul's batched branch
+ * (Tensor.cpp:196-227) and the batched QK^T / P*V / dV / dP / dQ / dK products
+ * of GQA attention (Attention.cpp:236-280, 292-348; flash_attn_fwd and
+ * fused_attn_bwd, MetalBridge.hpp:49-57).
+ */
+int mi_gemm_batched(void* stream, int transA, int transB, int64_t M, int64_t N, int64_t K,
+                    float alpha, const void* A, int64_t lda, const void* B, int64_t ldb,
+                    int32_t dtype_in, float beta, void* C, int64_t ldc, int32_t dtype_c,
+                    const mi_batch* batch, const mi_epilogue* epi, void* workspace,
+                    size_t workspace_bytes);
+
+/* a[i] += b[i] for i < n (dtype MI_F32 or MI_BF16).  Replaces
+ * metal_bridge::residual_add (MetalBridge.hpp:78, residual_add.metal:15-28). */
+int mi_residual_add(void* stream, void* a, const void* b, int64_t n, int32_t dtype);
+
+/*
+ * Row softmax of causal attention scores, in place on S [rows, T] (row r of a
+ * head is query position r % T): P[q,k] = exp(S[q,k]-max)/sum over k <= q,
+ * zero for k > q (Attention.cpp:261-266).  S dtype MI_F32 or MI_BF16.
+ */
+int mi_softmax_causal(void* stream, void* S, int64_t rows, int64_t T, int64_t ld,
+                      int32_t dtype);
+
+/*
+ * Softmax backward for attention: dS = P (.) (dP - rowsum(P (.) dP)) * scale,
+ * written over dP (Attention.cpp:336-345).  Same shape conventions as above.
+ */
+int mi_softmax_bwd(void* stream, const void* P, void* dP, int64_t rows, int64_t T,
+                   int64_t ld, float scale, int32_t dtype);
+
+/* Synchronise `stream`; replaces metal_bridge::end_scope's wait
+ * (MetalBridge.hpp:29-30, MetalBridge.mm:2176-2225). */
+int mi_stream_sync(void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* MI_GEMM_H */

@@ -1,0 +1,202 @@
+// gemm_bridge.cpp -- C++ mirror of the reference GEMM operator layer over the
+// C ABI (declarations and the reference citations are in include/gemm_bridge.hpp).
+#include "../../include/gemm_bridge.hpp"
+
+#include <hip/hip_runtime.h>
+
+#include <cstdio>
+#include <cstring>
+
+namespace mi_bridge {
+namespace {
+
+thread_local int t_status = MI_OK;
+thread_local bool t_in_scope = false;
+thread_local hipStream_t t_stream = nullptr;
+
+hipStream_t get_stream() {
+  if (!t_stream) {
+    if (hipStreamCreateWithFlags(&t_stream, hipStreamNonBlocking) != hipSuccess) t_stream = nullptr;
+  }
+  return t_stream;
+}
+
+// Record the status; print like the reference bridge; wait when outside a scope.
+void finish(const char* fn, int st) {
+  t_status = st;
+  if (st != MI_OK) {
+    std::fprintf(stderr, "[mi_bridge] %s: %s\n", fn, mi_last_error());
+    return;
+  }
+  if (!t_in_scope) {
+    st = mi_stream_sync(get_stream());
+    t_status = st;
+    if (st != MI_OK) std::fprintf(stderr, "[mi_bridge] %s: %s\n", fn, mi_last_error());
+  }
+}
+
+int gemm(int ta, int tb, size_t M, size_t N, size_t K, float alpha, const void* A, const void* B,
+         int dt_in, float beta, void* C, int dt_c, const mi_epilogue* epi) {
+  const int64_t lda = ta ? (int64_t)M : (int64_t)K;
+  const int64_t ldb = tb ? (int64_t)K : (int64_t)N;
+  return mi_gemm(get_stream(), ta, tb, (int64_t)M, (int64_t)N, (int64_t)K, alpha, A, lda, B, ldb,
+                 dt_in, beta, C, (int64_t)N, dt_c, epi, nullptr, 0);
+}
+
+}  // namespace
+
+void initialize() { t_status = mi_init(); }
+bool is_available() { return mi_init() == MI_OK; }
+
+void begin_scope() {
+  get_stream();
+  t_in_scope = true;
+}
+
+void end_scope() {
+  t_in_scope = false;
+  t_status = mi_stream_sync(get_stream());
+  if (t_status != MI_OK) std::fprintf(stderr, "[mi_bridge] end_scope: %s\n", mi_last_error());
+}
+
+void* stream() { return (void*)get_stream(); }
+int last_status() { return t_status; }
+
+void gemm_bf16(const void* A, const void* B, void* C, size_t M, size_t N, size_t K, bool transA,
+               bool transB, bool is_forward) {
+  (void)is_forward;
+  if (M == 0 || N == 0 || K == 0) {  // silent no-op, as MetalBridge.mm:622-623,693
+    t_status = MI_OK;
+    return;
+  }
+  finish("gemm_bf16", gemm(transA, transB, M, N, K, 1.0f, A, B, MI_BF16, 0.0f, C, MI_BF16, nullptr));
+}
+
+void fused_swiglu_gemm(const void* gate_proj, const void* up_proj, const void* B, void* C, size_t M,
+                       size_t N, size_t K) {
+  if (M == 0 || N == 0 || K == 0) {
+    t_status = MI_OK;
+    return;
+  }
+  mi_epilogue e;
+  std::memset(&e, 0, sizeof(e));
+  e.A2 = up_proj;
+  finish("fused_swiglu_gemm",
+         gemm(0, 0, M, N, K, 1.0f, gate_proj, B, MI_BF16, 0.0f, C, MI_BF16, &e));
+}
+
+void gemm_ffn(const float* a, const float* b_gate, const float* b_up, float* c, size_t M, size_t N,
+              size_t K) {
+  if (M == 0 || N == 0 || K == 0) {
+    t_status = MI_OK;
+    return;
+  }
+  mi_epilogue e;
+  std::memset(&e, 0, sizeof(e));
+  e.B2 = b_up;
+  finish("gemm_ffn", gemm(0, 0, M, N, K, 1.0f, a, b_gate, MI_F32, 0.0f, c, MI_F32, &e));
+}
+
+void gemm_proj(const float* a, const float* b, float* c, size_t M, size_t N, size_t K) {
+  if (M == 0 || N == 0 || K == 0) {
+    t_status = MI_OK;
+    return;
+  }
+  finish("gemm_proj", gemm(0, 0, M, N, K, 1.0f, a, b, MI_F32, 0.0f, c, MI_F32, nullptr));
+}
+
+void gemm_backward(const float* a_transposed, const float* b, float* c, size_t M, size_t N,
+                   size_t K) {
+  if (M == 0 || N == 0 || K == 0) {
+    t_status = MI_OK;
+    return;
+  }
+  finish("gemm_backward",
+         gemm(1, 0, M, N, K, 1.0f, a_transposed, b, MI_BF16, 0.0f, c, MI_BF16, nullptr));
+}
+
+void gemm_backward_accumulate(const void* a_transposed, const void* b, float* c, size_t M, size_t N,
+                              size_t K) {
+  if (M == 0 || N == 0 || K == 0) {
+    t_status = MI_OK;
+    return;
+  }
+  finish("gemm_backward_accumulate",
+         gemm(1, 0, M, N, K, 1.0f, a_transposed, b, MI_BF16, 1.0f, c, MI_F32, nullptr));
+}
+
+void gemm_proj_trans_b(const float* a, const float* b_transposed, float* c, size_t M, size_t N,
+                       size_t K) {
+  if (M == 0 || N == 0 || K == 0) {
+    t_status = MI_OK;
+    return;
+  }
+  finish("gemm_proj_trans_b",
+         gemm(0, 1, M, N, K, 1.0f, a, b_transposed, MI_BF16, 0.0f, c, MI_BF16, nullptr));
+}
+
+void residual_add(float* a, const float* b, size_t n) {
+  finish("residual_add", mi_residual_add(get_stream(), a, b, (int64_t)n, MI_BF16));
+}
+
+void residual_add_f32(float* a, const float* b, size_t n) {
+  finish("residual_add_f32", mi_residual_add(get_stream(), a, b, (int64_t)n, MI_F32));
+}
+
+std::vector<size_t> matmul_shape(const DeviceTensor& a, const DeviceTensor& b) {
+  const size_t ra = a.shape.size(), rb = b.shape.size();
+  if (ra < 2 || rb < 2) throw std::invalid_argument("Matmul requires at least 2 dimensions");
+  if (rb == 2 && ra != 2) {
+    if (a.shape.back() != b.shape[0])
+      throw std::invalid_argument("Inner dimensions must match for projection");
+    std::vector<size_t> s = a.shape;
+    s.back() = b.shape[1];
+    return s;
+  }
+  if (ra != rb) throw std::invalid_argument("Batch size must match for matrix multiplication");
+  for (size_t i = 0; i + 2 < ra; ++i)
+    if (a.shape[i] != b.shape[i])
+      throw std::invalid_argument("Batch dimension must match for matmul");
+  if (a.shape[ra - 1] != b.shape[rb - 2])
+    throw std::invalid_argument("Inner dimensions must match for matmul");
+  std::vector<size_t> s = a.shape;
+  s.back() = b.shape.back();
+  return s;
+}
+
+void matmul(const DeviceTensor& a, const DeviceTensor& b, DeviceTensor& out) {
+  const std::vector<size_t> s = matmul_shape(a, b);
+  if (a.dtype != b.dtype) throw std::invalid_argument("Matmul operands must share a dtype");
+  out.shape = s;
+  out.dtype = a.dtype;
+  const int dt = a.dtype == DType::BF16 ? MI_BF16 : MI_F32;
+  const size_t ra = a.shape.size();
+  int st;
+  if (b.shape.size() == 2 && ra != 2) {
+    size_t M = 1;
+    for (size_t i = 0; i + 1 < ra; ++i) M *= a.shape[i];
+    const size_t K = a.shape.back(), N = b.shape[1];
+    st = mi_gemm(get_stream(), 0, 0, (int64_t)M, (int64_t)N, (int64_t)K, 1.0f, a.data, (int64_t)K,
+                 b.data, (int64_t)N, dt, 0.0f, out.data, (int64_t)N, dt, nullptr, nullptr, 0);
+  } else {
+    size_t nb = 1;
+    for (size_t i = 0; i + 2 < ra; ++i) nb *= a.shape[i];
+    const size_t M = a.shape[ra - 2], K = a.shape[ra - 1], N = b.shape.back();
+    mi_batch bt;
+    std::memset(&bt, 0, sizeof(bt));
+    bt.batch = (int64_t)nb;
+    bt.heads = 1;
+    bt.a_outer = (int64_t)(M * K);
+    bt.b_outer = (int64_t)(K * N);
+    bt.c_outer = (int64_t)(M * N);
+    bt.a_group = bt.b_group = bt.c_group = 1;
+    bt.k_segments = 1;
+    st = mi_gemm_batched(get_stream(), 0, 0, (int64_t)M, (int64_t)N, (int64_t)K, 1.0f, a.data,
+                         (int64_t)K, b.data, (int64_t)N, dt, 0.0f, out.data, (int64_t)N, dt, &bt,
+                         nullptr, nullptr, 0);
+  }
+  if (st != MI_OK) throw std::runtime_error(std::string("mi_gemm: ") + mi_last_error());
+  finish("matmul", st);
+}
+
+}  // namespace mi_bridge

@@ -1,0 +1,531 @@
+// mi_gemm.hip -- host dispatch and C ABI of the gfx950 GEMM core (include/mi_gemm.h).
+//
+// Replaces the GEMM entry points of the reference engine's Metal bridge
+// (metal_bridge::gemm_bf16 / gemm_backward / gemm_proj_trans_b / gemm_proj /
+// gemm_ffn / fused_swiglu_gemm, MetalBridge.hpp:39-46,119-125) and the batched
+// branch of Tensor::matmul (Tensor.cpp:196-227).  Arguments are validated on the
+// host and reported as status codes (the reference bridge printed and returned,
+// MetalBridge.mm:1360; Tensor::matmul threw, Tensor.cpp:175-205 -- the C++ and
+// Python mirrors above this ABI restore those behaviours).
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cmath>
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <mutex>
+#include <string>
+
+#include "../../include/mi_gemm.h"
+#include "mi_gemm_kernels.hpp"
+
+using namespace mig;
+
+namespace {
+
+thread_local std::string g_err;
+
+int fail(int code, const char* fmt, ...) {
+  char buf[512];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof(buf), fmt, ap);
+  va_end(ap);
+  g_err = buf;
+  return code;
+}
+
+struct DeviceInfo {
+  bool ok = false;
+  int cus = 256;
+};
+std::once_flag g_once;
+DeviceInfo g_dev[64];
+int g_init_status = MI_ERR_NO_DEVICE;
+
+int init_devices() {
+  std::call_once(g_once, [] {
+    int n = 0;
+    if (hipGetDeviceCount(&n) != hipSuccess || n <= 0) {
+      g_init_status = MI_ERR_NO_DEVICE;
+      return;
+    }
+    bool any = false;
+    for (int d = 0; d < n && d < 64; ++d) {
+      hipDeviceProp_t prop;
+      if (hipGetDeviceProperties(&prop, d) != hipSuccess) continue;
+      if (std::strncmp(prop.gcnArchName, "gfx950", 6) != 0) continue;
+      g_dev[d].ok = true;
+      g_dev[d].cus = prop.multiProcessorCount;
+      any = true;
+    }
+    g_init_status = any ? MI_OK : MI_ERR_NO_DEVICE;
+  });
+  if (g_init_status != MI_OK) return fail(g_init_status, "no gfx950 device visible");
+  int d = 0;
+  if (hipGetDevice(&d) != hipSuccess || d < 0 || d >= 64 || !g_dev[d].ok)
+    return fail(MI_ERR_NO_DEVICE, "current device %d is not a gfx950", d);
+  return MI_OK;
+}
+
+int current_cus() {
+  int d = 0;
+  if (hipGetDevice(&d) != hipSuccess) return 256;
+  return (d >= 0 && d < 64 && g_dev[d].ok) ? g_dev[d].cus : 256;
+}
+
+// ---- kernel table ------------------------------------------------------------
+
+KernelFn pick_kernel(int dtype_in, int transA, int transB, int cfg) {
+  const int lay = (transA ? 2 : 0) | (transB ? 1 : 0);
+  if (dtype_in == MI_BF16) {
+    switch (lay) {
+      case 0: return pick_bf16_00(cfg);
+      case 1: return pick_bf16_01(cfg);
+      case 2: return pick_bf16_10(cfg);
+      default: return pick_bf16_11(cfg);
+    }
+  }
+  switch (lay) {
+    case 0: return pick_f32_00(cfg);
+    case 1: return pick_f32_01(cfg);
+    case 2: return pick_f32_10(cfg);
+    default: return pick_f32_11(cfg);
+  }
+}
+
+CfgShape shape_of(int dtype_in, int cfg) { return cfg_shape(dtype_in == MI_BF16, cfg); }
+
+// Split-K reduction: C = epilogue(alpha * sum_s ws[z][s]) in fixed split order.
+__global__ void __launch_bounds__(256) splitk_reduce_kernel(Params p) {
+  const int64_t per_z = (int64_t)p.M * ((p.N + 3) / 4);
+  const int64_t total = per_z * p.batch;
+  for (int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x; idx < total;
+       idx += (int64_t)gridDim.x * 256) {
+    const int z = (int)(idx / per_z);
+    const int64_t r = idx - (int64_t)z * per_z;
+    const int m = (int)(r / ((p.N + 3) / 4));
+    const int n = (int)(r - (int64_t)m * ((p.N + 3) / 4)) * 4;
+    float v[4] = {0.f, 0.f, 0.f, 0.f};
+    for (int s = 0; s < p.splits; ++s) {
+      const float* W = p.ws + ((int64_t)z * p.splits + s) * (int64_t)p.M * p.N + (int64_t)m * p.N;
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        if (n + e < p.N) v[e] += W[n + e];
+    }
+#pragma unroll
+    for (int e = 0; e < 4; ++e) v[e] *= p.alpha;
+    const int zo = z / p.heads, zi = z - (z / p.heads) * p.heads;
+    const int64_t coff = (int64_t)zo * p.cO + (int64_t)(zi / p.gC) * p.cI;
+    void* Cz = (char*)p.C + coff * (p.c_bf16 ? 2 : 4);
+    const void* Rz = p.R ? (const char*)p.R + ((int64_t)zo * p.rO + (int64_t)zi * p.rI) * (p.r_bf16 ? 2 : 4)
+                         : nullptr;
+    epilogue4(p, Cz, Rz, m, n, v);
+  }
+}
+
+// ---- planning ------------------------------------------------------------------
+
+struct Plan {
+  int cfg;
+  int splits;
+  int tiles_m, tiles_n;
+};
+
+int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
+
+// Pick the tile configuration and split-K factor with a small cost model:
+// time ~ (waves of workgroups over the CUs) x (per-workgroup MFMA time at the
+// configuration's sustained rate) + (split-K partial write/read traffic).
+Plan make_plan(int dtype_in, int64_t M, int64_t N, int64_t Ktot, int64_t batch, int mode,
+               bool allow_split, int64_t ws_limit_elems, int cus) {
+  Plan best{CFG_L, 1, 1, 1};
+  if (mode == MODE_DUAL) {
+    const CfgShape s = shape_of(dtype_in, CFG_DUAL);
+    return Plan{CFG_DUAL, 1, (int)cdiv(M, s.bm), (int)cdiv(N, s.bn)};
+  }
+  if (mode == MODE_PROLOGUE) {
+    const CfgShape s = shape_of(dtype_in, CFG_PRO);
+    return Plan{CFG_PRO, 1, (int)cdiv(M, s.bm), (int)cdiv(N, s.bn)};
+  }
+  const double peak_cu = (dtype_in == MI_BF16 ? 4096.0 : 256.0) * 2.4e9;  // FLOP/s per CU
+  const double hbm = 5.0e12;                                               // sustained B/s
+  double best_t = 1e30;
+  const int cfgs[2] = {CFG_L, CFG_S};
+  for (int ci = 0; ci < 2; ++ci) {
+    const int cfg = cfgs[ci];
+    const CfgShape s = shape_of(dtype_in, cfg);
+    const double eff = (cfg == CFG_L || dtype_in != MI_BF16) ? 0.80 : 0.55;
+    const int64_t tm = cdiv(M, s.bm), tn = cdiv(N, s.bn);
+    const int64_t tiles = tm * tn * batch;
+    for (int sp = 1; sp <= 16; ++sp) {
+      if (sp > 1 && (!allow_split || mode != MODE_PLAIN)) break;
+      if (sp > 1 && (int64_t)sp * M * N * batch > ws_limit_elems) break;
+      const int kt = dtype_in == MI_BF16 ? 64 : 32;
+      if (sp > 1 && cdiv(Ktot, kt) < 4 * sp) break;
+      const int64_t units = tiles * sp;
+      const double waves = std::ceil((double)units / cus);
+      const double t_unit = 2.0 * s.bm * s.bn * ((double)Ktot / sp) / (peak_cu * eff) + 2.0e-6 / 1.0;
+      double t = waves * t_unit;
+      if (sp > 1) t += (double)sp * M * N * batch * 4.0 * 2.0 / hbm + 4.0e-6;
+      if (t < best_t * 0.97) {
+        best_t = t;
+        best = Plan{cfg, sp, (int)tm, (int)tn};
+      }
+    }
+  }
+  return best;
+}
+
+bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
+
+struct Problem {
+  int transA, transB;
+  int64_t M, N, K;
+  float alpha, beta;
+  const void *A, *B;
+  int64_t lda, ldb;
+  int dtype_in;
+  void* C;
+  int64_t ldc;
+  int dtype_c;
+  mi_batch bt;
+  mi_epilogue ep;
+  void* ws;
+  size_t ws_bytes;
+};
+
+int validate(const Problem& P) {
+  if (P.M < 0 || P.N < 0 || P.K < 0) return fail(MI_ERR_SHAPE, "negative size M=%lld N=%lld K=%lld",
+                                                 (long long)P.M, (long long)P.N, (long long)P.K);
+  if (P.M > INT32_MAX || P.N > INT32_MAX || P.K > INT32_MAX)
+    return fail(MI_ERR_SHAPE, "size exceeds 2^31-1");
+  if (P.dtype_in != MI_F32 && P.dtype_in != MI_BF16)
+    return fail(MI_ERR_DTYPE, "input dtype %d not supported", P.dtype_in);
+  if (P.dtype_c != MI_F32 && P.dtype_c != MI_BF16)
+    return fail(MI_ERR_DTYPE, "output dtype %d not supported", P.dtype_c);
+  if (P.M == 0 || P.N == 0) return MI_OK;
+  if (!P.C) return fail(MI_ERR_NULL, "C is NULL");
+  if (P.ldc < P.N) return fail(MI_ERR_LD, "ldc=%lld < N=%lld", (long long)P.ldc, (long long)P.N);
+  if (P.K > 0) {
+    if (!P.A || !P.B) return fail(MI_ERR_NULL, "A or B is NULL");
+    const int64_t a_row = P.transA ? P.M : P.K, b_row = P.transB ? P.K : P.N;
+    if (P.lda < a_row) return fail(MI_ERR_LD, "lda=%lld < %lld", (long long)P.lda, (long long)a_row);
+    if (P.ldb < b_row) return fail(MI_ERR_LD, "ldb=%lld < %lld", (long long)P.ldb, (long long)b_row);
+  }
+  const mi_batch& b = P.bt;
+  if (b.batch < 1 || b.heads < 1 || b.a_group < 1 || b.b_group < 1 || b.c_group < 1 ||
+      b.k_segments < 1)
+    return fail(MI_ERR_SHAPE, "batch, heads, groups and k_segments must be >= 1");
+  if (b.batch > 65535LL * 1024) return fail(MI_ERR_SHAPE, "batch too large");
+  if (b.causal < MI_CAUSAL_NONE || b.causal > MI_CAUSAL_A_UPPER)
+    return fail(MI_ERR_SHAPE, "unknown causal mode %d", b.causal);
+  if (b.k_segments * P.K > INT32_MAX) return fail(MI_ERR_SHAPE, "total K exceeds 2^31-1");
+  const mi_epilogue& e = P.ep;
+  if (e.A2 && e.B2) return fail(MI_ERR_UNSUPPORTED, "A2 prologue and B2 dual-B cannot be combined");
+  if (e.A2 && P.transA) return fail(MI_ERR_UNSUPPORTED, "SiLU-gate prologue needs transA = 0");
+  if (e.residual && e.ldr < P.N) return fail(MI_ERR_LD, "ldr=%lld < N", (long long)e.ldr);
+  if (e.bias && e.bias_dtype != MI_F32 && e.bias_dtype != MI_BF16)
+    return fail(MI_ERR_DTYPE, "bias dtype %d", e.bias_dtype);
+  if (e.residual && e.residual_dtype != MI_F32 && e.residual_dtype != MI_BF16)
+    return fail(MI_ERR_DTYPE, "residual dtype %d", e.residual_dtype);
+  if (e.B2 && b.causal == MI_CAUSAL_OUT_LOWER)
+    return fail(MI_ERR_UNSUPPORTED, "dual-B with causal output mask");
+  return MI_OK;
+}
+
+int run(const Problem& P, hipStream_t stream) {
+  int st = validate(P);
+  if (st != MI_OK) return st;
+  if (P.M == 0 || P.N == 0) return MI_OK;
+  st = init_devices();
+  if (st != MI_OK) return st;
+
+  const int mode = P.ep.B2 ? MODE_DUAL : (P.ep.A2 ? MODE_PROLOGUE : MODE_PLAIN);
+  const int CH = P.dtype_in == MI_BF16 ? 8 : 4;
+  const mi_batch& b = P.bt;
+
+  // 16-byte operand loads need every chunk start 16-byte aligned.
+  auto mult = [&](int64_t v) { return v % CH == 0; };
+  const bool vecA = aligned16(P.A) && (!P.ep.A2 || aligned16(P.ep.A2)) && mult(P.lda) &&
+                    mult(b.a_outer) && mult(b.a_inner) && mult(b.seg_a);
+  const bool vecB = aligned16(P.B) && (!P.ep.B2 || aligned16(P.ep.B2)) && mult(P.ldb) &&
+                    mult(b.b_outer) && mult(b.b_inner) && mult(b.seg_b);
+  const int ce = P.dtype_c == MI_BF16 ? 8 : 16;  // bytes of 4 C elements
+  auto al = [](const void* p, int a) { return ((uintptr_t)p % a) == 0; };
+  const bool cvec = al(P.C, ce) && P.ldc % 4 == 0 && b.c_outer % 4 == 0 && b.c_inner % 4 == 0 &&
+                    (!P.ep.bias || al(P.ep.bias, P.ep.bias_dtype == MI_BF16 ? 8 : 16)) &&
+                    (!P.ep.residual || (al(P.ep.residual, P.ep.residual_dtype == MI_BF16 ? 8 : 16) &&
+                                        P.ep.ldr % 4 == 0 && b.r_outer % 4 == 0 && b.r_inner % 4 == 0));
+
+  const int64_t Ktot = P.K * b.k_segments;
+  const int64_t ws_elems = P.ws ? (int64_t)(P.ws_bytes / sizeof(float)) : 0;
+  const bool allow_split = ws_elems > 0 && aligned16(P.ws);
+  Plan plan = make_plan(P.dtype_in, P.M, P.N, Ktot, b.batch, mode, allow_split, ws_elems,
+                        current_cus());
+
+  KernelFn fn = pick_kernel(P.dtype_in, P.transA, P.transB, plan.cfg);
+  if (!fn) return fail(MI_ERR_UNSUPPORTED, "no kernel for this layout / mode");
+
+  Params p;
+  std::memset(&p, 0, sizeof(p));
+  p.A = P.A;
+  p.A2 = P.ep.A2;
+  p.B = P.B;
+  p.B2 = P.ep.B2;
+  p.C = P.C;
+  p.bias = P.ep.bias;
+  p.R = P.ep.residual;
+  p.ws = (float*)P.ws;
+  p.lda = P.lda;
+  p.ldb = P.ldb;
+  p.ldc = P.ldc;
+  p.ldr = P.ep.ldr;
+  p.segA = b.seg_a;
+  p.segB = b.seg_b;
+  p.aO = b.a_outer; p.aI = b.a_inner;
+  p.bO = b.b_outer; p.bI = b.b_inner;
+  p.cO = b.c_outer; p.cI = b.c_inner;
+  p.rO = b.r_outer; p.rI = b.r_inner;
+  p.M = (int)P.M;
+  p.N = (int)P.N;
+  p.K = (int)P.K;
+  p.nseg = (int)b.k_segments;
+  p.heads = (int)b.heads;
+  p.gA = (int)b.a_group;
+  p.gB = (int)b.b_group;
+  p.gC = (int)b.c_group;
+  p.tiles_m = plan.tiles_m;
+  p.tiles_n = plan.tiles_n;
+  p.splits = plan.splits;
+  p.batch = (int)b.batch;
+  p.causal = b.causal;
+  p.mask_value = b.mask_value;
+  p.alpha = P.alpha;
+  p.beta = P.beta;
+  p.c_bf16 = P.dtype_c == MI_BF16;
+  p.bias_bf16 = P.ep.bias_dtype == MI_BF16;
+  p.r_bf16 = P.ep.residual_dtype == MI_BF16;
+  p.vecA = vecA;
+  p.vecB = vecB;
+  p.cvec = cvec;
+
+  const int64_t nblocks = (int64_t)plan.tiles_m * plan.tiles_n * plan.splits * b.batch;
+  if (nblocks > INT32_MAX) return fail(MI_ERR_SHAPE, "too many tiles");
+  hipLaunchKernelGGL(fn, dim3((unsigned)nblocks), dim3(256), 0, stream, p);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return fail(MI_ERR_HIP, "gemm launch: %s", hipGetErrorString(e));
+  if (plan.splits > 1) {
+    const int64_t work = b.batch * P.M * ((P.N + 3) / 4);
+    const int64_t grid = std::min<int64_t>(cdiv(work, 256), 8 * (int64_t)current_cus());
+    hipLaunchKernelGGL(splitk_reduce_kernel, dim3((unsigned)grid), dim3(256), 0, stream, p);
+    e = hipGetLastError();
+    if (e != hipSuccess) return fail(MI_ERR_HIP, "split-K reduce launch: %s", hipGetErrorString(e));
+  }
+  return MI_OK;
+}
+
+mi_batch single_batch() {
+  mi_batch b;
+  std::memset(&b, 0, sizeof(b));
+  b.batch = 1;
+  b.heads = 1;
+  b.a_group = b.b_group = b.c_group = 1;
+  b.k_segments = 1;
+  return b;
+}
+
+// ---- aux kernels -----------------------------------------------------------------
+
+template <bool BF>
+__device__ __forceinline__ float ldv(const void* p, int64_t i) {
+  if constexpr (BF) return bf16_bits_to_f32(((const uint16_t*)p)[i]);
+  else return ((const float*)p)[i];
+}
+template <bool BF>
+__device__ __forceinline__ void stv(void* p, int64_t i, float v) {
+  if constexpr (BF) ((uint16_t*)p)[i] = (uint16_t)f32_to_bf16_rne(v);
+  else ((float*)p)[i] = v;
+}
+
+template <bool BF>
+__global__ void __launch_bounds__(256) residual_add_kernel(void* a, const void* b, int64_t n) {
+  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (int64_t)gridDim.x * 256)
+    stv<BF>(a, i, ldv<BF>(a, i) + ldv<BF>(b, i));
+}
+
+__device__ __forceinline__ float block_reduce(float v, bool is_max, float* red) {
+  for (int o = 32; o > 0; o >>= 1) {
+    const float w = __shfl_xor(v, o, 64);
+    v = is_max ? fmaxf(v, w) : v + w;
+  }
+  const int wid = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  __syncthreads();
+  if (lane == 0) red[wid] = v;
+  __syncthreads();
+  float r = red[0];
+  for (int i = 1; i < 4; ++i) r = is_max ? fmaxf(r, red[i]) : r + red[i];
+  return r;
+}
+
+// One workgroup per row; row r is query position q = r % T.
+template <bool BF>
+__global__ void __launch_bounds__(256) softmax_causal_kernel(void* S, int64_t T, int64_t ld) {
+  __shared__ float red[4];
+  const int64_t row = blockIdx.x;
+  const int64_t q = row % T;
+  const int64_t base = row * ld;
+  float mx = -INFINITY;
+  for (int64_t k = threadIdx.x; k <= q; k += 256) mx = fmaxf(mx, ldv<BF>(S, base + k));
+  mx = block_reduce(mx, true, red);
+  float sum = 0.f;
+  for (int64_t k = threadIdx.x; k <= q; k += 256) sum += __expf(ldv<BF>(S, base + k) - mx);
+  sum = block_reduce(sum, false, red);
+  const float inv = 1.0f / sum;
+  for (int64_t k = threadIdx.x; k < T; k += 256)
+    stv<BF>(S, base + k, k <= q ? __expf(ldv<BF>(S, base + k) - mx) * inv : 0.0f);
+}
+
+template <bool BF>
+__global__ void __launch_bounds__(256) softmax_bwd_kernel(const void* P, void* dP, int64_t T,
+                                                          int64_t ld, float scale) {
+  __shared__ float red[4];
+  const int64_t row = blockIdx.x;
+  const int64_t base = row * ld;
+  float s = 0.f;
+  for (int64_t k = threadIdx.x; k < T; k += 256) s += ldv<BF>(P, base + k) * ldv<BF>(dP, base + k);
+  s = block_reduce(s, false, red);
+  for (int64_t k = threadIdx.x; k < T; k += 256) {
+    const float p = ldv<BF>(P, base + k);
+    stv<BF>(dP, base + k, p * (ldv<BF>(dP, base + k) - s) * scale);
+  }
+}
+
+}  // namespace
+
+// ---- C ABI -------------------------------------------------------------------------
+
+extern "C" {
+
+int mi_init(void) { return init_devices(); }
+
+const char* mi_last_error(void) { return g_err.c_str(); }
+
+const char* mi_version(void) { return "mi_gemm 0.1 (gfx950)"; }
+
+size_t mi_gemm_workspace_size(int transA, int transB, int64_t M, int64_t N, int64_t K,
+                              int32_t dtype_in, int32_t dtype_c, int64_t batch) {
+  (void)transA; (void)transB; (void)dtype_c;
+  if (M <= 0 || N <= 0 || K <= 0 || batch <= 0) return 0;
+  int cus = 256;
+  if (init_devices() == MI_OK) cus = current_cus();
+  const Plan pl = make_plan(dtype_in, M, N, K, batch, MODE_PLAIN, true, INT64_MAX / 8, cus);
+  return pl.splits > 1 ? (size_t)pl.splits * (size_t)M * (size_t)N * (size_t)batch * sizeof(float) : 0;
+}
+
+int mi_gemm(void* stream, int transA, int transB, int64_t M, int64_t N, int64_t K, float alpha,
+            const void* A, int64_t lda, const void* B, int64_t ldb, int32_t dtype_in, float beta,
+            void* C, int64_t ldc, int32_t dtype_c, const mi_epilogue* epi, void* workspace,
+            size_t workspace_bytes) {
+  Problem P;
+  P.transA = transA;
+  P.transB = transB;
+  P.M = M; P.N = N; P.K = K;
+  P.alpha = alpha; P.beta = beta;
+  P.A = A; P.B = B; P.lda = lda; P.ldb = ldb;
+  P.dtype_in = dtype_in;
+  P.C = C; P.ldc = ldc; P.dtype_c = dtype_c;
+  P.bt = single_batch();
+  if (epi) P.ep = *epi;
+  else std::memset(&P.ep, 0, sizeof(P.ep));
+  P.ws = workspace;
+  P.ws_bytes = workspace_bytes;
+  return run(P, (hipStream_t)stream);
+}
+
+int mi_gemm_batched(void* stream, int transA, int transB, int64_t M, int64_t N, int64_t K,
+                    float alpha, const void* A, int64_t lda, const void* B, int64_t ldb,
+                    int32_t dtype_in, float beta, void* C, int64_t ldc, int32_t dtype_c,
+                    const mi_batch* batch, const mi_epilogue* epi, void* workspace,
+                    size_t workspace_bytes) {
+  if (!batch) return fail(MI_ERR_NULL, "batch descriptor is NULL");
+  Problem P;
+  P.transA = transA;
+  P.transB = transB;
+  P.M = M; P.N = N; P.K = K;
+  P.alpha = alpha; P.beta = beta;
+  P.A = A; P.B = B; P.lda = lda; P.ldb = ldb;
+  P.dtype_in = dtype_in;
+  P.C = C; P.ldc = ldc; P.dtype_c = dtype_c;
+  P.bt = *batch;
+  if (epi) P.ep = *epi;
+  else std::memset(&P.ep, 0, sizeof(P.ep));
+  P.ws = workspace;
+  P.ws_bytes = workspace_bytes;
+  return run(P, (hipStream_t)stream);
+}
+
+int mi_residual_add(void* stream, void* a, const void* b, int64_t n, int32_t dtype) {
+  if (n < 0) return fail(MI_ERR_SHAPE, "negative n");
+  if (n == 0) return MI_OK;
+  if (!a || !b) return fail(MI_ERR_NULL, "a or b is NULL");
+  if (dtype != MI_F32 && dtype != MI_BF16) return fail(MI_ERR_DTYPE, "dtype %d", dtype);
+  int st = init_devices();
+  if (st != MI_OK) return st;
+  const int64_t grid = std::min<int64_t>(cdiv(n, 256), 16 * (int64_t)current_cus());
+  if (dtype == MI_BF16)
+    hipLaunchKernelGGL(residual_add_kernel<true>, dim3((unsigned)grid), dim3(256), 0,
+                       (hipStream_t)stream, a, b, n);
+  else
+    hipLaunchKernelGGL(residual_add_kernel<false>, dim3((unsigned)grid), dim3(256), 0,
+                       (hipStream_t)stream, a, b, n);
+  hipError_t e = hipGetLastError();
+  return e == hipSuccess ? MI_OK : fail(MI_ERR_HIP, "residual_add: %s", hipGetErrorString(e));
+}
+
+int mi_softmax_causal(void* stream, void* S, int64_t rows, int64_t T, int64_t ld, int32_t dtype) {
+  if (rows < 0 || T < 0) return fail(MI_ERR_SHAPE, "negative size");
+  if (rows == 0 || T == 0) return MI_OK;
+  if (!S) return fail(MI_ERR_NULL, "S is NULL");
+  if (ld < T) return fail(MI_ERR_LD, "ld < T");
+  if (rows > INT32_MAX) return fail(MI_ERR_SHAPE, "too many rows");
+  if (dtype != MI_F32 && dtype != MI_BF16) return fail(MI_ERR_DTYPE, "dtype %d", dtype);
+  int st = init_devices();
+  if (st != MI_OK) return st;
+  if (dtype == MI_BF16)
+    hipLaunchKernelGGL(softmax_causal_kernel<true>, dim3((unsigned)rows), dim3(256), 0,
+                       (hipStream_t)stream, S, T, ld);
+  else
+    hipLaunchKernelGGL(softmax_causal_kernel<false>, dim3((unsigned)rows), dim3(256), 0,
+                       (hipStream_t)stream, S, T, ld);
+  hipError_t e = hipGetLastError();
+  return e == hipSuccess ? MI_OK : fail(MI_ERR_HIP, "softmax: %s", hipGetErrorString(e));
+}
+
+int mi_softmax_bwd(void* stream, const void* P, void* dP, int64_t rows, int64_t T, int64_t ld,
+                   float scale, int32_t dtype) {
+  if (rows < 0 || T < 0) return fail(MI_ERR_SHAPE, "negative size");
+  if (rows == 0 || T == 0) return MI_OK;
+  if (!P || !dP) return fail(MI_ERR_NULL, "P or dP is NULL");
+  if (ld < T) return fail(MI_ERR_LD, "ld < T");
+  if (rows > INT32_MAX) return fail(MI_ERR_SHAPE, "too many rows");
+  if (dtype != MI_F32 && dtype != MI_BF16) return fail(MI_ERR_DTYPE, "dtype %d", dtype);
+  int st = init_devices();
+  if (st != MI_OK) return st;
+  if (dtype == MI_BF16)
+    hipLaunchKernelGGL(softmax_bwd_kernel<true>, dim3((unsigned)rows), dim3(256), 0,
+                       (hipStream_t)stream, P, dP, T, ld, scale);
+  else
+    hipLaunchKernelGGL(softmax_bwd_kernel<false>, dim3((unsigned)rows), dim3(256), 0,
+                       (hipStream_t)stream, P, dP, T, ld, scale);
+  hipError_t e = hipGetLastError();
+  return e == hipSuccess ? MI_OK : fail(MI_ERR_HIP, "softmax_bwd: %s", hipGetErrorString(e));
+}
+
+int mi_stream_sync(void* stream) {
+  hipError_t e = hipStreamSynchronize((hipStream_t)stream);
+  return e == hipSuccess ? MI_OK : fail(MI_ERR_HIP, "sync: %s", hipGetErrorString(e));
+}
+
+}  // extern "C"

@@ -1,0 +1,579 @@
+// mi_gemm_device.hpp -- device code of the gfx950 GEMM core.
+//
+// One kernel template covers every matmul of the reference engine's decoder
+// block (Tensor::matmul, Tensor.cpp:174-228, and the metal_bridge GEMM entry
+// points, MetalBridge.hpp:39-46,119-125):
+//   * bf16 inputs -> v_mfma_f32_32x32x16_bf16, fp32 inputs -> v_mfma_f32_32x32x2f32,
+//     fp32 accumulation in both cases;
+//   * any transpose combination: an operand whose K index is contiguous in memory
+//     ("K-contiguous") is copied chunk-for-chunk into LDS; an operand whose M/N
+//     index is contiguous is loaded as 16-byte rows of a small (k x row) block and
+//     transposed in registers before the LDS write, so LDS always holds
+//     [row][K-tile] tiles and the MFMA fragments are single ds_read_b128s;
+//   * LDS rows are 128 bytes (64 bf16 / 32 fp32) in 16-byte chunks whose position
+//     is XOR-swizzled by the row, so the fragment reads (16 consecutive rows per
+//     LDS cycle, one chunk column) and the tile writes are bank-conflict free;
+//   * two LDS buffers: global loads for tile k+1 are issued into registers before
+//     the MFMAs of tile k, stored to the other buffer after, one barrier per tile;
+//   * fused epilogue (alpha, bias, beta*C, residual, bf16/fp32 output, causal
+//     mask), dual-B SiLU-gate (gemm_ffn.metal:160-181) and SiLU-gate A prologue
+//     (fused_swiglu_gemm.metal:48-77);
+//   * strided batches with a GQA head->kv-head map and K segments (the KV-group
+//     reduction of Attention.cpp:332,344-345) and causal tile skipping;
+//   * split-K over a caller workspace, reduced deterministically by a second kernel.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace mig {
+
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef float f32x16_t __attribute__((ext_vector_type(16)));
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
+
+enum { MODE_PLAIN = 0, MODE_DUAL = 1, MODE_PROLOGUE = 2 };
+enum { CAUSAL_NONE = 0, CAUSAL_OUT_LOWER = 1, CAUSAL_A_LOWER = 2, CAUSAL_A_UPPER = 3 };
+
+struct Params {
+  const void* A;
+  const void* A2;
+  const void* B;
+  const void* B2;
+  void* C;
+  const void* bias;
+  const void* R;
+  float* ws;
+  int64_t lda, ldb, ldc, ldr;
+  int64_t segA, segB;
+  int64_t aO, aI, bO, bI, cO, cI, rO, rI;
+  int M, N, K, nseg;
+  int heads, gA, gB, gC;
+  int tiles_m, tiles_n, splits, batch;
+  int causal;
+  float mask_value;
+  float alpha, beta;
+  int c_bf16, bias_bf16, r_bf16;
+  int vecA, vecB;  // 16-byte global loads legal for A (and A2) / B (and B2)
+  int cvec;        // 4-wide C / R / bias accesses legal
+};
+
+// ---------------------------------------------------------------------------
+// scalar helpers
+
+__device__ __forceinline__ float bf16_bits_to_f32(uint32_t h) {
+  return __uint_as_float(h << 16);
+}
+
+__device__ __forceinline__ uint32_t f32_to_bf16_rne(float f) {
+  uint32_t b = __float_as_uint(f);
+  if ((b & 0x7fffffffu) > 0x7f800000u) return (b >> 16) | 0x40u;  // quiet NaN
+  b += 0x7fffu + ((b >> 16) & 1u);
+  return b >> 16;
+}
+
+__device__ __forceinline__ float silu_f(float x) { return x / (1.0f + __expf(-x)); }
+
+// Chunk position of chunk c (0..7) in LDS row r.  For any 16 consecutive rows
+// read at one chunk column, (r & 1, position) is distinct, and for any 8
+// consecutive rows the position is distinct: conflict-free for both a 32-bank
+// and a 64-bank 4-byte LDS.
+__device__ __forceinline__ int swz(int r, int c) { return c ^ ((r ^ (r >> 3)) & 7); }
+
+template <typename T>
+struct ElemTraits;
+template <>
+struct ElemTraits<float> {
+  static constexpr int CH = 4;  // elements per 16-byte chunk
+  __device__ static uint32_t bits(const void* p, int64_t i) { return ((const uint32_t*)p)[i]; }
+};
+template <>
+struct ElemTraits<__bf16> {
+  static constexpr int CH = 8;
+  __device__ static uint32_t bits(const void* p, int64_t i) { return ((const uint16_t*)p)[i]; }
+};
+
+// Pack CH scalar bit patterns into a 16-byte chunk.
+template <typename T>
+__device__ __forceinline__ u32x4_t pack_chunk(const uint32_t* e) {
+  u32x4_t v;
+  if constexpr (sizeof(T) == 4) {
+    v[0] = e[0]; v[1] = e[1]; v[2] = e[2]; v[3] = e[3];
+  } else {
+    v[0] = e[0] | (e[1] << 16); v[1] = e[2] | (e[3] << 16);
+    v[2] = e[4] | (e[5] << 16); v[3] = e[6] | (e[7] << 16);
+  }
+  return v;
+}
+
+// Load the 16-byte chunk of CH consecutive elements starting at element index
+// `i` of `p`, `n_ok` of which are in bounds (0..CH).  vec: the chunk is
+// 16-byte aligned and the fast path may be used.
+template <typename T>
+__device__ __forceinline__ u32x4_t load_chunk(const void* p, int64_t i, int n_ok, bool vec) {
+  constexpr int CH = ElemTraits<T>::CH;
+  if (n_ok >= CH && vec) return *(const u32x4_t*)((const T*)p + i);
+  uint32_t e[CH];
+#pragma unroll
+  for (int j = 0; j < CH; ++j) e[j] = (j < n_ok) ? ElemTraits<T>::bits(p, i + j) : 0u;
+  return pack_chunk<T>(e);
+}
+
+// Transpose a CH x CH block held as CH chunks (chunk kk = CH consecutive rows at
+// k = kk) into CH chunks (chunk j = CH consecutive k of row j).
+template <typename T>
+__device__ __forceinline__ void transpose_block(const u32x4_t* in, u32x4_t* out) {
+  if constexpr (sizeof(T) == 4) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      out[j][0] = in[0][j]; out[j][1] = in[1][j]; out[j][2] = in[2][j]; out[j][3] = in[3][j];
+    }
+  } else {
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const uint32_t a = in[2 * q][j >> 1], b = in[2 * q + 1][j >> 1];
+        out[j][q] = (j & 1) ? ((a >> 16) | (b & 0xffff0000u)) : ((a & 0xffffu) | (b << 16));
+      }
+    }
+  }
+}
+
+// SiLU(g)*u on a chunk pair, re-encoded in T.
+template <typename T>
+__device__ __forceinline__ u32x4_t swiglu_chunk(u32x4_t g, u32x4_t u) {
+  u32x4_t o;
+  if constexpr (sizeof(T) == 4) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      o[j] = __float_as_uint(silu_f(__uint_as_float(g[j])) * __uint_as_float(u[j]));
+  } else {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const float g0 = bf16_bits_to_f32(g[j] & 0xffffu), g1 = bf16_bits_to_f32(g[j] >> 16);
+      const float u0 = bf16_bits_to_f32(u[j] & 0xffffu), u1 = bf16_bits_to_f32(u[j] >> 16);
+      o[j] = f32_to_bf16_rne(silu_f(g0) * u0) | (f32_to_bf16_rne(silu_f(g1) * u1) << 16);
+    }
+  }
+  return o;
+}
+
+// ---------------------------------------------------------------------------
+// Tile loader: R rows x KT (= 8 chunks) of one operand, global -> registers -> LDS.
+//   KC = true : element (r, k) at r*ld + k   (K-contiguous)
+//   KC = false: element (r, k) at k*ld + r   (row-contiguous; transposed in registers)
+// PRO (prologue): the operand is SiLU(X) * X2, computed at LDS-store time.
+
+template <typename T, int R, bool KC, bool PRO>
+struct TileLoader {
+  static constexpr int CH = ElemTraits<T>::CH;
+  static constexpr int NT = 256;
+  // K-contiguous: R*8 chunks over 256 threads.
+  static constexpr int NCK = (R * 8 + NT - 1) / NT;
+  // Row-contiguous: 8*(R/CH) blocks of CH x CH, each CH chunks.
+  static constexpr int NBLK_TOT = 8 * (R / CH);
+  static constexpr int NBLK = (NBLK_TOT + NT - 1) / NT;
+  static constexpr int NREG = KC ? NCK : NBLK * CH;
+  u32x4_t st[NREG];
+  u32x4_t st2[PRO ? NREG : 1];
+
+  // base: operand pointer for the current batch/segment.  rows: valid row count
+  // (M or N).  row0: first tile row.  k0: first K of the tile; kseg: K extent.
+  __device__ __forceinline__ void load(const void* base, const void* base2, int64_t ld, int rows,
+                                       int row0, int k0, int kseg, bool vec) {
+    const int tid = threadIdx.x;
+    if constexpr (KC) {
+#pragma unroll
+      for (int i = 0; i < NCK; ++i) {
+        const int idx = tid + NT * i;
+        const int r = idx >> 3, c = idx & 7;
+        const int grow = row0 + r, gk = k0 + c * CH;
+        int n_ok = (grow < rows && idx < R * 8) ? kseg - gk : 0;
+        n_ok = n_ok < 0 ? 0 : (n_ok > CH ? CH : n_ok);
+        const int64_t off = (int64_t)grow * ld + gk;
+        st[i] = load_chunk<T>(base, off, n_ok, vec);
+        if constexpr (PRO) st2[i] = load_chunk<T>(base2, off, n_ok, vec);
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < NBLK; ++i) {
+        const int b = tid + NT * i;
+        const int rb = b % (R / CH), kb = b / (R / CH);
+        const int grow = row0 + rb * CH;
+        int n_ok = (b < NBLK_TOT) ? rows - grow : 0;
+        n_ok = n_ok < 0 ? 0 : (n_ok > CH ? CH : n_ok);
+#pragma unroll
+        for (int kk = 0; kk < CH; ++kk) {
+          const int gk = k0 + kb * CH + kk;
+          const int nk = (gk < kseg) ? n_ok : 0;
+          const int64_t off = (int64_t)gk * ld + grow;
+          st[i * CH + kk] = load_chunk<T>(base, off, nk, vec);
+          if constexpr (PRO) st2[i * CH + kk] = load_chunk<T>(base2, off, nk, vec);
+        }
+      }
+    }
+  }
+
+  // lds: this operand's region, R rows of 8 chunks.
+  __device__ __forceinline__ void store(u32x4_t* lds) {
+    const int tid = threadIdx.x;
+    if constexpr (KC) {
+#pragma unroll
+      for (int i = 0; i < NCK; ++i) {
+        const int idx = tid + NT * i;
+        if (NCK * NT == R * 8 || idx < R * 8) {
+          const int r = idx >> 3, c = idx & 7;
+          u32x4_t v = st[i];
+          if constexpr (PRO) v = swiglu_chunk<T>(st[i], st2[i]);
+          lds[r * 8 + swz(r, c)] = v;
+        }
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < NBLK; ++i) {
+        const int b = tid + NT * i;
+        if (NBLK * NT == NBLK_TOT || b < NBLK_TOT) {
+          const int rb = b % (R / CH), kb = b / (R / CH);
+          u32x4_t in[CH], out[CH];
+#pragma unroll
+          for (int kk = 0; kk < CH; ++kk) {
+            in[kk] = st[i * CH + kk];
+            if constexpr (PRO) in[kk] = swiglu_chunk<T>(st[i * CH + kk], st2[i * CH + kk]);
+          }
+          transpose_block<T>(in, out);
+#pragma unroll
+          for (int j = 0; j < CH; ++j) {
+            const int r = rb * CH + j;
+            lds[r * 8 + swz(r, kb)] = out[j];
+          }
+        }
+      }
+    }
+  }
+};
+
+// ---------------------------------------------------------------------------
+// Epilogue for 4 consecutive columns n..n+3 of row m.  v holds the finished
+// alpha-scaled (or SiLU-gated) accumulator values.
+
+__device__ __forceinline__ float ld_any(const void* p, int64_t i, int is_bf16) {
+  return is_bf16 ? bf16_bits_to_f32(((const uint16_t*)p)[i]) : ((const float*)p)[i];
+}
+
+__device__ __forceinline__ void epilogue4(const Params& p, void* Cz, const void* Rz, int m, int n,
+                                          float v[4]) {
+  if (m >= p.M || n >= p.N) return;
+  const bool full = (n + 3 < p.N) && p.cvec;
+  const int64_t ci = (int64_t)m * p.ldc + n;
+  if (p.bias) {
+    if (full) {
+      if (p.bias_bf16) {
+        const u32x2_t b = *(const u32x2_t*)((const uint16_t*)p.bias + n);
+        v[0] += bf16_bits_to_f32(b[0] & 0xffffu); v[1] += bf16_bits_to_f32(b[0] >> 16);
+        v[2] += bf16_bits_to_f32(b[1] & 0xffffu); v[3] += bf16_bits_to_f32(b[1] >> 16);
+      } else {
+        const f32x4_t b = *(const f32x4_t*)((const float*)p.bias + n);
+        v[0] += b[0]; v[1] += b[1]; v[2] += b[2]; v[3] += b[3];
+      }
+    } else {
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        if (n + e < p.N) v[e] += ld_any(p.bias, n + e, p.bias_bf16);
+    }
+  }
+  if (p.beta != 0.0f) {
+    if (full) {
+      if (p.c_bf16) {
+        const u32x2_t c = *(const u32x2_t*)((const uint16_t*)Cz + ci);
+        v[0] += p.beta * bf16_bits_to_f32(c[0] & 0xffffu);
+        v[1] += p.beta * bf16_bits_to_f32(c[0] >> 16);
+        v[2] += p.beta * bf16_bits_to_f32(c[1] & 0xffffu);
+        v[3] += p.beta * bf16_bits_to_f32(c[1] >> 16);
+      } else {
+        const f32x4_t c = *(const f32x4_t*)((const float*)Cz + ci);
+        v[0] += p.beta * c[0]; v[1] += p.beta * c[1];
+        v[2] += p.beta * c[2]; v[3] += p.beta * c[3];
+      }
+    } else {
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        if (n + e < p.N) v[e] += p.beta * ld_any(Cz, ci + e, p.c_bf16);
+    }
+  }
+  if (Rz) {
+    const int64_t ri = (int64_t)m * p.ldr + n;
+    if (full) {
+      if (p.r_bf16) {
+        const u32x2_t r = *(const u32x2_t*)((const uint16_t*)Rz + ri);
+        v[0] += bf16_bits_to_f32(r[0] & 0xffffu); v[1] += bf16_bits_to_f32(r[0] >> 16);
+        v[2] += bf16_bits_to_f32(r[1] & 0xffffu); v[3] += bf16_bits_to_f32(r[1] >> 16);
+      } else {
+        const f32x4_t r = *(const f32x4_t*)((const float*)Rz + ri);
+        v[0] += r[0]; v[1] += r[1]; v[2] += r[2]; v[3] += r[3];
+      }
+    } else {
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        if (n + e < p.N) v[e] += ld_any(Rz, ri + e, p.r_bf16);
+    }
+  }
+  if (p.causal == CAUSAL_OUT_LOWER) {
+#pragma unroll
+    for (int e = 0; e < 4; ++e)
+      if (n + e > m) v[e] = p.mask_value;
+  }
+  if (full) {
+    if (p.c_bf16) {
+      u32x2_t o;
+      o[0] = f32_to_bf16_rne(v[0]) | (f32_to_bf16_rne(v[1]) << 16);
+      o[1] = f32_to_bf16_rne(v[2]) | (f32_to_bf16_rne(v[3]) << 16);
+      *(u32x2_t*)((uint16_t*)Cz + ci) = o;
+    } else {
+      f32x4_t o = {v[0], v[1], v[2], v[3]};
+      *(f32x4_t*)((float*)Cz + ci) = o;
+    }
+  } else {
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      if (n + e < p.N) {
+        if (p.c_bf16)
+          ((uint16_t*)Cz)[ci + e] = (uint16_t)f32_to_bf16_rne(v[e]);
+        else
+          ((float*)Cz)[ci + e] = v[e];
+      }
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Work decomposition shared by the GEMM and the split-K reduction.
+
+struct TileCoord {
+  int z, split, tm, tn;
+};
+
+// Hardware hands workgroup b to XCD (b mod 8).  Renumber so each XCD receives a
+// contiguous range of logical tiles, then order tiles in groups of GROUP_M tile
+// rows so that the workgroups resident on one XCD share A and B panels in its L2.
+__device__ __forceinline__ TileCoord map_tile(int bid, int nblocks, int tiles_m, int tiles_n,
+                                              int splits) {
+  constexpr int NXCD = 8, GROUP_M = 8;
+  const int q = nblocks / NXCD, rem = nblocks % NXCD;
+  const int x = bid % NXCD, j = bid / NXCD;
+  const int lid = x * q + (x < rem ? x : rem) + j;
+  const int tiles = tiles_m * tiles_n;
+  TileCoord tc;
+  const int zs = lid / tiles;
+  int t = lid - zs * tiles;
+  tc.z = zs / splits;
+  tc.split = zs - tc.z * splits;
+  const int group = GROUP_M * tiles_n;
+  const int g = t / group;
+  const int first_m = g * GROUP_M;
+  const int gm = (tiles_m - first_m) < GROUP_M ? (tiles_m - first_m) : GROUP_M;
+  t -= g * group;
+  tc.tm = first_m + t % gm;
+  tc.tn = t / gm;
+  return tc;
+}
+
+// ---------------------------------------------------------------------------
+// The GEMM kernel.
+//   AK: A is K-contiguous (transA == 0).   BK: B is K-contiguous (transB == 1).
+//   Tile BM x BN (output), KT = 8 chunks of K per LDS stage, 4 waves in a
+//   WGM x WGN grid, each wave computing a (BM/WGM) x (BN/WGN) block from 32x32
+//   MFMA tiles.  MODE_DUAL keeps a second accumulator set for B2 (LDS B region
+//   holds 2*BN rows: B then B2).
+
+template <typename T, int BM, int BN, int WGM, int WGN, bool AK, bool BK, int MODE>
+__global__ void __launch_bounds__(256) gemm_kernel(Params p) {
+  constexpr int CH = ElemTraits<T>::CH;
+  constexpr int KT = 8 * CH;
+  constexpr int BROWS = (MODE == MODE_DUAL) ? 2 * BN : BN;
+  constexpr int WTM = BM / WGM, WTN = BN / WGN;
+  constexpr int TM = WTM / 32, TN = WTN / 32;
+  constexpr int NB = (MODE == MODE_DUAL) ? 2 * TN : TN;
+  constexpr bool PRO = (MODE == MODE_PROLOGUE);
+  static_assert(WGM * WGN == 4, "4 waves per workgroup");
+  static_assert(TM >= 1 && TN >= 1, "wave tile must hold one 32x32 MFMA tile");
+
+  __shared__ u32x4_t smem[2][(BM + BROWS) * 8];
+
+  const int nblocks = gridDim.x;
+  const TileCoord tc = map_tile(blockIdx.x, nblocks, p.tiles_m, p.tiles_n, p.splits);
+  const int m0 = tc.tm * BM, n0 = tc.tn * BN;
+  const int zo = tc.z / p.heads, zi = tc.z - (tc.z / p.heads) * p.heads;
+  const T* Ab = (const T*)p.A + (int64_t)zo * p.aO + (int64_t)(zi / p.gA) * p.aI;
+  const T* A2b = PRO ? (const T*)p.A2 + (int64_t)zo * p.aO + (int64_t)(zi / p.gA) * p.aI : nullptr;
+  const T* Bb = (const T*)p.B + (int64_t)zo * p.bO + (int64_t)(zi / p.gB) * p.bI;
+  const T* B2b = (MODE == MODE_DUAL) ? (const T*)p.B2 + (int64_t)zo * p.bO + (int64_t)(zi / p.gB) * p.bI
+                                      : nullptr;
+  const int64_t coff = (int64_t)zo * p.cO + (int64_t)(zi / p.gC) * p.cI;
+  const int esz_c = p.c_bf16 ? 2 : 4;
+  void* Cz = (char*)p.C + coff * esz_c;
+  const void* Rz = p.R ? (const char*)p.R + ((int64_t)zo * p.rO + (int64_t)zi * p.rI) * (p.r_bf16 ? 2 : 4)
+                       : nullptr;
+
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int wm = wave / WGN, wn = wave % WGN;
+
+  // Fully masked causal tile: only the mask value is written.
+  if (p.causal == CAUSAL_OUT_LOWER && n0 > m0 + BM - 1) {
+    if (p.splits > 1) return;  // the reduction kernel writes the mask
+    for (int idx = threadIdx.x; idx < BM * (BN / 4); idx += 256) {
+      const int r = idx / (BN / 4), c4 = idx % (BN / 4);
+      float v[4] = {0.f, 0.f, 0.f, 0.f};
+      Params q = p;
+      q.bias = nullptr;
+      q.beta = 0.f;
+      epilogue4(q, Cz, nullptr, m0 + r, n0 + c4 * 4, v);
+    }
+    return;
+  }
+
+  // K iteration space: per segment, K tiles [klo, khi); causal skipping.
+  const int kt_seg = (p.K + KT - 1) / KT;
+  int klo = 0, khi = kt_seg;
+  if (p.causal == CAUSAL_A_LOWER) {
+    const int lim = (m0 + BM + KT - 1) / KT;
+    khi = khi < lim ? khi : lim;
+  } else if (p.causal == CAUSAL_A_UPPER) {
+    klo = m0 / KT;
+  }
+  const int per_seg = khi > klo ? khi - klo : 0;
+  const int total = per_seg * p.nseg;
+  const int it0 = (int)((int64_t)total * tc.split / p.splits);
+  const int it1 = (int)((int64_t)total * (tc.split + 1) / p.splits);
+
+  f32x16_t acc[TM][NB];
+#pragma unroll
+  for (int i = 0; i < TM; ++i)
+#pragma unroll
+    for (int j = 0; j < NB; ++j)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.0f;
+
+  TileLoader<T, BM, AK, PRO> la;
+  TileLoader<T, BN, BK, false> lb;
+  TileLoader<T, (MODE == MODE_DUAL) ? BN : 32, BK, false> lb2;
+
+  auto issue_loads = [&](int it) {
+    const int seg = it / per_seg;
+    const int k0 = (klo + (it - seg * per_seg)) * KT;
+    la.load(Ab + (int64_t)seg * p.segA, PRO ? (const void*)(A2b + (int64_t)seg * p.segA) : nullptr,
+            p.lda, p.M, m0, k0, p.K, p.vecA);
+    lb.load(Bb + (int64_t)seg * p.segB, nullptr, p.ldb, p.N, n0, k0, p.K, p.vecB);
+    if constexpr (MODE == MODE_DUAL)
+      lb2.load(B2b + (int64_t)seg * p.segB, nullptr, p.ldb, p.N, n0, k0, p.K, p.vecB);
+  };
+  auto commit_stores = [&](int buf) {
+    la.store(&smem[buf][0]);
+    lb.store(&smem[buf][BM * 8]);
+    if constexpr (MODE == MODE_DUAL) lb2.store(&smem[buf][(BM + BN) * 8]);
+  };
+
+  if (it0 < it1) {
+    issue_loads(it0);
+    commit_stores(0);
+  }
+  __syncthreads();
+
+  const int lrow = lane & 31, lhalf = lane >> 5;
+  for (int it = it0; it < it1; ++it) {
+    const int cur = (it - it0) & 1;
+    const bool more = it + 1 < it1;
+    if (more) issue_loads(it + 1);
+
+    const u32x4_t* sA = &smem[cur][0];
+    const u32x4_t* sB = &smem[cur][BM * 8];
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+      const int c = 2 * s + lhalf;
+      u32x4_t af[TM], bfr[NB];
+#pragma unroll
+      for (int i = 0; i < TM; ++i) {
+        const int r = wm * WTM + i * 32 + lrow;
+        af[i] = sA[r * 8 + swz(r, c)];
+      }
+#pragma unroll
+      for (int j = 0; j < NB; ++j) {
+        const int half = (MODE == MODE_DUAL) ? (j / TN) : 0;
+        const int jj = (MODE == MODE_DUAL) ? (j % TN) : j;
+        const int r = half * BN + wn * WTN + jj * 32 + lrow;
+        bfr[j] = sB[r * 8 + swz(r, c)];
+      }
+#pragma unroll
+      for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int j = 0; j < NB; ++j) {
+          if constexpr (sizeof(T) == 2) {
+            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
+                __builtin_bit_cast(bf16x8_t, bfr[j]), __builtin_bit_cast(bf16x8_t, af[i]),
+                acc[i][j], 0, 0, 0);
+          } else {
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+              acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(
+                  __uint_as_float(bfr[j][e]), __uint_as_float(af[i][e]), acc[i][j], 0, 0, 0);
+          }
+        }
+    }
+
+    if (more) commit_stores(cur ^ 1);
+    __syncthreads();
+  }
+
+  // Epilogue.  acc[i][j][4q + e] holds C[m][n + e] with
+  //   m = m0 + wm*WTM + i*32 + (lane & 31),  n = n0 + wn*WTN + j*32 + 8q + 4*(lane >> 5).
+  // One 32-row block per pass is staged through LDS (rows padded by 4 floats so
+  // the 16-byte writes of 16 consecutive rows hit distinct banks); each wave then
+  // walks its own block row-major, 4 columns per lane, through one rolled copy of
+  // the epilogue: coalesced C accesses and no per-fragment epilogue code.
+  constexpr int PITCH = WTN + 4;
+  float* stg = reinterpret_cast<float*>(&smem[0][0]) + wave * (32 * PITCH);
+  float* W = (p.splits > 1) ? p.ws + ((int64_t)tc.z * p.splits + tc.split) * (int64_t)p.M * p.N
+                            : nullptr;
+#pragma unroll
+  for (int i = 0; i < TM; ++i) {
+#pragma unroll
+    for (int j = 0; j < TN; ++j)
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        f32x4_t v;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          if constexpr (MODE == MODE_DUAL)
+            v[e] = silu_f(p.alpha * acc[i][j][4 * q + e]) * (p.alpha * acc[i][j + TN][4 * q + e]);
+          else
+            v[e] = acc[i][j][4 * q + e];
+        }
+        *reinterpret_cast<f32x4_t*>(stg + lrow * PITCH + j * 32 + 8 * q + 4 * lhalf) = v;
+      }
+    __syncthreads();
+    const int mrow0 = m0 + wm * WTM + i * 32;
+    const int ncol0 = n0 + wn * WTN;
+#pragma unroll 2
+    for (int idx = lane; idx < 32 * (WTN / 4); idx += 64) {
+      const int r = idx / (WTN / 4), c4 = idx - r * (WTN / 4);
+      const f32x4_t sv = *reinterpret_cast<const f32x4_t*>(stg + r * PITCH + c4 * 4);
+      const int m = mrow0 + r, n = ncol0 + c4 * 4;
+      if (W) {
+        if (m < p.M) {
+#pragma unroll
+          for (int e = 0; e < 4; ++e)
+            if (n + e < p.N) W[(int64_t)m * p.N + n + e] = sv[e];
+        }
+      } else {
+        float v[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) v[e] = (MODE == MODE_DUAL) ? sv[e] : p.alpha * sv[e];
+        epilogue4(p, Cz, Rz, m, n, v);
+      }
+    }
+    __syncthreads();
+  }
+}
+
+}  // namespace mig

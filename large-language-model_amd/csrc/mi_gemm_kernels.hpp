@@ -1,0 +1,43 @@
+// mi_gemm_kernels.hpp -- kernel table shared by the host dispatch (mi_gemm.hip)
+// and the per-layout instantiation units (mi_gemm_inst.hip, compiled once per
+// input dtype x operand layout so the instantiations build in parallel).
+#pragma once
+#include "mi_gemm_device.hpp"
+
+namespace mig {
+
+typedef void (*KernelFn)(Params);
+
+// Tile configurations.  Output tile (BM x BN) per configuration and dtype:
+//   bf16: L 256x256 (4 waves of 128x128), S 128x128 (4 waves of 64x64),
+//         DUAL 256x128 (+ second B), PRO 256x256 with the SiLU-gate A prologue.
+//   fp32: L = S 128x128, DUAL 128x64, PRO 128x128.
+enum Cfg { CFG_L = 0, CFG_S = 1, CFG_DUAL = 2, CFG_PRO = 3, NCFG = 4 };
+
+struct CfgShape {
+  int bm, bn;
+};
+
+inline CfgShape cfg_shape(bool bf16, int cfg) {
+  if (bf16)
+    return cfg == CFG_L ? CfgShape{256, 256}
+         : cfg == CFG_S ? CfgShape{128, 128}
+         : cfg == CFG_DUAL ? CfgShape{256, 128}
+                           : CfgShape{256, 256};
+  return cfg == CFG_DUAL ? CfgShape{128, 64} : CfgShape{128, 128};
+}
+
+// One function per (dtype, transA, transB): returns the kernel for `cfg`, or
+// nullptr when the combination does not exist (prologue with transA = 1).
+#define MI_DECL_PICK(dt, ta, tb) KernelFn pick_##dt##_##ta##tb(int cfg);
+MI_DECL_PICK(bf16, 0, 0)
+MI_DECL_PICK(bf16, 0, 1)
+MI_DECL_PICK(bf16, 1, 0)
+MI_DECL_PICK(bf16, 1, 1)
+MI_DECL_PICK(f32, 0, 0)
+MI_DECL_PICK(f32, 0, 1)
+MI_DECL_PICK(f32, 1, 0)
+MI_DECL_PICK(f32, 1, 1)
+#undef MI_DECL_PICK
+
+}  // namespace mig

@@ -1,0 +1,413 @@
+"""Python mirror of the reference engine's GEMM operator layer, over libmi_gemm.so.
+
+The functions keep the names, argument meaning and error behaviour of the
+reference's operator interface:
+
+* ``gemm_bf16 / fused_swiglu_gemm / gemm_ffn / gemm_proj / gemm_backward /
+  gemm_proj_trans_b / residual_add / begin_scope / end_scope`` --
+  ``metal_bridge::`` (cpp/include/gpu_kernel/MetalBridge.hpp:29-46,78,119-125);
+* ``matmul(a, b)`` -- ``Tensor::matmul`` (cpp/src/Tensor.cpp:174-228), raising
+  ``ValueError`` (the reference's ``std::invalid_argument``) with the same messages;
+* ``attention_forward / attention_backward`` -- the batched GQA products of
+  ``Attention::forward/backward`` (cpp/src/Attention.cpp:236-280, 292-348) composed
+  from ``gemm_batched`` plus the row softmax kernels.
+
+Tensors are torch CUDA tensors; torch only provides device memory and the current
+stream. All arithmetic runs in the HIP kernels of libmi_gemm.so; importing this
+module on a machine where the library is missing raises immediately, and there
+is no CPU fallback.
+"""
+from __future__ import annotations
+
+import ctypes
+import math
+import os
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(_HERE, "libmi_gemm.so")
+
+MI_F32, MI_BF16 = 0, 1
+MI_CAUSAL_NONE, MI_CAUSAL_OUT_LOWER, MI_CAUSAL_A_LOWER, MI_CAUSAL_A_UPPER = 0, 1, 2, 3
+
+# Exported C-ABI symbols (include/mi_gemm.h).
+C_SYMBOLS = (
+    "mi_init", "mi_last_error", "mi_version", "mi_gemm_workspace_size", "mi_gemm",
+    "mi_gemm_batched", "mi_residual_add", "mi_softmax_causal", "mi_softmax_bwd",
+    "mi_stream_sync",
+)
+
+
+class MiError(RuntimeError):
+    """A non-zero mi_status from the C ABI."""
+
+    def __init__(self, fn: str, code: int, msg: str):
+        super().__init__(f"{fn}: status {code}: {msg}")
+        self.code = code
+
+
+class MiEpilogue(ctypes.Structure):
+    _fields_ = [
+        ("bias", ctypes.c_void_p), ("bias_dtype", ctypes.c_int32),
+        ("residual", ctypes.c_void_p), ("residual_dtype", ctypes.c_int32),
+        ("ldr", ctypes.c_int64),
+        ("B2", ctypes.c_void_p), ("A2", ctypes.c_void_p),
+    ]
+
+
+class MiBatch(ctypes.Structure):
+    _fields_ = [
+        ("batch", ctypes.c_int64), ("heads", ctypes.c_int64),
+        ("a_outer", ctypes.c_int64), ("a_inner", ctypes.c_int64), ("a_group", ctypes.c_int64),
+        ("b_outer", ctypes.c_int64), ("b_inner", ctypes.c_int64), ("b_group", ctypes.c_int64),
+        ("c_outer", ctypes.c_int64), ("c_inner", ctypes.c_int64), ("c_group", ctypes.c_int64),
+        ("r_outer", ctypes.c_int64), ("r_inner", ctypes.c_int64),
+        ("k_segments", ctypes.c_int64), ("seg_a", ctypes.c_int64), ("seg_b", ctypes.c_int64),
+        ("causal", ctypes.c_int32), ("mask_value", ctypes.c_float),
+    ]
+
+
+_lib = None
+
+
+def load_library():
+    """Load libmi_gemm.so (built by __graft_entry__.build()); raises if absent."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not os.path.exists(LIB_PATH):
+        raise ImportError(f"{LIB_PATH} is not built; run __graft_entry__.build()")
+    L = ctypes.CDLL(LIB_PATH)
+    vp, i64, i32, f32 = ctypes.c_void_p, ctypes.c_int64, ctypes.c_int32, ctypes.c_float
+    L.mi_init.restype = ctypes.c_int
+    L.mi_last_error.restype = ctypes.c_char_p
+    L.mi_version.restype = ctypes.c_char_p
+    L.mi_gemm_workspace_size.restype = ctypes.c_size_t
+    L.mi_gemm_workspace_size.argtypes = [ctypes.c_int, ctypes.c_int, i64, i64, i64, i32, i32, i64]
+    L.mi_gemm.restype = ctypes.c_int
+    L.mi_gemm.argtypes = [vp, ctypes.c_int, ctypes.c_int, i64, i64, i64, f32, vp, i64, vp, i64,
+                          i32, f32, vp, i64, i32, ctypes.POINTER(MiEpilogue), vp, ctypes.c_size_t]
+    L.mi_gemm_batched.restype = ctypes.c_int
+    L.mi_gemm_batched.argtypes = [vp, ctypes.c_int, ctypes.c_int, i64, i64, i64, f32, vp, i64,
+                                  vp, i64, i32, f32, vp, i64, i32, ctypes.POINTER(MiBatch),
+                                  ctypes.POINTER(MiEpilogue), vp, ctypes.c_size_t]
+    L.mi_residual_add.restype = ctypes.c_int
+    L.mi_residual_add.argtypes = [vp, vp, vp, i64, i32]
+    L.mi_softmax_causal.restype = ctypes.c_int
+    L.mi_softmax_causal.argtypes = [vp, vp, i64, i64, i64, i32]
+    L.mi_softmax_bwd.restype = ctypes.c_int
+    L.mi_softmax_bwd.argtypes = [vp, vp, vp, i64, i64, i64, f32, i32]
+    L.mi_stream_sync.restype = ctypes.c_int
+    L.mi_stream_sync.argtypes = [vp]
+    _lib = L
+    return L
+
+
+def _check(fn: str, st: int):
+    if st != 0:
+        raise MiError(fn, st, load_library().mi_last_error().decode())
+
+
+def version() -> str:
+    return load_library().mi_version().decode()
+
+
+def init():
+    _check("mi_init", load_library().mi_init())
+
+
+# ---- torch plumbing -----------------------------------------------------------
+
+def _torch():
+    import torch
+    return torch
+
+
+def _dt(t) -> int:
+    torch = _torch()
+    if t.dtype == torch.bfloat16:
+        return MI_BF16
+    if t.dtype == torch.float32:
+        return MI_F32
+    raise ValueError(f"unsupported dtype {t.dtype}")
+
+
+def _ptr(t):
+    return None if t is None else ctypes.c_void_p(t.data_ptr())
+
+
+def _stream():
+    return ctypes.c_void_p(_torch().cuda.current_stream().cuda_stream)
+
+
+_scope_depth = 0
+
+
+def begin_scope():
+    """MetalBridge.hpp:29: calls enqueue without waiting until end_scope()."""
+    global _scope_depth
+    _scope_depth += 1
+
+
+def end_scope():
+    """MetalBridge.hpp:30: wait once for everything enqueued in the scope."""
+    global _scope_depth
+    _scope_depth = max(0, _scope_depth - 1)
+    _check("mi_stream_sync", load_library().mi_stream_sync(_stream()))
+
+
+def _finish(fn, st):
+    _check(fn, st)
+    if _scope_depth == 0:
+        _check("mi_stream_sync", load_library().mi_stream_sync(_stream()))
+
+
+# ---- general entry points -----------------------------------------------------
+
+def _epilogue(bias=None, residual=None, ldr=None, B2=None, A2=None):
+    if bias is None and residual is None and B2 is None and A2 is None:
+        return None
+    e = MiEpilogue()
+    if bias is not None:
+        e.bias, e.bias_dtype = bias.data_ptr(), _dt(bias)
+    if residual is not None:
+        e.residual, e.residual_dtype = residual.data_ptr(), _dt(residual)
+        e.ldr = ldr if ldr is not None else residual.shape[-1]
+    if B2 is not None:
+        e.B2 = B2.data_ptr()
+    if A2 is not None:
+        e.A2 = A2.data_ptr()
+    return ctypes.byref(e)
+
+
+def gemm(A, B, C, M, N, K, *, transA=False, transB=False, alpha=1.0, beta=0.0, lda=None,
+         ldb=None, ldc=None, bias=None, residual=None, ldr=None, B2=None, A2=None,
+         workspace=None, sync=None):
+    """mi_gemm on torch device tensors; C = epilogue(alpha*op(A)op(B))."""
+    L = load_library()
+    lda = lda if lda is not None else (M if transA else K)
+    ldb = ldb if ldb is not None else (K if transB else N)
+    ldc = ldc if ldc is not None else N
+    ws = _ptr(workspace)
+    wsb = 0 if workspace is None else workspace.numel() * workspace.element_size()
+    st = L.mi_gemm(_stream(), int(transA), int(transB), M, N, K, alpha, _ptr(A), lda, _ptr(B),
+                   ldb, _dt(A), beta, _ptr(C), ldc, _dt(C),
+                   _epilogue(bias, residual, ldr, B2, A2), ws, wsb)
+    if sync is None:
+        _finish("mi_gemm", st)
+    else:
+        _check("mi_gemm", st)
+
+
+def make_batch(batch, heads=1, a=(0, 0, 1), b=(0, 0, 1), c=(0, 0, 1), r=(0, 0), k_segments=1,
+               seg_a=0, seg_b=0, causal=MI_CAUSAL_NONE, mask_value=0.0) -> MiBatch:
+    d = MiBatch()
+    d.batch, d.heads = batch, heads
+    d.a_outer, d.a_inner, d.a_group = a
+    d.b_outer, d.b_inner, d.b_group = b
+    d.c_outer, d.c_inner, d.c_group = c
+    d.r_outer, d.r_inner = r
+    d.k_segments, d.seg_a, d.seg_b = k_segments, seg_a, seg_b
+    d.causal, d.mask_value = causal, mask_value
+    return d
+
+
+def gemm_batched(A, B, C, M, N, K, batch: MiBatch, *, transA=False, transB=False, alpha=1.0,
+                 beta=0.0, lda=None, ldb=None, ldc=None, bias=None, residual=None, ldr=None,
+                 B2=None, A2=None, workspace=None, sync=None):
+    """mi_gemm_batched on torch device tensors (GQA head map, K segments, causal)."""
+    L = load_library()
+    lda = lda if lda is not None else (M if transA else K)
+    ldb = ldb if ldb is not None else (K if transB else N)
+    ldc = ldc if ldc is not None else N
+    ws = _ptr(workspace)
+    wsb = 0 if workspace is None else workspace.numel() * workspace.element_size()
+    st = L.mi_gemm_batched(_stream(), int(transA), int(transB), M, N, K, alpha, _ptr(A), lda,
+                           _ptr(B), ldb, _dt(A), beta, _ptr(C), ldc, _dt(C), ctypes.byref(batch),
+                           _epilogue(bias, residual, ldr, B2, A2), ws, wsb)
+    if sync is None:
+        _finish("mi_gemm_batched", st)
+    else:
+        _check("mi_gemm_batched", st)
+
+
+def workspace_size(transA, transB, M, N, K, dtype_in=MI_BF16, dtype_c=MI_F32, batch=1) -> int:
+    return int(load_library().mi_gemm_workspace_size(int(transA), int(transB), M, N, K, dtype_in,
+                                                     dtype_c, batch))
+
+
+# ---- reference-named entry points (MetalBridge.hpp) ---------------------------
+
+def gemm_bf16(A, B, C, M, N, K, transA=False, transB=False, is_forward=False):
+    """MetalBridge.hpp:39-42. bf16 in/out: C[M,N] = op(A) op(B). No-op if a size is 0."""
+    if M == 0 or N == 0 or K == 0:
+        return
+    gemm(A, B, C, M, N, K, transA=transA, transB=transB)
+
+
+def fused_swiglu_gemm(gate_proj, up_proj, B, C, M, N, K):
+    """MetalBridge.hpp:44-46: C = (SiLU(gate) * up) @ B (fused_swiglu_gemm.metal:48-77)."""
+    if M == 0 or N == 0 or K == 0:
+        return
+    gemm(gate_proj, B, C, M, N, K, A2=up_proj)
+
+
+def gemm_ffn(a, b_gate, b_up, c, M, N, K):
+    """MetalBridge.hpp:119-120: C = SiLU(A Bg) * (A Bu) (gemm_ffn.metal:160-181)."""
+    if M == 0 or N == 0 or K == 0:
+        return
+    gemm(a, b_gate, c, M, N, K, B2=b_up)
+
+
+def gemm_proj(a, b, c, M, N, K):
+    """MetalBridge.hpp:121 (cblas_sgemm NN, MetalBridge.mm:695-697), on the GPU."""
+    if M == 0 or N == 0 or K == 0:
+        return
+    gemm(a, b, c, M, N, K)
+
+
+def gemm_backward(a_transposed, b, c, M, N, K, accumulate=False):
+    """MetalBridge.hpp:122-123: C[M,N] = A^T B, A stored [K,M] (overwrites, MetalBridge.mm:1928).
+
+    accumulate=True gives the engine's dW semantics C += A^T B (Transformer.cpp:236,
+    gemm_backward.metal:104-115); C may then be fp32.
+    """
+    if M == 0 or N == 0 or K == 0:
+        return
+    gemm(a_transposed, b, c, M, N, K, transA=True, beta=1.0 if accumulate else 0.0)
+
+
+def gemm_proj_trans_b(a, b_transposed, c, M, N, K):
+    """MetalBridge.hpp:124-125: C = A B^T, B stored [N,K]."""
+    if M == 0 or N == 0 or K == 0:
+        return
+    gemm(a, b_transposed, c, M, N, K, transB=True)
+
+
+def residual_add(a, b, n=None):
+    """MetalBridge.hpp:78: a[i] += b[i] (residual_add.metal:27)."""
+    n = a.numel() if n is None else n
+    _finish("mi_residual_add", load_library().mi_residual_add(_stream(), _ptr(a), _ptr(b), n,
+                                                              _dt(a)))
+
+
+# ---- Tensor::matmul mirror ------------------------------------------------------
+
+def matmul_shape(a_shape, b_shape):
+    """Tensor.cpp:174-209 shape rules; ValueError carries the reference's messages."""
+    ra, rb = len(a_shape), len(b_shape)
+    if ra < 2 or rb < 2:
+        raise ValueError("Matmul requires at least 2 dimensions")
+    if rb == 2 and ra != 2:
+        if a_shape[-1] != b_shape[0]:
+            raise ValueError("Inner dimensions must match for projection")
+        return tuple(a_shape[:-1]) + (b_shape[1],)
+    if ra != rb:
+        raise ValueError("Batch size must match for matrix multiplication")
+    for i in range(ra - 2):
+        if a_shape[i] != b_shape[i]:
+            raise ValueError("Batch dimension must match for matmul")
+    if a_shape[-1] != b_shape[-2]:
+        raise ValueError("Inner dimensions must match for matmul")
+    return tuple(a_shape[:-1]) + (b_shape[-1],)
+
+
+def matmul(a, b):
+    """Tensor::matmul: result dtype = a's dtype, zero-initialised then written."""
+    torch = _torch()
+    shape = matmul_shape(tuple(a.shape), tuple(b.shape))
+    if a.dtype != b.dtype:
+        raise ValueError("Matmul operands must share a dtype")
+    a = a.contiguous()
+    b = b.contiguous()
+    out = torch.zeros(shape, dtype=a.dtype, device=a.device)
+    if b.dim() == 2 and a.dim() != 2:
+        K, N = b.shape
+        M = a.numel() // K if K else math.prod(a.shape[:-1])
+        gemm(a, b, out, M, N, K)
+    else:
+        M, K, N = a.shape[-2], a.shape[-1], b.shape[-1]
+        nb = math.prod(a.shape[:-2])
+        bt = make_batch(nb, 1, a=(M * K, 0, 1), b=(K * N, 0, 1), c=(M * N, 0, 1))
+        gemm_batched(a, b, out, M, N, K, bt)
+    return out
+
+
+# ---- GQA attention composed from the batched GEMM forms ------------------------
+
+def softmax_causal_(S, T):
+    """In-place causal row softmax of S [..., T, T] (Attention.cpp:261-266)."""
+    rows = S.numel() // T
+    _check("mi_softmax_causal", load_library().mi_softmax_causal(_stream(), _ptr(S), rows, T, T,
+                                                                 _dt(S)))
+
+
+def softmax_bwd_(P, dP, T, scale):
+    """dP <- P * (dP - rowsum(P * dP)) * scale (Attention.cpp:336-345)."""
+    rows = P.numel() // T
+    _check("mi_softmax_bwd", load_library().mi_softmax_bwd(_stream(), _ptr(P), _ptr(dP), rows, T,
+                                                           T, scale, _dt(P)))
+
+
+def attention_forward(Q4, K4, V4, out_dtype=None):
+    """Q4 [B,nH,T,d], K4/V4 [B,nKV,T,d] -> (O [B,T,nH*d], P [B,nH,T,T]).
+
+    S = Q K^T / sqrt(d) (NT, kv map, causal output mask), softmax, O = P V (NN,
+    kv map, causal K skipping) written straight into the [B,T,nH*d] layout.
+    """
+    torch = _torch()
+    Bn, nH, T, d = Q4.shape
+    nKV = K4.shape[1]
+    g = nH // nKV
+    dt = Q4.dtype
+    S = torch.empty((Bn, nH, T, T), dtype=dt, device=Q4.device)
+    bt = make_batch(Bn * nH, nH, a=(nH * T * d, T * d, 1), b=(nKV * T * d, T * d, g),
+                    c=(nH * T * T, T * T, 1), causal=MI_CAUSAL_OUT_LOWER, mask_value=-math.inf)
+    gemm_batched(Q4, K4, S, T, T, d, bt, transB=True, alpha=1.0 / math.sqrt(d), sync=False)
+    softmax_causal_(S, T)
+    O = torch.empty((Bn, T, nH * d), dtype=out_dtype or dt, device=Q4.device)
+    bt = make_batch(Bn * nH, nH, a=(nH * T * T, T * T, 1), b=(nKV * T * d, T * d, g),
+                    c=(T * nH * d, d, 1), causal=MI_CAUSAL_A_LOWER)
+    gemm_batched(S, V4, O, T, d, T, bt, ldc=nH * d, sync=False)
+    _finish("attention_forward", 0)
+    return O, S
+
+
+def attention_backward(Q4, K4, V4, dO, P, grad_dtype=None):
+    """Batched backward products (Attention.cpp:292-348) -> (dQ4, dK4, dV4).
+
+    dV = P^T dO and dK = dS^T Q run as one product per (b, kv head) whose K loop
+    covers the nH/nKV query heads of the group (the KV-group reduction).
+    """
+    torch = _torch()
+    Bn, nH, T, d = Q4.shape
+    nKV = K4.shape[1]
+    g = nH // nKV
+    dt = Q4.dtype
+    gd = grad_dtype or dt
+    scale = 1.0 / math.sqrt(d)
+    # dV[b,kv] = sum_{h in group} P[b,h]^T dO[b,:,h]   (TN, K = g segments of T)
+    dV = torch.empty(V4.shape, dtype=gd, device=Q4.device)
+    bt = make_batch(Bn * nKV, nKV, a=(nH * T * T, g * T * T, 1), b=(T * nH * d, g * d, 1),
+                    c=(nKV * T * d, T * d, 1), k_segments=g, seg_a=T * T, seg_b=d,
+                    causal=MI_CAUSAL_A_UPPER)
+    gemm_batched(P, dO, dV, T, d, T, bt, transA=True, ldb=nH * d, sync=False)
+    # dP[b,h] = dO[b,:,h] V[b,kv]^T   (NT, kv map)
+    dP = torch.empty((Bn, nH, T, T), dtype=dt, device=Q4.device)
+    bt = make_batch(Bn * nH, nH, a=(T * nH * d, d, 1), b=(nKV * T * d, T * d, g),
+                    c=(nH * T * T, T * T, 1), causal=MI_CAUSAL_OUT_LOWER, mask_value=0.0)
+    gemm_batched(dO, V4, dP, T, T, d, bt, transB=True, lda=nH * d, sync=False)
+    # dS = P * (dP - rowsum(P * dP)) * scale, in place over dP
+    softmax_bwd_(P, dP, T, scale)
+    # dQ[b,h] = dS[b,h] K[b,kv]   (NN, kv map, causal K skipping)
+    dQ = torch.empty(Q4.shape, dtype=gd, device=Q4.device)
+    bt = make_batch(Bn * nH, nH, a=(nH * T * T, T * T, 1), b=(nKV * T * d, T * d, g),
+                    c=(nH * T * d, T * d, 1), causal=MI_CAUSAL_A_LOWER)
+    gemm_batched(dP, K4, dQ, T, d, T, bt, sync=False)
+    # dK[b,kv] = sum_{h in group} dS[b,h]^T Q[b,h]   (TN, K = g segments of T)
+    dK = torch.empty(K4.shape, dtype=gd, device=Q4.device)
+    bt = make_batch(Bn * nKV, nKV, a=(nH * T * T, g * T * T, 1), b=(nH * T * d, g * T * d, 1),
+                    c=(nKV * T * d, T * d, 1), k_segments=g, seg_a=T * T, seg_b=T * d,
+                    causal=MI_CAUSAL_A_UPPER)
+    gemm_batched(dP, Q4, dK, T, d, T, bt, transA=True, sync=False)
+    _finish("attention_backward", 0)
+    return dQ, dK, dV

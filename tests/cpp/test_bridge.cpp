@@ -1,0 +1,249 @@
+// test_bridge.cpp -- the reference engine's GEMM tests, run through the C++
+// mirror (include/gemm_bridge.hpp) on the GPU.  Prints one PASS/FAIL row per
+// check like the reference's test programs (test_math_ops.cpp, test_gpu_kernels.cpp)
+// and exits non-zero on any failure.  Expected values are the reference's own
+// known answers (TC-12/TC-13, test_math_ops.cpp:167-189), exact small-integer
+// products (bf16-exact inputs, fp32-exact sums) and the accumulate semantics of
+// TC-28 (test_transformer.cpp:615-636).
+#include <hip/hip_runtime.h>
+
+#include <cmath>
+#include <cstdint>
+#include <cstdio>
+#include <cstring>
+#include <stdexcept>
+#include <string>
+#include <vector>
+
+#include "gemm_bridge.hpp"
+
+static int g_total = 0, g_passed = 0;
+
+static void row(const char* id, const char* what, bool pass, const std::string& detail = "") {
+  ++g_total;
+  if (pass) ++g_passed;
+  std::printf("%-8s %-52s %-6s %s\n", id, what, pass ? "PASS" : "FAIL", detail.c_str());
+}
+
+static uint16_t bf(float v) {  // exact for the small integers used here
+  uint32_t b;
+  std::memcpy(&b, &v, 4);
+  return (uint16_t)(b >> 16);
+}
+static float fb(uint16_t h) {
+  uint32_t b = (uint32_t)h << 16;
+  float f;
+  std::memcpy(&f, &b, 4);
+  return f;
+}
+
+static void dfree(void* p) { (void)hipFree(p); }
+
+template <typename T>
+static T* dev(const std::vector<T>& h) {
+  T* d = nullptr;
+  if (hipMalloc(&d, h.size() * sizeof(T) + 16) != hipSuccess) throw std::runtime_error("hipMalloc");
+  if (hipMemcpy(d, h.data(), h.size() * sizeof(T), hipMemcpyHostToDevice) != hipSuccess)
+    throw std::runtime_error("hipMemcpy");
+  return d;
+}
+template <typename T>
+static std::vector<T> host(const T* d, size_t n) {
+  std::vector<T> h(n);
+  if (hipMemcpy(h.data(), d, n * sizeof(T), hipMemcpyDeviceToHost) != hipSuccess)
+    throw std::runtime_error("hipMemcpy");
+  return h;
+}
+
+// Small-integer matrices: entries in [-4, 4], exact in bf16, sums exact in fp32.
+static std::vector<float> ints(size_t n, int seed) {
+  std::vector<float> v(n);
+  uint32_t s = 2654435761u * (uint32_t)(seed + 1);
+  for (auto& x : v) {
+    s = s * 1664525u + 1013904223u;
+    x = (float)((int)((s >> 24) % 9) - 4);
+  }
+  return v;
+}
+
+template <typename F>
+static bool throws_with(F f, const char* msg) {
+  try {
+    f();
+  } catch (const std::invalid_argument& e) {
+    return std::string(e.what()) == msg;
+  }
+  return false;
+}
+
+int main() {
+  mi_bridge::initialize();
+  if (!mi_bridge::is_available()) {
+    std::printf("no gfx950 device\n");
+    return 2;
+  }
+  using mi_bridge::DeviceTensor;
+  using mi_bridge::DType;
+
+  // TC-12: [2x3] x [3x2] -> [[58, 64], [139, 154]]
+  {
+    std::vector<float> a = {1, 2, 3, 4, 5, 6}, b = {7, 8, 9, 10, 11, 12};
+    DeviceTensor A{dev(a), {2, 3}, DType::FP32}, B{dev(b), {3, 2}, DType::FP32};
+    float* c = dev(std::vector<float>(4, 0.f));
+    DeviceTensor C{c, {}, DType::FP32};
+    mi_bridge::matmul(A, B, C);
+    auto h = host(c, 4);
+    row("TC-12", "2D matmul correctness (58 64 139 154)",
+        C.shape == std::vector<size_t>({2, 2}) && h[0] == 58 && h[1] == 64 && h[2] == 139 &&
+            h[3] == 154,
+        std::to_string(h[3]));
+    dfree(A.data); dfree(B.data); dfree(c);
+  }
+  // TC-13: batched 3-D matmul, [0,0,0] = 58 and [1,1,1] = 24, fp32 and bf16
+  for (int use_bf = 0; use_bf < 2; ++use_bf) {
+    std::vector<float> a = {1, 2, 3, 4, 5, 6, 1, 1, 1, 2, 2, 2};
+    std::vector<float> b = {7, 8, 9, 10, 11, 12, 1, 2, 3, 4, 5, 6};
+    std::vector<float> got(8);
+    if (use_bf) {
+      std::vector<uint16_t> ab, bb;
+      for (float x : a) ab.push_back(bf(x));
+      for (float x : b) bb.push_back(bf(x));
+      DeviceTensor A{dev(ab), {2, 2, 3}, DType::BF16}, B{dev(bb), {2, 3, 2}, DType::BF16};
+      uint16_t* c = dev(std::vector<uint16_t>(8, 0));
+      DeviceTensor C{c, {}, DType::BF16};
+      mi_bridge::matmul(A, B, C);
+      auto h = host(c, 8);
+      for (int i = 0; i < 8; ++i) got[i] = fb(h[i]);
+      dfree(A.data); dfree(B.data); dfree(c);
+    } else {
+      DeviceTensor A{dev(a), {2, 2, 3}, DType::FP32}, B{dev(b), {2, 3, 2}, DType::FP32};
+      float* c = dev(std::vector<float>(8, 0.f));
+      DeviceTensor C{c, {}, DType::FP32};
+      mi_bridge::matmul(A, B, C);
+      got = host(c, 8);
+      dfree(A.data); dfree(B.data); dfree(c);
+    }
+    row(use_bf ? "TC-13b" : "TC-13", use_bf ? "Batched 3D matmul, bf16 (58, 24)" : "Batched 3D matmul (58, 24)",
+        got[0] == 58 && got[7] == 24 && got[1] == 64 && got[4] == 9, std::to_string(got[7]));
+  }
+  // TC-17/18 style: shape errors throw std::invalid_argument with the reference messages
+  {
+    DeviceTensor v{nullptr, {3}, DType::FP32}, m{nullptr, {3, 2}, DType::FP32};
+    DeviceTensor a3{nullptr, {2, 2, 3}, DType::FP32}, w{nullptr, {4, 2}, DType::FP32};
+    DeviceTensor b3{nullptr, {3, 3, 2}, DType::FP32}, c3{nullptr, {2, 4, 2}, DType::FP32};
+    DeviceTensor a4{nullptr, {1, 2, 2, 3}, DType::FP32};
+    bool ok = throws_with([&] { mi_bridge::matmul_shape(v, m); }, "Matmul requires at least 2 dimensions") &&
+              throws_with([&] { mi_bridge::matmul_shape(a3, w); }, "Inner dimensions must match for projection") &&
+              throws_with([&] { mi_bridge::matmul_shape(a3, b3); }, "Batch dimension must match for matmul") &&
+              throws_with([&] { mi_bridge::matmul_shape(a3, c3); }, "Inner dimensions must match for matmul") &&
+              throws_with([&] { mi_bridge::matmul_shape(a4, b3); }, "Batch size must match for matrix multiplication");
+    row("TC-17", "Shape errors throw invalid_argument (5 cases)", ok);
+  }
+  // gemm_bf16 NN / NT / TN on exact small integers: bit-exact
+  {
+    const size_t M = 67, N = 130, K = 93;
+    auto a = ints(M * K, 1), b = ints(K * N, 2);
+    std::vector<float> bt(N * K, 0.f), at(K * M, 0.f);
+    for (size_t k = 0; k < K; ++k)
+      for (size_t n = 0; n < N; ++n) bt[n * K + k] = b[k * N + n];
+    for (size_t m = 0; m < M; ++m)
+      for (size_t k = 0; k < K; ++k) at[k * M + m] = a[m * K + k];
+    std::vector<float> ref(M * N, 0.f);
+    for (size_t m = 0; m < M; ++m)
+      for (size_t n = 0; n < N; ++n) {
+        float s = 0.f;
+        for (size_t k = 0; k < K; ++k) s += a[m * K + k] * b[k * N + n];
+        ref[m * N + n] = s;
+      }
+    auto tob = [](const std::vector<float>& v) {
+      std::vector<uint16_t> o(v.size());
+      for (size_t i = 0; i < v.size(); ++i) o[i] = bf(v[i]);
+      return o;
+    };
+    uint16_t *dA = dev(tob(a)), *dB = dev(tob(b)), *dBt = dev(tob(bt)), *dAt = dev(tob(at));
+    uint16_t* dC = dev(std::vector<uint16_t>(M * N, 0));
+    const char* names[3] = {"gemm_bf16 NN exact small integers", "gemm_proj_trans_b (NT) exact",
+                            "gemm_backward (TN, overwrite) exact"};
+    for (int mode = 0; mode < 3; ++mode) {
+      if (mode == 0) mi_bridge::gemm_bf16(dA, dB, dC, M, N, K);
+      if (mode == 1) mi_bridge::gemm_proj_trans_b((const float*)dA, (const float*)dBt, (float*)dC, M, N, K);
+      if (mode == 2) mi_bridge::gemm_backward((const float*)dAt, (const float*)dB, (float*)dC, M, N, K);
+      auto h = host(dC, M * N);
+      bool ok = mi_bridge::last_status() == MI_OK;
+      for (size_t i = 0; i < M * N && ok; ++i) ok = fb(bf(ref[i])) == fb(h[i]);
+      row(mode == 0 ? "GB-01" : mode == 1 ? "GB-02" : "GB-03", names[mode], ok);
+    }
+    // TC-28: the accumulate variant adds into a pre-filled fp32 gradient
+    float* dW = dev(std::vector<float>(M * N, 1.0f));
+    mi_bridge::gemm_backward_accumulate(dAt, dB, dW, M, N, K);
+    auto h = host(dW, M * N);
+    bool ok = mi_bridge::last_status() == MI_OK;
+    for (size_t i = 0; i < M * N && ok; ++i) ok = h[i] == ref[i] + 1.0f;
+    row("TC-28", "gemm_backward_accumulate: dW += A^T B (pre-filled 1.0)", ok);
+    // gemm_proj: fp32 NN (cblas_sgemm semantics), exact on integers
+    std::vector<float> zero(M * N, 0.f);
+    float *fA = dev(a), *fB = dev(b), *fC = dev(zero);
+    mi_bridge::gemm_proj(fA, fB, fC, M, N, K);
+    auto hc = host(fC, M * N);
+    ok = mi_bridge::last_status() == MI_OK;
+    for (size_t i = 0; i < M * N && ok; ++i) ok = hc[i] == ref[i];
+    row("GB-04", "gemm_proj fp32 NN exact small integers", ok);
+    // residual_add, fp32 and bf16 storage
+    mi_bridge::residual_add_f32(fC, fC, M * N);
+    hc = host(fC, M * N);
+    ok = true;
+    for (size_t i = 0; i < M * N && ok; ++i) ok = hc[i] == 2.0f * ref[i];
+    row("GB-05", "residual_add_f32 a += b", ok);
+    mi_bridge::gemm_bf16(dA, dB, dC, M, N, K);
+    mi_bridge::residual_add((float*)dC, (const float*)dC, M * N);
+    h = std::vector<float>();
+    auto hb = host(dC, M * N);
+    ok = true;
+    for (size_t i = 0; i < M * N && ok; ++i) ok = fb(hb[i]) == fb(bf(fb(bf(ref[i])) * 2.0f));
+    row("GB-06", "residual_add on bf16 storage", ok);
+    // scope: several calls, one wait
+    mi_bridge::begin_scope();
+    for (int r = 0; r < 4; ++r) mi_bridge::gemm_bf16(dA, dB, dC, M, N, K);
+    mi_bridge::end_scope();
+    hb = host(dC, M * N);
+    ok = mi_bridge::last_status() == MI_OK;
+    for (size_t i = 0; i < M * N && ok; ++i) ok = fb(bf(ref[i])) == fb(hb[i]);
+    row("GB-07", "begin_scope / end_scope batching", ok);
+    // zero sizes are silent no-ops (MetalBridge.mm:622-623)
+    mi_bridge::gemm_bf16(dA, dB, dC, 0, N, K);
+    mi_bridge::gemm_backward(nullptr, nullptr, nullptr, M, N, 0);
+    row("GB-08", "zero-size calls are no-ops", mi_bridge::last_status() == MI_OK);
+    // invalid argument: status and message, no crash
+    mi_bridge::gemm_bf16(nullptr, dB, dC, M, N, K);
+    row("GB-09", "NULL operand reports MI_ERR_NULL", mi_bridge::last_status() == MI_ERR_NULL);
+    dfree(dA); dfree(dB); dfree(dBt); dfree(dAt); dfree(dC); dfree(dW);
+    dfree(fA); dfree(fB); dfree(fC);
+  }
+  // gemm_ffn (fp32 dual-B SiLU gate) and fused_swiglu_gemm (bf16 prologue)
+  {
+    const size_t M = 96, N = 80, K = 72;
+    auto a = ints(M * K, 3), bg = ints(K * N, 4), bu = ints(K * N, 5);
+    for (auto& x : a) x *= 0.125f;
+    std::vector<double> g(M * N, 0.0), u(M * N, 0.0);
+    for (size_t m = 0; m < M; ++m)
+      for (size_t n = 0; n < N; ++n)
+        for (size_t k = 0; k < K; ++k) {
+          g[m * N + n] += (double)a[m * K + k] * bg[k * N + n];
+          u[m * N + n] += (double)a[m * K + k] * bu[k * N + n];
+        }
+    float *dA = dev(a), *dG = dev(bg), *dU = dev(bu), *dC = dev(std::vector<float>(M * N, 0.f));
+    mi_bridge::gemm_ffn(dA, dG, dU, dC, M, N, K);
+    auto h = host(dC, M * N);
+    double mx = 0, err = 0;
+    for (size_t i = 0; i < M * N; ++i) {
+      const double ref = g[i] / (1.0 + std::exp(-g[i])) * u[i];
+      mx = std::fmax(mx, std::fabs(ref));
+      err = std::fmax(err, std::fabs(ref - h[i]));
+    }
+    row("GB-10", "gemm_ffn SiLU(A Bg)*(A Bu) fp32, max rel <= 1e-4", err <= 1e-4 * mx,
+        std::to_string(err / mx));
+    dfree(dA); dfree(dG); dfree(dU); dfree(dC);
+  }
+  std::printf("%d/%d checks passed\n", g_passed, g_total);
+  return g_passed == g_total ? 0 : 1;
+}

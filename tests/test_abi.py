@@ -1,0 +1,133 @@
+"""CPU-side tests of the C-ABI library: it loads, exports every declared symbol,
+and validates arguments (status codes and messages) without touching a GPU.
+Also the host-side shape rules of the Tensor::matmul mirror (Tensor.cpp:174-209)."""
+import ctypes
+import os
+import re
+import subprocess
+
+import pytest
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+
+def _declared_c_functions():
+    text = open(os.path.join(ROOT, "include", "mi_gemm.h")).read()
+    return sorted(set(re.findall(r"\b(mi_[a-z_0-9]+)\s*\(", text)))
+
+
+def test_header_symbols_exported(mi):
+    names = _declared_c_functions()
+    assert len(names) >= 10
+    lib = mi.load_library()
+    for n in names:
+        assert hasattr(lib, n), n
+    assert set(names) == set(mi.C_SYMBOLS)
+
+
+def test_cpp_bridge_symbols_exported(mi):
+    out = subprocess.run(["nm", "-DC", "--defined-only", mi.LIB_PATH], capture_output=True,
+                         text=True, check=True).stdout
+    hdr = open(os.path.join(ROOT, "include", "gemm_bridge.hpp")).read()
+    decl = set(re.findall(r"^(?:void|bool|int|void\*|std::vector<size_t>)\s+([a-z_0-9]+)\(",
+                          hdr, flags=re.M))
+    assert {"gemm_bf16", "gemm_backward", "gemm_proj_trans_b", "gemm_proj", "gemm_ffn",
+            "fused_swiglu_gemm", "residual_add", "matmul"} <= decl
+    for n in decl:
+        assert f"mi_bridge::{n}(" in out, n
+
+
+def test_version(mi):
+    assert "gfx950" in mi.version()
+
+
+def _call(mi, M=64, N=64, K=64, lda=None, ldb=None, ldc=None, A=16, B=32, C=48, dt_in=1, dt_c=1,
+          transA=0, transB=0, epi=None):
+    lib = mi.load_library()
+    lda = lda if lda is not None else (M if transA else K)
+    ldb = ldb if ldb is not None else (K if transB else N)
+    ldc = ldc if ldc is not None else N
+    st = lib.mi_gemm(None, transA, transB, M, N, K, 1.0, ctypes.c_void_p(A), lda,
+                     ctypes.c_void_p(B), ldb, dt_in, 0.0, ctypes.c_void_p(C), ldc, dt_c,
+                     epi, None, 0)
+    return st, lib.mi_last_error().decode()
+
+
+def test_validation_status_codes(mi):
+    # Arguments are rejected before any device work, so these run without a GPU.
+    assert _call(mi, M=-1)[0] == 1                         # MI_ERR_SHAPE
+    st, msg = _call(mi, lda=10)
+    assert st == 2 and "lda" in msg                        # MI_ERR_LD
+    assert _call(mi, transA=1, lda=32)[0] == 2
+    assert _call(mi, ldb=3, transB=1)[0] == 2
+    assert _call(mi, ldc=8)[0] == 2
+    assert _call(mi, A=0)[0] == 3                          # MI_ERR_NULL
+    assert _call(mi, C=0)[0] == 3
+    assert _call(mi, dt_in=7)[0] == 4                      # MI_ERR_DTYPE
+    assert _call(mi, dt_c=9)[0] == 4
+    e = mi.MiEpilogue()
+    e.A2, e.B2 = 64, 128
+    assert _call(mi, epi=ctypes.byref(e))[0] == 5          # MI_ERR_UNSUPPORTED
+    e2 = mi.MiEpilogue()
+    e2.A2 = 64
+    assert _call(mi, epi=ctypes.byref(e2), transA=1, lda=64)[0] == 5
+    # empty outputs are a successful no-op (MetalBridge.mm:622-623,693)
+    assert _call(mi, M=0, A=0, B=0, C=0)[0] == 0
+    assert _call(mi, N=0, A=0, B=0, C=0)[0] == 0
+
+
+def test_batch_validation(mi):
+    lib = mi.load_library()
+    bt = mi.make_batch(0)
+    st = lib.mi_gemm_batched(None, 0, 0, 8, 8, 8, 1.0, ctypes.c_void_p(16), 8,
+                             ctypes.c_void_p(16), 8, 1, 0.0, ctypes.c_void_p(16), 8, 1,
+                             ctypes.byref(bt), None, None, 0)
+    assert st == 1
+    bt = mi.make_batch(4, heads=2, causal=9)
+    st = lib.mi_gemm_batched(None, 0, 0, 8, 8, 8, 1.0, ctypes.c_void_p(16), 8,
+                             ctypes.c_void_p(16), 8, 1, 0.0, ctypes.c_void_p(16), 8, 1,
+                             ctypes.byref(bt), None, None, 0)
+    assert st == 1 and "causal" in lib.mi_last_error().decode()
+    st = lib.mi_gemm_batched(None, 0, 0, 8, 8, 8, 1.0, None, 8, None, 8, 1, 0.0, None, 8, 1,
+                             None, None, None, 0)
+    assert st == 3
+
+
+def test_no_device_reports_status(mi):
+    import torch
+
+    if torch.cuda.is_available():
+        pytest.skip("a GPU is visible")
+    assert mi.load_library().mi_init() == 8                 # MI_ERR_NO_DEVICE
+    assert "gfx950" in mi.load_library().mi_last_error().decode()
+
+
+def test_aux_validation(mi):
+    lib = mi.load_library()
+    assert lib.mi_residual_add(None, None, None, 0, 1) == 0
+    assert lib.mi_residual_add(None, None, None, 5, 1) == 3
+    assert lib.mi_residual_add(None, ctypes.c_void_p(16), ctypes.c_void_p(16), 5, 3) == 4
+    assert lib.mi_softmax_causal(None, ctypes.c_void_p(16), 4, 8, 4, 1) == 2
+    assert lib.mi_softmax_bwd(None, None, None, 4, 8, 8, 1.0, 1) == 3
+
+
+def test_matmul_shape_rules(mi):
+    assert mi.matmul_shape((2, 3), (3, 2)) == (2, 2)
+    assert mi.matmul_shape((8, 1024, 2048), (2048, 3072)) == (8, 1024, 3072)
+    assert mi.matmul_shape((8, 16, 1024, 128), (8, 16, 128, 1024)) == (8, 16, 1024, 1024)
+    cases = [((3,), (3, 2), "Matmul requires at least 2 dimensions"),
+             ((2, 2, 3), (4, 2), "Inner dimensions must match for projection"),
+             ((2, 2, 3), (3, 3, 2), "Batch dimension must match for matmul"),
+             ((2, 2, 3), (2, 4, 2), "Inner dimensions must match for matmul"),
+             ((1, 2, 2, 3), (3, 3, 2), "Batch size must match for matrix multiplication"),
+             ((2, 3), (4, 2), "Inner dimensions must match for matmul")]
+    for a, b, msg in cases:
+        with pytest.raises(ValueError, match=msg):
+            mi.matmul_shape(a, b)
+
+
+def test_workspace_query(mi):
+    # few output tiles and a very long K: split-K space is requested
+    assert mi.workspace_size(1, 0, 1024, 1024, 65536) > 0
+    assert mi.workspace_size(0, 0, 8192, 5632, 2048) == 0
+    assert mi.workspace_size(0, 0, 0, 5, 5) == 0

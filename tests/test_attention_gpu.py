@@ -1,0 +1,99 @@
+"""GQA attention batched GEMM forms on the GPU vs the oracle's restatement of
+Attention.cpp:236-280 (forward) and 292-348 (backward), bf16 in / fp32 accumulate.
+
+S = Q K^T / sqrt(d) (NT, kv-head map, causal output mask), softmax, O = P V (NN,
+causal K skipping), dV = P^T dO and dK = dS^T Q (TN, K loop over the query heads
+of a KV group = the KV-group reduction), dP = dO V^T (NT), dQ = dS K (NN).
+"""
+import numpy as np
+import pytest
+
+from gpu_cases import TOL_BF16, check, host, inputs, layout, to_dev
+
+pytestmark = pytest.mark.gpu
+
+
+def _qkv(oracle, Bn, nH, nKV, T, d, seed):
+    q = inputs(oracle, (Bn, nH, T, d), seed)
+    k = inputs(oracle, (Bn, nKV, T, d), seed + 1)
+    v = inputs(oracle, (Bn, nKV, T, d), seed + 2)
+    do = inputs(oracle, (Bn, T, nH * d), seed + 3, 1e-2)
+    return q, k, v, do
+
+
+@pytest.mark.parametrize("Bn,nH,nKV,T,d", [(2, 16, 4, 256, 128), (1, 4, 2, 96, 64),
+                                           (2, 8, 8, 130, 32)])
+def test_attention_forward_backward(mi, dev, oracle, Bn, nH, nKV, T, d):
+    q, k, v, do = _qkv(oracle, Bn, nH, nKV, T, d, 900 + T)
+    Q, K, V, dO = (to_dev(x, dev, True) for x in (q, k, v, do))
+    O, P = mi.attention_forward(Q, K, V)
+    O_ref, P_ref = oracle.attention_fwd(q, k, v, want_p=True)
+    check(host(O), O_ref, TOL_BF16, "O")
+    check(host(P), P_ref, TOL_BF16, "P")
+    dQ, dK, dV = mi.attention_backward(Q, K, V, dO, P)
+    dQ_ref, dK_ref, dV_ref = oracle.attention_bwd(q, k, v, do)
+    check(host(dV), dV_ref, TOL_BF16, "dV")
+    check(host(dQ), dQ_ref, TOL_BF16, "dQ")
+    check(host(dK), dK_ref, TOL_BF16, "dK")
+
+
+def test_attention_config4_full_size(mi, dev, oracle):
+    """BASELINE config 4 (B=8, 16 q heads / 4 kv heads, T=1024, d=128): the whole batch
+    on the GPU, the oracle on batch elements 0 and 7."""
+    Bn, nH, nKV, T, d = 8, 16, 4, 1024, 128
+    q, k, v, do = _qkv(oracle, Bn, nH, nKV, T, d, 4000)
+    Q, K, V, dO = (to_dev(x, dev, True) for x in (q, k, v, do))
+    O, P = mi.attention_forward(Q, K, V)
+    dQ, dK, dV = mi.attention_backward(Q, K, V, dO, P)
+    Oh, dQh, dKh, dVh = host(O), host(dQ), host(dK), host(dV)
+    rows = host(P[:, :, ::97, :]).sum(axis=-1)
+    assert np.all(np.abs(rows - 1.0) < 2e-2), "softmax rows must sum to 1"
+    for b in (0, 7):
+        sl = slice(b, b + 1)
+        O_ref = oracle.attention_fwd(q[sl], k[sl], v[sl])
+        check(Oh[sl], O_ref, TOL_BF16, f"O[{b}]")
+        dQ_ref, dK_ref, dV_ref = oracle.attention_bwd(q[sl], k[sl], v[sl], do[sl])
+        check(dQh[sl], dQ_ref, TOL_BF16, f"dQ[{b}]")
+        check(dKh[sl], dK_ref, TOL_BF16, f"dK[{b}]")
+        check(dVh[sl], dV_ref, TOL_BF16, f"dV[{b}]")
+
+
+@pytest.mark.parametrize("bf16", [True, False], ids=["bf16", "f32"])
+def test_causal_modes(mi, dev, oracle, bf16):
+    """The three causal modes of mi_gemm_batched against dense products with zeros."""
+    import torch
+
+    T, d, nb = 200, 64, 3
+    tol = TOL_BF16 if bf16 else 1e-4
+    low = np.tril(np.ones((T, T), np.float32))
+    # OUT_LOWER: S = Q K^T, masked entries take mask_value
+    q = inputs(oracle, (nb, T, d), 11, 1.0, bf16)
+    kk = inputs(oracle, (nb, T, d), 12, 1.0, bf16)
+    S = torch.empty((nb, T, T), dtype=torch.float32, device=dev)
+    bt = mi.make_batch(nb, 1, a=(T * d, 0, 1), b=(T * d, 0, 1), c=(T * T, 0, 1),
+                       causal=mi.MI_CAUSAL_OUT_LOWER, mask_value=-7.0)
+    mi.gemm_batched(to_dev(q, dev, bf16), to_dev(kk, dev, bf16), S, T, T, d, bt, transB=True)
+    s = host(S)
+    for i in range(nb):
+        ref = oracle.gemm(0, 1, T, T, d, q[i], kk[i])
+        check(s[i] * low, ref * low, tol, "OUT_LOWER values")
+        assert np.all(s[i][low == 0] == -7.0)
+    # A_LOWER: C = P V with P lower triangular (k <= m)
+    p = inputs(oracle, (nb, T, T), 13, 1.0, bf16) * low
+    v = inputs(oracle, (nb, T, d), 14, 1.0, bf16)
+    C = torch.empty((nb, T, d), dtype=torch.float32, device=dev)
+    bt = mi.make_batch(nb, 1, a=(T * T, 0, 1), b=(T * d, 0, 1), c=(T * d, 0, 1),
+                       causal=mi.MI_CAUSAL_A_LOWER)
+    mi.gemm_batched(to_dev(p, dev, bf16), to_dev(v, dev, bf16), C, T, d, T, bt)
+    c = host(C)
+    for i in range(nb):
+        check(c[i], oracle.gemm(0, 0, T, d, T, p[i], v[i]), tol, "A_LOWER")
+    # A_UPPER with K segments: C = sum_j P_j^T V_j, op(A) = P^T upper triangular
+    g = 3
+    p = inputs(oracle, (g, T, T), 15, 1.0, bf16) * low
+    v = inputs(oracle, (g, T, d), 16, 1.0, bf16)
+    C = torch.empty((T, d), dtype=torch.float32, device=dev)
+    bt = mi.make_batch(1, 1, k_segments=g, seg_a=T * T, seg_b=T * d, causal=mi.MI_CAUSAL_A_UPPER)
+    mi.gemm_batched(to_dev(p, dev, bf16), to_dev(v, dev, bf16), C, T, d, T, bt, transA=True)
+    ref = oracle.gemm(1, 0, T, d, T, p, v, nseg=g, segA=T * T, segB=T * d)
+    check(host(C), ref, tol, "A_UPPER segments")

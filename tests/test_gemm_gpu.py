@@ -1,0 +1,301 @@
+"""GPU parity of the HIP GEMM core against the CPU oracle, through the C ABI.
+
+Bar: fp32 inputs within max relative error 1e-4, bf16 inputs within 1e-2 of the
+float64 oracle fed the same bf16-rounded inputs (max relative error =
+max|y - ref| / max|ref|). Small integers give bit-exact expectations. Full-size
+BASELINE configurations are checked on sampled rows against the oracle and on
+every element through row/column checksums.
+"""
+import numpy as np
+import pytest
+
+from gpu_cases import (TOL_BF16, TOL_F32, check, checksums, host, inputs, layout, sample_rows,
+                       to_dev)
+
+pytestmark = pytest.mark.gpu
+
+
+def _tol(bf16):
+    return TOL_BF16 if bf16 else TOL_F32
+
+
+def _run(mi, dev, oracle, M, N, K, tA, tB, bf16, seed, *, out_bf16=None, alpha=1.0, beta=0.0,
+         bias=False, residual=False, dual=False, prologue=False, pad=(0, 0, 0), ws=None,
+         a_std=1.0, b_std=0.02):
+    import torch
+
+    out_bf16 = bf16 if out_bf16 is None else out_bf16
+    a = inputs(oracle, (M, K), seed, a_std, bf16)
+    b = inputs(oracle, (K, N), seed + 1, b_std, bf16)
+    A = layout(a, tA)
+    B = layout(b, tB)
+    lda, ldb, ldc = A.shape[1] + pad[0], B.shape[1] + pad[1], N + pad[2]
+    Ap = np.zeros((A.shape[0], lda), np.float32); Ap[:, :A.shape[1]] = A
+    Bp = np.zeros((B.shape[0], ldb), np.float32); Bp[:, :B.shape[1]] = B
+    kw = {}
+    ref_kw = {}
+    if bias:
+        bv = inputs(oracle, (N,), seed + 2, 0.02, bf16)
+        kw["bias"] = to_dev(bv, dev, bf16)
+        ref_kw["bias"] = bv
+    c0 = inputs(oracle, (M, N), seed + 3, 0.5, out_bf16)
+    C0 = np.zeros((M, ldc), np.float32); C0[:, :N] = c0
+    if beta != 0.0:
+        ref_kw.update(beta=beta, C0=c0)
+    if residual:
+        rv = inputs(oracle, (M, N), seed + 4, 0.5, bf16)
+        kw["residual"] = to_dev(rv, dev, bf16)
+        ref_kw["R"] = rv
+    mode = 0
+    if dual:
+        b2 = inputs(oracle, (K, N), seed + 5, b_std, bf16)
+        B2 = layout(b2, tB)
+        B2p = np.zeros_like(Bp); B2p[:, :B2.shape[1]] = B2
+        kw["B2"] = to_dev(B2p, dev, bf16)
+        ref_kw["B2"] = b2
+        mode = 1
+    if prologue:
+        a2 = inputs(oracle, (M, K), seed + 6, 1.0, bf16)
+        A2p = np.zeros_like(Ap); A2p[:, :K] = a2
+        kw["A2"] = to_dev(A2p, dev, bf16)
+        ref_kw["A2"] = a2
+        mode = 2
+    C = to_dev(C0, dev, out_bf16)
+    mi.gemm(to_dev(Ap, dev, bf16), to_dev(Bp, dev, bf16), C, M, N, K, transA=tA, transB=tB,
+            alpha=alpha, beta=beta, lda=lda, ldb=ldb, ldc=ldc, workspace=ws, **kw)
+    torch.cuda.synchronize()
+    got = host(C)[:, :N]
+    ref = oracle.gemm(0, 0, M, N, K, a, b, alpha=alpha, mode=mode, **ref_kw)
+    return got, ref
+
+
+@pytest.mark.parametrize("bf16", [True, False], ids=["bf16", "f32"])
+@pytest.mark.parametrize("tA,tB", [(0, 0), (0, 1), (1, 0), (1, 1)], ids=["NN", "NT", "TN", "TT"])
+@pytest.mark.parametrize("shape", [(77, 130, 95), (320, 384, 256), (1, 1, 1), (5, 300, 17),
+                                   (513, 257, 136)])
+def test_layouts(mi, dev, oracle, bf16, tA, tB, shape):
+    M, N, K = shape
+    got, ref = _run(mi, dev, oracle, M, N, K, tA, tB, bf16, seed=100 + M)
+    check(got, ref, _tol(bf16), f"{shape} tA={tA} tB={tB}")
+
+
+@pytest.mark.parametrize("bf16", [True, False], ids=["bf16", "f32"])
+def test_leading_dimension_padding(mi, dev, oracle, bf16):
+    for tA, tB in [(0, 0), (1, 1), (0, 1), (1, 0)]:
+        got, ref = _run(mi, dev, oracle, 200, 136, 72, tA, tB, bf16, seed=7, pad=(8, 16, 4))
+        check(got, ref, _tol(bf16), f"padded tA={tA} tB={tB}")
+    # leading dimensions that break 16-byte alignment take the element-wise path
+    got, ref = _run(mi, dev, oracle, 64, 40, 48, 0, 0, bf16, seed=8, pad=(3, 1, 1))
+    check(got, ref, _tol(bf16), "unaligned ld")
+
+
+def test_small_integers_bit_exact(mi, dev, oracle):
+    """Integers in [-8, 8]: exact in bf16, sums exact in fp32 -> bit-exact outputs."""
+    import torch
+
+    rng = np.random.default_rng(5)
+    for (M, N, K), (tA, tB) in [((300, 260, 520), (0, 0)), ((64, 96, 1000), (1, 0)),
+                                ((129, 65, 33), (0, 1)), ((256, 256, 512), (1, 1))]:
+        a = rng.integers(-8, 9, (M, K)).astype(np.float32)
+        b = rng.integers(-8, 9, (K, N)).astype(np.float32)
+        for bf16 in (True, False):
+            C = torch.zeros((M, N), dtype=torch.float32, device=dev)
+            mi.gemm(to_dev(layout(a, tA), dev, bf16), to_dev(layout(b, tB), dev, bf16), C, M, N, K,
+                    transA=tA, transB=tB)
+            assert np.array_equal(C.cpu().numpy(), a.astype(np.int64) @ b.astype(np.int64))
+
+
+def test_config1_fp32_linear_bias(mi, dev, oracle):
+    """Y = X W^T + b, X [512x768], W [768x768] ~ N(0,0.02), fp32."""
+    got, ref = _run(mi, dev, oracle, 512, 768, 768, 0, 1, False, seed=1, bias=True)
+    check(got, ref, TOL_F32, "config 1")
+    assert oracle.l2_rel_err(got, ref) < 1e-4  # test_gpu_kernels.cpp:87-116 metric
+
+
+@pytest.mark.parametrize("bf16", [True, False], ids=["bf16", "f32"])
+def test_epilogues(mi, dev, oracle, bf16):
+    for kw in [dict(bias=True), dict(beta=1.0), dict(beta=-0.5, alpha=2.0), dict(residual=True),
+               dict(bias=True, beta=1.0, residual=True, alpha=0.5)]:
+        for tA, tB in [(0, 0), (1, 0), (0, 1)]:
+            got, ref = _run(mi, dev, oracle, 264, 200, 144, tA, tB, bf16, seed=21, **kw)
+            check(got, ref, _tol(bf16), f"{kw} tA={tA} tB={tB}")
+    # bf16 inputs with an fp32 output (dW) accumulating into the existing value
+    got, ref = _run(mi, dev, oracle, 256, 320, 512, 1, 0, True, seed=22, out_bf16=False, beta=1.0)
+    check(got, ref, TOL_BF16, "bf16 in / fp32 out, beta=1")
+
+
+@pytest.mark.parametrize("bf16", [True, False], ids=["bf16", "f32"])
+def test_dual_silu_gate(mi, dev, oracle, bf16):
+    """gemm_ffn: C = SiLU(A Bg) * (A Bu) (gemm_ffn.metal:160-181)."""
+    for (M, N, K), (tA, tB) in [((300, 200, 160), (0, 0)), ((512, 384, 256), (0, 1)),
+                                ((96, 72, 40), (1, 0))]:
+        got, ref = _run(mi, dev, oracle, M, N, K, tA, tB, bf16, seed=31, dual=True, b_std=0.1)
+        check(got, ref, _tol(bf16), f"dual {M}x{N}x{K}")
+
+
+@pytest.mark.parametrize("bf16", [True, False], ids=["bf16", "f32"])
+def test_prologue_silu_gate(mi, dev, oracle, bf16):
+    """fused_swiglu_gemm: C = (SiLU(G) * U) B (fused_swiglu_gemm.metal:48-77)."""
+    for (M, N, K), tB in [((300, 200, 160), 0), ((512, 256, 512), 1), ((33, 17, 24), 0)]:
+        got, ref = _run(mi, dev, oracle, M, N, K, 0, tB, bf16, seed=41, prologue=True)
+        check(got, ref, _tol(bf16), f"prologue {M}x{N}x{K}")
+
+
+def test_split_k(mi, dev, oracle):
+    import torch
+
+    ws = torch.empty(64 << 20, dtype=torch.float32, device=dev)
+    for M, N, K, beta in [(1024, 1024, 65536, 0.0), (256, 384, 30000, 1.0), (100, 60, 70000, 0.0)]:
+        need = mi.workspace_size(1, 0, M, N, K)
+        got, ref = _run(mi, dev, oracle, M, N, K, 1, 0, True, seed=51, out_bf16=False, beta=beta,
+                        ws=ws)
+        check(got, ref, TOL_BF16, f"split-K {M}x{N}x{K} (ws {need} B)")
+
+
+def test_zero_k(mi, dev, oracle):
+    got, ref = _run(mi, dev, oracle, 70, 90, 0, 0, 0, False, seed=61, beta=0.5, bias=True)
+    check(got, ref, TOL_F32, "K=0")
+
+
+# ---- BASELINE decoder-block GEMM sets -------------------------------------------
+
+def _block_set(mi, dev, oracle, M, H, Nqkv, I, bf16, seed):
+    """Forward (NN), dX (NT) and dW (TN) for QKV, O, gate, up, down: engine layout W[in,out]."""
+    import torch
+
+    shapes = {"qkv": (H, Nqkv), "o": (H, H), "gate": (H, I), "up": (H, I), "down": (I, H)}
+    rows = sample_rows(M, 6, seed)
+    for name, (din, dout) in shapes.items():
+        x = inputs(oracle, (M, din), seed + 1, 1.0, bf16)
+        w = inputs(oracle, (din, dout), seed + 2, 0.02, bf16)
+        dy = inputs(oracle, (M, dout), seed + 3, 1e-2, bf16)
+        X, W, dY = to_dev(x, dev, bf16), to_dev(w, dev, bf16), to_dev(dy, dev, bf16)
+        odt = torch.bfloat16 if bf16 else torch.float32
+        Y = torch.empty((M, dout), dtype=odt, device=dev)
+        dX = torch.empty((M, din), dtype=odt, device=dev)
+        dW = torch.zeros((din, dout), dtype=torch.float32, device=dev)
+        mi.gemm(X, W, Y, M, dout, din)                                  # Y = X W
+        mi.gemm(dY, W, dX, M, din, dout, transB=True)                   # dX = dY W^T
+        mi.gemm(X, dY, dW, din, dout, M, transA=True, beta=1.0)         # dW += X^T dY
+        torch.cuda.synchronize()
+        tol = TOL_BF16 if bf16 else TOL_F32
+        y, dx, dw = host(Y), host(dX), host(dW)
+        check(y[rows], oracle.gemm(0, 0, M, dout, din, x, w, rows=rows), tol, f"{name} fwd")
+        check(dx[rows], oracle.gemm(0, 1, M, din, dout, dy, w, rows=rows), tol, f"{name} dX")
+        wrows = sample_rows(din, 6, seed + 9)
+        check(dw[wrows], oracle.gemm(1, 0, din, dout, M, x, dy, rows=wrows), tol, f"{name} dW")
+        for got, (a_op, b_op) in [(y, (x, w)), (dx, (dy, w.T)), (dw, (x.T, dy))]:
+            col, row = checksums(a_op, b_op)
+            check(got.sum(axis=0), col, tol, f"{name} column checksum")
+            check(got.sum(axis=1), row, tol, f"{name} row checksum")
+
+
+def test_config2_gpt_small_fp32(mi, dev, oracle):
+    """d=768, 12 heads MHA (QKV 768->2304), SwiGLU 2048, M=2048, fp32."""
+    _block_set(mi, dev, oracle, 2048, 768, 2304, 2048, False, seed=200)
+
+
+def test_config3_1p6b_bf16(mi, dev, oracle):
+    """d=2048, GQA 16/4 x 128 (QKV 2048->3072), SwiGLU 5632, M=8192, bf16."""
+    _block_set(mi, dev, oracle, 8192, 2048, 3072, 5632, True, seed=300)
+
+
+def test_config5_lm_head(mi, dev, oracle):
+    """logits = X E^T (NT), dX = dL E (NN), dE = dL^T X (TN, fp32)."""
+    import torch
+
+    M, H, V = 8192, 2048, 32000
+    x = inputs(oracle, (M, H), 501, 1.0)
+    e = inputs(oracle, (V, H), 502, 0.02)
+    dl = inputs(oracle, (M, V), 503, 1e-3)
+    X, E, dL = to_dev(x, dev, True), to_dev(e, dev, True), to_dev(dl, dev, True)
+    logits = torch.empty((M, V), dtype=torch.bfloat16, device=dev)
+    dX = torch.empty((M, H), dtype=torch.bfloat16, device=dev)
+    dE = torch.zeros((V, H), dtype=torch.float32, device=dev)
+    mi.gemm(X, E, logits, M, V, H, transB=True)
+    mi.gemm(dL, E, dX, M, H, V)
+    mi.gemm(dL, X, dE, V, H, M, transA=True, beta=1.0)
+    torch.cuda.synchronize()
+    rows = sample_rows(M, 4, 5)
+    check(host(logits[rows]), oracle.gemm(0, 1, M, V, H, x, e, rows=rows), TOL_BF16, "logits")
+    check(host(dX[rows]), oracle.gemm(0, 0, M, H, V, dl, e, rows=rows), TOL_BF16, "dX")
+    vrows = sample_rows(V, 4, 6)
+    check(host(dE[vrows]), oracle.gemm(1, 0, V, H, M, dl, x, rows=vrows), TOL_BF16, "dE")
+    for got, (a_op, b_op) in [(logits, (x, e.T)), (dX, (dl, e)), (dE, (dl.T, x))]:
+        g = host(got)
+        col, row = checksums(a_op, b_op)
+        check(g.sum(axis=0), col, TOL_BF16, "column checksum")
+        check(g.sum(axis=1), row, TOL_BF16, "row checksum")
+
+
+# ---- Tensor::matmul mirror --------------------------------------------------------
+
+@pytest.mark.parametrize("bf16", [True, False], ids=["bf16", "f32"])
+def test_tensor_matmul_mirror(mi, dev, oracle, bf16):
+    # TC-12 / TC-13 known answers (test_math_ops.cpp:167-189)
+    A = to_dev(np.array([[1, 2, 3], [4, 5, 6]], np.float32), dev, bf16)
+    B = to_dev(np.array([[7, 8], [9, 10], [11, 12]], np.float32), dev, bf16)
+    assert host(mi.matmul(A, B)).tolist() == [[58, 64], [139, 154]]
+    A3 = to_dev(np.array([1, 2, 3, 4, 5, 6, 1, 1, 1, 2, 2, 2], np.float32).reshape(2, 2, 3), dev,
+                bf16)
+    B3 = to_dev(np.array([7, 8, 9, 10, 11, 12, 1, 2, 3, 4, 5, 6], np.float32).reshape(2, 3, 2),
+                dev, bf16)
+    C3 = host(mi.matmul(A3, B3))
+    assert C3[0, 0, 0] == 58 and C3[1, 1, 1] == 24
+    # projection branch: [2, 96, 160] x [160, 72]
+    x = inputs(oracle, (2, 96, 160), 71, 1.0, bf16)
+    w = inputs(oracle, (160, 72), 72, 0.05, bf16)
+    y = host(mi.matmul(to_dev(x, dev, bf16), to_dev(w, dev, bf16)))
+    check(y.reshape(192, 72), oracle.gemm(0, 0, 192, 72, 160, x.reshape(192, 160), w), _tol(bf16))
+    # batched branch: [2, 3, 40, 24] x [2, 3, 24, 56]
+    a = inputs(oracle, (2, 3, 40, 24), 73, 1.0, bf16)
+    b = inputs(oracle, (2, 3, 24, 56), 74, 1.0, bf16)
+    c = host(mi.matmul(to_dev(a, dev, bf16), to_dev(b, dev, bf16)))
+    for i in range(2):
+        for j in range(3):
+            check(c[i, j], oracle.gemm(0, 0, 40, 56, 24, a[i, j], b[i, j]), _tol(bf16))
+    with pytest.raises(ValueError, match="Inner dimensions must match for projection"):
+        mi.matmul(to_dev(x, dev, bf16), to_dev(x[0], dev, bf16))
+
+
+def test_reference_named_entry_points(mi, dev, oracle):
+    import torch
+
+    M, N, K = 192, 160, 128
+    a = inputs(oracle, (M, K), 81)
+    b = inputs(oracle, (K, N), 82, 0.05)
+    A, B = to_dev(a, dev, True), to_dev(b, dev, True)
+    C = torch.empty((M, N), dtype=torch.bfloat16, device=dev)
+    mi.begin_scope()
+    mi.gemm_bf16(A, B, C, M, N, K)
+    mi.end_scope()
+    check(host(C), oracle.gemm(0, 0, M, N, K, a, b), TOL_BF16, "gemm_bf16")
+    Bt = to_dev(layout(b, 1), dev, True)
+    mi.gemm_proj_trans_b(A, Bt, C, M, N, K)
+    check(host(C), oracle.gemm(0, 0, M, N, K, a, b), TOL_BF16, "gemm_proj_trans_b")
+    At = to_dev(layout(a, 1), dev, True)
+    mi.gemm_backward(At, B, C, M, N, K)
+    check(host(C), oracle.gemm(0, 0, M, N, K, a, b), TOL_BF16, "gemm_backward")
+    D = torch.ones((M, N), dtype=torch.float32, device=dev)
+    mi.gemm_backward(At, B, D, M, N, K, accumulate=True)
+    check(host(D), oracle.gemm(0, 0, M, N, K, a, b) + 1.0, TOL_BF16, "gemm_backward +=")
+    af, bf = inputs(oracle, (M, K), 83, bf16=False), inputs(oracle, (K, N), 84, 0.05, bf16=False)
+    Cf = torch.empty((M, N), dtype=torch.float32, device=dev)
+    mi.gemm_proj(to_dev(af, dev, False), to_dev(bf, dev, False), Cf, M, N, K)
+    check(host(Cf), oracle.gemm(0, 0, M, N, K, af, bf), TOL_F32, "gemm_proj")
+    R = torch.full((M, N), 0.25, dtype=torch.float32, device=dev)
+    mi.residual_add(Cf, R)
+    check(host(Cf), oracle.gemm(0, 0, M, N, K, af, bf) + 0.25, TOL_F32, "residual_add")
+    mi.gemm_bf16(A, B, C, 0, N, K)  # zero-size no-op
+
+
+def test_cpp_bridge_program():
+    """The C++ mirror (include/gemm_bridge.hpp) run by tests/cpp/test_bridge."""
+    import os
+    import subprocess
+
+    exe = os.path.join(os.path.dirname(__file__), "cpp", "test_bridge")
+    assert os.path.exists(exe), "tests/cpp/test_bridge not built (run __graft_entry__.build())"
+    r = subprocess.run([exe], capture_output=True, text=True, timeout=120)
+    print(r.stdout)
+    assert r.returncode == 0, r.stdout + r.stderr
