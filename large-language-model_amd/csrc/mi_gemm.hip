@@ -77,21 +77,21 @@ int current_cus() {
 
 // ---- kernel table ------------------------------------------------------------
 
-KernelFn pick_kernel(int dtype_in, int transA, int transB, int cfg) {
+KernelFn pick_kernel(int dtype_in, int transA, int transB, int cfg, bool fast) {
   const int lay = (transA ? 2 : 0) | (transB ? 1 : 0);
   if (dtype_in == MI_BF16) {
     switch (lay) {
-      case 0: return pick_bf16_00(cfg);
-      case 1: return pick_bf16_01(cfg);
-      case 2: return pick_bf16_10(cfg);
-      default: return pick_bf16_11(cfg);
+      case 0: return pick_bf16_00(cfg, fast);
+      case 1: return pick_bf16_01(cfg, fast);
+      case 2: return pick_bf16_10(cfg, fast);
+      default: return pick_bf16_11(cfg, fast);
     }
   }
   switch (lay) {
-    case 0: return pick_f32_00(cfg);
-    case 1: return pick_f32_01(cfg);
-    case 2: return pick_f32_10(cfg);
-    default: return pick_f32_11(cfg);
+    case 0: return pick_f32_00(cfg, fast);
+    case 1: return pick_f32_01(cfg, fast);
+    case 2: return pick_f32_10(cfg, fast);
+    default: return pick_f32_11(cfg, fast);
   }
 }
 
@@ -139,7 +139,7 @@ int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
 // time ~ (waves of workgroups over the CUs) x (per-workgroup MFMA time at the
 // configuration's sustained rate) + (split-K partial write/read traffic).
 Plan make_plan(int dtype_in, int64_t M, int64_t N, int64_t Ktot, int64_t batch, int mode,
-               bool allow_split, int64_t ws_limit_elems, int cus) {
+               bool allow_split, int64_t ws_limit_elems, int cus, bool fast) {
   Plan best{CFG_L, 1, 1, 1};
   if (mode == MODE_DUAL) {
     const CfgShape s = shape_of(dtype_in, CFG_DUAL);
@@ -153,7 +153,7 @@ Plan make_plan(int dtype_in, int64_t M, int64_t N, int64_t Ktot, int64_t batch, 
   const double hbm = 5.0e12;                                               // sustained B/s
   double best_t = 1e30;
   const int cfgs[2] = {CFG_L, CFG_S};
-  for (int ci = 0; ci < 2; ++ci) {
+  for (int ci = fast ? 0 : 1; ci < 2; ++ci) {
     const int cfg = cfgs[ci];
     const CfgShape s = shape_of(dtype_in, cfg);
     const double eff = (cfg == CFG_L || dtype_in != MI_BF16) ? 0.80 : 0.55;
@@ -259,13 +259,30 @@ int run(const Problem& P, hipStream_t stream) {
                     (!P.ep.residual || (al(P.ep.residual, P.ep.residual_dtype == MI_BF16 ? 8 : 16) &&
                                         P.ep.ldr % 4 == 0 && b.r_outer % 4 == 0 && b.r_inner % 4 == 0));
 
+  // Fast (buffer-load) path: chunks never straddle a matrix edge and every byte
+  // offset the loaders form stays below 2^31.
+  const int esz = P.dtype_in == MI_BF16 ? 2 : 4;
+  const int64_t a_rows = P.M, b_rows = P.N;
+  const int64_t a_contig = P.transA ? P.M : P.K, b_contig = P.transB ? P.K : P.N;
+  const int64_t extA = P.K == 0 ? 0 : (P.transA ? (P.K - 1) * P.lda + P.M : (P.M - 1) * P.lda + P.K) * esz;
+  const int64_t extB = P.K == 0 ? 0 : (P.transB ? (P.N - 1) * P.ldb + P.K : (P.K - 1) * P.ldb + P.N) * esz;
+  const int64_t lim = (int64_t)1 << 31;
+  auto span_ok = [&](bool kc, int64_t rows, int64_t ld) {
+    // largest offset formed: a row/k line one tile (<= 512 rows, <= 64 k) past the edge
+    const int64_t far = kc ? (rows + 512) * ld * esz + (P.K + 64) * esz
+                           : (P.K + 64) * ld * esz + (rows + 512) * esz;
+    return far < lim;
+  };
+  const bool fast = vecA && vecB && mult(a_contig) && mult(b_contig) && extA < lim && extB < lim &&
+                    span_ok(!P.transA, a_rows, P.lda) && span_ok(P.transB != 0, b_rows, P.ldb);
+
   const int64_t Ktot = P.K * b.k_segments;
   const int64_t ws_elems = P.ws ? (int64_t)(P.ws_bytes / sizeof(float)) : 0;
   const bool allow_split = ws_elems > 0 && aligned16(P.ws);
   Plan plan = make_plan(P.dtype_in, P.M, P.N, Ktot, b.batch, mode, allow_split, ws_elems,
-                        current_cus());
+                        current_cus(), fast);
 
-  KernelFn fn = pick_kernel(P.dtype_in, P.transA, P.transB, plan.cfg);
+  KernelFn fn = pick_kernel(P.dtype_in, P.transA, P.transB, plan.cfg, fast);
   if (!fn) return fail(MI_ERR_UNSUPPORTED, "no kernel for this layout / mode");
 
   Params p;
@@ -310,6 +327,8 @@ int run(const Problem& P, hipStream_t stream) {
   p.vecA = vecA;
   p.vecB = vecB;
   p.cvec = cvec;
+  p.extA = (uint32_t)(fast ? extA : 0);
+  p.extB = (uint32_t)(fast ? extB : 0);
 
   const int64_t nblocks = (int64_t)plan.tiles_m * plan.tiles_n * plan.splits * b.batch;
   if (nblocks > INT32_MAX) return fail(MI_ERR_SHAPE, "too many tiles");
@@ -420,7 +439,7 @@ size_t mi_gemm_workspace_size(int transA, int transB, int64_t M, int64_t N, int6
   if (M <= 0 || N <= 0 || K <= 0 || batch <= 0) return 0;
   int cus = 256;
   if (init_devices() == MI_OK) cus = current_cus();
-  const Plan pl = make_plan(dtype_in, M, N, K, batch, MODE_PLAIN, true, INT64_MAX / 8, cus);
+  const Plan pl = make_plan(dtype_in, M, N, K, batch, MODE_PLAIN, true, INT64_MAX / 8, cus, true);
   return pl.splits > 1 ? (size_t)pl.splits * (size_t)M * (size_t)N * (size_t)batch * sizeof(float) : 0;
 }
 

@@ -57,6 +57,7 @@ struct Params {
   int c_bf16, bias_bf16, r_bf16;
   int vecA, vecB;  // 16-byte global loads legal for A (and A2) / B (and B2)
   int cvec;        // 4-wide C / R / bias accesses legal
+  uint32_t extA, extB;  // byte extent of one batch/segment matrix of A (A2) / B (B2)
 };
 
 // ---------------------------------------------------------------------------
@@ -165,10 +166,46 @@ __device__ __forceinline__ u32x4_t swiglu_chunk(u32x4_t g, u32x4_t u) {
 //   KC = true : element (r, k) at r*ld + k   (K-contiguous)
 //   KC = false: element (r, k) at k*ld + r   (row-contiguous; transposed in registers)
 // PRO (prologue): the operand is SiLU(X) * X2, computed at LDS-store time.
+// FAST: buffer loads through a resource descriptor whose num_records is the
+//   operand's byte extent.  Offsets past the extent return zero in hardware, so
+//   rows past the matrix edge (K-contiguous) and K past the edge (row-contiguous)
+//   need no code; the remaining edge (K tail of a K-contiguous row, row tail of a
+//   row-contiguous k line) is sent to an offset past the extent.  Every chunk is
+//   one branch-free buffer_load_dwordx4.  Requires every chunk fully inside or
+//   fully outside the matrix, 16-byte alignment and 31-bit byte offsets (checked
+//   on the host).
+// !FAST: element-granular bounds for any shape, leading dimension or alignment.
 
-template <typename T, int R, bool KC, bool PRO>
+constexpr uint32_t kBufOOB = 0x80000000u;          // offset past any extent < 2^31
+constexpr int kBufFlags = 0x00020000;               // raw-buffer dword3 for gfx9-family
+
+// Values that are uniform across the workgroup but which the compiler may have
+// computed in vector registers (integer division lowers through VALU).  Moving
+// them to scalar registers keeps buffer descriptors scalar: a descriptor the
+// compiler believes divergent is wrapped in a per-load waterfall loop.
+__device__ __forceinline__ int uniform(int v) { return __builtin_amdgcn_readfirstlane(v); }
+
+template <typename P>
+__device__ __forceinline__ P* uniform(P* ptr) {
+  const uint64_t v = (uint64_t)ptr;
+  const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)v);
+  const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(v >> 32));
+  return (P*)(((uint64_t)hi << 32) | lo);
+}
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t ext) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(uniform(base)), (short)0,
+                                           (int)uniform((int)ext), kBufFlags);
+}
+
+__device__ __forceinline__ u32x4_t buf_load16(__amdgpu_buffer_rsrc_t r, uint32_t voff) {
+  return __builtin_amdgcn_raw_buffer_load_b128(r, (int)voff, 0, 0);
+}
+
+template <typename T, int R, bool KC, bool PRO, bool FAST>
 struct TileLoader {
   static constexpr int CH = ElemTraits<T>::CH;
+  static constexpr int ESZ = (int)sizeof(T);
   static constexpr int NT = 256;
   // K-contiguous: R*8 chunks over 256 threads.
   static constexpr int NCK = (R * 8 + NT - 1) / NT;
@@ -178,39 +215,93 @@ struct TileLoader {
   static constexpr int NREG = KC ? NCK : NBLK * CH;
   u32x4_t st[NREG];
   u32x4_t st2[PRO ? NREG : 1];
+  // fast path: per-thread byte offsets fixed for the tile
+  uint32_t off0;             // KC: chunk 0 of this thread at k = 0
+  uint32_t boff[KC ? 1 : NBLK];  // !KC: block i at k = 0 (kBufOOB when its rows are outside)
+  int ldb;                   // leading dimension in bytes
+  int koff;                  // KC: this thread's chunk column * CH
 
-  // base: operand pointer for the current batch/segment.  rows: valid row count
-  // (M or N).  row0: first tile row.  k0: first K of the tile; kseg: K extent.
-  __device__ __forceinline__ void load(const void* base, const void* base2, int64_t ld, int rows,
-                                       int row0, int k0, int kseg, bool vec) {
+  __device__ __forceinline__ void init(int64_t ld, int rows, int row0) {
     const int tid = threadIdx.x;
-    if constexpr (KC) {
+    if constexpr (FAST) {
+      ldb = (int)ld * ESZ;
+      if constexpr (KC) {
+        koff = (tid & 7) * CH;
+        off0 = (uint32_t)((row0 + (tid >> 3)) * ldb + koff * ESZ);
+      } else {
 #pragma unroll
-      for (int i = 0; i < NCK; ++i) {
-        const int idx = tid + NT * i;
-        const int r = idx >> 3, c = idx & 7;
-        const int grow = row0 + r, gk = k0 + c * CH;
-        int n_ok = (grow < rows && idx < R * 8) ? kseg - gk : 0;
-        n_ok = n_ok < 0 ? 0 : (n_ok > CH ? CH : n_ok);
-        const int64_t off = (int64_t)grow * ld + gk;
-        st[i] = load_chunk<T>(base, off, n_ok, vec);
-        if constexpr (PRO) st2[i] = load_chunk<T>(base2, off, n_ok, vec);
+        for (int i = 0; i < NBLK; ++i) {
+          const int b = tid + NT * i;
+          const int rb = b % (R / CH), kb = b / (R / CH);
+          const int grow = row0 + rb * CH;
+          boff[i] = (b < NBLK_TOT && grow < rows) ? (uint32_t)(grow * ESZ + kb * CH * ldb) : kBufOOB;
+        }
+      }
+    }
+  }
+
+  // base/base2: operand pointers of the current batch and K segment; ext: their
+  // byte extent.  k0: first K of the tile; kseg: K extent of the segment.
+  __device__ __forceinline__ void load(const void* base, const void* base2, uint32_t ext, int64_t ld,
+                                       int rows, int row0, int k0, int kseg, bool vec) {
+    const int tid = threadIdx.x;
+    if constexpr (FAST) {
+      (void)ld; (void)rows; (void)row0; (void)vec;
+      const __amdgpu_buffer_rsrc_t rs = make_rsrc(base, ext);
+      __amdgpu_buffer_rsrc_t rs2;
+      if constexpr (PRO) rs2 = make_rsrc(base2, ext);
+      if constexpr (KC) {
+        // offsets stay below 2^31, so OR-ing the top bit moves a chunk out of range
+        const uint32_t kmask = (koff + k0 < kseg) ? 0u : kBufOOB;
+        const uint32_t v0 = off0 + (uint32_t)(k0 * ESZ);
+#pragma unroll
+        for (int i = 0; i < NCK; ++i) {
+          const uint32_t vo = (v0 + (uint32_t)(i * 32 * ldb)) | kmask;
+          st[i] = buf_load16(rs, vo);
+          if constexpr (PRO) st2[i] = buf_load16(rs2, vo);
+        }
+      } else {
+#pragma unroll
+        for (int i = 0; i < NBLK; ++i) {
+#pragma unroll
+          for (int kk = 0; kk < CH; ++kk) {
+            // boff[i] >= 2^31 for rows outside; adding < 2^31 keeps it outside
+            const uint32_t vo = boff[i] + (uint32_t)((k0 + kk) * ldb);
+            st[i * CH + kk] = buf_load16(rs, vo);
+            if constexpr (PRO) st2[i * CH + kk] = buf_load16(rs2, vo);
+          }
+        }
       }
     } else {
+      (void)ext;
+      if constexpr (KC) {
 #pragma unroll
-      for (int i = 0; i < NBLK; ++i) {
-        const int b = tid + NT * i;
-        const int rb = b % (R / CH), kb = b / (R / CH);
-        const int grow = row0 + rb * CH;
-        int n_ok = (b < NBLK_TOT) ? rows - grow : 0;
-        n_ok = n_ok < 0 ? 0 : (n_ok > CH ? CH : n_ok);
+        for (int i = 0; i < NCK; ++i) {
+          const int idx = tid + NT * i;
+          const int r = idx >> 3, c = idx & 7;
+          const int grow = row0 + r, gk = k0 + c * CH;
+          int n_ok = (grow < rows && idx < R * 8) ? kseg - gk : 0;
+          n_ok = n_ok < 0 ? 0 : (n_ok > CH ? CH : n_ok);
+          const int64_t off = (int64_t)grow * ld + gk;
+          st[i] = load_chunk<T>(base, off, n_ok, vec);
+          if constexpr (PRO) st2[i] = load_chunk<T>(base2, off, n_ok, vec);
+        }
+      } else {
 #pragma unroll
-        for (int kk = 0; kk < CH; ++kk) {
-          const int gk = k0 + kb * CH + kk;
-          const int nk = (gk < kseg) ? n_ok : 0;
-          const int64_t off = (int64_t)gk * ld + grow;
-          st[i * CH + kk] = load_chunk<T>(base, off, nk, vec);
-          if constexpr (PRO) st2[i * CH + kk] = load_chunk<T>(base2, off, nk, vec);
+        for (int i = 0; i < NBLK; ++i) {
+          const int b = tid + NT * i;
+          const int rb = b % (R / CH), kb = b / (R / CH);
+          const int grow = row0 + rb * CH;
+          int n_ok = (b < NBLK_TOT) ? rows - grow : 0;
+          n_ok = n_ok < 0 ? 0 : (n_ok > CH ? CH : n_ok);
+#pragma unroll
+          for (int kk = 0; kk < CH; ++kk) {
+            const int gk = k0 + kb * CH + kk;
+            const int nk = (gk < kseg) ? n_ok : 0;
+            const int64_t off = (int64_t)gk * ld + grow;
+            st[i * CH + kk] = load_chunk<T>(base, off, nk, vec);
+            if constexpr (PRO) st2[i * CH + kk] = load_chunk<T>(base2, off, nk, vec);
+          }
         }
       }
     }
@@ -386,9 +477,19 @@ __device__ __forceinline__ TileCoord map_tile(int bid, int nblocks, int tiles_m,
 //   WGM x WGN grid, each wave computing a (BM/WGM) x (BN/WGN) block from 32x32
 //   MFMA tiles.  MODE_DUAL keeps a second accumulator set for B2 (LDS B region
 //   holds 2*BN rows: B then B2).
+//
+// Main loop (two LDS buffers, one barrier per K tile, fragments double-buffered
+// in registers):
+//   issue global loads of tile k+1
+//   substeps 0..2:  read fragments of substep s+1 | MFMAs of substep s
+//   store tile k+1 to the other LDS buffer;  barrier
+//   read fragments of substep 0 of tile k+1 | MFMAs of substep 3 of tile k
+// so the LDS latency after the barrier hides under the last substep's MFMAs.
 
-template <typename T, int BM, int BN, int WGM, int WGN, bool AK, bool BK, int MODE>
-__global__ void __launch_bounds__(256) gemm_kernel(Params p) {
+template <typename T, int BM, int BN, int WGM, int WGN, bool AK, bool BK, int MODE, bool FAST>
+__global__ void __launch_bounds__(256)
+    __attribute__((amdgpu_waves_per_eu(BM * BN >= 256 * 128 ? 1 : 2)))
+    gemm_kernel(Params p) {
   constexpr int CH = ElemTraits<T>::CH;
   constexpr int KT = 8 * CH;
   constexpr int BROWS = (MODE == MODE_DUAL) ? 2 * BN : BN;
@@ -403,14 +504,15 @@ __global__ void __launch_bounds__(256) gemm_kernel(Params p) {
 
   const int nblocks = gridDim.x;
   const TileCoord tc = map_tile(blockIdx.x, nblocks, p.tiles_m, p.tiles_n, p.splits);
-  const int m0 = tc.tm * BM, n0 = tc.tn * BN;
-  const int zo = tc.z / p.heads, zi = tc.z - (tc.z / p.heads) * p.heads;
-  const T* Ab = (const T*)p.A + (int64_t)zo * p.aO + (int64_t)(zi / p.gA) * p.aI;
-  const T* A2b = PRO ? (const T*)p.A2 + (int64_t)zo * p.aO + (int64_t)(zi / p.gA) * p.aI : nullptr;
-  const T* Bb = (const T*)p.B + (int64_t)zo * p.bO + (int64_t)(zi / p.gB) * p.bI;
-  const T* B2b = (MODE == MODE_DUAL) ? (const T*)p.B2 + (int64_t)zo * p.bO + (int64_t)(zi / p.gB) * p.bI
+  const int m0 = uniform(tc.tm * BM), n0 = uniform(tc.tn * BN);
+  const int zo = uniform(tc.z / p.heads), zi = uniform(tc.z - (tc.z / p.heads) * p.heads);
+  const int ziA = uniform(zi / p.gA), ziB = uniform(zi / p.gB), ziC = uniform(zi / p.gC);
+  const T* Ab = uniform((const T*)p.A + (int64_t)zo * p.aO + (int64_t)ziA * p.aI);
+  const T* A2b = PRO ? uniform((const T*)p.A2 + (int64_t)zo * p.aO + (int64_t)ziA * p.aI) : nullptr;
+  const T* Bb = uniform((const T*)p.B + (int64_t)zo * p.bO + (int64_t)ziB * p.bI);
+  const T* B2b = (MODE == MODE_DUAL) ? uniform((const T*)p.B2 + (int64_t)zo * p.bO + (int64_t)ziB * p.bI)
                                       : nullptr;
-  const int64_t coff = (int64_t)zo * p.cO + (int64_t)(zi / p.gC) * p.cI;
+  const int64_t coff = (int64_t)zo * p.cO + (int64_t)ziC * p.cI;
   const int esz_c = p.c_bf16 ? 2 : 4;
   void* Cz = (char*)p.C + coff * esz_c;
   const void* Rz = p.R ? (const char*)p.R + ((int64_t)zo * p.rO + (int64_t)zi * p.rI) * (p.r_bf16 ? 2 : 4)
@@ -422,13 +524,15 @@ __global__ void __launch_bounds__(256) gemm_kernel(Params p) {
   // Fully masked causal tile: only the mask value is written.
   if (p.causal == CAUSAL_OUT_LOWER && n0 > m0 + BM - 1) {
     if (p.splits > 1) return;  // the reduction kernel writes the mask
-    for (int idx = threadIdx.x; idx < BM * (BN / 4); idx += 256) {
-      const int r = idx / (BN / 4), c4 = idx % (BN / 4);
-      float v[4] = {0.f, 0.f, 0.f, 0.f};
-      Params q = p;
-      q.bias = nullptr;
-      q.beta = 0.f;
-      epilogue4(q, Cz, nullptr, m0 + r, n0 + c4 * 4, v);
+    for (int idx = threadIdx.x; idx < BM * BN; idx += 256) {
+      const int m = m0 + idx / BN, n = n0 + idx % BN;
+      if (m < p.M && n < p.N) {
+        const int64_t ci = (int64_t)m * p.ldc + n;
+        if (p.c_bf16)
+          ((uint16_t*)Cz)[ci] = (uint16_t)f32_to_bf16_rne(p.mask_value);
+        else
+          ((float*)Cz)[ci] = p.mask_value;
+      }
     }
     return;
   }
@@ -444,8 +548,8 @@ __global__ void __launch_bounds__(256) gemm_kernel(Params p) {
   }
   const int per_seg = khi > klo ? khi - klo : 0;
   const int total = per_seg * p.nseg;
-  const int it0 = (int)((int64_t)total * tc.split / p.splits);
-  const int it1 = (int)((int64_t)total * (tc.split + 1) / p.splits);
+  const int it0 = uniform((int)((int64_t)total * tc.split / p.splits));
+  const int it1 = uniform((int)((int64_t)total * (tc.split + 1) / p.splits));
 
   f32x16_t acc[TM][NB];
 #pragma unroll
@@ -455,18 +559,21 @@ __global__ void __launch_bounds__(256) gemm_kernel(Params p) {
 #pragma unroll
       for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.0f;
 
-  TileLoader<T, BM, AK, PRO> la;
-  TileLoader<T, BN, BK, false> lb;
-  TileLoader<T, (MODE == MODE_DUAL) ? BN : 32, BK, false> lb2;
+  TileLoader<T, BM, AK, PRO, FAST> la;
+  TileLoader<T, BN, BK, false, FAST> lb;
+  TileLoader<T, (MODE == MODE_DUAL) ? BN : 32, BK, false, FAST> lb2;
+  la.init(p.lda, p.M, m0);
+  lb.init(p.ldb, p.N, n0);
+  if constexpr (MODE == MODE_DUAL) lb2.init(p.ldb, p.N, n0);
 
   auto issue_loads = [&](int it) {
     const int seg = it / per_seg;
     const int k0 = (klo + (it - seg * per_seg)) * KT;
     la.load(Ab + (int64_t)seg * p.segA, PRO ? (const void*)(A2b + (int64_t)seg * p.segA) : nullptr,
-            p.lda, p.M, m0, k0, p.K, p.vecA);
-    lb.load(Bb + (int64_t)seg * p.segB, nullptr, p.ldb, p.N, n0, k0, p.K, p.vecB);
+            p.extA, p.lda, p.M, m0, k0, p.K, p.vecA);
+    lb.load(Bb + (int64_t)seg * p.segB, nullptr, p.extB, p.ldb, p.N, n0, k0, p.K, p.vecB);
     if constexpr (MODE == MODE_DUAL)
-      lb2.load(B2b + (int64_t)seg * p.segB, nullptr, p.ldb, p.N, n0, k0, p.K, p.vecB);
+      lb2.load(B2b + (int64_t)seg * p.segB, nullptr, p.extB, p.ldb, p.N, n0, k0, p.K, p.vecB);
   };
   auto commit_stores = [&](int buf) {
     la.store(&smem[buf][0]);
@@ -474,55 +581,64 @@ __global__ void __launch_bounds__(256) gemm_kernel(Params p) {
     if constexpr (MODE == MODE_DUAL) lb2.store(&smem[buf][(BM + BN) * 8]);
   };
 
+  const int lrow = lane & 31, lhalf = lane >> 5;
+  // Fragment register sets: fa/fb[set][tile]; substep s uses set s & 1.
+  u32x4_t fa[2][TM], fb[2][NB];
+  auto read_frags = [&](int buf, int s, u32x4_t* af, u32x4_t* bfr) {
+    const u32x4_t* sA = &smem[buf][0];
+    const u32x4_t* sB = &smem[buf][BM * 8];
+    const int c = 2 * s + lhalf;
+#pragma unroll
+    for (int i = 0; i < TM; ++i) {
+      const int r = wm * WTM + i * 32 + lrow;
+      af[i] = sA[r * 8 + swz(r, c)];
+    }
+#pragma unroll
+    for (int j = 0; j < NB; ++j) {
+      const int half = (MODE == MODE_DUAL) ? (j / TN) : 0;
+      const int jj = (MODE == MODE_DUAL) ? (j % TN) : j;
+      const int r = half * BN + wn * WTN + jj * 32 + lrow;
+      bfr[j] = sB[r * 8 + swz(r, c)];
+    }
+  };
+  auto mfmas = [&](const u32x4_t* af, const u32x4_t* bfr) {
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+      for (int j = 0; j < NB; ++j) {
+        if constexpr (sizeof(T) == 2) {
+          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
+              __builtin_bit_cast(bf16x8_t, bfr[j]), __builtin_bit_cast(bf16x8_t, af[i]), acc[i][j],
+              0, 0, 0);
+        } else {
+#pragma unroll
+          for (int e = 0; e < 4; ++e)
+            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(
+                __uint_as_float(bfr[j][e]), __uint_as_float(af[i][e]), acc[i][j], 0, 0, 0);
+        }
+      }
+  };
+
   if (it0 < it1) {
     issue_loads(it0);
     commit_stores(0);
   }
   __syncthreads();
+  if (it0 < it1) read_frags(0, 0, fa[0], fb[0]);
 
-  const int lrow = lane & 31, lhalf = lane >> 5;
   for (int it = it0; it < it1; ++it) {
     const int cur = (it - it0) & 1;
     const bool more = it + 1 < it1;
     if (more) issue_loads(it + 1);
-
-    const u32x4_t* sA = &smem[cur][0];
-    const u32x4_t* sB = &smem[cur][BM * 8];
 #pragma unroll
-    for (int s = 0; s < 4; ++s) {
-      const int c = 2 * s + lhalf;
-      u32x4_t af[TM], bfr[NB];
-#pragma unroll
-      for (int i = 0; i < TM; ++i) {
-        const int r = wm * WTM + i * 32 + lrow;
-        af[i] = sA[r * 8 + swz(r, c)];
-      }
-#pragma unroll
-      for (int j = 0; j < NB; ++j) {
-        const int half = (MODE == MODE_DUAL) ? (j / TN) : 0;
-        const int jj = (MODE == MODE_DUAL) ? (j % TN) : j;
-        const int r = half * BN + wn * WTN + jj * 32 + lrow;
-        bfr[j] = sB[r * 8 + swz(r, c)];
-      }
-#pragma unroll
-      for (int i = 0; i < TM; ++i)
-#pragma unroll
-        for (int j = 0; j < NB; ++j) {
-          if constexpr (sizeof(T) == 2) {
-            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
-                __builtin_bit_cast(bf16x8_t, bfr[j]), __builtin_bit_cast(bf16x8_t, af[i]),
-                acc[i][j], 0, 0, 0);
-          } else {
-#pragma unroll
-            for (int e = 0; e < 4; ++e)
-              acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(
-                  __uint_as_float(bfr[j][e]), __uint_as_float(af[i][e]), acc[i][j], 0, 0, 0);
-          }
-        }
+    for (int s = 0; s < 3; ++s) {
+      read_frags(cur, s + 1, fa[(s + 1) & 1], fb[(s + 1) & 1]);
+      mfmas(fa[s & 1], fb[s & 1]);
     }
-
     if (more) commit_stores(cur ^ 1);
     __syncthreads();
+    if (more) read_frags(cur ^ 1, 0, fa[0], fb[0]);
+    mfmas(fa[1], fb[1]);
   }
 
   // Epilogue.  acc[i][j][4q + e] holds C[m][n + e] with

@@ -20,34 +20,33 @@ typedef float elem_t;
 #define MI_CAT5(a, b, c, d, e) a##b##c##d##e
 #define MI_PICK_NAME(dt, ta, tb) MI_CAT5(pick_, dt, _, ta, tb)
 
-KernelFn MI_PICK_NAME(MI_DTN, MI_TA, MI_TB)(int cfg) {
+KernelFn MI_PICK_NAME(MI_DTN, MI_TA, MI_TB)(int cfg, bool fast) {
   constexpr bool AK = (MI_TA == 0);  // A is K-contiguous when not transposed
   constexpr bool BK = (MI_TB == 1);  // B is K-contiguous when transposed
 #if MI_DT_BF16
-  switch (cfg) {
-    case CFG_L: return gemm_kernel<elem_t, 256, 256, 2, 2, AK, BK, MODE_PLAIN>;
-    case CFG_S: return gemm_kernel<elem_t, 128, 128, 2, 2, AK, BK, MODE_PLAIN>;
-    case CFG_DUAL: return gemm_kernel<elem_t, 256, 128, 2, 2, AK, BK, MODE_DUAL>;
-    case CFG_PRO:
-#if MI_TA == 0
-      return gemm_kernel<elem_t, 256, 256, 2, 2, AK, BK, MODE_PROLOGUE>;
+  constexpr int LM = 256, LN = 256, SM = 128, SN = 128, DM = 256, DN = 128, PM = 256, PN = 256;
 #else
-      return nullptr;
+  constexpr int LM = 128, LN = 128, SM = 128, SN = 128, DM = 128, DN = 64, PM = 128, PN = 128;
 #endif
+  if (fast) {
+    switch (cfg) {
+      case CFG_L: return gemm_kernel<elem_t, LM, LN, 2, 2, AK, BK, MODE_PLAIN, true>;
+      case CFG_S: return gemm_kernel<elem_t, SM, SN, 2, 2, AK, BK, MODE_PLAIN, true>;
+      case CFG_DUAL: return gemm_kernel<elem_t, DM, DN, 2, 2, AK, BK, MODE_DUAL, true>;
+      case CFG_PRO:
+        if constexpr (AK) return gemm_kernel<elem_t, PM, PN, 2, 2, AK, BK, MODE_PROLOGUE, true>;
+        return nullptr;
+    }
+  } else {
+    switch (cfg) {
+      case CFG_S: return gemm_kernel<elem_t, SM, SN, 2, 2, AK, BK, MODE_PLAIN, false>;
+      case CFG_DUAL: return gemm_kernel<elem_t, DM, DN, 2, 2, AK, BK, MODE_DUAL, false>;
+      case CFG_PRO:
+        if constexpr (AK) return gemm_kernel<elem_t, PM, PN, 2, 2, AK, BK, MODE_PROLOGUE, false>;
+        return nullptr;
+      default: return nullptr;
+    }
   }
-#else
-  switch (cfg) {
-    case CFG_L:
-    case CFG_S: return gemm_kernel<elem_t, 128, 128, 2, 2, AK, BK, MODE_PLAIN>;
-    case CFG_DUAL: return gemm_kernel<elem_t, 128, 64, 2, 2, AK, BK, MODE_DUAL>;
-    case CFG_PRO:
-#if MI_TA == 0
-      return gemm_kernel<elem_t, 128, 128, 2, 2, AK, BK, MODE_PROLOGUE>;
-#else
-      return nullptr;
-#endif
-  }
-#endif
   return nullptr;
 }
 

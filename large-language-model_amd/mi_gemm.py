@@ -76,6 +76,12 @@ def load_library():
         return _lib
     if not os.path.exists(LIB_PATH):
         raise ImportError(f"{LIB_PATH} is not built; run __graft_entry__.build()")
+    # torch ships its own libamdhip64.so.7.  Loading torch first makes the
+    # library's libamdhip64.so.7 dependency resolve to that already-loaded copy;
+    # loading the library first would bring a second HIP/HSA runtime into the
+    # process, and the two cannot share the device.
+    import torch  # noqa: F401
+
     L = ctypes.CDLL(LIB_PATH)
     vp, i64, i32, f32 = ctypes.c_void_p, ctypes.c_int64, ctypes.c_int32, ctypes.c_float
     L.mi_init.restype = ctypes.c_int
