@@ -25,6 +25,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <type_traits>
+
 namespace mig {
 
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
@@ -80,7 +82,20 @@ __device__ __forceinline__ float silu_f(float x) { return x / (1.0f + __expf(-x)
 // read at one chunk column, (r & 1, position) is distinct, and for any 8
 // consecutive rows the position is distinct: conflict-free for both a 32-bank
 // and a 64-bank 4-byte LDS.
-__device__ __forceinline__ int swz(int r, int c) { return c ^ ((r ^ (r >> 3)) & 7); }
+#ifndef MI_SWZ
+#define MI_SWZ 0
+#endif
+__device__ __forceinline__ int swz(int r, int c) {
+#if MI_SWZ == 0
+  return c ^ ((r ^ (r >> 3)) & 7);
+#elif MI_SWZ == 1
+  return c ^ (r & 7);
+#elif MI_SWZ == 2
+  return c ^ ((r >> 1) & 7);
+#else
+  return c;
+#endif
+}
 
 template <typename T>
 struct ElemTraits;
@@ -119,27 +134,6 @@ __device__ __forceinline__ u32x4_t load_chunk(const void* p, int64_t i, int n_ok
 #pragma unroll
   for (int j = 0; j < CH; ++j) e[j] = (j < n_ok) ? ElemTraits<T>::bits(p, i + j) : 0u;
   return pack_chunk<T>(e);
-}
-
-// Transpose a CH x CH block held as CH chunks (chunk kk = CH consecutive rows at
-// k = kk) into CH chunks (chunk j = CH consecutive k of row j).
-template <typename T>
-__device__ __forceinline__ void transpose_block(const u32x4_t* in, u32x4_t* out) {
-  if constexpr (sizeof(T) == 4) {
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      out[j][0] = in[0][j]; out[j][1] = in[1][j]; out[j][2] = in[2][j]; out[j][3] = in[3][j];
-    }
-  } else {
-#pragma unroll
-    for (int j = 0; j < 8; ++j) {
-#pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        const uint32_t a = in[2 * q][j >> 1], b = in[2 * q + 1][j >> 1];
-        out[j][q] = (j & 1) ? ((a >> 16) | (b & 0xffff0000u)) : ((a & 0xffffu) | (b << 16));
-      }
-    }
-  }
 }
 
 // SiLU(g)*u on a chunk pair, re-encoded in T.
@@ -212,17 +206,32 @@ struct TileLoader {
   // Row-contiguous: 8*(R/CH) blocks of CH x CH, each CH chunks.
   static constexpr int NBLK_TOT = 8 * (R / CH);
   static constexpr int NBLK = (NBLK_TOT + NT - 1) / NT;
-  static constexpr int NREG = KC ? NCK : NBLK * CH;
-  u32x4_t st[NREG];
-  u32x4_t st2[PRO ? NREG : 1];
+  // Work is issued in units so the main loop can spread it between MFMAs:
+  // a load unit is one 16-byte chunk load; a store unit is one 16-byte LDS write
+  // (for a row-contiguous operand: one row of a transposed block).
+  static constexpr int NUNIT = KC ? NCK : NBLK * CH;
+  u32x4_t st[NUNIT];
+  u32x4_t st2[PRO ? NUNIT : 1];
   // fast path: per-thread byte offsets fixed for the tile
-  uint32_t off0;             // KC: chunk 0 of this thread at k = 0
-  uint32_t boff[KC ? 1 : NBLK];  // !KC: block i at k = 0 (kBufOOB when its rows are outside)
-  int ldb;                   // leading dimension in bytes
-  int koff;                  // KC: this thread's chunk column * CH
+  uint32_t off0;                  // KC: chunk 0 of this thread at k = 0
+  uint32_t boff[KC ? 1 : NBLK];   // !KC: block i at k = 0 (>= 2^31 when its rows are outside)
+  int ldb;                        // leading dimension in bytes
+  int koff;                       // KC: this thread's chunk column * CH
+  int rows_, row0_;
+  int64_t ld_;
+  // per K tile
+  __amdgpu_buffer_rsrc_t rs, rs2;
+  const void* base_;
+  const void* base2_;
+  uint32_t kv0, kmask;
+  int k0_, kseg_;
+  bool vec_;
 
   __device__ __forceinline__ void init(int64_t ld, int rows, int row0) {
     const int tid = threadIdx.x;
+    rows_ = rows;
+    row0_ = row0;
+    ld_ = ld;
     if constexpr (FAST) {
       ldb = (int)ld * ESZ;
       if constexpr (KC) {
@@ -240,106 +249,102 @@ struct TileLoader {
     }
   }
 
-  // base/base2: operand pointers of the current batch and K segment; ext: their
-  // byte extent.  k0: first K of the tile; kseg: K extent of the segment.
-  __device__ __forceinline__ void load(const void* base, const void* base2, uint32_t ext, int64_t ld,
-                                       int rows, int row0, int k0, int kseg, bool vec) {
-    const int tid = threadIdx.x;
+  // Select the K tile: base/base2 are the operand pointers of the current batch
+  // and K segment, ext their byte extent, k0 the tile's first K, kseg the K extent.
+  // live = false turns every load of the tile into an out-of-range no-op.
+  __device__ __forceinline__ void set_tile(const void* base, const void* base2, uint32_t ext, int k0,
+                                           int kseg, bool vec, bool live) {
+    k0_ = k0;
+    kseg_ = live ? kseg : 0;
     if constexpr (FAST) {
-      (void)ld; (void)rows; (void)row0; (void)vec;
-      const __amdgpu_buffer_rsrc_t rs = make_rsrc(base, ext);
-      __amdgpu_buffer_rsrc_t rs2;
+      (void)vec;
+      rs = make_rsrc(base, ext);
       if constexpr (PRO) rs2 = make_rsrc(base2, ext);
+      // offsets stay below 2^31, so OR-ing the top bit moves a chunk out of range
       if constexpr (KC) {
-        // offsets stay below 2^31, so OR-ing the top bit moves a chunk out of range
-        const uint32_t kmask = (koff + k0 < kseg) ? 0u : kBufOOB;
-        const uint32_t v0 = off0 + (uint32_t)(k0 * ESZ);
-#pragma unroll
-        for (int i = 0; i < NCK; ++i) {
-          const uint32_t vo = (v0 + (uint32_t)(i * 32 * ldb)) | kmask;
-          st[i] = buf_load16(rs, vo);
-          if constexpr (PRO) st2[i] = buf_load16(rs2, vo);
-        }
+        kmask = (live && koff + k0 < kseg) ? 0u : kBufOOB;
+        kv0 = off0 + (uint32_t)(k0 * ESZ);
       } else {
-#pragma unroll
-        for (int i = 0; i < NBLK; ++i) {
-#pragma unroll
-          for (int kk = 0; kk < CH; ++kk) {
-            // boff[i] >= 2^31 for rows outside; adding < 2^31 keeps it outside
-            const uint32_t vo = boff[i] + (uint32_t)((k0 + kk) * ldb);
-            st[i * CH + kk] = buf_load16(rs, vo);
-            if constexpr (PRO) st2[i * CH + kk] = buf_load16(rs2, vo);
-          }
-        }
+        kmask = live ? 0u : kBufOOB;
       }
     } else {
       (void)ext;
+      base_ = base;
+      base2_ = base2;
+      vec_ = vec;
+    }
+  }
+
+  __device__ __forceinline__ void load_unit(int u) {
+    const int tid = threadIdx.x;
+    if constexpr (FAST) {
       if constexpr (KC) {
-#pragma unroll
-        for (int i = 0; i < NCK; ++i) {
-          const int idx = tid + NT * i;
-          const int r = idx >> 3, c = idx & 7;
-          const int grow = row0 + r, gk = k0 + c * CH;
-          int n_ok = (grow < rows && idx < R * 8) ? kseg - gk : 0;
-          n_ok = n_ok < 0 ? 0 : (n_ok > CH ? CH : n_ok);
-          const int64_t off = (int64_t)grow * ld + gk;
-          st[i] = load_chunk<T>(base, off, n_ok, vec);
-          if constexpr (PRO) st2[i] = load_chunk<T>(base2, off, n_ok, vec);
-        }
+        const uint32_t vo = (kv0 + (uint32_t)(u * 32 * ldb)) | kmask;
+        st[u] = buf_load16(rs, vo);
+        if constexpr (PRO) st2[u] = buf_load16(rs2, vo);
       } else {
-#pragma unroll
-        for (int i = 0; i < NBLK; ++i) {
-          const int b = tid + NT * i;
-          const int rb = b % (R / CH), kb = b / (R / CH);
-          const int grow = row0 + rb * CH;
-          int n_ok = (b < NBLK_TOT) ? rows - grow : 0;
-          n_ok = n_ok < 0 ? 0 : (n_ok > CH ? CH : n_ok);
-#pragma unroll
-          for (int kk = 0; kk < CH; ++kk) {
-            const int gk = k0 + kb * CH + kk;
-            const int nk = (gk < kseg) ? n_ok : 0;
-            const int64_t off = (int64_t)gk * ld + grow;
-            st[i * CH + kk] = load_chunk<T>(base, off, nk, vec);
-            if constexpr (PRO) st2[i * CH + kk] = load_chunk<T>(base2, off, nk, vec);
-          }
-        }
+        const int i = u / CH, kk = u % CH;
+        // boff[i] >= 2^31 for rows outside; adding < 2^31 keeps it outside
+        const uint32_t vo = (boff[i] + (uint32_t)((k0_ + kk) * ldb)) | kmask;
+        st[u] = buf_load16(rs, vo);
+        if constexpr (PRO) st2[u] = buf_load16(rs2, vo);
+      }
+    } else {
+      if constexpr (KC) {
+        const int idx = tid + NT * u;
+        const int r = idx >> 3, c = idx & 7;
+        const int grow = row0_ + r, gk = k0_ + c * CH;
+        int n_ok = (grow < rows_ && idx < R * 8) ? kseg_ - gk : 0;
+        n_ok = n_ok < 0 ? 0 : (n_ok > CH ? CH : n_ok);
+        const int64_t off = (int64_t)grow * ld_ + gk;
+        st[u] = load_chunk<T>(base_, off, n_ok, vec_);
+        if constexpr (PRO) st2[u] = load_chunk<T>(base2_, off, n_ok, vec_);
+      } else {
+        const int i = u / CH, kk = u % CH;
+        const int b = tid + NT * i;
+        const int rb = b % (R / CH), kb = b / (R / CH);
+        const int grow = row0_ + rb * CH;
+        int n_ok = (b < NBLK_TOT) ? rows_ - grow : 0;
+        n_ok = n_ok < 0 ? 0 : (n_ok > CH ? CH : n_ok);
+        const int gk = k0_ + kb * CH + kk;
+        const int nk = (gk < kseg_) ? n_ok : 0;
+        const int64_t off = (int64_t)gk * ld_ + grow;
+        st[u] = load_chunk<T>(base_, off, nk, vec_);
+        if constexpr (PRO) st2[u] = load_chunk<T>(base2_, off, nk, vec_);
       }
     }
   }
 
   // lds: this operand's region, R rows of 8 chunks.
-  __device__ __forceinline__ void store(u32x4_t* lds) {
+  __device__ __forceinline__ void store_unit(int u, u32x4_t* lds) {
     const int tid = threadIdx.x;
     if constexpr (KC) {
-#pragma unroll
-      for (int i = 0; i < NCK; ++i) {
-        const int idx = tid + NT * i;
-        if (NCK * NT == R * 8 || idx < R * 8) {
-          const int r = idx >> 3, c = idx & 7;
-          u32x4_t v = st[i];
-          if constexpr (PRO) v = swiglu_chunk<T>(st[i], st2[i]);
-          lds[r * 8 + swz(r, c)] = v;
-        }
+      const int idx = tid + NT * u;
+      if (NCK * NT == R * 8 || idx < R * 8) {
+        const int r = idx >> 3, c = idx & 7;
+        u32x4_t v = st[u];
+        if constexpr (PRO) v = swiglu_chunk<T>(st[u], st2[u]);
+        lds[r * 8 + swz(r, c)] = v;
       }
     } else {
+      const int i = u / CH, j = u % CH;
+      const int b = tid + NT * i;
+      if (NBLK * NT == NBLK_TOT || b < NBLK_TOT) {
+        const int rb = b % (R / CH), kb = b / (R / CH);
+        // row j of the transposed block: element j of each of the CH k-chunks
+        u32x4_t o;
+        if constexpr (sizeof(T) == 4) {
 #pragma unroll
-      for (int i = 0; i < NBLK; ++i) {
-        const int b = tid + NT * i;
-        if (NBLK * NT == NBLK_TOT || b < NBLK_TOT) {
-          const int rb = b % (R / CH), kb = b / (R / CH);
-          u32x4_t in[CH], out[CH];
+          for (int kk = 0; kk < 4; ++kk) o[kk] = st[i * CH + kk][j];
+        } else {
 #pragma unroll
-          for (int kk = 0; kk < CH; ++kk) {
-            in[kk] = st[i * CH + kk];
-            if constexpr (PRO) in[kk] = swiglu_chunk<T>(st[i * CH + kk], st2[i * CH + kk]);
-          }
-          transpose_block<T>(in, out);
-#pragma unroll
-          for (int j = 0; j < CH; ++j) {
-            const int r = rb * CH + j;
-            lds[r * 8 + swz(r, kb)] = out[j];
+          for (int q = 0; q < 4; ++q) {
+            const uint32_t a = st[i * CH + 2 * q][j >> 1], bb = st[i * CH + 2 * q + 1][j >> 1];
+            o[q] = (j & 1) ? ((a >> 16) | (bb & 0xffff0000u)) : ((a & 0xffffu) | (bb << 16));
           }
         }
+        const int r = rb * CH + j;
+        lds[r * 8 + swz(r, kb)] = o;
       }
     }
   }
@@ -448,12 +453,26 @@ struct TileCoord {
 // Hardware hands workgroup b to XCD (b mod 8).  Renumber so each XCD receives a
 // contiguous range of logical tiles, then order tiles in groups of GROUP_M tile
 // rows so that the workgroups resident on one XCD share A and B panels in its L2.
+#ifndef MI_GROUP_M
+#define MI_GROUP_M 8
+#endif
+#ifndef MI_XCD_REMAP
+#define MI_XCD_REMAP 1
+#endif
+#ifndef MI_SCHED
+#define MI_SCHED 0
+#endif
+
 __device__ __forceinline__ TileCoord map_tile(int bid, int nblocks, int tiles_m, int tiles_n,
                                               int splits) {
-  constexpr int NXCD = 8, GROUP_M = 8;
+  constexpr int NXCD = 8, GROUP_M = MI_GROUP_M;
+#if MI_XCD_REMAP
   const int q = nblocks / NXCD, rem = nblocks % NXCD;
   const int x = bid % NXCD, j = bid / NXCD;
   const int lid = x * q + (x < rem ? x : rem) + j;
+#else
+  const int lid = bid;
+#endif
   const int tiles = tiles_m * tiles_n;
   TileCoord tc;
   const int zs = lid / tiles;
@@ -566,80 +585,124 @@ __global__ void __launch_bounds__(256)
   lb.init(p.ldb, p.N, n0);
   if constexpr (MODE == MODE_DUAL) lb2.init(p.ldb, p.N, n0);
 
-  auto issue_loads = [&](int it) {
-    const int seg = it / per_seg;
-    const int k0 = (klo + (it - seg * per_seg)) * KT;
-    la.load(Ab + (int64_t)seg * p.segA, PRO ? (const void*)(A2b + (int64_t)seg * p.segA) : nullptr,
-            p.extA, p.lda, p.M, m0, k0, p.K, p.vecA);
-    lb.load(Bb + (int64_t)seg * p.segB, nullptr, p.extB, p.ldb, p.N, n0, k0, p.K, p.vecB);
+  // Point the loaders at K tile `it` (clamped into range; a tile past it1 is
+  // loaded as out-of-range no-ops so the main loop needs no branches).
+  auto set_tiles = [&](int it) {
+    const bool live = it < it1;
+    const int itc = live ? it : it1 - 1;
+    const int seg = itc / per_seg;
+    const int k0 = (klo + (itc - seg * per_seg)) * KT;
+    la.set_tile(Ab + (int64_t)seg * p.segA, PRO ? (const void*)(A2b + (int64_t)seg * p.segA) : nullptr,
+                p.extA, k0, p.K, p.vecA, live);
+    lb.set_tile(Bb + (int64_t)seg * p.segB, nullptr, p.extB, k0, p.K, p.vecB, live);
     if constexpr (MODE == MODE_DUAL)
-      lb2.load(B2b + (int64_t)seg * p.segB, nullptr, p.extB, p.ldb, p.N, n0, k0, p.K, p.vecB);
+      lb2.set_tile(B2b + (int64_t)seg * p.segB, nullptr, p.extB, k0, p.K, p.vecB, live);
   };
-  auto commit_stores = [&](int buf) {
-    la.store(&smem[buf][0]);
-    lb.store(&smem[buf][BM * 8]);
-    if constexpr (MODE == MODE_DUAL) lb2.store(&smem[buf][(BM + BN) * 8]);
+  constexpr int NLA = TileLoader<T, BM, AK, PRO, FAST>::NUNIT;
+  constexpr int NLB = TileLoader<T, BN, BK, false, FAST>::NUNIT;
+  constexpr int NLB2 = (MODE == MODE_DUAL) ? NLB : 0;
+  constexpr int NUNITS = NLA + NLB + NLB2;
+  auto load_op = [&](int o) {
+    if (o < NLA) la.load_unit(o);
+    else if (o < NLA + NLB) lb.load_unit(o - NLA);
+    else lb2.load_unit(o - NLA - NLB);
+  };
+  auto store_op = [&](int o, int buf) {
+    if (o < NLA) la.store_unit(o, &smem[buf][0]);
+    else if (o < NLA + NLB) lb.store_unit(o - NLA, &smem[buf][BM * 8]);
+    else lb2.store_unit(o - NLA - NLB, &smem[buf][(BM + BN) * 8]);
   };
 
   const int lrow = lane & 31, lhalf = lane >> 5;
   // Fragment register sets: fa/fb[set][tile]; substep s uses set s & 1.
   u32x4_t fa[2][TM], fb[2][NB];
-  auto read_frags = [&](int buf, int s, u32x4_t* af, u32x4_t* bfr) {
-    const u32x4_t* sA = &smem[buf][0];
-    const u32x4_t* sB = &smem[buf][BM * 8];
+  constexpr int NREAD = TM + NB;
+  auto read_op = [&](int o, int buf, int s, int set) {
     const int c = 2 * s + lhalf;
-#pragma unroll
-    for (int i = 0; i < TM; ++i) {
-      const int r = wm * WTM + i * 32 + lrow;
-      af[i] = sA[r * 8 + swz(r, c)];
-    }
-#pragma unroll
-    for (int j = 0; j < NB; ++j) {
+    if (o < TM) {
+      const int r = wm * WTM + o * 32 + lrow;
+      fa[set][o] = smem[buf][r * 8 + swz(r, c)];
+    } else {
+      const int j = o - TM;
       const int half = (MODE == MODE_DUAL) ? (j / TN) : 0;
       const int jj = (MODE == MODE_DUAL) ? (j % TN) : j;
-      const int r = half * BN + wn * WTN + jj * 32 + lrow;
-      bfr[j] = sB[r * 8 + swz(r, c)];
+      const int r = BM + half * BN + wn * WTN + jj * 32 + lrow;
+      fb[set][j] = smem[buf][r * 8 + swz(r, c)];
     }
   };
-  auto mfmas = [&](const u32x4_t* af, const u32x4_t* bfr) {
+  auto mfma_op = [&](int set, int i, int j) {
+    if constexpr (sizeof(T) == 2) {
+      acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
+          __builtin_bit_cast(bf16x8_t, fb[set][j]), __builtin_bit_cast(bf16x8_t, fa[set][i]),
+          acc[i][j], 0, 0, 0);
+    } else {
 #pragma unroll
-    for (int i = 0; i < TM; ++i)
-#pragma unroll
-      for (int j = 0; j < NB; ++j) {
-        if constexpr (sizeof(T) == 2) {
-          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
-              __builtin_bit_cast(bf16x8_t, bfr[j]), __builtin_bit_cast(bf16x8_t, af[i]), acc[i][j],
-              0, 0, 0);
-        } else {
-#pragma unroll
-          for (int e = 0; e < 4; ++e)
-            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(
-                __uint_as_float(bfr[j][e]), __uint_as_float(af[i][e]), acc[i][j], 0, 0, 0);
-        }
-      }
+      for (int e = 0; e < 4; ++e)
+        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(
+            __uint_as_float(fb[set][j][e]), __uint_as_float(fa[set][i][e]), acc[i][j], 0, 0, 0);
+    }
   };
 
+  // One substep: TM*NB MFMA slots.  Each slot holds one MFMA (one 32x32 output
+  // tile, 16 K) and an even share of the side work of this substep: the
+  // fragment reads of the next substep, and in substep 2 the LDS stores of the
+  // next K tile, in substep 3 the global loads of the K tile after it.  The
+  // scheduling fence after every slot keeps this order, so the wave never
+  // waits on an LDS read or a global load it issued in the same slot.
+  constexpr int NS = TM * NB;
+  auto substep = [&](auto S_c, int rbuf, int sbuf) {
+    constexpr int S = decltype(S_c)::value;
+    constexpr int set = S & 1, rset = (S + 1) & 1, rs_sub = (S + 1) & 3;
+#pragma unroll
+    for (int q = 0; q < NS; ++q) {
+      mfma_op(set, q / NB, q % NB);
+#pragma unroll
+      for (int o = (q * NREAD + NS - 1) / NS; o < ((q + 1) * NREAD + NS - 1) / NS; ++o)
+        read_op(o, rbuf, rs_sub, rset);
+      if constexpr (S == 2) {
+#pragma unroll
+        for (int o = (q * NUNITS + NS - 1) / NS; o < ((q + 1) * NUNITS + NS - 1) / NS; ++o)
+          store_op(o, sbuf);
+      }
+      if constexpr (S == 3) {
+#pragma unroll
+        for (int o = (q * NUNITS + NS - 1) / NS; o < ((q + 1) * NUNITS + NS - 1) / NS; ++o)
+          load_op(o);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  };
+
+  // Prologue: tile it0 into LDS buffer 0, tile it0+1 into the staging registers,
+  // fragments of substep 0.
   if (it0 < it1) {
-    issue_loads(it0);
-    commit_stores(0);
+    set_tiles(it0);
+#pragma unroll
+    for (int o = 0; o < NUNITS; ++o) load_op(o);
+#pragma unroll
+    for (int o = 0; o < NUNITS; ++o) store_op(o, 0);
+    set_tiles(it0 + 1);
+#pragma unroll
+    for (int o = 0; o < NUNITS; ++o) load_op(o);
   }
   __syncthreads();
-  if (it0 < it1) read_frags(0, 0, fa[0], fb[0]);
-
-  for (int it = it0; it < it1; ++it) {
-    const int cur = (it - it0) & 1;
-    const bool more = it + 1 < it1;
-    if (more) issue_loads(it + 1);
+  if (it0 < it1) {
 #pragma unroll
-    for (int s = 0; s < 3; ++s) {
-      read_frags(cur, s + 1, fa[(s + 1) & 1], fb[(s + 1) & 1]);
-      mfmas(fa[s & 1], fb[s & 1]);
-    }
-    if (more) commit_stores(cur ^ 1);
-    __syncthreads();
-    if (more) read_frags(cur ^ 1, 0, fa[0], fb[0]);
-    mfmas(fa[1], fb[1]);
+    for (int o = 0; o < NREAD; ++o) read_op(o, 0, 0, 0);
   }
+
+  // Main loop over K tiles; LDS buffer `cur` holds tile it, the staging
+  // registers tile it+1.
+  for (int it = it0; it < it1; ++it) {
+    const int cur = (it - it0) & 1, nxt = cur ^ 1;
+    substep(std::integral_constant<int, 0>{}, cur, nxt);
+    substep(std::integral_constant<int, 1>{}, cur, nxt);
+    substep(std::integral_constant<int, 2>{}, cur, nxt);   // + stores of tile it+1 -> nxt
+    __syncthreads();
+    set_tiles(it + 2);
+    substep(std::integral_constant<int, 3>{}, nxt, nxt);   // + loads of tile it+2
+  }
+  __syncthreads();  // the epilogue reuses LDS
 
   // Epilogue.  acc[i][j][4q + e] holds C[m][n + e] with
   //   m = m0 + wm*WTM + i*32 + (lane & 31),  n = n0 + wn*WTN + j*32 + 8q + 4*(lane >> 5).
