@@ -1,0 +1,417 @@
+// mi_gemm_dlds.hpp -- bf16 GEMM main loop with direct-to-LDS loads (gfx950).
+//
+// Operand tiles move global -> LDS with buffer_load_dwordx4 ... lds: each lane's
+// 16 bytes land at M0 + 16*lane, so the LDS layout (and its bank swizzle) is set
+// by which global chunk each lane fetches.  No staging registers, no LDS store
+// instructions and no register transposes are involved, which frees the VGPRs
+// for a STAGES-deep ring of LDS tiles (loads run STAGES-1 K tiles ahead).
+//
+// LDS layouts per stage:
+//   K-contiguous operand  [R rows][BK]  (NCH = BK/8 chunks of 16 bytes per row,
+//       chunk position XOR-swizzled by the row); MFMA fragments are ds_read_b128.
+//   row-contiguous operand [BK k-rows][R]  (R/8 chunks per k-row, chunk index
+//       XOR-swizzled by the k-row); MFMA fragments are two ds_read_b64_tr_b16,
+//       whose 16-lane groups turn a 4 (k) x 16 (row) block into 16 lanes x 4 k.
+// Both read patterns are bank-conflict free on the 64-bank LDS.
+#pragma once
+#include "mi_gemm_device.hpp"
+
+namespace mig {
+
+typedef short v4i16_t __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) v4i16_t lds_v4i16_t;
+
+#define MIG_LDS_PTR(p) ((__attribute__((address_space(3))) void*)(p))
+
+// s_waitcnt vmcnt(N) with expcnt and lgkmcnt left unconstrained (gfx9 encoding:
+// vmcnt[3:0] bits 3:0, vmcnt[5:4] bits 15:14, expcnt bits 6:4, lgkmcnt bits 11:8).
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((N & 0xF) | ((N >> 4) << 14) | (0x7 << 4) | (0xF << 8));
+}
+
+// Workgroup barrier for the LDS ring: this wave's LDS reads and writes are
+// complete (lgkmcnt(0)) but its DMA loads may still be in flight -- the caller
+// waits for the ones it needs with wait_vmcnt first.  (__syncthreads() would
+// also wait for every outstanding DMA load, emptying the ring.)  The empty asm
+// statements keep the compiler from moving memory accesses across the barrier.
+__device__ __forceinline__ void lds_ring_barrier() {
+  __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0); vmcnt(63), expcnt(7) = no constraint
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+}
+
+// Chunk position of K-chunk c in row r of a K-contiguous tile with NCH chunks
+// per row.  16 consecutive rows read at one c hit 16 distinct 16-byte bank
+// groups of the 64-bank LDS (rows of 64 or 128 bytes).
+template <int NCH>
+__device__ __forceinline__ int kc_swz(int r, int c) {
+  if constexpr (NCH == 4) return c ^ ((r >> 2) & 3);
+  else return c ^ ((r ^ (r >> 3)) & 7);
+}
+
+// Physical chunk of logical chunk q in k-row kr of a row-contiguous tile: the
+// four k-rows one transpose read touches land in four different 64-byte bank
+// groups.
+__device__ __forceinline__ int mc_swz(int kr, int q) { return q ^ ((kr & 3) << 2); }
+
+// One operand of the direct-to-LDS pipeline.  R: tile rows (M or N extent),
+// BK: K extent of a stage, KC: K-contiguous in memory.
+template <int R, int BK, bool KC>
+struct DldsOperand {
+  static constexpr int NCH = BK / 8;                         // KC: 16-byte chunks per row
+  static constexpr int BYTES = R * BK * 2;                   // one stage of this operand
+  static constexpr int NBLK = BYTES / 1024;                  // 1 KB DMA blocks per stage
+  static constexpr int NU = NBLK / 4;                        // DMA instructions per wave
+  static_assert(NBLK % 4 == 0, "tile must split into whole DMA blocks per wave");
+  uint32_t voff[NU];   // per unit: byte offset at k = 0 (>= 2^31 when outside the rows)
+  int kch[NU];         // KC: element K offset of the unit's chunk (for the K-tail mask)
+  int ldb;
+
+  __device__ __forceinline__ void init(int64_t ld, int rows, int row0) {
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    ldb = (int)ld * 2;
+#pragma unroll
+    for (int u = 0; u < NU; ++u) {
+      const int b = wave * NU + u;
+      if constexpr (KC) {
+        const int row = b * (64 / NCH) + lane / NCH;
+        const int c = kc_swz<NCH>(row, lane % NCH);
+        kch[u] = c * 8;
+        voff[u] = (uint32_t)((row0 + row) * ldb + c * 16);
+      } else {
+        constexpr int CPR = R / 8;  // chunks per k-row
+        const int kr = b * (64 / CPR) + lane / CPR;
+        const int q = mc_swz(kr, lane % CPR);
+        const int grow = row0 + q * 8;
+        voff[u] = grow < rows ? (uint32_t)(kr * ldb + grow * 2) : kBufOOB;
+        kch[u] = 0;
+      }
+    }
+  }
+
+  // Issue DMA unit u of K tile k0 into stage memory `dst` (this operand's region).
+  // live = false: an out-of-range no-op (still counted by vmcnt).
+  __device__ __forceinline__ void load(int u, __amdgpu_buffer_rsrc_t rs, int k0, int kseg, bool live,
+                                       u32x4_t* dst) {
+    const int wave = threadIdx.x >> 6;
+    uint32_t vo;
+    if constexpr (KC) {
+      const uint32_t mask = (live && kch[u] + k0 < kseg) ? 0u : kBufOOB;
+      vo = (voff[u] + (uint32_t)(k0 * 2)) | mask;
+    } else {
+      const uint32_t mask = live ? 0u : kBufOOB;
+      vo = (voff[u] + (uint32_t)(k0 * ldb)) | mask;
+    }
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, MIG_LDS_PTR(dst + (wave * NU + u) * 64), 16, (int)vo,
+                                             0, 0, 0);
+  }
+
+  // MFMA fragment: rows r0..r0+31 (lane & 31), K substep s (16 K), as 8 bf16.
+  __device__ __forceinline__ u32x4_t frag(const u32x4_t* src, int r0, int s) const {
+    const int lane = threadIdx.x & 63;
+    if constexpr (KC) {
+      const int r = r0 + (lane & 31);
+      const int c = 2 * s + (lane >> 5);
+      return src[r * NCH + kc_swz<NCH>(r, c)];
+    } else {
+      const int g = lane >> 4, j = lane & 15;
+      const int col = r0 + (g & 1) * 16 + 4 * (j & 3);
+      const int q = col >> 3, sub = (col & 7) * 2;
+      const char* base = (const char*)src;
+      u32x4_t out;
+#pragma unroll
+      for (int t = 0; t < 2; ++t) {
+        const int kr = 16 * s + 8 * (g >> 1) + 4 * t + (j >> 2);
+        const char* a = base + kr * (R * 2) + 16 * mc_swz(kr, q) + sub;
+        u32x2_t w = {0u, 0u};
+#if defined(__HIP_DEVICE_COMPILE__)
+        // Issued as inline asm: the compiler makes the transpose-read builtin wait
+        // for every LDS-DMA load in flight (vmcnt(0)), which would drain the ring.
+        // The result is pending until the substep-start lgkmcnt(0) wait that
+        // precedes its first use (see substep()).
+        const uint32_t la = (uint32_t)(uintptr_t)((__attribute__((address_space(3))) const char*)a);
+        asm volatile("ds_read_b64_tr_b16 %0, %1" : "=v"(w) : "v"(la));
+#endif
+        out[2 * t] = w[0];
+        out[2 * t + 1] = w[1];
+      }
+      return out;
+    }
+  }
+  static constexpr int READS_PER_FRAG = KC ? 1 : 2;
+};
+
+// bf16 GEMM, 4 waves (2 x 2), wave tile (BM/2) x (BN/2) of 32x32x16 MFMAs.
+template <int BM, int BN, int BK, int STAGES, bool AK, bool BKC, int MODE>
+__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1)))
+    gemm_dlds_kernel(Params p) {
+  constexpr int WGM = 2, WGN = 2;
+  constexpr int WTM = BM / WGM, WTN = BN / WGN;
+  constexpr int TM = WTM / 32, TN = WTN / 32;
+  constexpr bool DUAL = (MODE == MODE_DUAL);
+  constexpr int NB = DUAL ? 2 * TN : TN;
+  constexpr int NSUB = BK / 16;
+  static_assert(MODE != MODE_PROLOGUE, "the SiLU-gate prologue needs register staging");
+  static_assert(NSUB == 2 || NSUB == 4, "BK must be 32 or 64");
+  static_assert(STAGES >= 2 && STAGES <= 4, "2..4 stages");
+  static_assert(TN % 2 == 0, "epilogue stages 64-column halves");
+  using OpA = DldsOperand<BM, BK, AK>;
+  using OpB = DldsOperand<BN, BK, BKC>;
+  constexpr int A_OFF = 0;                                  // in 16-byte units
+  constexpr int B_OFF = OpA::BYTES / 16;
+  constexpr int B2_OFF = B_OFF + OpB::BYTES / 16;
+  constexpr int STAGE_UNITS = (OpA::BYTES + OpB::BYTES * (DUAL ? 2 : 1)) / 16;
+  constexpr int NL = OpA::NU + OpB::NU * (DUAL ? 2 : 1);   // DMA instructions per wave per tile
+  static_assert(NL * (STAGES - 1) < 64, "vmcnt range");
+
+  __shared__ u32x4_t smem[STAGES][STAGE_UNITS];
+  auto stage = [&](int j) -> u32x4_t* { return &smem[j][0]; };
+
+  const int nblocks = gridDim.x;
+  const TileCoord tc = map_tile(blockIdx.x, nblocks, p.tiles_m, p.tiles_n, p.splits);
+  const int m0 = uniform(tc.tm * BM), n0 = uniform(tc.tn * BN);
+  const int zo = uniform(tc.z / p.heads), zi = uniform(tc.z - (tc.z / p.heads) * p.heads);
+  const int ziA = uniform(zi / p.gA), ziB = uniform(zi / p.gB), ziC = uniform(zi / p.gC);
+  const __bf16* Ab = uniform((const __bf16*)p.A + (int64_t)zo * p.aO + (int64_t)ziA * p.aI);
+  const __bf16* Bb = uniform((const __bf16*)p.B + (int64_t)zo * p.bO + (int64_t)ziB * p.bI);
+  const __bf16* B2b = DUAL ? uniform((const __bf16*)p.B2 + (int64_t)zo * p.bO + (int64_t)ziB * p.bI)
+                           : nullptr;
+  const int64_t coff = (int64_t)zo * p.cO + (int64_t)ziC * p.cI;
+  void* Cz = (char*)p.C + coff * (p.c_bf16 ? 2 : 4);
+  const void* Rz = p.R ? (const char*)p.R + ((int64_t)zo * p.rO + (int64_t)zi * p.rI) * (p.r_bf16 ? 2 : 4)
+                       : nullptr;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int wm = wave / WGN, wn = wave % WGN;
+
+  if (p.causal == CAUSAL_OUT_LOWER && n0 > m0 + BM - 1) {
+    if (p.splits > 1) return;  // the reduction kernel writes the mask
+    for (int idx = threadIdx.x; idx < BM * BN; idx += 256) {
+      const int m = m0 + idx / BN, n = n0 + idx % BN;
+      if (m < p.M && n < p.N) {
+        const int64_t ci = (int64_t)m * p.ldc + n;
+        if (p.c_bf16)
+          ((uint16_t*)Cz)[ci] = (uint16_t)f32_to_bf16_rne(p.mask_value);
+        else
+          ((float*)Cz)[ci] = p.mask_value;
+      }
+    }
+    return;
+  }
+
+  const int kt_seg = (p.K + BK - 1) / BK;
+  int klo = 0, khi = kt_seg;
+  if (p.causal == CAUSAL_A_LOWER) {
+    const int lim = (m0 + BM + BK - 1) / BK;
+    khi = khi < lim ? khi : lim;
+  } else if (p.causal == CAUSAL_A_UPPER) {
+    klo = m0 / BK;
+  }
+  const int per_seg = khi > klo ? khi - klo : 0;
+  const int total = per_seg * p.nseg;
+  const int it0 = uniform((int)((int64_t)total * tc.split / p.splits));
+  const int it1 = uniform((int)((int64_t)total * (tc.split + 1) / p.splits));
+
+  f32x16_t acc[TM][NB];
+#pragma unroll
+  for (int i = 0; i < TM; ++i)
+#pragma unroll
+    for (int j = 0; j < NB; ++j)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.0f;
+
+  OpA oa;
+  OpB ob;
+  OpB ob2;
+  oa.init(p.lda, p.M, m0);
+  ob.init(p.ldb, p.N, n0);
+  if constexpr (DUAL) ob2.init(p.ldb, p.N, n0);
+
+  // DMA of K tile `it` into stage j: NL instructions, issued in slot order.
+  struct TileRef {
+    __amdgpu_buffer_rsrc_t ra, rb, rb2;
+    int k0;
+    bool live;
+  };
+  auto tile_ref = [&](int it) __attribute__((always_inline)) {
+    TileRef t;
+    t.live = it < it1;
+    const int itc = t.live ? it : (it1 > 0 ? it1 - 1 : 0);
+    const int seg = itc / (per_seg > 0 ? per_seg : 1);
+    t.k0 = (klo + (itc - seg * per_seg)) * BK;
+    t.ra = make_rsrc(Ab + (int64_t)seg * p.segA, p.extA);
+    t.rb = make_rsrc(Bb + (int64_t)seg * p.segB, p.extB);
+    if constexpr (DUAL) t.rb2 = make_rsrc(B2b + (int64_t)seg * p.segB, p.extB);
+    return t;
+  };
+  auto dma = [&](int o, const TileRef& t, u32x4_t* st) __attribute__((always_inline)) {
+    if (o < OpA::NU) oa.load(o, t.ra, t.k0, p.K, t.live, st + A_OFF);
+    else if (o < OpA::NU + OpB::NU) ob.load(o - OpA::NU, t.rb, t.k0, p.K, t.live, st + B_OFF);
+    else ob2.load(o - OpA::NU - OpB::NU, t.rb2, t.k0, p.K, t.live, st + B2_OFF);
+  };
+
+  // Fragment sets: substep s uses set s & 1 (NSUB is even).
+  u32x4_t fa[2][TM], fb[2][NB];
+  constexpr int NREAD = TM + NB;  // fragments per substep
+  auto read_op = [&](int o, const u32x4_t* st, int s, int set) __attribute__((always_inline)) {
+    if (o < TM) {
+      fa[set][o] = oa.frag(st + A_OFF, wm * WTM + o * 32, s);
+    } else {
+      const int j = o - TM;
+      const int half = DUAL ? (j / TN) : 0;
+      const int jj = DUAL ? (j % TN) : j;
+      fb[set][j] = ob.frag(st + (half ? B2_OFF : B_OFF), wn * WTN + jj * 32, s);
+    }
+  };
+  auto mfma_op = [&](int set, int i, int j) __attribute__((always_inline)) {
+    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, fb[set][j]),
+                                                        __builtin_bit_cast(bf16x8_t, fa[set][i]),
+                                                        acc[i][j], 0, 0, 0);
+  };
+
+  // One substep = TM*NB MFMA slots, each also issuing an even share of the
+  // fragment reads of the next substep and (substep 0) of the DMA of the K tile
+  // STAGES-1 ahead.  A scheduling fence after every slot keeps that order.
+  constexpr int NS = TM * NB;
+  // S: substep index within the tile (compile time; fragment set S & 1).
+  // RS: substep whose fragments are read into the other set.  DMA: whether this
+  // substep also issues the DMA of tile t into stage dst.
+  auto substep = [&](auto S_c, auto RS_c, auto DMA_c, const u32x4_t* rd, const TileRef& t,
+                     u32x4_t* dst) __attribute__((always_inline)) {
+    constexpr int S = decltype(S_c)::value, RS = decltype(RS_c)::value;
+    constexpr bool DMA = decltype(DMA_c)::value;
+    constexpr int set = S & 1;
+    if constexpr (!AK || !BKC) {
+      // fragments of this set issued by transpose-read asm are complete only
+      // after lgkmcnt(0); nothing may be scheduled above this point
+      __builtin_amdgcn_s_waitcnt(0xC07F);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+#pragma unroll
+    for (int q = 0; q < NS; ++q) {
+      mfma_op(set, q / NB, q % NB);
+#pragma unroll
+      for (int o = (q * NREAD + NS - 1) / NS; o < ((q + 1) * NREAD + NS - 1) / NS; ++o)
+        read_op(o, rd, RS, set ^ 1);
+      if constexpr (DMA) {
+#pragma unroll
+        for (int o = (q * NL + NS - 1) / NS; o < ((q + 1) * NL + NS - 1) / NS; ++o) dma(o, t, dst);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  };
+
+  // Prologue: K tiles it0 .. it0+STAGES-2 into stages 0 .. STAGES-2.
+  if (it0 < it1) {
+#pragma unroll
+    for (int j = 0; j < STAGES - 1; ++j) {
+      const TileRef t = tile_ref(it0 + j);
+#pragma unroll
+      for (int o = 0; o < NL; ++o) dma(o, t, stage(j));
+    }
+    wait_vmcnt<NL * (STAGES - 2)>();
+  }
+  lds_ring_barrier();
+  if (it0 < it1) {
+#pragma unroll
+    for (int o = 0; o < NREAD; ++o) read_op(o, stage(0), 0, 0);
+  }
+
+  // K tile `it` sits in stage j: substeps 0 .. NSUB-2 read stage j (the first
+  // one also issues the DMA of tile it+STAGES-1 into the stage freed by tile
+  // it-1), then -- once this wave's DMA of tile it+1 has landed -- a barrier,
+  // then the last substep runs while reading substep 0 of tile it+1.
+  int j = 0;
+  for (int it = it0; it < it1; ++it) {
+    const int jn = (j + 1 == STAGES) ? 0 : j + 1;
+    const int jf = (j == 0) ? STAGES - 1 : j - 1;
+    u32x4_t* cur = stage(j);
+    u32x4_t* nxt = stage(jn);
+    u32x4_t* fill = stage(jf);
+    const TileRef t = tile_ref(it + STAGES - 1);
+    using std::integral_constant;
+    substep(integral_constant<int, 0>{}, integral_constant<int, 1>{}, std::true_type{}, cur, t, fill);
+    if constexpr (NSUB == 4) {
+      substep(integral_constant<int, 1>{}, integral_constant<int, 2>{}, std::false_type{}, cur, t, fill);
+      substep(integral_constant<int, 2>{}, integral_constant<int, 3>{}, std::false_type{}, cur, t, fill);
+    }
+    wait_vmcnt<NL * (STAGES - 2)>();
+    lds_ring_barrier();
+    substep(integral_constant<int, NSUB - 1>{}, integral_constant<int, 0>{}, std::false_type{}, nxt, t,
+            fill);
+    j = jn;
+  }
+  if constexpr (!AK || !BKC) {
+    // The last substep issued transpose reads (asm) for a K tile that does not
+    // exist.  Their registers count as dead to the compiler while the reads are
+    // still in flight: wait for them, and keep the registers allocated until
+    // after the wait so nothing else is placed in them meanwhile.
+    __builtin_amdgcn_s_waitcnt(0xC07F);
+#pragma unroll
+    for (int i = 0; i < TM; ++i) asm volatile("" ::"v"(fa[0][i]));
+#pragma unroll
+    for (int jj = 0; jj < NB; ++jj) asm volatile("" ::"v"(fb[0][jj]));
+  }
+  wait_vmcnt<0>();
+  __syncthreads();  // the epilogue reuses LDS
+
+  // Epilogue: acc[i][j][4q + e] holds C[m][n + e] with
+  //   m = m0 + wm*WTM + i*32 + (lane & 31),  n = n0 + wn*WTN + j*32 + 8q + 4*(lane >> 5).
+  // Each pass stages 32 rows x 64 columns of one wave through LDS (rows padded
+  // to 68 floats) and walks them row-major: coalesced C accesses, one rolled
+  // copy of the epilogue.
+  constexpr int PITCH = 68;
+  static_assert(4 * 32 * PITCH * 4 <= STAGES * STAGE_UNITS * 16, "epilogue staging fits the ring");
+  float* stg = reinterpret_cast<float*>(&smem[0][0]) + wave * (32 * PITCH);
+  float* W = (p.splits > 1) ? p.ws + ((int64_t)tc.z * p.splits + tc.split) * (int64_t)p.M * p.N
+                            : nullptr;
+  const int lrow = lane & 31, lhalf = lane >> 5;
+#pragma unroll
+  for (int i = 0; i < TM; ++i) {
+#pragma unroll
+    for (int jh = 0; jh < TN / 2; ++jh) {
+#pragma unroll
+      for (int jj = 0; jj < 2; ++jj) {
+        const int j = 2 * jh + jj;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          f32x4_t v;
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            if constexpr (DUAL)
+              v[e] = silu_f(p.alpha * acc[i][j][4 * q + e]) * (p.alpha * acc[i][j + TN][4 * q + e]);
+            else
+              v[e] = acc[i][j][4 * q + e];
+          }
+          *reinterpret_cast<f32x4_t*>(stg + lrow * PITCH + jj * 32 + 8 * q + 4 * lhalf) = v;
+        }
+      }
+      __syncthreads();
+      const int mrow0 = m0 + wm * WTM + i * 32;
+      const int ncol0 = n0 + wn * WTN + jh * 64;
+#pragma unroll 2
+      for (int idx = lane; idx < 32 * 16; idx += 64) {
+        const int r = idx >> 4, c4 = idx & 15;
+        const f32x4_t sv = *reinterpret_cast<const f32x4_t*>(stg + r * PITCH + c4 * 4);
+        const int m = mrow0 + r, n = ncol0 + c4 * 4;
+        if (W) {
+          if (m < p.M) {
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+              if (n + e < p.N) W[(int64_t)m * p.N + n + e] = sv[e];
+          }
+        } else {
+          float v[4];
+#pragma unroll
+          for (int e = 0; e < 4; ++e) v[e] = DUAL ? sv[e] : p.alpha * sv[e];
+          epilogue4(p, Cz, Rz, m, n, v);
+        }
+      }
+      __syncthreads();
+    }
+  }
+}
+
+}  // namespace mig

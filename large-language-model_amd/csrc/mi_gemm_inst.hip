@@ -1,6 +1,7 @@
 // mi_gemm_inst.hip -- instantiates the GEMM kernels of one (dtype, transA,
 // transB) combination.  Compiled once per combination with
 //   -DMI_DT_BF16=0|1 -DMI_TA=0|1 -DMI_TB=0|1
+#include "mi_gemm_dlds.hpp"
 #include "mi_gemm_kernels.hpp"
 
 #if !defined(MI_DT_BF16) || !defined(MI_TA) || !defined(MI_TB)
@@ -17,6 +18,13 @@ typedef float elem_t;
 #define MI_DTN f32
 #endif
 
+#ifndef MI_DLDS_BK
+#define MI_DLDS_BK 64
+#endif
+#ifndef MI_DLDS_STAGES
+#define MI_DLDS_STAGES 2
+#endif
+
 #define MI_CAT5(a, b, c, d, e) a##b##c##d##e
 #define MI_PICK_NAME(dt, ta, tb) MI_CAT5(pick_, dt, _, ta, tb)
 
@@ -29,6 +37,17 @@ KernelFn MI_PICK_NAME(MI_DTN, MI_TA, MI_TB)(int cfg, bool fast) {
   constexpr int LM = 128, LN = 128, SM = 128, SN = 128, DM = 128, DN = 64, PM = 128, PN = 128;
 #endif
   if (fast) {
+#if MI_DT_BF16
+    // bf16: direct-to-LDS pipeline (K tile MI_DLDS_BK, MI_DLDS_STAGES-deep LDS ring)
+    switch (cfg) {
+      case CFG_L: return gemm_dlds_kernel<LM, LN, MI_DLDS_BK, MI_DLDS_STAGES, AK, BK, MODE_PLAIN>;
+      case CFG_S: return gemm_dlds_kernel<SM, SN, 32, 4, AK, BK, MODE_PLAIN>;
+      case CFG_DUAL: return gemm_dlds_kernel<DM, DN, 32, 4, AK, BK, MODE_DUAL>;
+      case CFG_PRO:
+        if constexpr (AK) return gemm_kernel<elem_t, PM, PN, 2, 2, AK, BK, MODE_PROLOGUE, true>;
+        return nullptr;
+    }
+#endif
     switch (cfg) {
       case CFG_L: return gemm_kernel<elem_t, LM, LN, 2, 2, AK, BK, MODE_PLAIN, true>;
       case CFG_S: return gemm_kernel<elem_t, SM, SN, 2, 2, AK, BK, MODE_PLAIN, true>;
