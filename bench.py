@@ -33,6 +33,26 @@ BLOCK = [("qkv", 2048, 3072), ("o", 2048, 2048), ("gate", 2048, 5632), ("up", 20
 M_TOKENS = 8192
 
 
+WS_BYTES = 512 << 20
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "gemm_block_set_bf16_m8192_hbm_bytes.md")
+
+
+def hbm_bytes_per_launch(kernel: str):
+    """HBM bytes per launch of `kernel` from the committed rocprofv3 --pmc summary
+    (FETCH_SIZE and WRITE_SIZE per dispatch, scaled by the copy-kernel calibration),
+    or None when the summary has no row for it."""
+    if not os.path.exists(TRAFFIC_FILE):
+        return None
+    for line in open(TRAFFIC_FILE):
+        cells = [c.strip() for c in line.strip().strip("|").split("|")]
+        if len(cells) >= 5 and cells[0] == kernel:
+            try:
+                return int(float(cells[4]))
+            except ValueError:
+                return None
+    return None
+
+
 def block_flops(M: int) -> int:
     return sum(3 * 2 * M * din * dout for _, din, dout in BLOCK)
 
@@ -91,6 +111,8 @@ def main():
     M = M_TOKENS
     g = torch.Generator(device=dev)
     g.manual_seed(1234)
+    # split-K workspace, as the bridge's pool provides it (the planner decides per GEMM)
+    ws = torch.empty(WS_BYTES // 4, dtype=torch.float32, device=dev)
     ops = []
     for name, din, dout in BLOCK:
         X = torch.randn((M, din), generator=g, device=dev).to(torch.bfloat16)
@@ -100,18 +122,22 @@ def main():
         dX = torch.empty((M, din), dtype=torch.bfloat16, device=dev)
         dW = torch.zeros((din, dout), dtype=torch.float32, device=dev)
         ops.append((name, "fwd NN", 2 * M * din * dout,
+                    mi.describe(0, 0, M, dout, din, workspace_bytes=WS_BYTES),
                     lambda X=X, W=W, Y=Y, din=din, dout=dout:
-                    mi.gemm(X, W, Y, M, dout, din, sync=False)))
+                    mi.gemm(X, W, Y, M, dout, din, workspace=ws, sync=False)))
         ops.append((name, "dX NT", 2 * M * din * dout,
+                    mi.describe(0, 1, M, din, dout, workspace_bytes=WS_BYTES),
                     lambda dY=dY, W=W, dX=dX, din=din, dout=dout:
-                    mi.gemm(dY, W, dX, M, din, dout, transB=True, sync=False)))
+                    mi.gemm(dY, W, dX, M, din, dout, transB=True, workspace=ws, sync=False)))
         ops.append((name, "dW TN", 2 * M * din * dout,
+                    mi.describe(1, 0, din, dout, M, workspace_bytes=WS_BYTES),
                     lambda X=X, dY=dY, dW=dW, din=din, dout=dout:
-                    mi.gemm(X, dY, dW, din, dout, M, transA=True, beta=1.0, sync=False)))
+                    mi.gemm(X, dY, dW, din, dout, M, transA=True, beta=1.0, workspace=ws,
+                            sync=False)))
 
     def step():
-        for _, _, _, fn in ops:
-            fn()
+        for op in ops:
+            op[-1]()
 
     for _ in range(args.warmup):
         step()
@@ -124,9 +150,9 @@ def main():
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     for s in range(args.steps):
-        for i, (_, _, _, fn) in enumerate(ops):
+        for i, op in enumerate(ops):
             evs[s][i][0].record(stream)
-            fn()
+            op[-1]()
             evs[s][i][1].record(stream)
     torch.cuda.synchronize()
     t1 = time.perf_counter()
@@ -134,21 +160,24 @@ def main():
     flops = block_flops(M)
     value = flops * args.steps / elapsed / 1e12
 
-    # Per-kernel (operand layout) totals over the timed region.
-    per_kind = {}
+    # Per-kernel totals over the timed region; a kernel is the planner's choice
+    # (tile configuration, operand layout, split-K factor) for a GEMM shape.
+    per_kernel = {}
     per_op = {}
     for s in range(args.steps):
-        for i, (name, kind, fl, _) in enumerate(ops):
+        for i, (name, kind, fl, desc, _) in enumerate(ops):
             ms = evs[s][i][0].elapsed_time(evs[s][i][1])
-            k = kind.split()[1]
-            tot = per_kind.setdefault(k, [0.0, 0, 0])
+            kern = desc.rsplit(" tiles", 1)[0]
+            tot = per_kernel.setdefault(kern, [0.0, 0, 0, set()])
             tot[0] += ms
             tot[1] += fl
             tot[2] += 1
+            tot[3].add(f"{name} {kind}")
             per_op.setdefault(f"{name} {kind}", [0.0, fl])[0] += ms
-    dom = max(per_kind, key=lambda k: per_kind[k][0])
-    ms_dom, fl_dom, n_dom = per_kind[dom]
+    dom = max(per_kernel, key=lambda k: per_kernel[k][0])
+    ms_dom, fl_dom, n_dom, dom_ops = per_kernel[dom]
     achieved = fl_dom / (ms_dom / 1e3) / 1e12
+    traffic = hbm_bytes_per_launch(dom)
     breakdown = {k: round(v[1] / (v[0] / args.steps / 1e3) / 1e12, 1) for k, v in per_op.items()}
 
     if args.copy_calibration:
@@ -178,8 +207,9 @@ def main():
                    "per_gemm_tflops": breakdown},
         "roofline": {"bound": "mfma", "achieved": round(achieved, 2), "peak": PEAK_BF16_TFLOPS,
                      "unit": "TFLOP/s", "frac": round(achieved / PEAK_BF16_TFLOPS, 4),
-                     "traffic": None, "kernel": f"gemm_kernel bf16 {dom} (256x256 tile)",
-                     "launches": n_dom, "avg_launch_ms": round(ms_dom / n_dom, 4)},
+                     "traffic": traffic, "kernel": dom, "gemms": sorted(dom_ops),
+                     "launches": n_dom, "avg_launch_ms": round(ms_dom / n_dom, 4),
+                     "time_share": round(ms_dom / sum(v[0] for v in per_kernel.values()), 3)},
     }
     if not args.no_cpu:
         out["cpu_baseline"] = cpu_baseline(args.cpu_rows)

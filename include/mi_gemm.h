@@ -150,6 +150,16 @@ int mi_softmax_causal(void* stream, void* S, int64_t rows, int64_t T, int64_t ld
 int mi_softmax_bwd(void* stream, const void* P, void* dP, int64_t rows, int64_t T,
                    int64_t ld, float scale, int32_t dtype);
 
+/*
+ * Describe the kernel mi_gemm_batched would launch for this problem (tile,
+ * loader, split-K factor) as text into buf (always NUL-terminated).  For
+ * measurement and logging; no reference counterpart.  epi_mode: 0 plain,
+ * 1 dual-B, 2 SiLU-gate prologue.
+ */
+int mi_gemm_describe(int transA, int transB, int64_t M, int64_t N, int64_t K, int32_t dtype_in,
+                     int64_t batch, int32_t epi_mode, size_t workspace_bytes, char* buf,
+                     size_t buf_len);
+
 /* Synchronise `stream`; replaces metal_bridge::end_scope's wait
  * (MetalBridge.hpp:29-30, MetalBridge.mm:2176-2225). */
 int mi_stream_sync(void* stream);

@@ -135,47 +135,46 @@ struct Plan {
 
 int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
 
-// Pick the tile configuration and split-K factor with a small cost model:
-// time ~ (waves of workgroups over the CUs) x (per-workgroup MFMA time at the
-// configuration's sustained rate) + (split-K partial write/read traffic).
+// Pick the tile configuration and split-K factor.  Rules measured on MI355X for
+// the decoder-block shapes (TFLOP/s of 256x256 "L" vs 128x128 "S" tiles and of
+// split-K): throughput is set by a chip-wide limit (fewer active CUs run faster
+// each), so
+//   * a grid of L tiles covering most CUs runs as is, unless its last wave is
+//     at most half full and S tiles fill whole waves (8192x3072: S 764 vs L 624);
+//   * L tiles that leave half of an L tile's area empty (N or M below 256) use S;
+//   * few L tiles with a long K split K until the units fill the CUs once
+//     (2048x3072x8192: split 2 752 vs 486; 2048x2048x8192: split 4 647 vs 322),
+//     given a workspace; without one, S when it fills the CUs.
 Plan make_plan(int dtype_in, int64_t M, int64_t N, int64_t Ktot, int64_t batch, int mode,
                bool allow_split, int64_t ws_limit_elems, int cus, bool fast) {
-  Plan best{CFG_L, 1, 1, 1};
-  if (mode == MODE_DUAL) {
-    const CfgShape s = shape_of(dtype_in, CFG_DUAL);
-    return Plan{CFG_DUAL, 1, (int)cdiv(M, s.bm), (int)cdiv(N, s.bn)};
-  }
-  if (mode == MODE_PROLOGUE) {
-    const CfgShape s = shape_of(dtype_in, CFG_PRO);
-    return Plan{CFG_PRO, 1, (int)cdiv(M, s.bm), (int)cdiv(N, s.bn)};
-  }
-  const double peak_cu = (dtype_in == MI_BF16 ? 4096.0 : 256.0) * 2.4e9;  // FLOP/s per CU
-  const double hbm = 5.0e12;                                               // sustained B/s
-  double best_t = 1e30;
-  const int cfgs[2] = {CFG_L, CFG_S};
-  for (int ci = fast ? 0 : 1; ci < 2; ++ci) {
-    const int cfg = cfgs[ci];
+  auto plan_for = [&](int cfg, int sp) {
     const CfgShape s = shape_of(dtype_in, cfg);
-    const double eff = (cfg == CFG_L || dtype_in != MI_BF16) ? 0.80 : 0.55;
-    const int64_t tm = cdiv(M, s.bm), tn = cdiv(N, s.bn);
-    const int64_t tiles = tm * tn * batch;
-    for (int sp = 1; sp <= 16; ++sp) {
-      if (sp > 1 && (!allow_split || mode != MODE_PLAIN)) break;
-      if (sp > 1 && (int64_t)sp * M * N * batch > ws_limit_elems) break;
-      const int kt = dtype_in == MI_BF16 ? 64 : 32;
-      if (sp > 1 && cdiv(Ktot, kt) < 4 * sp) break;
-      const int64_t units = tiles * sp;
-      const double waves = std::ceil((double)units / cus);
-      const double t_unit = 2.0 * s.bm * s.bn * ((double)Ktot / sp) / (peak_cu * eff) + 2.0e-6 / 1.0;
-      double t = waves * t_unit;
-      if (sp > 1) t += (double)sp * M * N * batch * 4.0 * 2.0 / hbm + 4.0e-6;
-      if (t < best_t * 0.97) {
-        best_t = t;
-        best = Plan{cfg, sp, (int)tm, (int)tn};
-      }
-    }
+    return Plan{cfg, sp, (int)cdiv(M, s.bm), (int)cdiv(N, s.bn)};
+  };
+  if (mode == MODE_DUAL) return plan_for(CFG_DUAL, 1);
+  if (mode == MODE_PROLOGUE) return plan_for(CFG_PRO, 1);
+  if (!fast) return plan_for(CFG_S, 1);
+  const CfgShape L = shape_of(dtype_in, CFG_L), S = shape_of(dtype_in, CFG_S);
+  const int64_t tilesL = cdiv(M, L.bm) * cdiv(N, L.bn) * batch;
+  const int64_t tilesS = cdiv(M, S.bm) * cdiv(N, S.bn) * batch;
+  const double fillL = (double)(M * N * batch) / ((double)tilesL * L.bm * L.bn);
+  const double fillS = (double)(M * N * batch) / ((double)tilesS * S.bm * S.bn);
+  const bool s_fills_cus = tilesS >= cus;
+  if (fillL < 0.75 && fillS > fillL) return plan_for(CFG_S, 1);
+  if (tilesL * 8 >= (int64_t)cus * 5) {
+    const double waves = (double)tilesL / cus;
+    const double frac = waves - std::floor(waves);
+    if (waves >= 1.0 && frac > 0.0 && frac <= 0.5 && s_fills_cus) return plan_for(CFG_S, 1);
+    return plan_for(CFG_L, 1);
   }
-  return best;
+  const int kt = dtype_in == MI_BF16 ? 64 : 32;
+  if (allow_split) {
+    int sp = (int)std::min<int64_t>(cus / std::max<int64_t>(tilesL, 1), 8);
+    while (sp > 1 && (cdiv(Ktot, kt) < 8 * sp || (int64_t)sp * M * N * batch > ws_limit_elems)) --sp;
+    if (sp >= 2) return plan_for(CFG_L, sp);
+  }
+  // few tiles either way: the smaller tile gives more parallel work
+  return plan_for(tilesS > tilesL ? CFG_S : CFG_L, 1);
 }
 
 bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
@@ -540,6 +539,25 @@ int mi_softmax_bwd(void* stream, const void* P, void* dP, int64_t rows, int64_t 
                        (hipStream_t)stream, P, dP, T, ld, scale);
   hipError_t e = hipGetLastError();
   return e == hipSuccess ? MI_OK : fail(MI_ERR_HIP, "softmax_bwd: %s", hipGetErrorString(e));
+}
+
+int mi_gemm_describe(int transA, int transB, int64_t M, int64_t N, int64_t K, int32_t dtype_in,
+                     int64_t batch, int32_t epi_mode, size_t workspace_bytes, char* buf,
+                     size_t buf_len) {
+  if (!buf || buf_len == 0) return fail(MI_ERR_NULL, "buf is NULL");
+  if (M <= 0 || N <= 0 || K < 0 || batch <= 0) return fail(MI_ERR_SHAPE, "bad shape");
+  if (dtype_in != MI_F32 && dtype_in != MI_BF16) return fail(MI_ERR_DTYPE, "dtype %d", dtype_in);
+  int cus = 256;
+  if (init_devices() == MI_OK) cus = current_cus();
+  const int mode = epi_mode == 1 ? MODE_DUAL : (epi_mode == 2 ? MODE_PROLOGUE : MODE_PLAIN);
+  const int64_t ws = (int64_t)(workspace_bytes / sizeof(float));
+  const Plan pl = make_plan(dtype_in, M, N, K, batch, mode, ws > 0, ws, cus, true);
+  const CfgShape sh = shape_of(dtype_in, pl.cfg);
+  const char* kind = (dtype_in == MI_BF16 && pl.cfg != CFG_PRO) ? "dlds" : "regstage";
+  std::snprintf(buf, buf_len, "%s %s %dx%d %s%s split%d tiles%d", kind,
+                dtype_in == MI_BF16 ? "bf16" : "f32", sh.bm, sh.bn, transA ? "T" : "N",
+                transB ? "T" : "N", pl.splits, pl.tiles_m * pl.tiles_n * (int)batch);
+  return MI_OK;
 }
 
 int mi_stream_sync(void* stream) {

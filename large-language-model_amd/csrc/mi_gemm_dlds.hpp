@@ -127,6 +127,7 @@ struct DldsOperand {
         const int kr = 16 * s + 8 * (g >> 1) + 4 * t + (j >> 2);
         const char* a = base + kr * (R * 2) + 16 * mc_swz(kr, q) + sub;
         u32x2_t w = {0u, 0u};
+        (void)a;
 #if defined(__HIP_DEVICE_COMPILE__)
         // Issued as inline asm: the compiler makes the transpose-read builtin wait
         // for every LDS-DMA load in flight (vmcnt(0)), which would drain the ring.

@@ -33,7 +33,7 @@ MI_CAUSAL_NONE, MI_CAUSAL_OUT_LOWER, MI_CAUSAL_A_LOWER, MI_CAUSAL_A_UPPER = 0, 1
 C_SYMBOLS = (
     "mi_init", "mi_last_error", "mi_version", "mi_gemm_workspace_size", "mi_gemm",
     "mi_gemm_batched", "mi_residual_add", "mi_softmax_causal", "mi_softmax_bwd",
-    "mi_stream_sync",
+    "mi_gemm_describe", "mi_stream_sync",
 )
 
 
@@ -102,6 +102,9 @@ def load_library():
     L.mi_softmax_causal.argtypes = [vp, vp, i64, i64, i64, i32]
     L.mi_softmax_bwd.restype = ctypes.c_int
     L.mi_softmax_bwd.argtypes = [vp, vp, vp, i64, i64, i64, f32, i32]
+    L.mi_gemm_describe.restype = ctypes.c_int
+    L.mi_gemm_describe.argtypes = [ctypes.c_int, ctypes.c_int, i64, i64, i64, i32, i64, i32,
+                                   ctypes.c_size_t, ctypes.c_char_p, ctypes.c_size_t]
     L.mi_stream_sync.restype = ctypes.c_int
     L.mi_stream_sync.argtypes = [vp]
     _lib = L
@@ -234,6 +237,14 @@ def gemm_batched(A, B, C, M, N, K, batch: MiBatch, *, transA=False, transB=False
         _finish("mi_gemm_batched", st)
     else:
         _check("mi_gemm_batched", st)
+
+
+def describe(transA, transB, M, N, K, dtype_in=MI_BF16, batch=1, epi_mode=0, workspace_bytes=0):
+    """Text description of the kernel the planner picks for this problem."""
+    buf = ctypes.create_string_buffer(160)
+    _check("mi_gemm_describe", load_library().mi_gemm_describe(
+        int(transA), int(transB), M, N, K, dtype_in, batch, epi_mode, workspace_bytes, buf, 160))
+    return buf.value.decode()
 
 
 def workspace_size(transA, transB, M, N, K, dtype_in=MI_BF16, dtype_c=MI_F32, batch=1) -> int:
