@@ -13,6 +13,28 @@ namespace {
 thread_local int t_status = MI_OK;
 thread_local bool t_in_scope = false;
 thread_local hipStream_t t_stream = nullptr;
+// Split-K workspace owned by the bridge, grown to the largest size a call asked
+// for; the library itself never allocates.
+thread_local void* t_ws = nullptr;
+thread_local size_t t_ws_bytes = 0;
+
+void* workspace_for(int ta, int tb, size_t M, size_t N, size_t K, int dt_in, int dt_c,
+                    size_t* bytes) {
+  const size_t need = mi_gemm_workspace_size(ta, tb, (int64_t)M, (int64_t)N, (int64_t)K, dt_in, dt_c, 1);
+  if (need > t_ws_bytes) {
+    if (t_ws) {
+      // the stream may still use the old buffer
+      if (hipStreamSynchronize(t_stream) != hipSuccess) return *bytes = 0, nullptr;
+      (void)hipFree(t_ws);
+    }
+    t_ws = nullptr;
+    t_ws_bytes = 0;
+    if (hipMalloc(&t_ws, need) != hipSuccess) return *bytes = 0, nullptr;
+    t_ws_bytes = need;
+  }
+  *bytes = t_ws_bytes;
+  return t_ws;
+}
 
 hipStream_t get_stream() {
   if (!t_stream) {
@@ -39,8 +61,11 @@ int gemm(int ta, int tb, size_t M, size_t N, size_t K, float alpha, const void* 
          int dt_in, float beta, void* C, int dt_c, const mi_epilogue* epi) {
   const int64_t lda = ta ? (int64_t)M : (int64_t)K;
   const int64_t ldb = tb ? (int64_t)K : (int64_t)N;
-  return mi_gemm(get_stream(), ta, tb, (int64_t)M, (int64_t)N, (int64_t)K, alpha, A, lda, B, ldb,
-                 dt_in, beta, C, (int64_t)N, dt_c, epi, nullptr, 0);
+  hipStream_t st = get_stream();
+  size_t ws_bytes = 0;
+  void* ws = epi ? nullptr : workspace_for(ta, tb, M, N, K, dt_in, dt_c, &ws_bytes);
+  return mi_gemm(st, ta, tb, (int64_t)M, (int64_t)N, (int64_t)K, alpha, A, lda, B, ldb, dt_in, beta,
+                 C, (int64_t)N, dt_c, epi, ws, ws_bytes);
 }
 
 }  // namespace
