@@ -252,13 +252,30 @@ def workspace_size(transA, transB, M, N, K, dtype_in=MI_BF16, dtype_c=MI_F32, ba
                                                      dtype_c, batch))
 
 
+_WS_POOL = {}
+
+
+def _pooled_workspace(transA, transB, M, N, K, A, C):
+    """Split-K workspace for the reference-named calls: one fp32 buffer per device,
+    grown to the largest size a call has asked for (the C++ bridge keeps the same pool)."""
+    need = workspace_size(transA, transB, M, N, K, _dt(A), _dt(C))
+    if need == 0:
+        return None
+    ws = _WS_POOL.get(C.device)
+    if ws is None or ws.numel() * 4 < need:
+        ws = _torch().empty((need + 3) // 4, dtype=_torch().float32, device=C.device)
+        _WS_POOL[C.device] = ws
+    return ws
+
+
 # ---- reference-named entry points (MetalBridge.hpp) ---------------------------
 
 def gemm_bf16(A, B, C, M, N, K, transA=False, transB=False, is_forward=False):
     """MetalBridge.hpp:39-42. bf16 in/out: C[M,N] = op(A) op(B). No-op if a size is 0."""
     if M == 0 or N == 0 or K == 0:
         return
-    gemm(A, B, C, M, N, K, transA=transA, transB=transB)
+    gemm(A, B, C, M, N, K, transA=transA, transB=transB,
+         workspace=_pooled_workspace(transA, transB, M, N, K, A, C))
 
 
 def fused_swiglu_gemm(gate_proj, up_proj, B, C, M, N, K):
@@ -279,7 +296,7 @@ def gemm_proj(a, b, c, M, N, K):
     """MetalBridge.hpp:121 (cblas_sgemm NN, MetalBridge.mm:695-697), on the GPU."""
     if M == 0 or N == 0 or K == 0:
         return
-    gemm(a, b, c, M, N, K)
+    gemm(a, b, c, M, N, K, workspace=_pooled_workspace(0, 0, M, N, K, a, c))
 
 
 def gemm_backward(a_transposed, b, c, M, N, K, accumulate=False):
@@ -290,14 +307,16 @@ def gemm_backward(a_transposed, b, c, M, N, K, accumulate=False):
     """
     if M == 0 or N == 0 or K == 0:
         return
-    gemm(a_transposed, b, c, M, N, K, transA=True, beta=1.0 if accumulate else 0.0)
+    gemm(a_transposed, b, c, M, N, K, transA=True, beta=1.0 if accumulate else 0.0,
+         workspace=_pooled_workspace(1, 0, M, N, K, a_transposed, c))
 
 
 def gemm_proj_trans_b(a, b_transposed, c, M, N, K):
     """MetalBridge.hpp:124-125: C = A B^T, B stored [N,K]."""
     if M == 0 or N == 0 or K == 0:
         return
-    gemm(a, b_transposed, c, M, N, K, transB=True)
+    gemm(a, b_transposed, c, M, N, K, transB=True,
+         workspace=_pooled_workspace(0, 1, M, N, K, a, c))
 
 
 def residual_add(a, b, n=None):
@@ -340,7 +359,7 @@ def matmul(a, b):
     if b.dim() == 2 and a.dim() != 2:
         K, N = b.shape
         M = a.numel() // K if K else math.prod(a.shape[:-1])
-        gemm(a, b, out, M, N, K)
+        gemm(a, b, out, M, N, K, workspace=_pooled_workspace(0, 0, M, N, K, a, out))
     else:
         M, K, N = a.shape[-2], a.shape[-1], b.shape[-1]
         nb = math.prod(a.shape[:-2])

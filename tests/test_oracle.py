@@ -63,6 +63,48 @@ def test_integer_exact(oracle):
     assert np.array_equal(C, (a @ b).astype(np.float64))
 
 
+def test_linearity_tc20(oracle):
+    """(A1 + 2 A2) B = A1 B + 2 A2 B and A (B1 + B2) = A B1 + A B2
+    (TC-20, test_transformer.cpp:450-482), in the NT layout of a projection."""
+    rng = _rng(21)
+    M, N, K = 23, 19, 37
+    a1, a2 = (rng.standard_normal((M, K)) for _ in range(2))
+    b1, b2 = (rng.standard_normal((N, K)) for _ in range(2))
+    g = lambda a, b: oracle.gemm(0, 1, M, N, K, a.astype(np.float32), b.astype(np.float32))
+    f32 = lambda x: x.astype(np.float32).astype(np.float64)
+    lhs = g(f32(a1) + 2 * f32(a2), b1)
+    assert np.allclose(lhs, g(a1, b1) + 2 * g(a2, b1), rtol=1e-6, atol=1e-6)
+    assert np.allclose(g(a1, f32(b1) + f32(b2)), g(a1, b1) + g(a1, b2), rtol=1e-6, atol=1e-6)
+
+
+def test_transpose_identity(oracle):
+    """(A B)^T = B^T A^T: the TN product of stored operands equals the transpose of
+    the NT product with the operands swapped."""
+    rng = _rng(22)
+    M, N, K = 14, 31, 26
+    x = rng.standard_normal((K, M)).astype(np.float32)   # activations [tokens, in]
+    dy = rng.standard_normal((K, N)).astype(np.float32)  # gradient [tokens, out]
+    dw = oracle.gemm(1, 0, M, N, K, x, dy)                # x^T dy
+    dwt = oracle.gemm(1, 0, N, M, K, dy, x)               # dy^T x
+    assert np.allclose(dw, dwt.T, rtol=1e-12, atol=1e-12)
+    assert not np.allclose(dw[:, :M], dwt[:M, :], atol=1e-3)
+
+
+def test_accumulate_tc28(oracle):
+    """Two backward passes accumulate into one weight gradient with beta = 1
+    (TC-28, test_transformer.cpp:615-636; Transformer.cpp:236,288-289)."""
+    rng = _rng(23)
+    M, N, K = 16, 12, 40
+    x1, x2 = (rng.standard_normal((K, M)).astype(np.float32) for _ in range(2))
+    d1, d2 = (rng.standard_normal((K, N)).astype(np.float32) for _ in range(2))
+    g1 = oracle.gemm(1, 0, M, N, K, x1, d1)
+    acc = oracle.gemm(1, 0, M, N, K, x2, d2, beta=1.0, C0=g1.astype(np.float32))
+    ref = x1.T.astype(np.float64) @ d1 + x2.T.astype(np.float64) @ d2
+    assert np.allclose(acc, ref, rtol=1e-6, atol=1e-6)
+    # overwrite semantics (beta = 0) would drop the first pass
+    assert np.max(np.abs(oracle.gemm(1, 0, M, N, K, x2, d2) - ref)) > 1e-2
+
+
 def test_epilogue_bias_beta_residual(oracle):
     rng = _rng(4)
     M, N, K = 12, 20, 9
