@@ -157,7 +157,7 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1)))
   constexpr int NSUB = BK / 16;
   static_assert(MODE != MODE_PROLOGUE, "the SiLU-gate prologue needs register staging");
   static_assert(NSUB == 2 || NSUB == 4, "BK must be 32 or 64");
-  static_assert(STAGES >= 2 && STAGES <= 4, "2..4 stages");
+  static_assert(STAGES >= 2 && STAGES <= 5, "2..5 stages");
   static_assert(TN % 2 == 0, "epilogue stages 64-column halves");
   using OpA = DldsOperand<BM, BK, AK>;
   using OpB = DldsOperand<BN, BK, BKC>;
@@ -166,7 +166,8 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1)))
   constexpr int B2_OFF = B_OFF + OpB::BYTES / 16;
   constexpr int STAGE_UNITS = (OpA::BYTES + OpB::BYTES * (DUAL ? 2 : 1)) / 16;
   constexpr int NL = OpA::NU + OpB::NU * (DUAL ? 2 : 1);   // DMA instructions per wave per tile
-  static_assert(NL * (STAGES - 1) < 64, "vmcnt range");
+  static_assert(NL * STAGES < 64, "vmcnt range");
+  static_assert(STAGES * STAGE_UNITS * 16 <= 160 * 1024, "LDS ring exceeds 160 KB");
 
   __shared__ u32x4_t smem[STAGES][STAGE_UNITS];
   auto stage = [&](int j) -> u32x4_t* { return &smem[j][0]; };
@@ -272,17 +273,30 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1)))
                                                         acc[i][j], 0, 0, 0);
   };
 
-  // One substep = TM*NB MFMA slots, each also issuing an even share of the
-  // fragment reads of the next substep and (substep 0) of the DMA of the K tile
-  // STAGES-1 ahead.  A scheduling fence after every slot keeps that order.
+  // One substep = TM*NB MFMA slots.  The fragment reads of the next substep go
+  // out one per slot from the first slot on, so they have most of the substep
+  // to land before its lgkmcnt wait.  DMA instructions are spread over MFMA
+  // slots: a wave that issues them faster than the memory pipeline accepts
+  // them stalls in order, and the MFMAs behind them with it.  With three or
+  // more stages (SPREAD) the DMA of the K tile STAGES-1 ahead goes into the
+  // stage freed at the previous barrier and is spread over every slot of the
+  // K tile; with two stages it can only start after this tile's barrier and is
+  // spread over the last substep.  A scheduling fence after every slot keeps
+  // that order.
   constexpr int NS = TM * NB;
+  constexpr int TOT = NSUB * NS;  // MFMA slots per K tile
+  constexpr bool SPREAD = STAGES >= 3;
+  // SPREAD: DMA instructions issued before the last substep of a K tile.
+  constexpr int DMA_EARLY = (NL * (NSUB - 1) * NS + TOT - 1) / TOT;
+  static_assert(NREAD <= NS, "one fragment read per MFMA slot at most");
   // S: substep index within the tile (compile time; fragment set S & 1).
-  // RS: substep whose fragments are read into the other set.  DMA: whether this
-  // substep also issues the DMA of tile t into stage dst.
+  // RS: substep whose fragments are read into the other set.  DMA: 0 none,
+  // 1 the whole DMA of tile t into stage dst spread over this substep, 2 the
+  // share of slots S*NS .. S*NS+NS-1 of a DMA spread over the K tile.
   auto substep = [&](auto S_c, auto RS_c, auto DMA_c, const u32x4_t* rd, const TileRef& t,
                      u32x4_t* dst) __attribute__((always_inline)) {
     constexpr int S = decltype(S_c)::value, RS = decltype(RS_c)::value;
-    constexpr bool DMA = decltype(DMA_c)::value;
+    constexpr int DMA = decltype(DMA_c)::value;
     constexpr int set = S & 1;
     if constexpr (!AK || !BKC) {
       // fragments of this set issued by transpose-read asm are complete only
@@ -293,26 +307,29 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1)))
 #pragma unroll
     for (int q = 0; q < NS; ++q) {
       mfma_op(set, q / NB, q % NB);
-#pragma unroll
-      for (int o = (q * NREAD + NS - 1) / NS; o < ((q + 1) * NREAD + NS - 1) / NS; ++o)
-        read_op(o, rd, RS, set ^ 1);
-      if constexpr (DMA) {
+      if (q < NREAD) read_op(q, rd, RS, set ^ 1);
+      if constexpr (DMA == 1) {
 #pragma unroll
         for (int o = (q * NL + NS - 1) / NS; o < ((q + 1) * NL + NS - 1) / NS; ++o) dma(o, t, dst);
+      } else if constexpr (DMA == 2) {
+        const int g = S * NS + q;
+#pragma unroll
+        for (int o = (g * NL + TOT - 1) / TOT; o < ((g + 1) * NL + TOT - 1) / TOT; ++o) dma(o, t, dst);
       }
       __builtin_amdgcn_sched_barrier(0);
     }
   };
 
-  // Prologue: K tiles it0 .. it0+STAGES-2 into stages 0 .. STAGES-2.
+  // Prologue: K tiles it0 .. it0+PRE-1 into stages 0 .. PRE-1.
+  constexpr int PRE = SPREAD ? STAGES - 1 : STAGES;
   if (it0 < it1) {
 #pragma unroll
-    for (int j = 0; j < STAGES - 1; ++j) {
+    for (int j = 0; j < PRE; ++j) {
       const TileRef t = tile_ref(it0 + j);
 #pragma unroll
       for (int o = 0; o < NL; ++o) dma(o, t, stage(j));
     }
-    wait_vmcnt<NL * (STAGES - 2)>();
+    wait_vmcnt<NL * (PRE - 1)>();
   }
   lds_ring_barrier();
   if (it0 < it1) {
@@ -320,28 +337,35 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1)))
     for (int o = 0; o < NREAD; ++o) read_op(o, stage(0), 0, 0);
   }
 
-  // K tile `it` sits in stage j: substeps 0 .. NSUB-2 read stage j (the first
-  // one also issues the DMA of tile it+STAGES-1 into the stage freed by tile
-  // it-1), then -- once this wave's DMA of tile it+1 has landed -- a barrier,
-  // then the last substep runs while reading substep 0 of tile it+1.
+  // K tile `it` sits in stage j: substeps 0 .. NSUB-2 read stage j, then --
+  // once this wave's DMA of tile it+1 has landed -- a barrier after which no
+  // wave reads stage j again, then the last substep runs while reading
+  // substep 0 of tile it+1.
+  //   SPREAD: every substep also issues its share of the DMA of tile
+  //   it+STAGES-1 into the stage of tile it-1 (free since the previous
+  //   barrier).  At the wait, the DMAs younger than tile it+1 are the STAGES-3
+  //   tiles after it and the DMA_EARLY instructions of this tile's share.
+  //   Two stages: the last substep issues the DMA of tile it+2 into stage j.
+  using std::integral_constant;
+  using DmaMode = integral_constant<int, SPREAD ? 2 : 0>;
+  using DmaLast = integral_constant<int, SPREAD ? 2 : 1>;
+  constexpr int VM_WAIT = SPREAD ? NL * (STAGES - 3) + DMA_EARLY : 0;
   int j = 0;
   for (int it = it0; it < it1; ++it) {
     const int jn = (j + 1 == STAGES) ? 0 : j + 1;
     const int jf = (j == 0) ? STAGES - 1 : j - 1;
     u32x4_t* cur = stage(j);
     u32x4_t* nxt = stage(jn);
-    u32x4_t* fill = stage(jf);
-    const TileRef t = tile_ref(it + STAGES - 1);
-    using std::integral_constant;
-    substep(integral_constant<int, 0>{}, integral_constant<int, 1>{}, std::true_type{}, cur, t, fill);
+    u32x4_t* fill = SPREAD ? stage(jf) : cur;
+    const TileRef t = tile_ref(it + (SPREAD ? STAGES - 1 : STAGES));
+    substep(integral_constant<int, 0>{}, integral_constant<int, 1>{}, DmaMode{}, cur, t, fill);
     if constexpr (NSUB == 4) {
-      substep(integral_constant<int, 1>{}, integral_constant<int, 2>{}, std::false_type{}, cur, t, fill);
-      substep(integral_constant<int, 2>{}, integral_constant<int, 3>{}, std::false_type{}, cur, t, fill);
+      substep(integral_constant<int, 1>{}, integral_constant<int, 2>{}, DmaMode{}, cur, t, fill);
+      substep(integral_constant<int, 2>{}, integral_constant<int, 3>{}, DmaMode{}, cur, t, fill);
     }
-    wait_vmcnt<NL * (STAGES - 2)>();
+    wait_vmcnt<VM_WAIT>();
     lds_ring_barrier();
-    substep(integral_constant<int, NSUB - 1>{}, integral_constant<int, 0>{}, std::false_type{}, nxt, t,
-            fill);
+    substep(integral_constant<int, NSUB - 1>{}, integral_constant<int, 0>{}, DmaLast{}, nxt, t, fill);
     j = jn;
   }
   if constexpr (!AK || !BKC) {
