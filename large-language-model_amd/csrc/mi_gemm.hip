@@ -77,21 +77,21 @@ int current_cus() {
 
 // ---- kernel table ------------------------------------------------------------
 
-KernelFn pick_kernel(int dtype_in, int transA, int transB, int cfg, bool fast) {
+KernelFn pick_kernel(int dtype_in, int transA, int transB, int cfg, bool fast, bool ktail) {
   const int lay = (transA ? 2 : 0) | (transB ? 1 : 0);
   if (dtype_in == MI_BF16) {
     switch (lay) {
-      case 0: return pick_bf16_00(cfg, fast);
-      case 1: return pick_bf16_01(cfg, fast);
-      case 2: return pick_bf16_10(cfg, fast);
-      default: return pick_bf16_11(cfg, fast);
+      case 0: return pick_bf16_00(cfg, fast, ktail);
+      case 1: return pick_bf16_01(cfg, fast, ktail);
+      case 2: return pick_bf16_10(cfg, fast, ktail);
+      default: return pick_bf16_11(cfg, fast, ktail);
     }
   }
   switch (lay) {
-    case 0: return pick_f32_00(cfg, fast);
-    case 1: return pick_f32_01(cfg, fast);
-    case 2: return pick_f32_10(cfg, fast);
-    default: return pick_f32_11(cfg, fast);
+    case 0: return pick_f32_00(cfg, fast, ktail);
+    case 1: return pick_f32_01(cfg, fast, ktail);
+    case 2: return pick_f32_10(cfg, fast, ktail);
+    default: return pick_f32_11(cfg, fast, ktail);
   }
 }
 
@@ -281,7 +281,7 @@ int run(const Problem& P, hipStream_t stream) {
   Plan plan = make_plan(P.dtype_in, P.M, P.N, Ktot, b.batch, mode, allow_split, ws_elems,
                         current_cus(), fast);
 
-  KernelFn fn = pick_kernel(P.dtype_in, P.transA, P.transB, plan.cfg, fast);
+  KernelFn fn = pick_kernel(P.dtype_in, P.transA, P.transB, plan.cfg, fast, P.K % 64 != 0);
   if (!fn) return fail(MI_ERR_UNSUPPORTED, "no kernel for this layout / mode");
 
   Params p;

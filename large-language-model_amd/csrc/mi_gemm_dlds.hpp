@@ -4,9 +4,18 @@
 // 16 bytes land at M0 + 16*lane, so the LDS layout (and its bank swizzle) is set
 // by which global chunk each lane fetches.  No staging registers, no LDS store
 // instructions and no register transposes are involved, which frees the VGPRs
-// for a STAGES-deep ring of LDS tiles (loads run STAGES-1 K tiles ahead).
+// for a STAGES-deep ring of LDS tiles.
 //
-// LDS layouts per stage:
+// The main loop is unrolled by STAGES so every LDS address is a per-lane base
+// register plus an immediate offset, and every DMA is one buffer load whose
+// per-lane offset never changes: the K position of a tile lives in the buffer
+// descriptor (base moved to the tile, extent shrunk by the same amount, so the
+// hardware bounds check still zero-fills everything outside the matrix) and M0
+// comes from scalar registers.  With one wave per SIMD the wave must issue
+// every MFMA itself; address arithmetic between them is issue time the MFMA
+// pipe loses.
+//
+// LDS layouts (one region per operand, STAGES stage buffers per region):
 //   K-contiguous operand  [R rows][BK]  (NCH = BK/8 chunks of 16 bytes per row,
 //       chunk position XOR-swizzled by the row); MFMA fragments are ds_read_b128.
 //   row-contiguous operand [BK k-rows][R]  (R/8 chunks per k-row, chunk index
@@ -18,8 +27,7 @@
 
 namespace mig {
 
-typedef short v4i16_t __attribute__((ext_vector_type(4)));
-typedef __attribute__((address_space(3))) v4i16_t lds_v4i16_t;
+typedef __attribute__((address_space(3))) u32x4_t lds_u32x4_t;
 
 #define MIG_LDS_PTR(p) ((__attribute__((address_space(3))) void*)(p))
 
@@ -57,84 +65,131 @@ __device__ __forceinline__ int kc_swz(int r, int c) {
 // groups.
 __device__ __forceinline__ int mc_swz(int kr, int q) { return q ^ ((kr & 3) << 2); }
 
-// One operand of the direct-to-LDS pipeline.  R: tile rows (M or N extent),
-// BK: K extent of a stage, KC: K-contiguous in memory.
-template <int R, int BK, bool KC>
-struct DldsOperand {
-  static constexpr int NCH = BK / 8;                         // KC: 16-byte chunks per row
-  static constexpr int BYTES = R * BK * 2;                   // one stage of this operand
-  static constexpr int NBLK = BYTES / 1024;                  // 1 KB DMA blocks per stage
-  static constexpr int NU = NBLK / 4;                        // DMA instructions per wave
-  static_assert(NBLK % 4 == 0, "tile must split into whole DMA blocks per wave");
-  uint32_t voff[NU];   // per unit: byte offset at k = 0 (>= 2^31 when outside the rows)
-  int kch[NU];         // KC: element K offset of the unit's chunk (for the K-tail mask)
-  int ldb;
+__device__ __forceinline__ uint32_t lds_addr(const void* p) {
+  return (uint32_t)(uintptr_t)MIG_LDS_PTR(p);
+}
 
-  __device__ __forceinline__ void init(int64_t ld, int rows, int row0) {
+// Buffer descriptor from values the caller keeps in scalar registers.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t scalar_rsrc(const void* base, uint32_t ext) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)ext, kBufFlags);
+}
+
+template <int I>
+using ic = std::integral_constant<int, I>;
+
+template <int N, int I = 0, typename F>
+__device__ __forceinline__ void static_for(F&& f) {
+  if constexpr (I < N) {
+    f(ic<I>{});
+    static_for<N, I + 1>(f);
+  }
+}
+
+// One operand of the direct-to-LDS pipeline.  R: tile rows (M or N extent),
+// BK: K extent of a stage, KC: K-contiguous in memory, WT: rows of the wave
+// tile (fragments of 32 rows each).
+template <int R, int BK, bool KC, int STAGES, int WT>
+struct DldsOperand {
+  static constexpr int NCH = BK / 8;                  // KC: 16-byte chunks per row
+  static constexpr int BYTES = R * BK * 2;            // one stage of this operand
+  static constexpr int NBLK = BYTES / 1024;           // 1 KB DMA blocks per stage
+  static constexpr int NU = NBLK / 4;                 // DMA instructions per wave
+  static constexpr int NSUB = BK / 16;
+  static constexpr int NF = WT / 32;                  // fragments per wave
+  static constexpr int NRB = KC ? 2 * NSUB : NF;      // read base registers
+  static_assert(NBLK % 4 == 0, "tile must split into whole DMA blocks per wave");
+  // largest immediate offset added to a read base must fit the 16-bit DS offset
+  static constexpr int MAX_IMM = KC ? ((NF - 1) / 2) * 64 * BK * 2 + (STAGES - 1) * BYTES
+                                    : (16 * (NSUB - 1) + 4) * R * 2 + (STAGES - 1) * BYTES;
+  static_assert(MAX_IMM < 65536, "LDS read offsets exceed the DS immediate");
+
+  uint32_t voff[NU];  // byte offset of unit u from the tile's first K (kBufOOB: row outside)
+  int klim[NU];       // KC: the unit's chunk is inside the K extent while k0 < klim[u]
+  uint32_t rb[NRB];   // LDS address of fragment reads, stage 0
+  uint32_t dma;       // wave-uniform LDS address of this wave's first DMA block, stage 0
+
+  // DMA offsets.  ld: leading dimension (elements), rows: M or N extent, row0:
+  // first tile row, kseg: K extent of a segment.
+  __device__ __forceinline__ void init_dma(int64_t ld, int rows, int row0, int kseg) {
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    ldb = (int)ld * 2;
+    const int ldb = (int)ld * 2;
 #pragma unroll
     for (int u = 0; u < NU; ++u) {
       const int b = wave * NU + u;
       if constexpr (KC) {
         const int row = b * (64 / NCH) + lane / NCH;
         const int c = kc_swz<NCH>(row, lane % NCH);
-        kch[u] = c * 8;
-        voff[u] = (uint32_t)((row0 + row) * ldb + c * 16);
+        voff[u] = (uint32_t)((row0 + row) * ldb + c * 16);  // rows >= M lie past the extent
+        klim[u] = kseg - c * 8;
       } else {
         constexpr int CPR = R / 8;  // chunks per k-row
         const int kr = b * (64 / CPR) + lane / CPR;
         const int q = mc_swz(kr, lane % CPR);
         const int grow = row0 + q * 8;
         voff[u] = grow < rows ? (uint32_t)(kr * ldb + grow * 2) : kBufOOB;
-        kch[u] = 0;
+        klim[u] = 0;
       }
     }
   }
 
-  // Issue DMA unit u of K tile k0 into stage memory `dst` (this operand's region).
-  // live = false: an out-of-range no-op (still counted by vmcnt).
-  __device__ __forceinline__ void load(int u, __amdgpu_buffer_rsrc_t rs, int k0, int kseg, bool live,
-                                       u32x4_t* dst) {
-    const int wave = threadIdx.x >> 6;
-    uint32_t vo;
-    if constexpr (KC) {
-      const uint32_t mask = (live && kch[u] + k0 < kseg) ? 0u : kBufOOB;
-      vo = (voff[u] + (uint32_t)(k0 * 2)) | mask;
-    } else {
-      const uint32_t mask = live ? 0u : kBufOOB;
-      vo = (voff[u] + (uint32_t)(k0 * ldb)) | mask;
-    }
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, MIG_LDS_PTR(dst + (wave * NU + u) * 64), 16, (int)vo,
-                                             0, 0, 0);
-  }
-
-  // MFMA fragment: rows r0..r0+31 (lane & 31), K substep s (16 K), as 8 bf16.
-  __device__ __forceinline__ u32x4_t frag(const u32x4_t* src, int r0, int s) const {
+  // LDS addresses.  region: LDS address of this operand's stage 0; w0: first row
+  // of the wave tile; wave_u: wave index held in a scalar register.
+  __device__ __forceinline__ void init_lds(uint32_t region, int w0, int wave_u) {
     const int lane = threadIdx.x & 63;
+    dma = region + (uint32_t)(wave_u * NU * 1024);
     if constexpr (KC) {
-      const int r = r0 + (lane & 31);
-      const int c = 2 * s + (lane >> 5);
-      return src[r * NCH + kc_swz<NCH>(r, c)];
+#pragma unroll
+      for (int s = 0; s < NSUB; ++s)
+#pragma unroll
+        for (int par = 0; par < 2; ++par) {
+          const int r = w0 + 32 * par + (lane & 31);
+          const int c = 2 * s + (lane >> 5);
+          rb[2 * s + par] = region + (uint32_t)(r * (BK * 2) + 16 * kc_swz<NCH>(r, c));
+        }
     } else {
       const int g = lane >> 4, j = lane & 15;
-      const int col = r0 + (g & 1) * 16 + 4 * (j & 3);
-      const int q = col >> 3, sub = (col & 7) * 2;
-      const char* base = (const char*)src;
-      u32x4_t out;
+#pragma unroll
+      for (int f = 0; f < NF; ++f) {
+        const int col = w0 + 32 * f + (g & 1) * 16 + 4 * (j & 3);
+        const int q = col >> 3, sub = (col & 7) * 2;
+        const int krb = 8 * (g >> 1) + (j >> 2);
+        rb[f] = region + (uint32_t)(krb * (R * 2) + 16 * mc_swz(krb, q) + sub);
+      }
+    }
+  }
+
+  // DMA unit u of the K tile at element offset k0 (descriptor `rs` already
+  // positioned at that tile) into stage J of the region whose wave base is `dst`.
+  template <int J, bool KTAIL>
+  __device__ __forceinline__ void load(int u, __amdgpu_buffer_rsrc_t rs, int k0, uint32_t dst) const {
+    uint32_t vo = voff[u];
+    if constexpr (KC && KTAIL) vo = (k0 < klim[u]) ? vo : kBufOOB;
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(
+        rs, (__attribute__((address_space(3))) void*)(uintptr_t)(dst + (uint32_t)(J * BYTES + u * 1024)),
+        16, (int)vo, 0, 0, 0);
+  }
+
+  // MFMA fragment f (rows w0+32f .. +31 of the wave tile), K substep S of stage J,
+  // as 8 bf16 per lane.  In a K-contiguous tile fragments f and f+2 share the
+  // swizzle, 64 rows apart; a row-contiguous tile steps 16 k-rows per substep.
+  template <int S, int J>
+  __device__ __forceinline__ u32x4_t frag(int f) const {
+    if constexpr (KC) {
+      const uint32_t a = rb[2 * S + (f & 1)] + (uint32_t)((f >> 1) * 64 * BK * 2 + J * BYTES);
+      return *(const lds_u32x4_t*)(uintptr_t)a;
+    } else {
+      u32x4_t out = {0u, 0u, 0u, 0u};
 #pragma unroll
       for (int t = 0; t < 2; ++t) {
-        const int kr = 16 * s + 8 * (g >> 1) + 4 * t + (j >> 2);
-        const char* a = base + kr * (R * 2) + 16 * mc_swz(kr, q) + sub;
         u32x2_t w = {0u, 0u};
-        (void)a;
 #if defined(__HIP_DEVICE_COMPILE__)
         // Issued as inline asm: the compiler makes the transpose-read builtin wait
         // for every LDS-DMA load in flight (vmcnt(0)), which would drain the ring.
         // The result is pending until the substep-start lgkmcnt(0) wait that
         // precedes its first use (see substep()).
-        const uint32_t la = (uint32_t)(uintptr_t)((__attribute__((address_space(3))) const char*)a);
-        asm volatile("ds_read_b64_tr_b16 %0, %1" : "=v"(w) : "v"(la));
+        asm volatile("ds_read_b64_tr_b16 %0, %1 offset:%2"
+                     : "=v"(w)
+                     : "v"(rb[f]), "i"((16 * S + 4 * t) * R * 2 + J * BYTES));
 #endif
         out[2 * t] = w[0];
         out[2 * t + 1] = w[1];
@@ -142,11 +197,12 @@ struct DldsOperand {
       return out;
     }
   }
-  static constexpr int READS_PER_FRAG = KC ? 1 : 2;
 };
 
 // bf16 GEMM, 4 waves (2 x 2), wave tile (BM/2) x (BN/2) of 32x32x16 MFMAs.
-template <int BM, int BN, int BK, int STAGES, bool AK, bool BKC, int MODE>
+// KTAIL: the K segment length is not a multiple of BK (K-contiguous operands
+// then mask the chunks past the segment end).
+template <int BM, int BN, int BK, int STAGES, bool AK, bool BKC, int MODE, bool KTAIL>
 __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1)))
     gemm_dlds_kernel(Params p) {
   constexpr int WGM = 2, WGN = 2;
@@ -157,20 +213,20 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1)))
   constexpr int NSUB = BK / 16;
   static_assert(MODE != MODE_PROLOGUE, "the SiLU-gate prologue needs register staging");
   static_assert(NSUB == 2 || NSUB == 4, "BK must be 32 or 64");
-  static_assert(STAGES >= 2 && STAGES <= 5, "2..5 stages");
+  static_assert(STAGES >= 2 && STAGES <= 4, "2..4 stages");
   static_assert(TN % 2 == 0, "epilogue stages 64-column halves");
-  using OpA = DldsOperand<BM, BK, AK>;
-  using OpB = DldsOperand<BN, BK, BKC>;
-  constexpr int A_OFF = 0;                                  // in 16-byte units
-  constexpr int B_OFF = OpA::BYTES / 16;
-  constexpr int B2_OFF = B_OFF + OpB::BYTES / 16;
-  constexpr int STAGE_UNITS = (OpA::BYTES + OpB::BYTES * (DUAL ? 2 : 1)) / 16;
-  constexpr int NL = OpA::NU + OpB::NU * (DUAL ? 2 : 1);   // DMA instructions per wave per tile
+  using OpA = DldsOperand<BM, BK, AK, STAGES, WTM>;
+  using OpB = DldsOperand<BN, BK, BKC, STAGES, WTN>;
+  constexpr int A_REG = 0;                                   // LDS regions (bytes)
+  constexpr int B_REG = A_REG + STAGES * OpA::BYTES;
+  constexpr int B2_REG = B_REG + STAGES * OpB::BYTES;
+  constexpr int LDS_BYTES = B2_REG + (DUAL ? STAGES * OpB::BYTES : 0);
+  constexpr int NL = OpA::NU + OpB::NU * (DUAL ? 2 : 1);    // DMA instructions per wave per tile
   static_assert(NL * STAGES < 64, "vmcnt range");
-  static_assert(STAGES * STAGE_UNITS * 16 <= 160 * 1024, "LDS ring exceeds 160 KB");
+  static_assert(LDS_BYTES <= 160 * 1024, "LDS ring exceeds 160 KB");
 
-  __shared__ u32x4_t smem[STAGES][STAGE_UNITS];
-  auto stage = [&](int j) -> u32x4_t* { return &smem[j][0]; };
+  __shared__ __attribute__((aligned(16))) char smem[LDS_BYTES];
+  const uint32_t lds0 = lds_addr(smem);
 
   const int nblocks = gridDim.x;
   const TileCoord tc = map_tile(blockIdx.x, nblocks, p.tiles_m, p.tiles_n, p.splits);
@@ -186,6 +242,7 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1)))
   const void* Rz = p.R ? (const char*)p.R + ((int64_t)zo * p.rO + (int64_t)zi * p.rI) * (p.r_bf16 ? 2 : 4)
                        : nullptr;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int wave_u = uniform(wave);
   const int wm = wave / WGN, wn = wave % WGN;
 
   if (p.causal == CAUSAL_OUT_LOWER && n0 > m0 + BM - 1) {
@@ -211,7 +268,8 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1)))
   } else if (p.causal == CAUSAL_A_UPPER) {
     klo = m0 / BK;
   }
-  const int per_seg = khi > klo ? khi - klo : 0;
+  klo = uniform(klo);
+  const int per_seg = uniform(khi > klo ? khi - klo : 0);
   const int total = per_seg * p.nseg;
   const int it0 = uniform((int)((int64_t)total * tc.split / p.splits));
   const int it1 = uniform((int)((int64_t)total * (tc.split + 1) / p.splits));
@@ -226,45 +284,74 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1)))
 
   OpA oa;
   OpB ob;
-  OpB ob2;
-  oa.init(p.lda, p.M, m0);
-  ob.init(p.ldb, p.N, n0);
-  if constexpr (DUAL) ob2.init(p.ldb, p.N, n0);
+  OpB ob2;  // DUAL: LDS addresses of the second B (DMA offsets shared with ob)
+  oa.init_dma(p.lda, p.M, m0, p.K);
+  ob.init_dma(p.ldb, p.N, n0, p.K);
+  oa.init_lds(lds0 + A_REG, wm * WTM, wave_u);
+  ob.init_lds(lds0 + B_REG, wn * WTN, wave_u);
+  if constexpr (DUAL) ob2.init_lds(lds0 + B2_REG, wn * WTN, wave_u);
 
-  // DMA of K tile `it` into stage j: NL instructions, issued in slot order.
+  // Tile stream of the DMA.  Descriptors start at the tile (base + K offset,
+  // extent reduced by the same amount) and step by one K tile; crossing into
+  // the next K segment re-seats them at that segment's first tile.  A tile past
+  // it1 gets an empty extent and loads zeros.
+  const uint32_t a_step = (uint32_t)BK * (AK ? 2u : (uint32_t)p.lda * 2u);  // bytes per K tile
+  const uint32_t b_step = (uint32_t)BK * (BKC ? 2u : (uint32_t)p.ldb * 2u);
+  int d_it = it0;
+  int d_seg = uniform(per_seg > 0 ? it0 / per_seg : 0);
+  int d_kt = uniform(it0 - d_seg * per_seg);
+  const char* a_ptr = (const char*)(Ab + (int64_t)d_seg * p.segA) + (uint32_t)(klo + d_kt) * a_step;
+  const char* b_ptr = (const char*)(Bb + (int64_t)d_seg * p.segB) + (uint32_t)(klo + d_kt) * b_step;
+  const char* b2_ptr = DUAL ? (const char*)(B2b + (int64_t)d_seg * p.segB) + (uint32_t)(klo + d_kt) * b_step
+                            : nullptr;
+  uint32_t a_ext = p.extA - (uint32_t)(klo + d_kt) * a_step;
+  uint32_t b_ext = p.extB - (uint32_t)(klo + d_kt) * b_step;
   struct TileRef {
     __amdgpu_buffer_rsrc_t ra, rb, rb2;
     int k0;
-    bool live;
   };
-  auto tile_ref = [&](int it) __attribute__((always_inline)) {
+  auto next_tile = [&]() __attribute__((always_inline)) {
     TileRef t;
-    t.live = it < it1;
-    const int itc = t.live ? it : (it1 > 0 ? it1 - 1 : 0);
-    const int seg = itc / (per_seg > 0 ? per_seg : 1);
-    t.k0 = (klo + (itc - seg * per_seg)) * BK;
-    t.ra = make_rsrc(Ab + (int64_t)seg * p.segA, p.extA);
-    t.rb = make_rsrc(Bb + (int64_t)seg * p.segB, p.extB);
-    if constexpr (DUAL) t.rb2 = make_rsrc(B2b + (int64_t)seg * p.segB, p.extB);
+    const bool live = d_it < it1;
+    t.k0 = (klo + d_kt) * BK;
+    t.ra = scalar_rsrc(a_ptr, live ? a_ext : 0u);
+    t.rb = scalar_rsrc(b_ptr, live ? b_ext : 0u);
+    if constexpr (DUAL) t.rb2 = scalar_rsrc(b2_ptr, live ? b_ext : 0u);
+    ++d_it;
+    a_ptr += a_step;
+    b_ptr += b_step;
+    if constexpr (DUAL) b2_ptr += b_step;
+    a_ext -= a_step;
+    b_ext -= b_step;
+    if (++d_kt == per_seg) {  // next K segment
+      d_kt = 0;
+      a_ptr += (int64_t)p.segA * 2 - (int64_t)per_seg * a_step;
+      b_ptr += (int64_t)p.segB * 2 - (int64_t)per_seg * b_step;
+      if constexpr (DUAL) b2_ptr += (int64_t)p.segB * 2 - (int64_t)per_seg * b_step;
+      a_ext += per_seg * a_step;
+      b_ext += per_seg * b_step;
+    }
     return t;
   };
-  auto dma = [&](int o, const TileRef& t, u32x4_t* st) __attribute__((always_inline)) {
-    if (o < OpA::NU) oa.load(o, t.ra, t.k0, p.K, t.live, st + A_OFF);
-    else if (o < OpA::NU + OpB::NU) ob.load(o - OpA::NU, t.rb, t.k0, p.K, t.live, st + B_OFF);
-    else ob2.load(o - OpA::NU - OpB::NU, t.rb2, t.k0, p.K, t.live, st + B2_OFF);
+  constexpr bool KTA = KTAIL && AK, KTB = KTAIL && BKC;
+  auto dma = [&](int o, const TileRef& t, auto JF_c) __attribute__((always_inline)) {
+    constexpr int JF = decltype(JF_c)::value;
+    if (o < OpA::NU) oa.template load<JF, KTA>(o, t.ra, t.k0, oa.dma);
+    else if (o < OpA::NU + OpB::NU) ob.template load<JF, KTB>(o - OpA::NU, t.rb, t.k0, ob.dma);
+    else ob.template load<JF, KTB>(o - OpA::NU - OpB::NU, t.rb2, t.k0, ob2.dma);
   };
 
   // Fragment sets: substep s uses set s & 1 (NSUB is even).
   u32x4_t fa[2][TM], fb[2][NB];
   constexpr int NREAD = TM + NB;  // fragments per substep
-  auto read_op = [&](int o, const u32x4_t* st, int s, int set) __attribute__((always_inline)) {
+  auto read_op = [&](int o, auto JR_c, auto S_c, int set) __attribute__((always_inline)) {
+    constexpr int JR = decltype(JR_c)::value, S = decltype(S_c)::value;
     if (o < TM) {
-      fa[set][o] = oa.frag(st + A_OFF, wm * WTM + o * 32, s);
+      fa[set][o] = oa.template frag<S, JR>(o);
     } else {
       const int j = o - TM;
-      const int half = DUAL ? (j / TN) : 0;
-      const int jj = DUAL ? (j % TN) : j;
-      fb[set][j] = ob.frag(st + (half ? B2_OFF : B_OFF), wn * WTN + jj * 32, s);
+      if (DUAL && j >= TN) fb[set][j] = ob2.template frag<S, JR>(j - TN);
+      else fb[set][j] = ob.template frag<S, JR>(j);
     }
   };
   auto mfma_op = [&](int set, int i, int j) __attribute__((always_inline)) {
@@ -289,13 +376,13 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1)))
   // SPREAD: DMA instructions issued before the last substep of a K tile.
   constexpr int DMA_EARLY = (NL * (NSUB - 1) * NS + TOT - 1) / TOT;
   static_assert(NREAD <= NS, "one fragment read per MFMA slot at most");
-  // S: substep index within the tile (compile time; fragment set S & 1).
-  // RS: substep whose fragments are read into the other set.  DMA: 0 none,
-  // 1 the whole DMA of tile t into stage dst spread over this substep, 2 the
-  // share of slots S*NS .. S*NS+NS-1 of a DMA spread over the K tile.
-  auto substep = [&](auto S_c, auto RS_c, auto DMA_c, const u32x4_t* rd, const TileRef& t,
-                     u32x4_t* dst) __attribute__((always_inline)) {
-    constexpr int S = decltype(S_c)::value, RS = decltype(RS_c)::value;
+  // S: substep index within the tile (fragment set S & 1).  RS / JR: substep
+  // and stage whose fragments are read into the other set.  DMA: 0 none, 1 the
+  // whole DMA of tile t spread over this substep, 2 the share of slots
+  // S*NS .. S*NS+NS-1 of a DMA spread over the K tile.  JF: DMA stage.
+  auto substep = [&](auto S_c, auto RS_c, auto JR_c, auto DMA_c, auto JF_c, const TileRef& t)
+                     __attribute__((always_inline)) {
+    constexpr int S = decltype(S_c)::value;
     constexpr int DMA = decltype(DMA_c)::value;
     constexpr int set = S & 1;
     if constexpr (!AK || !BKC) {
@@ -307,14 +394,14 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1)))
 #pragma unroll
     for (int q = 0; q < NS; ++q) {
       mfma_op(set, q / NB, q % NB);
-      if (q < NREAD) read_op(q, rd, RS, set ^ 1);
+      if (q < NREAD) read_op(q, JR_c, RS_c, set ^ 1);
       if constexpr (DMA == 1) {
 #pragma unroll
-        for (int o = (q * NL + NS - 1) / NS; o < ((q + 1) * NL + NS - 1) / NS; ++o) dma(o, t, dst);
+        for (int o = (q * NL + NS - 1) / NS; o < ((q + 1) * NL + NS - 1) / NS; ++o) dma(o, t, JF_c);
       } else if constexpr (DMA == 2) {
         const int g = S * NS + q;
 #pragma unroll
-        for (int o = (g * NL + TOT - 1) / TOT; o < ((g + 1) * NL + TOT - 1) / TOT; ++o) dma(o, t, dst);
+        for (int o = (g * NL + TOT - 1) / TOT; o < ((g + 1) * NL + TOT - 1) / TOT; ++o) dma(o, t, JF_c);
       }
       __builtin_amdgcn_sched_barrier(0);
     }
@@ -323,51 +410,49 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1)))
   // Prologue: K tiles it0 .. it0+PRE-1 into stages 0 .. PRE-1.
   constexpr int PRE = SPREAD ? STAGES - 1 : STAGES;
   if (it0 < it1) {
+    static_for<PRE>([&](auto J_c) __attribute__((always_inline)) {
+      const TileRef t = next_tile();
 #pragma unroll
-    for (int j = 0; j < PRE; ++j) {
-      const TileRef t = tile_ref(it0 + j);
-#pragma unroll
-      for (int o = 0; o < NL; ++o) dma(o, t, stage(j));
-    }
+      for (int o = 0; o < NL; ++o) dma(o, t, J_c);
+    });
     wait_vmcnt<NL * (PRE - 1)>();
   }
   lds_ring_barrier();
   if (it0 < it1) {
 #pragma unroll
-    for (int o = 0; o < NREAD; ++o) read_op(o, stage(0), 0, 0);
+    for (int o = 0; o < NREAD; ++o) read_op(o, ic<0>{}, ic<0>{}, 0);
   }
 
-  // K tile `it` sits in stage j: substeps 0 .. NSUB-2 read stage j, then --
-  // once this wave's DMA of tile it+1 has landed -- a barrier after which no
-  // wave reads stage j again, then the last substep runs while reading
-  // substep 0 of tile it+1.
+  // K tile `it` sits in stage J = (it - it0) mod STAGES: substeps 0 .. NSUB-2
+  // read stage J, then -- once this wave's DMA of tile it+1 has landed -- a
+  // barrier after which no wave reads stage J again, then the last substep runs
+  // while reading substep 0 of tile it+1.
   //   SPREAD: every substep also issues its share of the DMA of tile
   //   it+STAGES-1 into the stage of tile it-1 (free since the previous
   //   barrier).  At the wait, the DMAs younger than tile it+1 are the STAGES-3
   //   tiles after it and the DMA_EARLY instructions of this tile's share.
-  //   Two stages: the last substep issues the DMA of tile it+2 into stage j.
-  using std::integral_constant;
-  using DmaMode = integral_constant<int, SPREAD ? 2 : 0>;
-  using DmaLast = integral_constant<int, SPREAD ? 2 : 1>;
+  //   Two stages: the last substep issues the DMA of tile it+2 into stage J.
+  // The loop runs in whole rounds of STAGES tiles; tiles past it1 are all-zero
+  // (empty descriptors) and add nothing.
+  using DmaMode = ic<SPREAD ? 2 : 0>;
+  using DmaLast = ic<SPREAD ? 2 : 1>;
   constexpr int VM_WAIT = SPREAD ? NL * (STAGES - 3) + DMA_EARLY : 0;
-  int j = 0;
-  for (int it = it0; it < it1; ++it) {
-    const int jn = (j + 1 == STAGES) ? 0 : j + 1;
-    const int jf = (j == 0) ? STAGES - 1 : j - 1;
-    u32x4_t* cur = stage(j);
-    u32x4_t* nxt = stage(jn);
-    u32x4_t* fill = SPREAD ? stage(jf) : cur;
-    const TileRef t = tile_ref(it + (SPREAD ? STAGES - 1 : STAGES));
-    substep(integral_constant<int, 0>{}, integral_constant<int, 1>{}, DmaMode{}, cur, t, fill);
+  auto iteration = [&](auto J_c) __attribute__((always_inline)) {
+    constexpr int J = decltype(J_c)::value;
+    constexpr int JN = (J + 1) % STAGES;
+    constexpr int JF = SPREAD ? (J + STAGES - 1) % STAGES : J;
+    const TileRef t = next_tile();
+    substep(ic<0>{}, ic<1>{}, ic<J>{}, DmaMode{}, ic<JF>{}, t);
     if constexpr (NSUB == 4) {
-      substep(integral_constant<int, 1>{}, integral_constant<int, 2>{}, DmaMode{}, cur, t, fill);
-      substep(integral_constant<int, 2>{}, integral_constant<int, 3>{}, DmaMode{}, cur, t, fill);
+      substep(ic<1>{}, ic<2>{}, ic<J>{}, DmaMode{}, ic<JF>{}, t);
+      substep(ic<2>{}, ic<3>{}, ic<J>{}, DmaMode{}, ic<JF>{}, t);
     }
     wait_vmcnt<VM_WAIT>();
     lds_ring_barrier();
-    substep(integral_constant<int, NSUB - 1>{}, integral_constant<int, 0>{}, DmaLast{}, nxt, t, fill);
-    j = jn;
-  }
+    substep(ic<NSUB - 1>{}, ic<0>{}, ic<JN>{}, DmaLast{}, ic<JF>{}, t);
+  };
+  for (int it = it0; it < it1; it += STAGES) static_for<STAGES>(iteration);
+
   if constexpr (!AK || !BKC) {
     // The last substep issued transpose reads (asm) for a K tile that does not
     // exist.  Their registers count as dead to the compiler while the reads are
@@ -388,8 +473,8 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1)))
   // to 68 floats) and walks them row-major: coalesced C accesses, one rolled
   // copy of the epilogue.
   constexpr int PITCH = 68;
-  static_assert(4 * 32 * PITCH * 4 <= STAGES * STAGE_UNITS * 16, "epilogue staging fits the ring");
-  float* stg = reinterpret_cast<float*>(&smem[0][0]) + wave * (32 * PITCH);
+  static_assert(4 * 32 * PITCH * 4 <= LDS_BYTES, "epilogue staging fits the ring");
+  float* stg = reinterpret_cast<float*>(smem) + wave * (32 * PITCH);
   float* W = (p.splits > 1) ? p.ws + ((int64_t)tc.z * p.splits + tc.split) * (int64_t)p.M * p.N
                             : nullptr;
   const int lrow = lane & 31, lhalf = lane >> 5;

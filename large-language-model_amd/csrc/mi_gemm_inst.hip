@@ -17,6 +17,8 @@ typedef __bf16 elem_t;
 typedef float elem_t;
 #define MI_DTN f32
 #endif
+// ktail: the K extent of a segment is not a multiple of 64 (bf16 direct-to-LDS
+// kernels then mask K-contiguous chunks past the end); ignored for fp32.
 
 #ifndef MI_DLDS_BK
 #define MI_DLDS_BK 64
@@ -28,7 +30,7 @@ typedef float elem_t;
 #define MI_CAT5(a, b, c, d, e) a##b##c##d##e
 #define MI_PICK_NAME(dt, ta, tb) MI_CAT5(pick_, dt, _, ta, tb)
 
-KernelFn MI_PICK_NAME(MI_DTN, MI_TA, MI_TB)(int cfg, bool fast) {
+KernelFn MI_PICK_NAME(MI_DTN, MI_TA, MI_TB)(int cfg, bool fast, bool ktail) {
   constexpr bool AK = (MI_TA == 0);  // A is K-contiguous when not transposed
   constexpr bool BK = (MI_TB == 1);  // B is K-contiguous when transposed
 #if MI_DT_BF16
@@ -38,11 +40,21 @@ KernelFn MI_PICK_NAME(MI_DTN, MI_TA, MI_TB)(int cfg, bool fast) {
 #endif
   if (fast) {
 #if MI_DT_BF16
-    // bf16: direct-to-LDS pipeline (K tile MI_DLDS_BK, MI_DLDS_STAGES-deep LDS ring)
+    // bf16: direct-to-LDS pipeline (K tile MI_DLDS_BK, MI_DLDS_STAGES-deep LDS ring).
+    // The K-tail variants exist only where an operand is K-contiguous.
+    constexpr bool HAS_KC = AK || BK;
+    if (HAS_KC && ktail) {
+      switch (cfg) {
+        case CFG_L: return gemm_dlds_kernel<LM, LN, MI_DLDS_BK, MI_DLDS_STAGES, AK, BK, MODE_PLAIN, HAS_KC>;
+        case CFG_S: return gemm_dlds_kernel<SM, SN, 32, 4, AK, BK, MODE_PLAIN, HAS_KC>;
+        case CFG_DUAL: return gemm_dlds_kernel<DM, DN, 32, 4, AK, BK, MODE_DUAL, HAS_KC>;
+        default: break;
+      }
+    }
     switch (cfg) {
-      case CFG_L: return gemm_dlds_kernel<LM, LN, MI_DLDS_BK, MI_DLDS_STAGES, AK, BK, MODE_PLAIN>;
-      case CFG_S: return gemm_dlds_kernel<SM, SN, 32, 4, AK, BK, MODE_PLAIN>;
-      case CFG_DUAL: return gemm_dlds_kernel<DM, DN, 32, 4, AK, BK, MODE_DUAL>;
+      case CFG_L: return gemm_dlds_kernel<LM, LN, MI_DLDS_BK, MI_DLDS_STAGES, AK, BK, MODE_PLAIN, false>;
+      case CFG_S: return gemm_dlds_kernel<SM, SN, 32, 4, AK, BK, MODE_PLAIN, false>;
+      case CFG_DUAL: return gemm_dlds_kernel<DM, DN, 32, 4, AK, BK, MODE_DUAL, false>;
       case CFG_PRO:
         if constexpr (AK) return gemm_kernel<elem_t, PM, PN, 2, 2, AK, BK, MODE_PROLOGUE, true>;
         return nullptr;
