@@ -77,21 +77,22 @@ int current_cus() {
 
 // ---- kernel table ------------------------------------------------------------
 
-KernelFn pick_kernel(int dtype_in, int transA, int transB, int cfg, bool fast, bool ktail) {
+KernelFn pick_kernel(int dtype_in, int transA, int transB, int cfg, bool fast, bool ktail,
+                     bool fast_epi) {
   const int lay = (transA ? 2 : 0) | (transB ? 1 : 0);
   if (dtype_in == MI_BF16) {
     switch (lay) {
-      case 0: return pick_bf16_00(cfg, fast, ktail);
-      case 1: return pick_bf16_01(cfg, fast, ktail);
-      case 2: return pick_bf16_10(cfg, fast, ktail);
-      default: return pick_bf16_11(cfg, fast, ktail);
+      case 0: return pick_bf16_00(cfg, fast, ktail, fast_epi);
+      case 1: return pick_bf16_01(cfg, fast, ktail, fast_epi);
+      case 2: return pick_bf16_10(cfg, fast, ktail, fast_epi);
+      default: return pick_bf16_11(cfg, fast, ktail, fast_epi);
     }
   }
   switch (lay) {
-    case 0: return pick_f32_00(cfg, fast, ktail);
-    case 1: return pick_f32_01(cfg, fast, ktail);
-    case 2: return pick_f32_10(cfg, fast, ktail);
-    default: return pick_f32_11(cfg, fast, ktail);
+    case 0: return pick_f32_00(cfg, fast, ktail, fast_epi);
+    case 1: return pick_f32_01(cfg, fast, ktail, fast_epi);
+    case 2: return pick_f32_10(cfg, fast, ktail, fast_epi);
+    default: return pick_f32_11(cfg, fast, ktail, fast_epi);
   }
 }
 
@@ -281,7 +282,10 @@ int run(const Problem& P, hipStream_t stream) {
   Plan plan = make_plan(P.dtype_in, P.M, P.N, Ktot, b.batch, mode, allow_split, ws_elems,
                         current_cus(), fast);
 
-  KernelFn fn = pick_kernel(P.dtype_in, P.transA, P.transB, plan.cfg, fast, P.K % 64 != 0);
+  const CfgShape ts = shape_of(P.dtype_in, plan.cfg);
+  const bool fast_epi = plan.splits == 1 && !P.ep.bias && !P.ep.residual && cvec &&
+                        b.causal != MI_CAUSAL_OUT_LOWER && P.M % ts.bm == 0 && P.N % ts.bn == 0;
+  KernelFn fn = pick_kernel(P.dtype_in, P.transA, P.transB, plan.cfg, fast, P.K % 64 != 0, fast_epi);
   if (!fn) return fail(MI_ERR_UNSUPPORTED, "no kernel for this layout / mode");
 
   Params p;

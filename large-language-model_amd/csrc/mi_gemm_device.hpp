@@ -69,12 +69,17 @@ __device__ __forceinline__ float bf16_bits_to_f32(uint32_t h) {
   return __uint_as_float(h << 16);
 }
 
-__device__ __forceinline__ uint32_t f32_to_bf16_rne(float f) {
-  uint32_t b = __float_as_uint(f);
-  if ((b & 0x7fffffffu) > 0x7f800000u) return (b >> 16) | 0x40u;  // quiet NaN
-  b += 0x7fffu + ((b >> 16) & 1u);
-  return b >> 16;
+typedef float f32x2_t __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+
+// Two floats to packed bf16 (lo in bits 15:0): one v_cvt_pk_bf16_f32, which
+// rounds to nearest even and keeps NaN a NaN.
+__device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
+  const f32x2_t v = {lo, hi};
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf16x2_t));
 }
+
+__device__ __forceinline__ uint32_t f32_to_bf16_rne(float f) { return pack_bf16x2(f, 0.0f) & 0xffffu; }
 
 __device__ __forceinline__ float silu_f(float x) { return x / (1.0f + __expf(-x)); }
 
@@ -149,7 +154,7 @@ __device__ __forceinline__ u32x4_t swiglu_chunk(u32x4_t g, u32x4_t u) {
     for (int j = 0; j < 4; ++j) {
       const float g0 = bf16_bits_to_f32(g[j] & 0xffffu), g1 = bf16_bits_to_f32(g[j] >> 16);
       const float u0 = bf16_bits_to_f32(u[j] & 0xffffu), u1 = bf16_bits_to_f32(u[j] >> 16);
-      o[j] = f32_to_bf16_rne(silu_f(g0) * u0) | (f32_to_bf16_rne(silu_f(g1) * u1) << 16);
+      o[j] = pack_bf16x2(silu_f(g0) * u0, silu_f(g1) * u1);
     }
   }
   return o;
@@ -423,8 +428,8 @@ __device__ __forceinline__ void epilogue4(const Params& p, void* Cz, const void*
   if (full) {
     if (p.c_bf16) {
       u32x2_t o;
-      o[0] = f32_to_bf16_rne(v[0]) | (f32_to_bf16_rne(v[1]) << 16);
-      o[1] = f32_to_bf16_rne(v[2]) | (f32_to_bf16_rne(v[3]) << 16);
+      o[0] = pack_bf16x2(v[0], v[1]);
+      o[1] = pack_bf16x2(v[2], v[3]);
       *(u32x2_t*)((uint16_t*)Cz + ci) = o;
     } else {
       f32x4_t o = {v[0], v[1], v[2], v[3]};

@@ -199,12 +199,19 @@ struct DldsOperand {
   }
 };
 
+// Kernel variants (VAR bits): the K segment length is not a multiple of BK
+// (K-contiguous operands then mask the chunks past the segment end), and the
+// problem takes the direct epilogue (every tile full, epilogue alpha / SiLU
+// gate, beta*C and the output conversion only, no split-K).  One kernel holding
+// both epilogues would need the accumulators in two places at once.
+enum { DLDS_KTAIL = 1, DLDS_FAST_EPI = 2 };
+
 // bf16 GEMM, 4 waves (2 x 2), wave tile (BM/2) x (BN/2) of 32x32x16 MFMAs.
-// KTAIL: the K segment length is not a multiple of BK (K-contiguous operands
-// then mask the chunks past the segment end).
-template <int BM, int BN, int BK, int STAGES, bool AK, bool BKC, int MODE, bool KTAIL>
+template <int BM, int BN, int BK, int STAGES, bool AK, bool BKC, int MODE, int VAR>
 __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1)))
     gemm_dlds_kernel(Params p) {
+  constexpr bool KTAIL = (VAR & DLDS_KTAIL) != 0;
+  constexpr bool FAST_EPI = (VAR & DLDS_FAST_EPI) != 0;
   constexpr int WGM = 2, WGN = 2;
   constexpr int WTM = BM / WGM, WTN = BN / WGN;
   constexpr int TM = WTM / 32, TN = WTN / 32;
@@ -464,63 +471,129 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1)))
 #pragma unroll
     for (int jj = 0; jj < NB; ++jj) asm volatile("" ::"v"(fb[0][jj]));
   }
-  wait_vmcnt<0>();
-  __syncthreads();  // the epilogue reuses LDS
+  wait_vmcnt<0>();  // DMAs of the all-zero tiles past it1
 
-  // Epilogue: acc[i][j][4q + e] holds C[m][n + e] with
+  // acc[i][j][4q + e] holds C[m][n + e] with
   //   m = m0 + wm*WTM + i*32 + (lane & 31),  n = n0 + wn*WTN + j*32 + 8q + 4*(lane >> 5).
-  // Each pass stages 32 rows x 64 columns of one wave through LDS (rows padded
-  // to 68 floats) and walks them row-major: coalesced C accesses, one rolled
-  // copy of the epilogue.
-  constexpr int PITCH = 68;
+  auto value = [&](int i, int j, int q, int e) __attribute__((always_inline)) {
+    if constexpr (DUAL)
+      return silu_f(p.alpha * acc[i][j][4 * q + e]) * (p.alpha * acc[i][j + TN][4 * q + e]);
+    else
+      return p.alpha * acc[i][j][4 * q + e];
+  };
+  if constexpr (FAST_EPI) {
+    // Full tiles, epilogue alpha (SiLU gate), beta*C and the output conversion.
+    // Each 32x32 MFMA block goes through a wave-private LDS patch (rows padded
+    // by 4 floats) and back out row-major, so a store instruction writes 8 rows
+    // of 32 contiguous columns (64 or 128 bytes per row) instead of 32 rows of
+    // 16 bytes.  One barrier first: the patches reuse the ring's LDS.
+    __syncthreads();
+    constexpr int PP = 36;  // patch pitch (floats)
+    static_assert(4 * 32 * PP * 4 <= LDS_BYTES, "epilogue patches fit the ring");
+    float* patch = reinterpret_cast<float*>(smem) + wave * (32 * PP);
+    const float beta = p.beta;
+    const int r_in = lane & 31, h_in = lane >> 5;
+    const int r_out = lane >> 3, c_out = (lane & 7) * 4;  // + 8 rows per step
+    // BF: bf16 C; BETA: beta*C is added.  Both uniform, hoisted out of the tile.
+    auto store_tile = [&](auto BF_c, auto BETA_c) __attribute__((always_inline)) {
+      constexpr bool BF = decltype(BF_c)::value, BETA = decltype(BETA_c)::value;
+#pragma unroll
+      for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int j = 0; j < TN; ++j) {
+#pragma unroll
+          for (int q = 0; q < 4; ++q) {
+            f32x4_t v;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) v[e] = value(i, j, q, e);
+            *reinterpret_cast<f32x4_t*>(patch + r_in * PP + 8 * q + 4 * h_in) = v;
+          }
+          const int64_t row0 = (int64_t)(m0 + wm * WTM + i * 32 + r_out);
+          const int col = n0 + wn * WTN + j * 32 + c_out;
+#pragma unroll
+          for (int st = 0; st < 4; ++st) {
+            f32x4_t v = *reinterpret_cast<const f32x4_t*>(patch + (r_out + 8 * st) * PP + c_out);
+            const int64_t ci = (row0 + 8 * st) * p.ldc + col;
+            if constexpr (BF) {
+              u32x2_t* c = (u32x2_t*)((uint16_t*)Cz + ci);
+              if constexpr (BETA) {
+                const u32x2_t o = *c;
+                v[0] += beta * bf16_bits_to_f32(o[0] & 0xffffu);
+                v[1] += beta * bf16_bits_to_f32(o[0] >> 16);
+                v[2] += beta * bf16_bits_to_f32(o[1] & 0xffffu);
+                v[3] += beta * bf16_bits_to_f32(o[1] >> 16);
+              }
+              *c = u32x2_t{pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3])};
+            } else {
+              f32x4_t* c = (f32x4_t*)((float*)Cz + ci);
+              if constexpr (BETA) {
+                const f32x4_t old = *c;
+                v[0] += beta * old[0]; v[1] += beta * old[1];
+                v[2] += beta * old[2]; v[3] += beta * old[3];
+              }
+              *c = v;
+            }
+          }
+          __builtin_amdgcn_sched_barrier(0);
+        }
+    };
+    if (p.c_bf16) {
+      if (beta != 0.0f) store_tile(std::true_type{}, std::true_type{});
+      else store_tile(std::true_type{}, std::false_type{});
+    } else {
+      if (beta != 0.0f) store_tile(std::false_type{}, std::true_type{});
+      else store_tile(std::false_type{}, std::false_type{});
+    }
+  } else {
+
+  // General epilogue (bias, residual, causal mask, edge tiles, split-K
+  // partials): each 32-row block of the wave tile is staged through LDS (rows
+  // padded by 4 floats) and walked row-major by a rolled loop around one
+  // epilogue4.  The staging area is private to the wave, so only the first use
+  // of the ring's LDS needs every wave past its last fragment read.
+  __syncthreads();
+  constexpr int PITCH = WTN + 4;
   static_assert(4 * 32 * PITCH * 4 <= LDS_BYTES, "epilogue staging fits the ring");
   float* stg = reinterpret_cast<float*>(smem) + wave * (32 * PITCH);
   float* W = (p.splits > 1) ? p.ws + ((int64_t)tc.z * p.splits + tc.split) * (int64_t)p.M * p.N
                             : nullptr;
   const int lrow = lane & 31, lhalf = lane >> 5;
+  constexpr int C4 = WTN / 4;  // float4 groups per staged row
 #pragma unroll
   for (int i = 0; i < TM; ++i) {
 #pragma unroll
-    for (int jh = 0; jh < TN / 2; ++jh) {
+    for (int j = 0; j < TN; ++j)
 #pragma unroll
-      for (int jj = 0; jj < 2; ++jj) {
-        const int j = 2 * jh + jj;
+      for (int q = 0; q < 4; ++q) {
+        f32x4_t v;
 #pragma unroll
-        for (int q = 0; q < 4; ++q) {
-          f32x4_t v;
-#pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            if constexpr (DUAL)
-              v[e] = silu_f(p.alpha * acc[i][j][4 * q + e]) * (p.alpha * acc[i][j + TN][4 * q + e]);
-            else
-              v[e] = acc[i][j][4 * q + e];
-          }
-          *reinterpret_cast<f32x4_t*>(stg + lrow * PITCH + jj * 32 + 8 * q + 4 * lhalf) = v;
-        }
+        for (int e = 0; e < 4; ++e) v[e] = DUAL ? value(i, j, q, e) : acc[i][j][4 * q + e];
+        *reinterpret_cast<f32x4_t*>(stg + lrow * PITCH + j * 32 + 8 * q + 4 * lhalf) = v;
       }
-      __syncthreads();
-      const int mrow0 = m0 + wm * WTM + i * 32;
-      const int ncol0 = n0 + wn * WTN + jh * 64;
-#pragma unroll 2
-      for (int idx = lane; idx < 32 * 16; idx += 64) {
-        const int r = idx >> 4, c4 = idx & 15;
-        const f32x4_t sv = *reinterpret_cast<const f32x4_t*>(stg + r * PITCH + c4 * 4);
-        const int m = mrow0 + r, n = ncol0 + c4 * 4;
-        if (W) {
-          if (m < p.M) {
+    __builtin_amdgcn_sched_barrier(0);
+    const int mrow0 = m0 + wm * WTM + i * 32;
+    const int ncol0 = n0 + wn * WTN;
+#pragma unroll 1
+    for (int idx = lane; idx < 32 * C4; idx += 64) {
+      const int r = idx / C4, c4 = idx % C4;
+      const f32x4_t sv = *reinterpret_cast<const f32x4_t*>(stg + r * PITCH + c4 * 4);
+      const int m = mrow0 + r, n = ncol0 + c4 * 4;
+      if (W) {
+        // split-K partials: alpha is applied by the reduction
+        if (m < p.M) {
 #pragma unroll
-            for (int e = 0; e < 4; ++e)
-              if (n + e < p.N) W[(int64_t)m * p.N + n + e] = sv[e];
-          }
-        } else {
-          float v[4];
-#pragma unroll
-          for (int e = 0; e < 4; ++e) v[e] = DUAL ? sv[e] : p.alpha * sv[e];
-          epilogue4(p, Cz, Rz, m, n, v);
+          for (int e = 0; e < 4; ++e)
+            if (n + e < p.N) W[(int64_t)m * p.N + n + e] = sv[e];
         }
+      } else {
+        float v[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) v[e] = DUAL ? sv[e] : p.alpha * sv[e];
+        epilogue4(p, Cz, Rz, m, n, v);
       }
-      __syncthreads();
     }
+    __builtin_amdgcn_sched_barrier(0);
+  }
   }
 }
 

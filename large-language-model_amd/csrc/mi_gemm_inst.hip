@@ -18,7 +18,8 @@ typedef float elem_t;
 #define MI_DTN f32
 #endif
 // ktail: the K extent of a segment is not a multiple of 64 (bf16 direct-to-LDS
-// kernels then mask K-contiguous chunks past the end); ignored for fp32.
+// kernels then mask K-contiguous chunks past the end); fast_epi: the problem
+// qualifies for the direct epilogue.  Both are ignored for fp32.
 
 #ifndef MI_DLDS_BK
 #define MI_DLDS_BK 64
@@ -30,7 +31,21 @@ typedef float elem_t;
 #define MI_CAT5(a, b, c, d, e) a##b##c##d##e
 #define MI_PICK_NAME(dt, ta, tb) MI_CAT5(pick_, dt, _, ta, tb)
 
-KernelFn MI_PICK_NAME(MI_DTN, MI_TA, MI_TB)(int cfg, bool fast, bool ktail) {
+#if MI_DT_BF16
+// bf16 direct-to-LDS kernels of one variant (K tile MI_DLDS_BK with an
+// MI_DLDS_STAGES-deep LDS ring for 256x256; 32 / 4 stages for the others).
+template <bool AK, bool BK, int V>
+KernelFn dlds_kernel(int cfg) {
+  switch (cfg) {
+    case CFG_L: return gemm_dlds_kernel<256, 256, MI_DLDS_BK, MI_DLDS_STAGES, AK, BK, MODE_PLAIN, V>;
+    case CFG_S: return gemm_dlds_kernel<128, 128, 32, 4, AK, BK, MODE_PLAIN, V>;
+    case CFG_DUAL: return gemm_dlds_kernel<256, 128, 32, 4, AK, BK, MODE_DUAL, V>;
+    default: return nullptr;
+  }
+}
+#endif
+
+KernelFn MI_PICK_NAME(MI_DTN, MI_TA, MI_TB)(int cfg, bool fast, bool ktail, bool fast_epi) {
   constexpr bool AK = (MI_TA == 0);  // A is K-contiguous when not transposed
   constexpr bool BK = (MI_TB == 1);  // B is K-contiguous when transposed
 #if MI_DT_BF16
@@ -40,21 +55,15 @@ KernelFn MI_PICK_NAME(MI_DTN, MI_TA, MI_TB)(int cfg, bool fast, bool ktail) {
 #endif
   if (fast) {
 #if MI_DT_BF16
-    // bf16: direct-to-LDS pipeline (K tile MI_DLDS_BK, MI_DLDS_STAGES-deep LDS ring).
-    // The K-tail variants exist only where an operand is K-contiguous.
-    constexpr bool HAS_KC = AK || BK;
-    if (HAS_KC && ktail) {
-      switch (cfg) {
-        case CFG_L: return gemm_dlds_kernel<LM, LN, MI_DLDS_BK, MI_DLDS_STAGES, AK, BK, MODE_PLAIN, HAS_KC>;
-        case CFG_S: return gemm_dlds_kernel<SM, SN, 32, 4, AK, BK, MODE_PLAIN, HAS_KC>;
-        case CFG_DUAL: return gemm_dlds_kernel<DM, DN, 32, 4, AK, BK, MODE_DUAL, HAS_KC>;
-        default: break;
+    if (cfg != CFG_PRO) {
+      // K-tail variants exist only where an operand is K-contiguous; a K tail
+      // takes the general epilogue.
+      if constexpr (AK || BK) {
+        if (ktail) return dlds_kernel<AK, BK, DLDS_KTAIL>(cfg);
       }
+      return fast_epi ? dlds_kernel<AK, BK, DLDS_FAST_EPI>(cfg) : dlds_kernel<AK, BK, 0>(cfg);
     }
     switch (cfg) {
-      case CFG_L: return gemm_dlds_kernel<LM, LN, MI_DLDS_BK, MI_DLDS_STAGES, AK, BK, MODE_PLAIN, false>;
-      case CFG_S: return gemm_dlds_kernel<SM, SN, 32, 4, AK, BK, MODE_PLAIN, false>;
-      case CFG_DUAL: return gemm_dlds_kernel<DM, DN, 32, 4, AK, BK, MODE_DUAL, false>;
       case CFG_PRO:
         if constexpr (AK) return gemm_kernel<elem_t, PM, PN, 2, 2, AK, BK, MODE_PROLOGUE, true>;
         return nullptr;

@@ -105,6 +105,34 @@ def test_small_integers_bit_exact(mi, dev, oracle):
             assert np.array_equal(C.cpu().numpy(), a.astype(np.int64) @ b.astype(np.int64))
 
 
+def test_bf16_output_rounds_to_nearest_even(mi, dev, oracle):
+    """bf16 outputs whose exact fp32 values sit on rounding ties (1 + odd multiples
+    of 2^-8 and their negatives) and off them: every output bit must equal the
+    oracle's round-to-nearest-even (mo_f32_to_bf16_rne).  Tile-aligned shapes take
+    the direct epilogue, an odd shape the general one; the beta = 1 pass adds a
+    bf16 C read."""
+    import torch
+
+    deltas = np.array([1, 3, 5, 7, 2, 0.5, 1.5, -1, -3, 9, 11, 13], np.float32) * 2.0 ** -8
+    for (M, N, K), (tA, tB) in [((512, 512, 64), (0, 1)), ((512, 256, 128), (0, 0)),
+                                ((256, 512, 64), (1, 0)), ((130, 70, 40), (0, 1))]:
+        a = np.zeros((M, K), np.float32)
+        a[:, 0] = np.where(np.arange(M) % 2 == 0, 1.0, -1.0)
+        a[:, 1] = deltas[np.arange(M) % len(deltas)]
+        b = np.zeros((K, N), np.float32)
+        b[0, :] = 1.0
+        b[1, :] = np.array([1.0, 2.0, 0.5, 4.0], np.float32)[np.arange(N) % 4]
+        exact = a.astype(np.float64) @ b.astype(np.float64)  # fp32-exact sums
+        for beta in (0.0, 1.0):
+            c0 = np.zeros((M, N), np.float32) if beta == 0.0 else oracle.round_bf16(exact)
+            C = to_dev(c0, dev, True)
+            mi.gemm(to_dev(layout(a, tA), dev, True), to_dev(layout(b, tB), dev, True), C, M, N, K,
+                    transA=tA, transB=tB, beta=beta)
+            want = oracle.to_bf16((exact + beta * c0.astype(np.float64)).astype(np.float32))
+            got = C.view(torch.int16).cpu().numpy().view(np.uint16)
+            assert np.array_equal(got, want), f"{M}x{N}x{K} tA={tA} tB={tB} beta={beta}"
+
+
 def test_config1_fp32_linear_bias(mi, dev, oracle):
     """Y = X W^T + b, X [512x768], W [768x768] ~ N(0,0.02), fp32."""
     got, ref = _run(mi, dev, oracle, 512, 768, 768, 0, 1, False, seed=1, bias=True)
