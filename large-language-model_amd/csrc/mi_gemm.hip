@@ -136,16 +136,21 @@ struct Plan {
 
 int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
 
-// Pick the tile configuration and split-K factor.  Rules measured on MI355X for
-// the decoder-block shapes (TFLOP/s of 256x256 "L" vs 128x128 "S" tiles and of
-// split-K): throughput is set by a chip-wide limit (fewer active CUs run faster
-// each), so
-//   * a grid of L tiles covering most CUs runs as is, unless its last wave is
-//     at most half full and S tiles fill whole waves (8192x3072: S 764 vs L 624);
-//   * L tiles that leave half of an L tile's area empty (N or M below 256) use S;
-//   * few L tiles with a long K split K until the units fill the CUs once
-//     (2048x3072x8192: split 2 752 vs 486; 2048x2048x8192: split 4 647 vs 322),
-//     given a workspace; without one, S when it fills the CUs.
+// Tile and split choice.  Rules fitted to forced-plan sweeps of the decoder-block
+// and LM-head shapes on MI355X (TFLOP/s of bf16 256x256 "L" vs 128x128 "S" tiles, split-K
+// factor after the letter):
+//   * a grid of L tiles covering the CUs at least once runs as is (8192x2048x
+//     5632 NT: L1 1284 vs S1 831; 8192x32000x2048: L1 1019 vs S1 774), unless
+//     its last wave is at most half full and S tiles fill whole waves
+//     (8192x3072x2048: S1 977 vs L1 932);
+//   * L tiles that leave a quarter of their area empty (N or M well below a
+//     multiple of 256) use S;
+//   * bf16 below one wave of L tiles: S tiles, two workgroups per CU, without
+//     split (2048x2048x8192: S1 946 vs L1 383, L4 672, S2 754; 2048x5632x8192:
+//     S1 1017 vs L1 950), unless even S tiles leave half the CUs idle -- then K
+//     is split over S tiles, given a workspace;
+//   * fp32 (both configurations 128x128): fewer tiles than 5/8 of the CUs split
+//     K, given a workspace.
 Plan make_plan(int dtype_in, int64_t M, int64_t N, int64_t Ktot, int64_t batch, int mode,
                bool allow_split, int64_t ws_limit_elems, int cus, bool fast) {
   auto plan_for = [&](int cfg, int sp) {
@@ -160,21 +165,28 @@ Plan make_plan(int dtype_in, int64_t M, int64_t N, int64_t Ktot, int64_t batch, 
   const int64_t tilesS = cdiv(M, S.bm) * cdiv(N, S.bn) * batch;
   const double fillL = (double)(M * N * batch) / ((double)tilesL * L.bm * L.bn);
   const double fillS = (double)(M * N * batch) / ((double)tilesS * S.bm * S.bn);
-  const bool s_fills_cus = tilesS >= cus;
   if (fillL < 0.75 && fillS > fillL) return plan_for(CFG_S, 1);
-  if (tilesL * 8 >= (int64_t)cus * 5) {
+  if (tilesL >= cus) {
     const double waves = (double)tilesL / cus;
     const double frac = waves - std::floor(waves);
-    if (waves >= 1.0 && frac > 0.0 && frac <= 0.5 && s_fills_cus) return plan_for(CFG_S, 1);
+    if (frac > 0.0 && frac <= 0.5 && tilesS >= cus) return plan_for(CFG_S, 1);
     return plan_for(CFG_L, 1);
   }
-  const int kt = dtype_in == MI_BF16 ? 64 : 32;
-  if (allow_split) {
-    int sp = (int)std::min<int64_t>(cus / std::max<int64_t>(tilesL, 1), 8);
+  // split K until the units cover the CUs once; each split keeps >= 8 K tiles
+  auto split_of = [&](int64_t tiles, int kt) {
+    int sp = (int)std::min<int64_t>(cus / std::max<int64_t>(tiles, 1), 8);
     while (sp > 1 && (cdiv(Ktot, kt) < 8 * sp || (int64_t)sp * M * N * batch > ws_limit_elems)) --sp;
+    return sp;
+  };
+  if (dtype_in == MI_BF16) {
+    if (tilesS * 2 >= cus || !allow_split) return plan_for(CFG_S, 1);
+    return plan_for(CFG_S, split_of(tilesS, 32));
+  }
+  if (tilesL * 8 >= (int64_t)cus * 5) return plan_for(CFG_L, 1);
+  if (allow_split) {
+    const int sp = split_of(tilesL, 32);
     if (sp >= 2) return plan_for(CFG_L, sp);
   }
-  // few tiles either way: the smaller tile gives more parallel work
   return plan_for(tilesS > tilesL ? CFG_S : CFG_L, 1);
 }
 
@@ -282,6 +294,11 @@ int run(const Problem& P, hipStream_t stream) {
   Plan plan = make_plan(P.dtype_in, P.M, P.N, Ktot, b.batch, mode, allow_split, ws_elems,
                         current_cus(), fast);
 
+  // The planner only splits within the workspace; checked again here because
+  // an undersized workspace would take out-of-bounds partial-sum writes.
+  if (plan.splits > 1 && ((int64_t)plan.splits * P.M * P.N * b.batch > ws_elems || !allow_split))
+    return fail(MI_ERR_WORKSPACE, "split-K by %d needs %lld floats of workspace, %lld given",
+                plan.splits, (long long)plan.splits * P.M * P.N * b.batch, (long long)ws_elems);
   const CfgShape ts = shape_of(P.dtype_in, plan.cfg);
   const bool fast_epi = plan.splits == 1 && !P.ep.bias && !P.ep.residual && cvec &&
                         b.causal != MI_CAUSAL_OUT_LOWER && P.M % ts.bm == 0 && P.N % ts.bn == 0;

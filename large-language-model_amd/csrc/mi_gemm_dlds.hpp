@@ -74,6 +74,10 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t scalar_rsrc(const void* base, 
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)ext, kBufFlags);
 }
 
+#ifndef MI_DLDS_EARLY
+#define MI_DLDS_EARLY 1
+#endif
+
 template <int I>
 using ic = std::integral_constant<int, I>;
 
@@ -348,8 +352,12 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1)))
     else ob.template load<JF, KTB>(o - OpA::NU - OpB::NU, t.rb2, t.k0, ob2.dma);
   };
 
-  // Fragment sets: substep s uses set s & 1 (NSUB is even).
-  u32x4_t fa[2][TM], fb[2][NB];
+  // EARLY (two stages of four substeps): each substep has its own fragment set,
+  // so a K tile's fragments are all read by the end of its second substep and
+  // its stage is free from then on; otherwise substep s uses set s & 1.
+  constexpr bool EARLY = MI_DLDS_EARLY && STAGES == 2 && NSUB == 4;
+  constexpr int NSET = EARLY ? 4 : 2;
+  u32x4_t fa[NSET][TM], fb[NSET][NB];
   constexpr int NREAD = TM + NB;  // fragments per substep
   auto read_op = [&](int o, auto JR_c, auto S_c, int set) __attribute__((always_inline)) {
     constexpr int JR = decltype(JR_c)::value, S = decltype(S_c)::value;
@@ -414,6 +422,29 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1)))
     }
   };
 
+  // EARLY substep S computes with set S, reads set RSET (substep RS of the
+  // tile in stage JR) one fragment per slot, and issues half DPART (1 or 2; 0
+  // none) of the DMA of tile t into stage JF spread over its slots.
+  auto substep4 = [&](auto S_c, auto RSET_c, auto RS_c, auto JR_c, auto DPART_c, auto JF_c,
+                      const TileRef& t) __attribute__((always_inline)) {
+    constexpr int S = decltype(S_c)::value, RSET = decltype(RSET_c)::value;
+    constexpr int DPART = decltype(DPART_c)::value;
+    constexpr int H0 = DPART > 0 ? (DPART - 1) * NL / 2 : 0, HN = DPART > 0 ? NL / 2 : 0;
+    if constexpr (!AK || !BKC) {
+      __builtin_amdgcn_s_waitcnt(0xC07F);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+#pragma unroll
+    for (int q = 0; q < NS; ++q) {
+      mfma_op(S, q / NB, q % NB);
+      if (q < NREAD) read_op(q, JR_c, RS_c, RSET);
+#pragma unroll
+      for (int o = H0 + (q * HN + NS - 1) / NS; o < H0 + ((q + 1) * HN + NS - 1) / NS; ++o)
+        dma(o, t, JF_c);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  };
+
   // Prologue: K tiles it0 .. it0+PRE-1 into stages 0 .. PRE-1.
   constexpr int PRE = SPREAD ? STAGES - 1 : STAGES;
   if (it0 < it1) {
@@ -428,6 +459,10 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1)))
   if (it0 < it1) {
 #pragma unroll
     for (int o = 0; o < NREAD; ++o) read_op(o, ic<0>{}, ic<0>{}, 0);
+    if constexpr (EARLY) {
+#pragma unroll
+      for (int o = 0; o < NREAD; ++o) read_op(o, ic<0>{}, ic<1>{}, 1);
+    }
   }
 
   // K tile `it` sits in stage J = (it - it0) mod STAGES: substeps 0 .. NSUB-2
@@ -458,7 +493,27 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1)))
     lds_ring_barrier();
     substep(ic<NSUB - 1>{}, ic<0>{}, ic<JN>{}, DmaLast{}, ic<JF>{}, t);
   };
-  for (int it = it0; it < it1; it += STAGES) static_for<STAGES>(iteration);
+  // EARLY: substeps 0 and 1 of tile it read sets 2 and 3 (the rest of tile it);
+  // then, once this wave's DMA of tile it+1 has landed, a barrier after which
+  // no wave reads stage J; substeps 2 and 3 read sets 0 and 1 of tile it+1 and
+  // issue the DMA of tile it+2 into stage J, half each.  That DMA has substeps
+  // 0 and 1 of the next K tile to land before it is waited for.
+  auto iteration4 = [&](auto J_c) __attribute__((always_inline)) {
+    constexpr int J = decltype(J_c)::value;
+    constexpr int JN = (J + 1) % STAGES;
+    const TileRef t = next_tile();
+    substep4(ic<0>{}, ic<2>{}, ic<2>{}, ic<J>{}, ic<0>{}, ic<J>{}, t);
+    substep4(ic<1>{}, ic<3>{}, ic<3>{}, ic<J>{}, ic<0>{}, ic<J>{}, t);
+    wait_vmcnt<0>();
+    lds_ring_barrier();
+    substep4(ic<2>{}, ic<0>{}, ic<0>{}, ic<JN>{}, ic<1>{}, ic<J>{}, t);
+    substep4(ic<3>{}, ic<1>{}, ic<1>{}, ic<JN>{}, ic<2>{}, ic<J>{}, t);
+  };
+  if constexpr (EARLY) {
+    for (int it = it0; it < it1; it += STAGES) static_for<STAGES>(iteration4);
+  } else {
+    for (int it = it0; it < it1; it += STAGES) static_for<STAGES>(iteration);
+  }
 
   if constexpr (!AK || !BKC) {
     // The last substep issued transpose reads (asm) for a K tile that does not
@@ -467,9 +522,12 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1)))
     // after the wait so nothing else is placed in them meanwhile.
     __builtin_amdgcn_s_waitcnt(0xC07F);
 #pragma unroll
-    for (int i = 0; i < TM; ++i) asm volatile("" ::"v"(fa[0][i]));
+    for (int st = 0; st < (EARLY ? 2 : 1); ++st) {
 #pragma unroll
-    for (int jj = 0; jj < NB; ++jj) asm volatile("" ::"v"(fb[0][jj]));
+      for (int i = 0; i < TM; ++i) asm volatile("" ::"v"(fa[st][i]));
+#pragma unroll
+      for (int jj = 0; jj < NB; ++jj) asm volatile("" ::"v"(fb[st][jj]));
+    }
   }
   wait_vmcnt<0>();  // DMAs of the all-zero tiles past it1
 
