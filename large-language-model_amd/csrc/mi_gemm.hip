@@ -137,20 +137,24 @@ struct Plan {
 int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
 
 // Tile and split choice.  Rules fitted to forced-plan sweeps of the decoder-block
-// and LM-head shapes on MI355X (TFLOP/s of bf16 256x256 "L" vs 128x128 "S" tiles, split-K
-// factor after the letter):
+// and LM-head shapes on MI355X (TFLOP/s of bf16 256x256 "L" vs 128x128 "S" tiles,
+// split-K factor after the letter):
 //   * a grid of L tiles covering the CUs at least once runs as is (8192x2048x
-//     5632 NT: L1 1284 vs S1 831; 8192x32000x2048: L1 1019 vs S1 774), unless
+//     5632 NT: L1 1375 vs S1 1180; 8192x32000x2048: L1 1256 vs S1 978), unless
 //     its last wave is at most half full and S tiles fill whole waves
-//     (8192x3072x2048: S1 977 vs L1 932);
+//     (8192x3072x2048: S1 1063 vs L1 1016);
 //   * L tiles that leave a quarter of their area empty (N or M well below a
 //     multiple of 256) use S;
 //   * bf16 below one wave of L tiles: S tiles, two workgroups per CU, without
-//     split (2048x2048x8192: S1 946 vs L1 383, L4 672, S2 754; 2048x5632x8192:
-//     S1 1017 vs L1 950), unless even S tiles leave half the CUs idle -- then K
-//     is split over S tiles, given a workspace;
+//     split (2048x2048x8192: S1 967 vs L2 640, S2 754; 2048x3072x8192: S1 887
+//     vs L2 836).  With inputs and an fp32 beta = 1 output cold in HBM, as in
+//     a training step, S also beats L1 on 2048x5632x8192 (931-951 vs 913): the
+//     second workgroup on a CU hides the first one's C read-modify-write, which
+//     L tiles all do at once (in a hot-cache loop L1 leads, 1143 vs 1038);
+//   * when even S tiles leave half the CUs idle, K is split over S tiles, given
+//     a workspace;
 //   * fp32 (both configurations 128x128): fewer tiles than 5/8 of the CUs split
-//     K, given a workspace.
+//     K over L tiles, given a workspace.
 Plan make_plan(int dtype_in, int64_t M, int64_t N, int64_t Ktot, int64_t batch, int mode,
                bool allow_split, int64_t ws_limit_elems, int cus, bool fast) {
   auto plan_for = [&](int cfg, int sp) {

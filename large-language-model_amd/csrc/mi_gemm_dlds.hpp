@@ -422,6 +422,10 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1)))
     }
   };
 
+  // LDS instructions that read one fragment set (transpose reads take two per
+  // fragment); the lgkmcnt field holds at most 15.
+  constexpr int READ_OPS = TM * (AK ? 1 : 2) + NB * (BKC ? 1 : 2);
+  constexpr int LGKM_KEEP = READ_OPS < 15 ? READ_OPS : 15;
   // EARLY substep S computes with set S, reads set RSET (substep RS of the
   // tile in stage JR) one fragment per slot, and issues half DPART (1 or 2; 0
   // none) of the DMA of tile t into stage JF spread over its slots.
@@ -431,7 +435,9 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1)))
     constexpr int DPART = decltype(DPART_c)::value;
     constexpr int H0 = DPART > 0 ? (DPART - 1) * NL / 2 : 0, HN = DPART > 0 ? NL / 2 : 0;
     if constexpr (!AK || !BKC) {
-      __builtin_amdgcn_s_waitcnt(0xC07F);
+      // set S was read two substeps ago; the previous substep's LDS reads (one
+      // set, READ_OPS instructions) may stay in flight: LDS returns in order
+      __builtin_amdgcn_s_waitcnt(0xC07F | (LGKM_KEEP << 8));
       __builtin_amdgcn_sched_barrier(0);
     }
 #pragma unroll

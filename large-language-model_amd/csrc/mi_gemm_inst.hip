@@ -27,18 +27,28 @@ typedef float elem_t;
 #ifndef MI_DLDS_STAGES
 #define MI_DLDS_STAGES 2
 #endif
+// 128x128: a K-contiguous A (NN, NT) runs the two-stage early-read ring at
+// K tile 64; with A row-contiguous (TN, TT) the four-stage K-32 ring measured
+// faster (2048x2048x8192 TN: 866 vs 672 TFLOP/s; 8192x3072x2048 NN: 991 vs 861).
+#ifndef MI_S_BK
+#define MI_S_BK(ak) ((ak) ? 64 : 32)
+#endif
+#ifndef MI_S_STAGES
+#define MI_S_STAGES(ak) ((ak) ? 2 : 4)
+#endif
 
 #define MI_CAT5(a, b, c, d, e) a##b##c##d##e
 #define MI_PICK_NAME(dt, ta, tb) MI_CAT5(pick_, dt, _, ta, tb)
 
 #if MI_DT_BF16
-// bf16 direct-to-LDS kernels of one variant (K tile MI_DLDS_BK with an
-// MI_DLDS_STAGES-deep LDS ring for 256x256; 32 / 4 stages for the others).
+// bf16 direct-to-LDS kernels of one variant (K tile and LDS ring depth:
+// MI_DLDS_BK / MI_DLDS_STAGES for 256x256, MI_S_BK / MI_S_STAGES of the A layout for 128x128,
+// 32 / 4 for the dual-B 256x128).
 template <bool AK, bool BK, int V>
 KernelFn dlds_kernel(int cfg) {
   switch (cfg) {
     case CFG_L: return gemm_dlds_kernel<256, 256, MI_DLDS_BK, MI_DLDS_STAGES, AK, BK, MODE_PLAIN, V>;
-    case CFG_S: return gemm_dlds_kernel<128, 128, 32, 4, AK, BK, MODE_PLAIN, V>;
+    case CFG_S: return gemm_dlds_kernel<128, 128, MI_S_BK(AK), MI_S_STAGES(AK), AK, BK, MODE_PLAIN, V>;
     case CFG_DUAL: return gemm_dlds_kernel<256, 128, 32, 4, AK, BK, MODE_DUAL, V>;
     default: return nullptr;
   }
