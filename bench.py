@@ -1,6 +1,6 @@
 """Benchmark: GEMM TFLOP/s of the 1.6B decoder-block set (fwd + dX + dW, M=8192) on one MI355X.
 
-One step = the 15 GEMMs a decoder block issues at BASELINE config 3 (d_model 2048,
+One step = the 15 GEMMs a decoder block issues in benchmark configuration 3 (d_model 2048,
 GQA 16 q / 4 kv heads x 128 -> fused QKV 2048->3072, attention-out 2048->2048,
 SwiGLU gate/up 2048->5632, down 5632->2048; tokens M = 8 x 1024 = 8192):
 forward Y = X W (NN, bf16 out), dX = dY W^T (NT, bf16 out), dW += X^T dY (TN, fp32
@@ -100,7 +100,7 @@ def main():
     args = parse()
     if args.gpus != 1:
         print(json.dumps({"error": "this build runs on one GPU only; --gpus must be 1 "
-                                   "(multi-GPU sharding is described in DESIGN.md, not run)"}))
+                                   "(the multi-GPU sharding is a design, not run)"}))
         sys.exit(2)
     import torch
 

@@ -38,7 +38,7 @@ def test_attention_forward_backward(mi, dev, oracle, Bn, nH, nKV, T, d):
 
 
 def test_attention_config4_full_size(mi, dev, oracle):
-    """BASELINE config 4 (B=8, 16 q heads / 4 kv heads, T=1024, d=128): the whole batch
+    """Benchmark configuration 4 (B=8, 16 q heads / 4 kv heads, T=1024, d=128): the whole batch
     on the GPU, the oracle on batch elements 0 and 7."""
     Bn, nH, nKV, T, d = 8, 16, 4, 1024, 128
     q, k, v, do = _qkv(oracle, Bn, nH, nKV, T, d, 4000)

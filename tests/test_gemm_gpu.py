@@ -3,7 +3,7 @@
 Bar: fp32 inputs within max relative error 1e-4, bf16 inputs within 1e-2 of the
 float64 oracle fed the same bf16-rounded inputs (max relative error =
 max|y - ref| / max|ref|). Small integers give bit-exact expectations. Full-size
-BASELINE configurations are checked on sampled rows against the oracle and on
+benchmark configurations are checked on sampled rows against the oracle and on
 every element through row/column checksums.
 """
 import numpy as np
@@ -134,7 +134,7 @@ def test_bf16_output_rounds_to_nearest_even(mi, dev, oracle):
 
 
 def test_config1_fp32_linear_bias(mi, dev, oracle):
-    """Y = X W^T + b, X [512x768], W [768x768] ~ N(0,0.02), fp32."""
+    """Benchmark configuration 1: Y = X W^T + b, X [512x768], W [768x768] ~ N(0,0.02), fp32."""
     got, ref = _run(mi, dev, oracle, 512, 768, 768, 0, 1, False, seed=1, bias=True)
     check(got, ref, TOL_F32, "config 1")
     assert oracle.l2_rel_err(got, ref) < 1e-4  # test_gpu_kernels.cpp:87-116 metric
@@ -185,7 +185,7 @@ def test_zero_k(mi, dev, oracle):
     check(got, ref, TOL_F32, "K=0")
 
 
-# ---- BASELINE decoder-block GEMM sets -------------------------------------------
+# ---- decoder-block GEMM sets of the benchmark configurations ----------------------
 
 def _block_set(mi, dev, oracle, M, H, Nqkv, I, bf16, seed):
     """Forward (NN), dX (NT) and dW (TN) for QKV, O, gate, up, down: engine layout W[in,out]."""
@@ -219,17 +219,17 @@ def _block_set(mi, dev, oracle, M, H, Nqkv, I, bf16, seed):
 
 
 def test_config2_gpt_small_fp32(mi, dev, oracle):
-    """d=768, 12 heads MHA (QKV 768->2304), SwiGLU 2048, M=2048, fp32."""
+    """Benchmark configuration 2: d=768, 12 heads MHA (QKV 768->2304), SwiGLU 2048, M=2048, fp32."""
     _block_set(mi, dev, oracle, 2048, 768, 2304, 2048, False, seed=200)
 
 
 def test_config3_1p6b_bf16(mi, dev, oracle):
-    """d=2048, GQA 16/4 x 128 (QKV 2048->3072), SwiGLU 5632, M=8192, bf16."""
+    """Benchmark configuration 3: d=2048, GQA 16/4 x 128 (QKV 2048->3072), SwiGLU 5632, M=8192, bf16."""
     _block_set(mi, dev, oracle, 8192, 2048, 3072, 5632, True, seed=300)
 
 
 def test_config5_lm_head(mi, dev, oracle):
-    """logits = X E^T (NT), dX = dL E (NN), dE = dL^T X (TN, fp32)."""
+    """Benchmark configuration 5: logits = X E^T (NT), dX = dL E (NN), dE = dL^T X (TN, fp32)."""
     import torch
 
     M, H, V = 8192, 2048, 32000
