@@ -150,6 +150,27 @@ int mi_softmax_causal(void* stream, void* S, int64_t rows, int64_t T, int64_t ld
 int mi_softmax_bwd(void* stream, const void* P, void* dP, int64_t rows, int64_t T,
                    int64_t ld, float scale, int32_t dtype);
 
+/* Output layouts of mi_flash_attn_fwd. */
+typedef enum mi_attn_layout {
+  MI_ATTN_O_BHTD = 0, /* O[b][h][t][c]           (flash_attn_fwd.metal)            */
+  MI_ATTN_O_BTHD = 1  /* O[b][t][h*d + c]        (Attention.cpp:270-278, [B,T,nH*d]) */
+} mi_attn_layout;
+
+/*
+ * Fused GQA attention forward: O = softmax(Q K^T / sqrt(d), causal k <= q) V with
+ * query head h reading KV head h / (n_heads / n_kv), S and P kept on chip (online
+ * softmax).  Q [batch, n_heads, seq_len, d], K and V [batch, n_kv, seq_len, d], O
+ * per o_layout, all bf16 and 16-byte aligned; lse (optional, fp32 [batch,
+ * n_heads, seq_len]) receives each row's natural-log log-sum-exp of the scaled
+ * scores, for a backward pass.  causal = 0 attends to every key.  head_dim must
+ * be 128; n_heads a multiple of n_kv.  Replaces metal_bridge::flash_attn_fwd
+ * (MetalBridge.hpp:49-51) and the forward of Attention::forward
+ * (Attention.cpp:236-280).
+ */
+int mi_flash_attn_fwd(void* stream, const void* Q, const void* K, const void* V, void* O,
+                      float* lse, int64_t batch, int64_t n_heads, int64_t n_kv, int64_t seq_len,
+                      int64_t head_dim, int32_t causal, int32_t o_layout);
+
 /*
  * Describe the kernel mi_gemm_batched would launch for this problem (tile,
  * loader, split-K factor) as text into buf (always NUL-terminated).  For

@@ -1,0 +1,341 @@
+// mi_attn.hip -- fused GQA flash-attention forward for gfx950 (bf16 in, fp32 softmax
+// and accumulation, bf16 out).
+//
+// Replaces the reference's attention forward: Attention::forward (Attention.cpp:
+// 236-280: kv_h = h / (nH/nKV), S = Q K^T / sqrt(d), causal k <= q, stable softmax,
+// O = P V written to [B, T, nH*d]) and metal_bridge::flash_attn_fwd
+// (MetalBridge.hpp:49-51, flash_attn_fwd.metal: online softmax, output
+// [B, nH, T, d]).  S and P never leave the chip: one workgroup owns 256 query rows of
+// one (batch, head), streams the 64-key K/V blocks of the shared KV head through a
+// two-stage LDS ring and keeps the running max, running sum and the 256 x d output
+// accumulator in registers (FlashAttention-2 style online softmax).
+//
+// Work split: 4 waves x 64 query rows.  Per 64-key block a wave computes
+//   S[64 q x 64 keys] = K Q^T  (first MFMA operand K, so each lane owns one query
+//                               row and 32 of the block's keys for that row),
+//   the online-softmax update on those registers, and
+//   O[64 q x d] += P V         (first operand V^T via the transposing LDS read, second
+//                               operand P straight from the S registers).
+// The S registers of a lane hold keys 8q + 4h + e (h = lane / 32) of each 32-key
+// half; reading the K rows in the order that swaps bits 2 and 3 of the key index
+// makes those registers hold, in order, exactly the 8-key runs the P operand of
+// v_mfma_f32_32x32x16_bf16 needs, so P never goes through LDS.
+#include <hip/hip_runtime.h>
+
+#include "mi_attn.hpp"
+#include "mi_gemm_dlds.hpp"
+
+namespace mig {
+
+namespace {
+
+constexpr int FA_BQ = 256;   // query rows per workgroup (64 per wave)
+constexpr int FA_BK = 64;    // keys per K/V block
+constexpr float FA_TAU = 8.0f;  // rescale threshold of the running max, log2 units
+
+// Workgroup b runs on XCD b mod 8; renumber so each XCD holds a contiguous range.
+__device__ __forceinline__ int fa_xcd_major(int bid, int n) {
+  const int q = n / 8, rem = n % 8, x = bid % 8, j = bid / 8;
+  return x * q + (x < rem ? x : rem) + j;
+}
+
+// Key row read by lane row p (0..31) of a 32-key half: bits 2 and 3 swapped.
+__device__ __forceinline__ int fa_key_perm(int p) {
+  return (p & ~0xC) | ((p & 4) << 1) | ((p & 8) >> 1);
+}
+
+template <int D>
+struct FaTile {
+  static constexpr int ROW = D * 2;            // bytes per key row
+  static constexpr int NCH = D / 8;            // 16-byte chunks per row
+  static constexpr int BYTES = FA_BK * ROW;    // one K or V block
+  static constexpr int NBLK = BYTES / 1024;    // 1 KB DMA blocks per block
+  static constexpr int NU = NBLK / 4;          // DMA instructions per wave per operand
+  static_assert(NCH == 16, "the LDS swizzles below assume 256-byte key rows (d = 128)");
+  // K tile [key][d]: chunk c of key row r sits at position c ^ (r & 15); the 16
+  // lanes of one ds_read_b128 phase read 16 rows with distinct r & 15.
+  __device__ static __forceinline__ int k_pos(int r, int c) { return c ^ (r & 15); }
+  // V tile [key][d]: chunk q of key row r at position q ^ ((r & 3) << 2); a
+  // transposing read touches 4 consecutive key rows -> 4 distinct 64-byte groups.
+  __device__ static __forceinline__ int v_pos(int r, int q) { return q ^ ((r & 3) << 2); }
+};
+
+template <int D>
+__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1)))
+    flash_fwd_kernel(FaParams p) {
+  using Tl = FaTile<D>;
+  constexpr int NS = D / 16;   // MFMA k-steps over d for S
+  constexpr int NC = D / 32;   // 32-column blocks of d for O
+  constexpr int STAGE = 2 * Tl::BYTES;  // K block then V block
+  __shared__ __attribute__((aligned(16))) char smem[2 * STAGE];
+  const uint32_t lds0 = lds_addr(smem);
+
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int wave_u = uniform(wave);
+  const int h32 = lane >> 5, l32 = lane & 31;
+
+  // Heaviest query blocks first (causal work grows with the block index); the
+  // (batch, head) pairs of one query block are spread XCD-major so the heads of a
+  // KV group share K/V in one L2.
+  const int BH = p.B * p.nH;
+  const int lid = uniform(fa_xcd_major(blockIdx.x, gridDim.x));
+  const int qb = uniform(p.q_blocks - 1 - lid / BH);
+  const int bh = uniform(lid - (lid / BH) * BH);
+  const int b = uniform(bh / p.nH), h = uniform(bh - (bh / p.nH) * p.nH);
+  const int kvh = uniform(h / p.group);
+  const int T = p.T;
+  const int q0 = qb * FA_BQ;
+  const int qw = q0 + 64 * wave_u;  // first query row of this wave
+
+  const __bf16* Qb = (const __bf16*)p.Q + ((int64_t)bh * T) * D;
+  const __bf16* Kb = (const __bf16*)p.K + ((int64_t)(b * p.nKV + kvh) * T) * D;
+  const __bf16* Vb = (const __bf16*)p.V + ((int64_t)(b * p.nKV + kvh) * T) * D;
+
+  // Q fragments (second MFMA operand of S): row qw + 32r + l32, d = 16s + 8*h32 .. +7.
+  u32x4_t qf[2][NS];
+#pragma unroll
+  for (int r = 0; r < 2; ++r) {
+    const int row = qw + 32 * r + l32;
+#pragma unroll
+    for (int s = 0; s < NS; ++s) {
+      if (row < T)
+        qf[r][s] = *(const u32x4_t*)(Qb + (int64_t)row * D + 16 * s + 8 * h32);
+      else
+        qf[r][s] = u32x4_t{0u, 0u, 0u, 0u};
+    }
+  }
+
+  // Keys this workgroup needs: causal -> up to its last query row.
+  const int kv_end = p.causal ? (q0 + FA_BQ < T ? q0 + FA_BQ : T) : T;
+  const int nblk = uniform((kv_end + FA_BK - 1) / FA_BK);
+
+  // DMA: wave w moves 1 KB blocks w*NU .. w*NU+NU-1 of the K and of the V block;
+  // lane l of block u covers key row 4u + l/16, LDS chunk position l % 16.
+  uint32_t k_off[Tl::NU], v_off[Tl::NU];
+#pragma unroll
+  for (int u = 0; u < Tl::NU; ++u) {
+    const int blk = wave * Tl::NU + u;
+    const int row = 4 * blk + (lane >> 4), pos = lane & 15;
+    k_off[u] = (uint32_t)(row * Tl::ROW + 16 * Tl::k_pos(row, pos));  // k_pos is an involution
+    v_off[u] = (uint32_t)(row * Tl::ROW + 16 * Tl::v_pos(row, pos));  // so is v_pos
+  }
+  const uint32_t dma_k = lds0 + (uint32_t)(wave_u * Tl::NU * 1024);
+  const uint32_t dma_v = dma_k + Tl::BYTES;
+  auto issue_block = [&](int j) __attribute__((always_inline)) {
+    const int k0 = j * FA_BK;
+    const uint32_t ext = (uint32_t)((T - k0) * Tl::ROW);  // keys >= T read as zero
+    const __amdgpu_buffer_rsrc_t rk = scalar_rsrc(uniform(Kb + (int64_t)k0 * D), ext);
+    const __amdgpu_buffer_rsrc_t rv = scalar_rsrc(uniform(Vb + (int64_t)k0 * D), ext);
+    const uint32_t st = (uint32_t)((j & 1) * STAGE);
+#pragma unroll
+    for (int u = 0; u < Tl::NU; ++u) {
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(
+          rk, (__attribute__((address_space(3))) void*)(uintptr_t)(dma_k + st + (uint32_t)(u * 1024)), 16,
+          (int)k_off[u], 0, 0, 0);
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(
+          rv, (__attribute__((address_space(3))) void*)(uintptr_t)(dma_v + st + (uint32_t)(u * 1024)), 16,
+          (int)v_off[u], 0, 0, 0);
+    }
+  };
+
+  // Fragment read addresses (stage 0).
+  // K: first operand of S, row = key 32kb + perm(l32), d chunk 2s + h32.
+  uint32_t k_rd[2];
+#pragma unroll
+  for (int kb = 0; kb < 2; ++kb) k_rd[kb] = (uint32_t)((32 * kb + fa_key_perm(l32)) * Tl::ROW);
+  const int k_row_lo = fa_key_perm(l32) & 15;  // r & 15 of both halves' rows
+  // V: first operand of P V (rows = d, k = keys) through ds_read_b64_tr_b16: the
+  // 16-lane group g reads key rows 8(g>>1) + (j>>2) (+4 for the second read) and
+  // d columns 32c + 16(g&1) + 4(j&3) .. +3 and hands lane j the column 32c +
+  // 16(g&1) + j with 4 consecutive keys.
+  uint32_t v_rd[NC];
+  {
+    const int g = lane >> 4, jj = lane & 15;
+    const int krb = 8 * (g >> 1) + (jj >> 2);
+#pragma unroll
+    for (int c = 0; c < NC; ++c) {
+      const int col = 32 * c + 16 * (g & 1) + 4 * (jj & 3);
+      v_rd[c] = (uint32_t)(Tl::BYTES + krb * Tl::ROW + 16 * Tl::v_pos(krb, col >> 3) + (col & 7) * 2);
+    }
+  }
+
+  f32x16_t o[2][NC];
+#pragma unroll
+  for (int r = 0; r < 2; ++r)
+#pragma unroll
+    for (int c = 0; c < NC; ++c)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) o[r][c][e] = 0.0f;
+  float m_run[2] = {-INFINITY, -INFINITY}, l_run[2] = {0.0f, 0.0f};
+  const float sl2 = p.scale_log2;
+
+  if (nblk > 0) issue_block(0);
+  for (int j = 0; j < nblk; ++j) {
+    wait_vmcnt<0>();  // this wave's share of block j (and the Q loads) landed
+    lds_ring_barrier();  // every share landed; every wave is done with block j-1
+    if (j + 1 < nblk) issue_block(j + 1);
+    const int k0 = j * FA_BK;
+    if (p.causal && k0 > qw + 63) continue;  // the whole block is above this wave's rows
+    const uint32_t st = lds0 + (uint32_t)((j & 1) * STAGE);
+
+    // ---- S = K Q^T for both 32-row halves and both 32-key halves ----
+    f32x16_t sacc[2][2];
+#pragma unroll
+    for (int r = 0; r < 2; ++r)
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) sacc[r][kb][e] = 0.0f;
+#pragma unroll
+    for (int s = 0; s < NS; ++s) {
+      u32x4_t kf[2];
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb) {
+        const int c = 2 * s + h32;
+        const uint32_t a = st + k_rd[kb] + (uint32_t)(16 * (c ^ k_row_lo));
+        kf[kb] = *(const lds_u32x4_t*)(uintptr_t)a;
+      }
+#pragma unroll
+      for (int r = 0; r < 2; ++r)
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb)
+          sacc[r][kb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
+              __builtin_bit_cast(bf16x8_t, kf[kb]), __builtin_bit_cast(bf16x8_t, qf[r][s]),
+              sacc[r][kb], 0, 0, 0);
+    }
+
+    // ---- online softmax (base 2), P fragments ----
+    // sacc[r][kb][4q + e] is key k0 + 32kb + 16(q>>1) + 8*h32 + 4(q&1) + e of row
+    // qw + 32r + l32.
+    u32x4_t pf[2][4];
+#pragma unroll
+    for (int r = 0; r < 2; ++r) {
+      const int row = qw + 32 * r + l32;
+      // keys visible to this row: below row + 1 (causal) or below T
+      const bool edge = p.causal ? (k0 + FA_BK - 1 > qw + 32 * r) : (k0 + FA_BK > T);
+      const int lim = p.causal ? row + 1 : T;
+      float mx = -INFINITY;
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb) {
+        // key of register i = k0 + 32kb + 8*h32 + (16((i>>2)>>1) + 4((i>>2)&1) + (i&3))
+        const int room = lim - (k0 + 32 * kb + 8 * h32);
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+          const int koff = 16 * ((i >> 2) >> 1) + 4 * ((i >> 2) & 1) + (i & 3);
+          float x = sacc[r][kb][i] * sl2;
+          if (edge) x = koff < room ? x : -INFINITY;
+          sacc[r][kb][i] = x;
+          mx = fmaxf(mx, x);
+        }
+      }
+      mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+      // Conditional rescaling: a row keeps its reference max until a block raises
+      // it by more than FA_TAU (log2 units), so p = 2^(x - m) stays below 2^FA_TAU
+      // and the O accumulators are rescaled only on the rare blocks where some row
+      // of the wave moves its reference (the result is the same for any reference
+      // max; only the rounding of intermediate values differs).  A row with no
+      // visible key yet (m = -inf) has O = 0 and l = 0 and just takes the new max.
+      const float m_old = m_run[r];
+      const bool fresh = m_old == -INFINITY;
+      const bool raise = !fresh && mx > m_old + FA_TAU;
+      const float m_ref = (fresh || raise) ? mx : m_old;
+      if (__any(raise)) {
+        const float alpha = raise ? __builtin_amdgcn_exp2f(m_old - m_ref) : 1.0f;
+        l_run[r] *= alpha;
+#pragma unroll
+        for (int c = 0; c < NC; ++c)
+#pragma unroll
+          for (int e = 0; e < 16; ++e) o[r][c][e] *= alpha;
+      }
+      m_run[r] = m_ref;
+      // rows with no visible key in any block so far (non-causal tail rows) stay
+      // at m = -inf; exp2 against 0 keeps their p at 0
+      const float m_use = m_ref == -INFINITY ? 0.0f : m_ref;
+      float sum = 0.0f;
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+          const float e = __builtin_amdgcn_exp2f(sacc[r][kb][i] - m_use);
+          sacc[r][kb][i] = e;
+          sum += e;
+        }
+      l_run[r] += sum;
+      // k-step ks covers keys 16ks .. 16ks+15: registers 8(ks&1) .. +7 of half ks>>1
+#pragma unroll
+      for (int ks = 0; ks < 4; ++ks) {
+        const int kb = ks >> 1, base = 8 * (ks & 1);
+#pragma unroll
+        for (int w2 = 0; w2 < 4; ++w2)
+          pf[r][ks][w2] = pack_bf16x2(sacc[r][kb][base + 2 * w2], sacc[r][kb][base + 2 * w2 + 1]);
+      }
+    }
+
+    // ---- O += P V ----
+    static_for<4>([&](auto ks_c) __attribute__((always_inline)) {
+      constexpr int ks = decltype(ks_c)::value;
+      u32x4_t vf[NC];
+#pragma unroll
+      for (int c = 0; c < NC; ++c) {
+        static_for<2>([&](auto t_c) __attribute__((always_inline)) {
+          constexpr int t = decltype(t_c)::value;
+          u32x2_t w2 = {0u, 0u};
+#if defined(__HIP_DEVICE_COMPILE__)
+          // inline asm: the builtin would also wait for the K/V DMA in flight
+          asm volatile("ds_read_b64_tr_b16 %0, %1 offset:%2"
+                       : "=v"(w2)
+                       : "v"(st + v_rd[c]), "i"((16 * ks + 4 * t) * Tl::ROW));
+#endif
+          vf[c][2 * t] = w2[0];
+          vf[c][2 * t + 1] = w2[1];
+        });
+      }
+      __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): the transposing reads are in
+#pragma unroll
+      for (int c = 0; c < NC; ++c)
+#pragma unroll
+        for (int r = 0; r < 2; ++r)
+          o[r][c] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, vf[c]),
+                                                            __builtin_bit_cast(bf16x8_t, pf[r][ks]),
+                                                            o[r][c], 0, 0, 0);
+    });
+  }
+
+  // ---- normalise and store ----
+#pragma unroll
+  for (int r = 0; r < 2; ++r) {
+    const int row = qw + 32 * r + l32;
+    const float l_tot = l_run[r] + __shfl_xor(l_run[r], 32, 64);
+    const float inv = l_tot > 0.0f ? 1.0f / l_tot : 0.0f;
+    if (row < T) {
+      uint16_t* orow = (uint16_t*)p.O + (p.o_bthd ? ((int64_t)(b * T + row) * p.nH + h) * D
+                                                  : ((int64_t)bh * T + row) * D);
+#pragma unroll
+      for (int c = 0; c < NC; ++c)
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const int d = 32 * c + 8 * q + 4 * h32;
+          *(u32x2_t*)(orow + d) = u32x2_t{pack_bf16x2(o[r][c][4 * q] * inv, o[r][c][4 * q + 1] * inv),
+                                          pack_bf16x2(o[r][c][4 * q + 2] * inv, o[r][c][4 * q + 3] * inv)};
+        }
+      if (p.lse && h32 == 0)
+        p.lse[(int64_t)bh * T + row] = l_tot > 0.0f ? (m_run[r] + __log2f(l_tot)) * 0.69314718055994531f
+                                                   : -INFINITY;
+    }
+  }
+}
+
+}  // namespace
+
+int flash_fwd_blocks(int T) { return (T + FA_BQ - 1) / FA_BQ; }
+
+hipError_t launch_flash_fwd(const FaParams& p, int head_dim, hipStream_t stream) {
+  const int64_t n = (int64_t)p.B * p.nH * p.q_blocks;
+  if (head_dim == 128)
+    hipLaunchKernelGGL(flash_fwd_kernel<128>, dim3((unsigned)n), dim3(256), 0, stream, p);
+  else
+    return hipErrorInvalidValue;
+  return hipGetLastError();
+}
+
+}  // namespace mig

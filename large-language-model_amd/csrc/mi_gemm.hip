@@ -18,6 +18,7 @@
 #include <string>
 
 #include "../../include/mi_gemm.h"
+#include "mi_attn.hpp"
 #include "mi_gemm_kernels.hpp"
 
 using namespace mig;
@@ -564,6 +565,42 @@ int mi_softmax_bwd(void* stream, const void* P, void* dP, int64_t rows, int64_t 
                        (hipStream_t)stream, P, dP, T, ld, scale);
   hipError_t e = hipGetLastError();
   return e == hipSuccess ? MI_OK : fail(MI_ERR_HIP, "softmax_bwd: %s", hipGetErrorString(e));
+}
+
+int mi_flash_attn_fwd(void* stream, const void* Q, const void* K, const void* V, void* O,
+                      float* lse, int64_t batch, int64_t n_heads, int64_t n_kv, int64_t seq_len,
+                      int64_t head_dim, int32_t causal, int32_t o_layout) {
+  if (batch < 0 || n_heads < 0 || n_kv < 0 || seq_len < 0)
+    return fail(MI_ERR_SHAPE, "negative size");
+  if (batch == 0 || n_heads == 0 || seq_len == 0) return MI_OK;
+  if (!Q || !K || !V || !O) return fail(MI_ERR_NULL, "Q, K, V or O is NULL");
+  if (n_kv <= 0 || n_heads % n_kv != 0)
+    return fail(MI_ERR_SHAPE, "n_heads=%lld is not a multiple of n_kv=%lld", (long long)n_heads,
+                (long long)n_kv);
+  if (head_dim != 128)
+    return fail(MI_ERR_UNSUPPORTED, "flash attention supports head_dim 128 (got %lld)",
+                (long long)head_dim);
+  if (o_layout != MI_ATTN_O_BHTD && o_layout != MI_ATTN_O_BTHD)
+    return fail(MI_ERR_SHAPE, "unknown output layout %d", o_layout);
+  if (!aligned16(Q) || !aligned16(K) || !aligned16(V) || ((uintptr_t)O & 7u) != 0 ||
+      ((uintptr_t)lse & 3u) != 0)
+    return fail(MI_ERR_UNSUPPORTED, "Q, K, V must be 16-byte aligned, O 8-byte, lse 4-byte");
+  // every byte offset of one (batch, kv head) matrix and the block count fit 31 bits
+  if (seq_len * head_dim * 2 >= ((int64_t)1 << 31) || batch * n_heads * seq_len > INT32_MAX)
+    return fail(MI_ERR_SHAPE, "sequence too long");
+  int st = init_devices();
+  if (st != MI_OK) return st;
+  FaParams p;
+  p.Q = Q; p.K = K; p.V = V; p.O = O; p.lse = lse;
+  p.B = (int)batch; p.nH = (int)n_heads; p.nKV = (int)n_kv; p.T = (int)seq_len;
+  p.group = (int)(n_heads / n_kv);
+  p.causal = causal != 0;
+  p.o_bthd = o_layout == MI_ATTN_O_BTHD;
+  p.q_blocks = flash_fwd_blocks(p.T);
+  p.scale_log2 = (float)(1.4426950408889634 / std::sqrt((double)head_dim));
+  if ((int64_t)p.B * p.nH * p.q_blocks > INT32_MAX) return fail(MI_ERR_SHAPE, "too many blocks");
+  hipError_t e = launch_flash_fwd(p, (int)head_dim, (hipStream_t)stream);
+  return e == hipSuccess ? MI_OK : fail(MI_ERR_HIP, "flash attention launch: %s", hipGetErrorString(e));
 }
 
 int mi_gemm_describe(int transA, int transB, int64_t M, int64_t N, int64_t K, int32_t dtype_in,

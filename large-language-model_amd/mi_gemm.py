@@ -33,8 +33,9 @@ MI_CAUSAL_NONE, MI_CAUSAL_OUT_LOWER, MI_CAUSAL_A_LOWER, MI_CAUSAL_A_UPPER = 0, 1
 C_SYMBOLS = (
     "mi_init", "mi_last_error", "mi_version", "mi_gemm_workspace_size", "mi_gemm",
     "mi_gemm_batched", "mi_residual_add", "mi_softmax_causal", "mi_softmax_bwd",
-    "mi_gemm_describe", "mi_stream_sync",
+    "mi_gemm_describe", "mi_stream_sync", "mi_flash_attn_fwd",
 )
+MI_ATTN_O_BHTD, MI_ATTN_O_BTHD = 0, 1
 
 
 class MiError(RuntimeError):
@@ -107,6 +108,8 @@ def load_library():
                                    ctypes.c_size_t, ctypes.c_char_p, ctypes.c_size_t]
     L.mi_stream_sync.restype = ctypes.c_int
     L.mi_stream_sync.argtypes = [vp]
+    L.mi_flash_attn_fwd.restype = ctypes.c_int
+    L.mi_flash_attn_fwd.argtypes = [vp, vp, vp, vp, vp, vp, i64, i64, i64, i64, i64, i32, i32]
     _lib = L
     return L
 
@@ -406,6 +409,30 @@ def attention_forward(Q4, K4, V4, out_dtype=None):
     gemm_batched(S, V4, O, T, d, T, bt, ldc=nH * d, sync=False)
     _finish("attention_forward", 0)
     return O, S
+
+
+def flash_attn_fwd(Q4, K4, V4, O=None, lse=None, causal=True, layout="bthd", sync=None):
+    """Fused forward (metal_bridge::flash_attn_fwd, MetalBridge.hpp:49-51; Attention.cpp:236-280):
+    Q4 [B,nH,T,d], K4/V4 [B,nKV,T,d] bf16 -> O [B,T,nH*d] (layout "bthd", the CPU path's)
+    or [B,nH,T,d] ("bhtd", the Metal kernel's).  lse: optional fp32 [B,nH,T] tensor that
+    receives each row's log-sum-exp of the scaled scores. Returns O."""
+    torch = _torch()
+    Bn, nH, T, d = Q4.shape
+    nKV = K4.shape[1]
+    for t in (Q4, K4, V4):
+        if t.dtype != torch.bfloat16 or not t.is_contiguous():
+            raise ValueError("Q, K, V must be contiguous bf16 tensors")
+    if O is None:
+        shape = (Bn, T, nH * d) if layout == "bthd" else (Bn, nH, T, d)
+        O = torch.empty(shape, dtype=torch.bfloat16, device=Q4.device)
+    code = MI_ATTN_O_BTHD if layout == "bthd" else MI_ATTN_O_BHTD
+    st = load_library().mi_flash_attn_fwd(_stream(), _ptr(Q4), _ptr(K4), _ptr(V4), _ptr(O),
+                                          _ptr(lse), Bn, nH, nKV, T, d, int(bool(causal)), code)
+    if sync is None:
+        _finish("mi_flash_attn_fwd", st)
+    else:
+        _check("mi_flash_attn_fwd", st)
+    return O
 
 
 def attention_backward(Q4, K4, V4, dO, P, grad_dtype=None):

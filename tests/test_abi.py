@@ -109,6 +109,14 @@ def test_aux_validation(mi):
     assert lib.mi_residual_add(None, ctypes.c_void_p(16), ctypes.c_void_p(16), 5, 3) == 4
     assert lib.mi_softmax_causal(None, ctypes.c_void_p(16), 4, 8, 4, 1) == 2
     assert lib.mi_softmax_bwd(None, None, None, 4, 8, 8, 1.0, 1) == 3
+    p16 = ctypes.c_void_p(16)
+    fa = lib.mi_flash_attn_fwd
+    assert fa(None, None, None, None, None, None, 0, 4, 2, 64, 128, 1, 1) == 0   # empty batch
+    assert fa(None, None, p16, p16, p16, None, 1, 4, 2, 64, 128, 1, 1) == 3      # Q NULL
+    assert fa(None, p16, p16, p16, p16, None, 1, 4, 3, 64, 128, 1, 1) == 1       # 4 % 3 heads
+    assert fa(None, p16, p16, p16, p16, None, 1, 4, 2, 64, 96, 1, 1) == 5        # head_dim 96
+    assert fa(None, p16, p16, p16, p16, None, 1, 4, 2, 64, 128, 1, 7) == 1       # layout
+    assert fa(None, ctypes.c_void_p(18), p16, p16, p16, None, 1, 4, 2, 64, 128, 1, 1) == 5
 
 
 def test_matmul_shape_rules(mi):

@@ -97,3 +97,67 @@ def test_causal_modes(mi, dev, oracle, bf16):
     mi.gemm_batched(to_dev(p, dev, bf16), to_dev(v, dev, bf16), C, T, d, T, bt, transA=True)
     ref = oracle.gemm(1, 0, T, d, T, p, v, nseg=g, segA=T * T, segB=T * d)
     check(host(C), ref, tol, "A_UPPER segments")
+
+
+# ---- fused flash-attention forward ------------------------------------------------
+
+def _dense_attention(q, k, v, causal):
+    """float64 softmax(Q K^T / sqrt(d)) V and the row log-sum-exp, [B,nH,T,d] layouts
+    (the closed form; the causal case is also checked against the oracle)."""
+    Bn, nH, T, d = q.shape
+    g = nH // k.shape[1]
+    kk = np.repeat(k.astype(np.float64), g, axis=1)
+    vv = np.repeat(v.astype(np.float64), g, axis=1)
+    s = np.einsum("bhqc,bhkc->bhqk", q.astype(np.float64), kk) / np.sqrt(d)
+    if causal:
+        s = np.where(np.tril(np.ones((T, T), bool)), s, -np.inf)
+    mx = s.max(axis=-1, keepdims=True)
+    e = np.exp(s - mx)
+    lse = (np.log(e.sum(axis=-1)) + mx[..., 0])
+    o = np.einsum("bhqk,bhkc->bhqc", e / e.sum(axis=-1, keepdims=True), vv)
+    return o, lse
+
+
+@pytest.mark.parametrize("Bn,nH,nKV,T", [(2, 16, 4, 256), (1, 4, 2, 300), (1, 2, 1, 64),
+                                         (1, 4, 4, 520)])
+def test_flash_forward(mi, dev, oracle, Bn, nH, nKV, T):
+    """Fused forward vs the oracle (causal, Attention.cpp:236-280) in both output layouts,
+    and the row log-sum-exp vs its closed form."""
+    import torch
+
+    d = 128
+    q, k, v, _ = _qkv(oracle, Bn, nH, nKV, T, d, 1300 + T)
+    Q, K, V = (to_dev(x, dev, True) for x in (q, k, v))
+    lse = torch.empty((Bn, nH, T), dtype=torch.float32, device=dev)
+    O = mi.flash_attn_fwd(Q, K, V, lse=lse)
+    O2 = mi.flash_attn_fwd(Q, K, V, layout="bhtd")
+    O_ref = oracle.attention_fwd(q, k, v)
+    check(host(O), O_ref, TOL_BF16, "O [B,T,nH*d]")
+    check(host(O2).transpose(0, 2, 1, 3).reshape(Bn, T, nH * d), O_ref, TOL_BF16, "O [B,nH,T,d]")
+    _, lse_ref = _dense_attention(q, k, v, True)
+    err = np.abs(host(lse) - lse_ref).max()
+    assert err < 1e-3, f"lse max abs err {err:.3e}"
+
+
+def test_flash_forward_noncausal(mi, dev, oracle):
+    """causal = 0 attends to every key, including the zero-padded tail block (T % 64 != 0)."""
+    d, Bn, nH, nKV, T = 128, 1, 4, 2, 200
+    q, k, v, _ = _qkv(oracle, Bn, nH, nKV, T, d, 1700)
+    Q, K, V = (to_dev(x, dev, True) for x in (q, k, v))
+    O = mi.flash_attn_fwd(Q, K, V, causal=False, layout="bhtd")
+    o_ref, _ = _dense_attention(q, k, v, False)
+    check(host(O), o_ref, TOL_BF16, "non-causal O")
+
+
+def test_flash_forward_config4(mi, dev, oracle):
+    """Benchmark configuration 4 forward (B=8, 16/4 heads, T=1024, d=128): the fused kernel vs
+    the oracle on batch elements 0 and 7 and vs the materialised S/P path on the whole batch."""
+    Bn, nH, nKV, T, d = 8, 16, 4, 1024, 128
+    q, k, v, _ = _qkv(oracle, Bn, nH, nKV, T, d, 4000)
+    Q, K, V = (to_dev(x, dev, True) for x in (q, k, v))
+    O = host(mi.flash_attn_fwd(Q, K, V))
+    O_mat, _ = mi.attention_forward(Q, K, V)
+    check(O, host(O_mat), TOL_BF16, "fused vs materialised")
+    for b in (0, 7):
+        sl = slice(b, b + 1)
+        check(O[sl], oracle.attention_fwd(q[sl], k[sl], v[sl]), TOL_BF16, f"O[{b}]")
