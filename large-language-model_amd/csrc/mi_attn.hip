@@ -5,16 +5,18 @@
 // 236-280: kv_h = h / (nH/nKV), S = Q K^T / sqrt(d), causal k <= q, stable softmax,
 // O = P V written to [B, T, nH*d]) and metal_bridge::flash_attn_fwd
 // (MetalBridge.hpp:49-51, flash_attn_fwd.metal: online softmax, output
-// [B, nH, T, d]).  S and P never leave the chip: one workgroup owns 256 query rows of
+// [B, nH, T, d]).  S and P never leave the chip: one workgroup owns 128 query rows of
 // one (batch, head), streams the 64-key K/V blocks of the shared KV head through a
-// two-stage LDS ring and keeps the running max, running sum and the 256 x d output
+// two-stage LDS ring and keeps the running max, running sum and the 128 x d output
 // accumulator in registers (FlashAttention-2 style online softmax).
 //
-// Work split: 4 waves x 64 query rows.  Per 64-key block a wave computes
-//   S[64 q x 64 keys] = K Q^T  (first MFMA operand K, so each lane owns one query
+// Work split: 4 waves x 32 query rows, two workgroups per CU, so each SIMD holds
+// two waves and one wave's softmax (VALU) runs under the other's MFMAs.  Per
+// 64-key block a wave computes
+//   S[32 q x 64 keys] = K Q^T  (first MFMA operand K, so each lane owns one query
 //                               row and 32 of the block's keys for that row),
 //   the online-softmax update on those registers, and
-//   O[64 q x d] += P V         (first operand V^T via the transposing LDS read, second
+//   O[32 q x d] += P V         (first operand V^T via the transposing LDS read, second
 //                               operand P straight from the S registers).
 // The S registers of a lane hold keys 8q + 4h + e (h = lane / 32) of each 32-key
 // half; reading the K rows in the order that swaps bits 2 and 3 of the key index
@@ -29,9 +31,9 @@ namespace mig {
 
 namespace {
 
-constexpr int FA_BQ = 256;   // query rows per workgroup (64 per wave)
+constexpr int FA_BQ = 128;   // query rows per workgroup (32 per wave)
 constexpr int FA_BK = 64;    // keys per K/V block
-constexpr float FA_TAU = 8.0f;  // rescale threshold of the running max, log2 units
+constexpr float FA_TAU = 8.0f;  // growth of a row max (log2 units of p) that forces a rescale
 
 // Workgroup b runs on XCD b mod 8; renumber so each XCD holds a contiguous range.
 __device__ __forceinline__ int fa_xcd_major(int bid, int n) {
@@ -61,7 +63,7 @@ struct FaTile {
 };
 
 template <int D>
-__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1)))
+__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2)))
     flash_fwd_kernel(FaParams p) {
   using Tl = FaTile<D>;
   constexpr int NS = D / 16;   // MFMA k-steps over d for S
@@ -85,24 +87,21 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1)))
   const int kvh = uniform(h / p.group);
   const int T = p.T;
   const int q0 = qb * FA_BQ;
-  const int qw = q0 + 64 * wave_u;  // first query row of this wave
+  const int qw = q0 + 32 * wave_u;  // first query row of this wave
+  const int row = qw + l32;          // this lane's query row
 
   const __bf16* Qb = (const __bf16*)p.Q + ((int64_t)bh * T) * D;
   const __bf16* Kb = (const __bf16*)p.K + ((int64_t)(b * p.nKV + kvh) * T) * D;
   const __bf16* Vb = (const __bf16*)p.V + ((int64_t)(b * p.nKV + kvh) * T) * D;
 
-  // Q fragments (second MFMA operand of S): row qw + 32r + l32, d = 16s + 8*h32 .. +7.
-  u32x4_t qf[2][NS];
+  // Q fragments (second MFMA operand of S): row qw + l32, d = 16s + 8*h32 .. +7.
+  u32x4_t qf[NS];
 #pragma unroll
-  for (int r = 0; r < 2; ++r) {
-    const int row = qw + 32 * r + l32;
-#pragma unroll
-    for (int s = 0; s < NS; ++s) {
-      if (row < T)
-        qf[r][s] = *(const u32x4_t*)(Qb + (int64_t)row * D + 16 * s + 8 * h32);
-      else
-        qf[r][s] = u32x4_t{0u, 0u, 0u, 0u};
-    }
+  for (int s = 0; s < NS; ++s) {
+    if (row < T)
+      qf[s] = *(const u32x4_t*)(Qb + (int64_t)row * D + 16 * s + 8 * h32);
+    else
+      qf[s] = u32x4_t{0u, 0u, 0u, 0u};
   }
 
   // Keys this workgroup needs: causal -> up to its last query row.
@@ -115,9 +114,9 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1)))
 #pragma unroll
   for (int u = 0; u < Tl::NU; ++u) {
     const int blk = wave * Tl::NU + u;
-    const int row = 4 * blk + (lane >> 4), pos = lane & 15;
-    k_off[u] = (uint32_t)(row * Tl::ROW + 16 * Tl::k_pos(row, pos));  // k_pos is an involution
-    v_off[u] = (uint32_t)(row * Tl::ROW + 16 * Tl::v_pos(row, pos));  // so is v_pos
+    const int r = 4 * blk + (lane >> 4), pos = lane & 15;
+    k_off[u] = (uint32_t)(r * Tl::ROW + 16 * Tl::k_pos(r, pos));  // k_pos is an involution
+    v_off[u] = (uint32_t)(r * Tl::ROW + 16 * Tl::v_pos(r, pos));  // so is v_pos
   }
   const uint32_t dma_k = lds0 + (uint32_t)(wave_u * Tl::NU * 1024);
   const uint32_t dma_v = dma_k + Tl::BYTES;
@@ -140,9 +139,7 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1)))
 
   // Fragment read addresses (stage 0).
   // K: first operand of S, row = key 32kb + perm(l32), d chunk 2s + h32.
-  uint32_t k_rd[2];
-#pragma unroll
-  for (int kb = 0; kb < 2; ++kb) k_rd[kb] = (uint32_t)((32 * kb + fa_key_perm(l32)) * Tl::ROW);
+  const uint32_t k_rd = (uint32_t)(fa_key_perm(l32) * Tl::ROW);
   const int k_row_lo = fa_key_perm(l32) & 15;  // r & 15 of both halves' rows
   // V: first operand of P V (rows = d, k = keys) through ds_read_b64_tr_b16: the
   // 16-lane group g reads key rows 8(g>>1) + (j>>2) (+4 for the second read) and
@@ -159,117 +156,96 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1)))
     }
   }
 
-  f32x16_t o[2][NC];
+  f32x16_t o[NC];
 #pragma unroll
-  for (int r = 0; r < 2; ++r)
+  for (int c = 0; c < NC; ++c)
 #pragma unroll
-    for (int c = 0; c < NC; ++c)
-#pragma unroll
-      for (int e = 0; e < 16; ++e) o[r][c][e] = 0.0f;
-  float m_run[2] = {-INFINITY, -INFINITY}, l_run[2] = {0.0f, 0.0f};
+    for (int e = 0; e < 16; ++e) o[c][e] = 0.0f;
+  float m_run = -INFINITY, l_run = 0.0f;  // m_run in raw score units
   const float sl2 = p.scale_log2;
+  // keys visible to this row: below row + 1 (causal) or below T
+  const int lim = p.causal ? row + 1 : T;
 
-  if (nblk > 0) issue_block(0);
-  for (int j = 0; j < nblk; ++j) {
-    wait_vmcnt<0>();  // this wave's share of block j (and the Q loads) landed
-    lds_ring_barrier();  // every share landed; every wave is done with block j-1
-    if (j + 1 < nblk) issue_block(j + 1);
-    const int k0 = j * FA_BK;
-    if (p.causal && k0 > qw + 63) continue;  // the whole block is above this wave's rows
-    const uint32_t st = lds0 + (uint32_t)((j & 1) * STAGE);
-
-    // ---- S = K Q^T for both 32-row halves and both 32-key halves ----
-    f32x16_t sacc[2][2];
+  // One 64-key block; MASK: some key of the block is invisible to some row of the wave.
+  auto block = [&](const int k0, const uint32_t st, auto MASK_c) __attribute__((always_inline)) {
+    constexpr bool MASK = decltype(MASK_c)::value;
+    // ---- S = K Q^T for both 32-key halves ----
+    f32x16_t sacc[2];
 #pragma unroll
-    for (int r = 0; r < 2; ++r)
+    for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
-      for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-        for (int e = 0; e < 16; ++e) sacc[r][kb][e] = 0.0f;
+      for (int e = 0; e < 16; ++e) sacc[kb][e] = 0.0f;
 #pragma unroll
     for (int s = 0; s < NS; ++s) {
       u32x4_t kf[2];
 #pragma unroll
       for (int kb = 0; kb < 2; ++kb) {
         const int c = 2 * s + h32;
-        const uint32_t a = st + k_rd[kb] + (uint32_t)(16 * (c ^ k_row_lo));
+        const uint32_t a = st + k_rd + (uint32_t)(32 * kb * Tl::ROW) + (uint32_t)(16 * (c ^ k_row_lo));
         kf[kb] = *(const lds_u32x4_t*)(uintptr_t)a;
       }
 #pragma unroll
-      for (int r = 0; r < 2; ++r)
-#pragma unroll
-        for (int kb = 0; kb < 2; ++kb)
-          sacc[r][kb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
-              __builtin_bit_cast(bf16x8_t, kf[kb]), __builtin_bit_cast(bf16x8_t, qf[r][s]),
-              sacc[r][kb], 0, 0, 0);
+      for (int kb = 0; kb < 2; ++kb)
+        sacc[kb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, kf[kb]),
+                                                          __builtin_bit_cast(bf16x8_t, qf[s]),
+                                                          sacc[kb], 0, 0, 0);
     }
 
-    // ---- online softmax (base 2), P fragments ----
-    // sacc[r][kb][4q + e] is key k0 + 32kb + 16(q>>1) + 8*h32 + 4(q&1) + e of row
-    // qw + 32r + l32.
-    u32x4_t pf[2][4];
+    // ---- online softmax, P fragments ----
+    // sacc[kb][i], i = 4q + e, is key k0 + 32kb + 8*h32 + 16(q>>1) + 4(q&1) + e of
+    // this lane's row.  The running max m is kept in raw score units; p =
+    // 2^(s*c - m*c) with c = log2(e)/sqrt(d) is one FMA and one exp2 per score.
+    float mx = -INFINITY;
 #pragma unroll
-    for (int r = 0; r < 2; ++r) {
-      const int row = qw + 32 * r + l32;
-      // keys visible to this row: below row + 1 (causal) or below T
-      const bool edge = p.causal ? (k0 + FA_BK - 1 > qw + 32 * r) : (k0 + FA_BK > T);
-      const int lim = p.causal ? row + 1 : T;
-      float mx = -INFINITY;
+    for (int kb = 0; kb < 2; ++kb) {
+      const int room = lim - (k0 + 32 * kb + 8 * h32);
 #pragma unroll
-      for (int kb = 0; kb < 2; ++kb) {
-        // key of register i = k0 + 32kb + 8*h32 + (16((i>>2)>>1) + 4((i>>2)&1) + (i&3))
-        const int room = lim - (k0 + 32 * kb + 8 * h32);
-#pragma unroll
-        for (int i = 0; i < 16; ++i) {
+      for (int i = 0; i < 16; ++i) {
+        if constexpr (MASK) {
           const int koff = 16 * ((i >> 2) >> 1) + 4 * ((i >> 2) & 1) + (i & 3);
-          float x = sacc[r][kb][i] * sl2;
-          if (edge) x = koff < room ? x : -INFINITY;
-          sacc[r][kb][i] = x;
-          mx = fmaxf(mx, x);
+          sacc[kb][i] = koff < room ? sacc[kb][i] : -INFINITY;
         }
-      }
-      mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
-      // Conditional rescaling: a row keeps its reference max until a block raises
-      // it by more than FA_TAU (log2 units), so p = 2^(x - m) stays below 2^FA_TAU
-      // and the O accumulators are rescaled only on the rare blocks where some row
-      // of the wave moves its reference (the result is the same for any reference
-      // max; only the rounding of intermediate values differs).  A row with no
-      // visible key yet (m = -inf) has O = 0 and l = 0 and just takes the new max.
-      const float m_old = m_run[r];
-      const bool fresh = m_old == -INFINITY;
-      const bool raise = !fresh && mx > m_old + FA_TAU;
-      const float m_ref = (fresh || raise) ? mx : m_old;
-      if (__any(raise)) {
-        const float alpha = raise ? __builtin_amdgcn_exp2f(m_old - m_ref) : 1.0f;
-        l_run[r] *= alpha;
-#pragma unroll
-        for (int c = 0; c < NC; ++c)
-#pragma unroll
-          for (int e = 0; e < 16; ++e) o[r][c][e] *= alpha;
-      }
-      m_run[r] = m_ref;
-      // rows with no visible key in any block so far (non-causal tail rows) stay
-      // at m = -inf; exp2 against 0 keeps their p at 0
-      const float m_use = m_ref == -INFINITY ? 0.0f : m_ref;
-      float sum = 0.0f;
-#pragma unroll
-      for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-        for (int i = 0; i < 16; ++i) {
-          const float e = __builtin_amdgcn_exp2f(sacc[r][kb][i] - m_use);
-          sacc[r][kb][i] = e;
-          sum += e;
-        }
-      l_run[r] += sum;
-      // k-step ks covers keys 16ks .. 16ks+15: registers 8(ks&1) .. +7 of half ks>>1
-#pragma unroll
-      for (int ks = 0; ks < 4; ++ks) {
-        const int kb = ks >> 1, base = 8 * (ks & 1);
-#pragma unroll
-        for (int w2 = 0; w2 < 4; ++w2)
-          pf[r][ks][w2] = pack_bf16x2(sacc[r][kb][base + 2 * w2], sacc[r][kb][base + 2 * w2 + 1]);
+        mx = fmaxf(mx, sacc[kb][i]);
       }
     }
+    mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+    // Conditional rescaling: a row keeps its reference max until a block raises
+    // it by more than FA_TAU (in log2 units of p), so p stays below 2^FA_TAU and O
+    // is rescaled only on the blocks where some row of the wave moves its
+    // reference -- the result is the same for any reference max, only the
+    // rounding of intermediate values differs.  A row with no visible key yet
+    // (m = -inf) has O = 0 and l = 0 and just takes the new max.
+    const float m_old = m_run;
+    const bool fresh = m_old == -INFINITY;
+    const bool raise = !fresh && (mx - m_old) * sl2 > FA_TAU;
+    const float m_ref = (fresh || raise) ? mx : m_old;
+    if (__any(raise)) {
+      const float alpha = raise ? __builtin_amdgcn_exp2f((m_old - m_ref) * sl2) : 1.0f;
+      l_run *= alpha;
+#pragma unroll
+      for (int c = 0; c < NC; ++c)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) o[c][e] *= alpha;
+    }
+    m_run = m_ref;
+    // rows with no visible key so far (non-causal tail rows) stay at m = -inf;
+    // their p is 2^(-inf) = 0
+    const float nmc = m_ref == -INFINITY ? 0.0f : -m_ref * sl2;
+    float sum = 0.0f;
+    u32x4_t pf[4];
+    // k-step ks covers keys 16ks .. 16ks+15: registers 8(ks&1) .. +7 of half ks>>1
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) {
+      const int kb = ks >> 1, base = 8 * (ks & 1);
+#pragma unroll
+      for (int w2 = 0; w2 < 4; ++w2) {
+        const float e0 = __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[kb][base + 2 * w2], sl2, nmc));
+        const float e1 = __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[kb][base + 2 * w2 + 1], sl2, nmc));
+        sum += e0 + e1;
+        pf[ks][w2] = pack_bf16x2(e0, e1);
+      }
+    }
+    l_run += sum;
 
     // ---- O += P V ----
     static_for<4>([&](auto ks_c) __attribute__((always_inline)) {
@@ -290,38 +266,57 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1)))
           vf[c][2 * t + 1] = w2[1];
         });
       }
-      __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): the transposing reads are in
+      // The asm results are only valid after lgkmcnt(0), which the compiler does
+      // not know: the scheduling barrier keeps the MFMAs below the wait.
+      __builtin_amdgcn_s_waitcnt(0xC07F);
+      __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
       for (int c = 0; c < NC; ++c)
-#pragma unroll
-        for (int r = 0; r < 2; ++r)
-          o[r][c] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, vf[c]),
-                                                            __builtin_bit_cast(bf16x8_t, pf[r][ks]),
-                                                            o[r][c], 0, 0, 0);
+        o[c] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, vf[c]),
+                                                       __builtin_bit_cast(bf16x8_t, pf[ks]), o[c],
+                                                       0, 0, 0);
     });
+  };
+
+  // Blocks 0 .. jd-1 are visible to every row of the wave (no mask); the rest
+  // hold the causal diagonal or the key tail.  Both loops run one ring step per
+  // block, so every wave passes the same barriers.
+  const int jd = uniform(p.causal ? (qw + 1) / FA_BK : T / FA_BK);
+  const int j_split = jd < nblk ? jd : nblk;
+  auto ring_step = [&](int j) __attribute__((always_inline)) {
+    wait_vmcnt<0>();     // this wave's share of block j (and the Q loads) landed
+    lds_ring_barrier();  // every share landed; every wave is done with block j-1
+    if (j + 1 < nblk) issue_block(j + 1);
+    return lds0 + (uint32_t)((j & 1) * STAGE);
+  };
+  if (nblk > 0) issue_block(0);
+  for (int j = 0; j < j_split; ++j) {
+    const uint32_t st = ring_step(j);
+    block(j * FA_BK, st, std::false_type{});
+  }
+  for (int j = j_split; j < nblk; ++j) {
+    const uint32_t st = ring_step(j);
+    if (p.causal && j * FA_BK > qw + 31) continue;  // above every row of this wave
+    block(j * FA_BK, st, std::true_type{});
   }
 
   // ---- normalise and store ----
+  const float l_tot = l_run + __shfl_xor(l_run, 32, 64);
+  const float inv = l_tot > 0.0f ? 1.0f / l_tot : 0.0f;
+  if (row < T) {
+    uint16_t* orow = (uint16_t*)p.O + (p.o_bthd ? ((int64_t)(b * T + row) * p.nH + h) * D
+                                                : ((int64_t)bh * T + row) * D);
 #pragma unroll
-  for (int r = 0; r < 2; ++r) {
-    const int row = qw + 32 * r + l32;
-    const float l_tot = l_run[r] + __shfl_xor(l_run[r], 32, 64);
-    const float inv = l_tot > 0.0f ? 1.0f / l_tot : 0.0f;
-    if (row < T) {
-      uint16_t* orow = (uint16_t*)p.O + (p.o_bthd ? ((int64_t)(b * T + row) * p.nH + h) * D
-                                                  : ((int64_t)bh * T + row) * D);
+    for (int c = 0; c < NC; ++c)
 #pragma unroll
-      for (int c = 0; c < NC; ++c)
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {
-          const int d = 32 * c + 8 * q + 4 * h32;
-          *(u32x2_t*)(orow + d) = u32x2_t{pack_bf16x2(o[r][c][4 * q] * inv, o[r][c][4 * q + 1] * inv),
-                                          pack_bf16x2(o[r][c][4 * q + 2] * inv, o[r][c][4 * q + 3] * inv)};
-        }
-      if (p.lse && h32 == 0)
-        p.lse[(int64_t)bh * T + row] = l_tot > 0.0f ? (m_run[r] + __log2f(l_tot)) * 0.69314718055994531f
-                                                   : -INFINITY;
-    }
+      for (int q = 0; q < 4; ++q) {
+        const int d = 32 * c + 8 * q + 4 * h32;
+        *(u32x2_t*)(orow + d) = u32x2_t{pack_bf16x2(o[c][4 * q] * inv, o[c][4 * q + 1] * inv),
+                                        pack_bf16x2(o[c][4 * q + 2] * inv, o[c][4 * q + 3] * inv)};
+      }
+    if (p.lse && h32 == 0)
+      p.lse[(int64_t)bh * T + row] = l_tot > 0.0f ? (m_run * sl2 + __log2f(l_tot)) * 0.69314718055994531f
+                                                 : -INFINITY;
   }
 }
 
