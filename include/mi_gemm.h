@@ -172,6 +172,23 @@ int mi_flash_attn_fwd(void* stream, const void* Q, const void* K, const void* V,
                       int64_t head_dim, int32_t causal, int32_t o_layout);
 
 /*
+ * Fused GQA attention backward (FlashAttention-2 form), causal as in the
+ * forward: from Q, K, V, the forward's O and lse and the output gradient dO,
+ * computes dQ [batch, n_heads, seq_len, d] and dK, dV [batch, n_kv, seq_len, d]
+ * (bf16), dK/dV summed over the n_heads/n_kv query heads of each KV head.  O
+ * and dO use o_layout; delta is caller workspace of batch*n_heads*seq_len fp32
+ * (receives rowsum(dO * O)).  Two kernels on `stream`, deterministic (no
+ * atomics).  head_dim must be 128.  Replaces metal_bridge::fused_attn_bwd
+ * (MetalBridge.hpp:54-57; that kernel recomputes the forward itself, this one
+ * takes the forward's O and lse) and the backward of Attention::backward
+ * (Attention.cpp:292-348).
+ */
+int mi_flash_attn_bwd(void* stream, const void* Q, const void* K, const void* V, const void* O,
+                      const void* dO, const float* lse, void* dQ, void* dK, void* dV, float* delta,
+                      int64_t batch, int64_t n_heads, int64_t n_kv, int64_t seq_len,
+                      int64_t head_dim, int32_t causal, int32_t o_layout);
+
+/*
  * Describe the kernel mi_gemm_batched would launch for this problem (tile,
  * loader, split-K factor) as text into buf (always NUL-terminated).  For
  * measurement and logging; no reference counterpart.  epi_mode: 0 plain,

@@ -60,6 +60,13 @@ struct FaTile {
   // V tile [key][d]: chunk q of key row r at position q ^ ((r & 3) << 2); a
   // transposing read touches 4 consecutive key rows -> 4 distinct 64-byte groups.
   __device__ static __forceinline__ int v_pos(int r, int q) { return q ^ ((r & 3) << 2); }
+  // Tiles read both ways (backward): chunk c of row r at c ^ f(r), f(r) = (r & 3) << 2
+  // | (r >> 2) & 3.  f is a bijection on r & 15, so the row reads stay conflict
+  // free, and the 4 rows of a transposing read share bits 0-1 of f, so their
+  // 32-byte chunk pairs still land in 4 distinct 64-byte groups.
+  __device__ static __forceinline__ int x_pos(int r, int c) {
+    return c ^ (((r & 3) << 2) | ((r >> 2) & 3));
+  }
 };
 
 template <int D>
@@ -175,21 +182,23 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2)))
     for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
       for (int e = 0; e < 16; ++e) sacc[kb][e] = 0.0f;
+    // all K fragments of the block first, so the MFMAs do not wait on each read
+    u32x4_t kf[NS][2];
 #pragma unroll
-    for (int s = 0; s < NS; ++s) {
-      u32x4_t kf[2];
+    for (int s = 0; s < NS; ++s)
 #pragma unroll
       for (int kb = 0; kb < 2; ++kb) {
         const int c = 2 * s + h32;
         const uint32_t a = st + k_rd + (uint32_t)(32 * kb * Tl::ROW) + (uint32_t)(16 * (c ^ k_row_lo));
-        kf[kb] = *(const lds_u32x4_t*)(uintptr_t)a;
+        kf[s][kb] = *(const lds_u32x4_t*)(uintptr_t)a;
       }
 #pragma unroll
+    for (int s = 0; s < NS; ++s)
+#pragma unroll
       for (int kb = 0; kb < 2; ++kb)
-        sacc[kb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, kf[kb]),
+        sacc[kb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, kf[s][kb]),
                                                           __builtin_bit_cast(bf16x8_t, qf[s]),
                                                           sacc[kb], 0, 0, 0);
-    }
 
     // ---- online softmax, P fragments ----
     // sacc[kb][i], i = 4q + e, is key k0 + 32kb + 8*h32 + 16(q>>1) + 4(q&1) + e of
@@ -320,9 +329,491 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2)))
   }
 }
 
+// Lane-row reads of a 32-row half of a [row][d] tile read with the bit-2/3 swapped
+// row order: rows 32*half + perm(l32), d chunk 2s + h32.  Transposing reads of the
+// same tile: rows 16ks + 8*(g>>1) + (j>>2) (+4), d columns 32c + 16(g&1) + 4(j&3).
+template <int D>
+struct FaReads {
+  uint32_t row_base;  // perm(l32) * ROW
+  int row_lo;         // perm(l32) & 15
+  // transposing-read bases for the rows krb (first read) and krb + 4 (second): the
+  // swizzle depends on row bits 2-3, so the two reads need their own base
+  uint32_t tr[D / 32][2];
+  __device__ __forceinline__ void init(int lane) {
+    using Tl = FaTile<D>;
+    const int l32 = lane & 31;
+    row_base = (uint32_t)(fa_key_perm(l32) * Tl::ROW);
+    row_lo = fa_key_perm(l32) & 15;
+    const int g = lane >> 4, jj = lane & 15;
+    const int krb = 8 * (g >> 1) + (jj >> 2);
+#pragma unroll
+    for (int c = 0; c < D / 32; ++c) {
+      const int col = 32 * c + 16 * (g & 1) + 4 * (jj & 3);
+#pragma unroll
+      for (int t = 0; t < 2; ++t) {
+        const int r = krb + 4 * t;
+        tr[c][t] = (uint32_t)(r * Tl::ROW + 16 * Tl::x_pos(r, col >> 3) + (col & 7) * 2);
+      }
+    }
+  }
+  // 16 bytes of row-read fragment (half, k-step s) of the tile at LDS address t
+  __device__ __forceinline__ u32x4_t row(uint32_t t, int half, int s, int h32) const {
+    using Tl = FaTile<D>;
+    const int c = 2 * s + h32;
+    // rows 32*half + perm(l32): (r & 15) is row_lo for both halves
+    const uint32_t a = t + row_base + (uint32_t)(32 * half * Tl::ROW) +
+                       (uint32_t)(16 * (c ^ (((row_lo & 3) << 2) | ((row_lo >> 2) & 3))));
+    return *(const lds_u32x4_t*)(uintptr_t)a;
+  }
+};
+
+// Transposing fragment (d block c, key/query k-step KS) of the tile at LDS address
+// t: two ds_read_b64_tr_b16.  The caller waits lgkmcnt(0) and fences the scheduler
+// before using the result.
+template <int D, int KS>
+__device__ __forceinline__ u32x4_t fa_tr_frag(uint32_t t, const uint32_t* tr) {
+  [[maybe_unused]] constexpr int ROW = FaTile<D>::ROW;
+  u32x4_t out = {0u, 0u, 0u, 0u};
+  static_for<2>([&](auto t_c) __attribute__((always_inline)) {
+    constexpr int TT = decltype(t_c)::value;
+    u32x2_t w2 = {0u, 0u};
+#if defined(__HIP_DEVICE_COMPILE__)
+    // rows 16KS + krb + 4TT: 16KS leaves the swizzle unchanged, an immediate offset
+    asm volatile("ds_read_b64_tr_b16 %0, %1 offset:%2"
+                 : "=v"(w2)
+                 : "v"(t + tr[TT]), "i"(16 * KS * ROW));
+#endif
+    out[2 * TT] = w2[0];
+    out[2 * TT + 1] = w2[1];
+  });
+  return out;
+}
+
+__device__ __forceinline__ void fa_lds_fence() {
+  __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
+  __builtin_amdgcn_sched_barrier(0);
+}
+
+// One 16-byte DMA of a [row][d] tile: lane l of 1 KB block u covers row 4u + l/16,
+// LDS position l % 16 (dual swizzle), reading row `r` of a matrix whose rows are
+// `stride` bytes apart.
+template <int D>
+__device__ __forceinline__ uint32_t fa_dma_off(int u, int lane, int stride) {
+  using Tl = FaTile<D>;
+  const int r = 4 * u + (lane >> 4), pos = lane & 15;
+  return (uint32_t)(r * stride + 16 * Tl::x_pos(r, pos));  // x_pos is an involution in c
+}
+
+// dQ for 128 query rows of one (batch, head): recompute S = Q K^T and P from the
+// forward's log-sum-exp, dP = dO V^T, dS = P (dP - D), dQ = scale * dS K, with the
+// K/V blocks streamed like the forward's.  D = rowsum(dO O) is computed here from
+// the rows this workgroup owns and written for the dK/dV kernel.
+template <int D>
+__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2)))
+    flash_bwd_dq_kernel(FbParams p) {
+  using Tl = FaTile<D>;
+  using Rd = FaReads<D>;
+  constexpr int NS = D / 16, NC = D / 32;
+  constexpr int STAGE = 2 * Tl::BYTES;
+  __shared__ __attribute__((aligned(16))) char smem[2 * STAGE];
+  const uint32_t lds0 = lds_addr(smem);
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int wave_u = uniform(wave);
+  const int h32 = lane >> 5, l32 = lane & 31;
+
+  const int BH = p.B * p.nH;
+  const int lid = uniform(fa_xcd_major(blockIdx.x, gridDim.x));
+  const int qb = uniform(p.q_blocks - 1 - lid / BH);
+  const int bh = uniform(lid - (lid / BH) * BH);
+  const int b = uniform(bh / p.nH), h = uniform(bh - (bh / p.nH) * p.nH);
+  const int kvh = uniform(h / p.group);
+  const int T = p.T;
+  const int q0 = qb * FA_BQ;
+  const int qw = q0 + 32 * wave_u;
+  const int row = qw + l32;
+  const bool live = row < T;
+
+  const __bf16* Qb = (const __bf16*)p.Q + ((int64_t)bh * T) * D;
+  const __bf16* Kb = (const __bf16*)p.K + ((int64_t)(b * p.nKV + kvh) * T) * D;
+  const __bf16* Vb = (const __bf16*)p.V + ((int64_t)(b * p.nKV + kvh) * T) * D;
+  const int64_t orow = p.o_bthd ? ((int64_t)(b * T + row) * p.nH + h) * D : ((int64_t)bh * T + row) * D;
+
+  // Q and dO fragments (second MFMA operands), the row's D and log-sum-exp.
+  u32x4_t qf[NS], gf[NS];
+  float dsum = 0.0f;
+#pragma unroll
+  for (int s = 0; s < NS; ++s) {
+    const int dd = 16 * s + 8 * h32;
+    if (live) {
+      qf[s] = *(const u32x4_t*)(Qb + (int64_t)row * D + dd);
+      gf[s] = *(const u32x4_t*)((const __bf16*)p.dO + orow + dd);
+      const u32x4_t of = *(const u32x4_t*)((const __bf16*)p.O + orow + dd);
+#pragma unroll
+      for (int w2 = 0; w2 < 4; ++w2)
+        dsum += bf16_bits_to_f32(gf[s][w2] & 0xffffu) * bf16_bits_to_f32(of[w2] & 0xffffu) +
+                bf16_bits_to_f32(gf[s][w2] >> 16) * bf16_bits_to_f32(of[w2] >> 16);
+    } else {
+      qf[s] = u32x4_t{0u, 0u, 0u, 0u};
+      gf[s] = u32x4_t{0u, 0u, 0u, 0u};
+    }
+  }
+  dsum += __shfl_xor(dsum, 32, 64);
+  if (live && h32 == 0) p.delta[(int64_t)bh * T + row] = dsum;
+  const float lse2 = live ? p.lse[(int64_t)bh * T + row] * 1.4426950408889634f : 0.0f;
+  const float sl2 = p.scale_log2;
+
+  const int kv_end = p.causal ? (q0 + FA_BQ < T ? q0 + FA_BQ : T) : T;
+  const int nblk = uniform((kv_end + FA_BK - 1) / FA_BK);
+
+  // DMA of the K and V blocks (dual swizzle: both are read as rows and transposed)
+  uint32_t offs[Tl::NU];
+#pragma unroll
+  for (int u = 0; u < Tl::NU; ++u) offs[u] = fa_dma_off<D>(wave * Tl::NU + u, lane, Tl::ROW);
+  const uint32_t dma_k = lds0 + (uint32_t)(wave_u * Tl::NU * 1024);
+  const uint32_t dma_v = dma_k + Tl::BYTES;
+  auto issue_block = [&](int j) __attribute__((always_inline)) {
+    const int k0 = j * FA_BK;
+    const uint32_t ext = (uint32_t)((T - k0) * Tl::ROW);
+    const __amdgpu_buffer_rsrc_t rk = scalar_rsrc(uniform(Kb + (int64_t)k0 * D), ext);
+    const __amdgpu_buffer_rsrc_t rv = scalar_rsrc(uniform(Vb + (int64_t)k0 * D), ext);
+    const uint32_t st = (uint32_t)((j & 1) * STAGE);
+#pragma unroll
+    for (int u = 0; u < Tl::NU; ++u) {
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(
+          rk, (__attribute__((address_space(3))) void*)(uintptr_t)(dma_k + st + (uint32_t)(u * 1024)), 16,
+          (int)offs[u], 0, 0, 0);
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(
+          rv, (__attribute__((address_space(3))) void*)(uintptr_t)(dma_v + st + (uint32_t)(u * 1024)), 16,
+          (int)offs[u], 0, 0, 0);
+    }
+  };
+  Rd rd;
+  rd.init(lane);
+
+  f32x16_t dq[NC];
+#pragma unroll
+  for (int c = 0; c < NC; ++c)
+#pragma unroll
+    for (int e = 0; e < 16; ++e) dq[c][e] = 0.0f;
+  const int lim = p.causal ? row + 1 : T;
+
+  auto block = [&](const int k0, const uint32_t st, auto MASK_c) __attribute__((always_inline)) {
+    constexpr bool MASK = decltype(MASK_c)::value;
+    const uint32_t tk = st, tv = st + Tl::BYTES;
+    f32x16_t sacc[2], pacc[2];
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) sacc[kb][e] = pacc[kb][e] = 0.0f;
+#pragma unroll
+    for (int s = 0; s < NS; ++s)
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb) {
+        const u32x4_t kf = rd.row(tk, kb, s, h32);
+        const u32x4_t vf = rd.row(tv, kb, s, h32);
+        sacc[kb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, kf),
+                                                          __builtin_bit_cast(bf16x8_t, qf[s]),
+                                                          sacc[kb], 0, 0, 0);
+        pacc[kb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, vf),
+                                                          __builtin_bit_cast(bf16x8_t, gf[s]),
+                                                          pacc[kb], 0, 0, 0);
+      }
+    // register i of half kb: key k0 + 32kb + 8*h32 + 16((i>>2)>>1) + 4((i>>2)&1) + (i&3)
+    u32x4_t df[4];
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) {
+      const int kb = ks >> 1, base = 8 * (ks & 1);
+      const int room = lim - (k0 + 32 * kb + 8 * h32);
+#pragma unroll
+      for (int w2 = 0; w2 < 4; ++w2) {
+        float ds[2];
+#pragma unroll
+        for (int u = 0; u < 2; ++u) {
+          const int i = base + 2 * w2 + u;
+          float x = __builtin_fmaf(sacc[kb][i], sl2, -lse2);
+          if constexpr (MASK) {
+            const int koff = 16 * ((i >> 2) >> 1) + 4 * ((i >> 2) & 1) + (i & 3);
+            x = koff < room ? x : -INFINITY;
+          }
+          ds[u] = __builtin_amdgcn_exp2f(x) * (pacc[kb][i] - dsum);
+        }
+        df[ks][w2] = pack_bf16x2(ds[0], ds[1]);
+      }
+    }
+    // dQ += dS K: first operand K^T through the transposing read of the K tile
+    static_for<4>([&](auto ks_c) __attribute__((always_inline)) {
+      constexpr int KS = decltype(ks_c)::value;
+      u32x4_t kt[NC];
+#pragma unroll
+      for (int c = 0; c < NC; ++c) kt[c] = fa_tr_frag<D, KS>(tk, rd.tr[c]);
+      fa_lds_fence();
+#pragma unroll
+      for (int c = 0; c < NC; ++c)
+        dq[c] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, kt[c]),
+                                                        __builtin_bit_cast(bf16x8_t, df[KS]), dq[c],
+                                                        0, 0, 0);
+    });
+  };
+
+  const int jd = uniform(p.causal ? (qw + 1) / FA_BK : T / FA_BK);
+  const int j_split = jd < nblk ? jd : nblk;
+  auto ring_step = [&](int j) __attribute__((always_inline)) {
+    wait_vmcnt<0>();
+    lds_ring_barrier();
+    if (j + 1 < nblk) issue_block(j + 1);
+    return lds0 + (uint32_t)((j & 1) * STAGE);
+  };
+  if (nblk > 0) issue_block(0);
+  for (int j = 0; j < j_split; ++j) {
+    const uint32_t st = ring_step(j);
+    block(j * FA_BK, st, std::false_type{});
+  }
+  for (int j = j_split; j < nblk; ++j) {
+    const uint32_t st = ring_step(j);
+    if (p.causal && j * FA_BK > qw + 31) continue;
+    block(j * FA_BK, st, std::true_type{});
+  }
+
+  if (live) {
+    uint16_t* out = (uint16_t*)p.dQ + ((int64_t)bh * T + row) * D;
+#pragma unroll
+    for (int c = 0; c < NC; ++c)
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const int d = 32 * c + 8 * q + 4 * h32;
+        *(u32x2_t*)(out + d) = u32x2_t{pack_bf16x2(dq[c][4 * q] * p.scale, dq[c][4 * q + 1] * p.scale),
+                                       pack_bf16x2(dq[c][4 * q + 2] * p.scale, dq[c][4 * q + 3] * p.scale)};
+      }
+  }
+}
+
+// dK and dV for 128 keys of one (batch, KV head): the query tiles (64 rows) of
+// every query head of the KV group stream through a two-stage LDS ring (Q, dO,
+// the forward's log-sum-exp and D); a wave keeps its 32 keys' K and V fragments
+// and dK / dV accumulators in registers, computes S^T = K Q^T and dP^T = V dO^T
+// with one lane per key, P^T and dS^T = P^T (dP^T - D) in registers, and
+// accumulates dV += P^T dO and dK += scale * dS^T Q.  The KV-group reduction
+// (Attention.cpp:332,344-345) is the loop over the group's heads.
+template <int D>
+__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1)))
+    flash_bwd_dkdv_kernel(FbParams p) {
+  using Tl = FaTile<D>;
+  using Rd = FaReads<D>;
+  constexpr int NS = D / 16, NC = D / 32;
+  constexpr int QT = FA_BK;                      // query rows per tile
+  constexpr int STAGE = 2 * Tl::BYTES + 2 * QT * 4;  // Q, dO, lse, D
+  __shared__ __attribute__((aligned(16))) char smem[2 * STAGE];
+  const uint32_t lds0 = lds_addr(smem);
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int wave_u = uniform(wave);
+  const int h32 = lane >> 5, l32 = lane & 31;
+
+  // Key blocks with the most query tiles (the first ones, causal) go first.
+  const int BKV = p.B * p.nKV;
+  const int lid = uniform(fa_xcd_major(blockIdx.x, gridDim.x));
+  const int kbi = uniform(lid / BKV);
+  const int bkv = uniform(lid - kbi * BKV);
+  const int b = uniform(bkv / p.nKV), kvh = uniform(bkv - (bkv / p.nKV) * p.nKV);
+  const int T = p.T;
+  const int k0 = kbi * 128;
+  const int kw = k0 + 32 * wave_u;
+  const int key = kw + l32;
+  const bool live = key < T;
+
+  const __bf16* Kb = (const __bf16*)p.K + ((int64_t)bkv * T) * D;
+  const __bf16* Vb = (const __bf16*)p.V + ((int64_t)bkv * T) * D;
+  u32x4_t kf[NS], vf[NS];
+#pragma unroll
+  for (int s = 0; s < NS; ++s) {
+    const int dd = 16 * s + 8 * h32;
+    if (live) {
+      kf[s] = *(const u32x4_t*)(Kb + (int64_t)key * D + dd);
+      vf[s] = *(const u32x4_t*)(Vb + (int64_t)key * D + dd);
+    } else {
+      kf[s] = u32x4_t{0u, 0u, 0u, 0u};
+      vf[s] = u32x4_t{0u, 0u, 0u, 0u};
+    }
+  }
+
+  const int nqt = (T + QT - 1) / QT;
+  const int qt0 = uniform(p.causal ? k0 / QT : 0);
+  const int per_h = uniform(nqt - qt0);
+  const int total = uniform(per_h > 0 ? per_h * p.group : 0);
+  const int go_stride = (p.o_bthd ? p.nH * D : D) * 2;  // bytes between dO rows
+
+  uint32_t q_off[Tl::NU], g_off[Tl::NU];
+#pragma unroll
+  for (int u = 0; u < Tl::NU; ++u) {
+    q_off[u] = fa_dma_off<D>(wave * Tl::NU + u, lane, Tl::ROW);
+    g_off[u] = fa_dma_off<D>(wave * Tl::NU + u, lane, go_stride);
+  }
+  const uint32_t dma_q = lds0 + (uint32_t)(wave_u * Tl::NU * 1024);
+  const uint32_t dma_g = dma_q + Tl::BYTES;
+  const uint32_t dma_l = lds0 + 2 * Tl::BYTES + (uint32_t)(wave_u * QT * 4);  // waves 0, 1
+  auto tile_of = [&](int it, int& h, int& q0) __attribute__((always_inline)) {
+    const int hh = it / per_h;
+    h = kvh * p.group + hh;
+    q0 = (qt0 + (it - hh * per_h)) * QT;
+  };
+  auto issue = [&](int it) __attribute__((always_inline)) {
+    int h, q0;
+    tile_of(it, h, q0);
+    const int bh = b * p.nH + h;
+    const int rows = T - q0;
+    const __amdgpu_buffer_rsrc_t rq =
+        scalar_rsrc(uniform((const __bf16*)p.Q + ((int64_t)bh * T + q0) * D), (uint32_t)(rows * Tl::ROW));
+    const int64_t g0 = p.o_bthd ? ((int64_t)(b * T + q0) * p.nH + h) * D : ((int64_t)bh * T + q0) * D;
+    const __amdgpu_buffer_rsrc_t rg = scalar_rsrc(uniform((const __bf16*)p.dO + g0),
+                                                  (uint32_t)((rows - 1) * go_stride + Tl::ROW));
+    const uint32_t st = (uint32_t)((it & 1) * STAGE);
+#pragma unroll
+    for (int u = 0; u < Tl::NU; ++u) {
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(
+          rq, (__attribute__((address_space(3))) void*)(uintptr_t)(dma_q + st + (uint32_t)(u * 1024)), 16,
+          (int)q_off[u], 0, 0, 0);
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(
+          rg, (__attribute__((address_space(3))) void*)(uintptr_t)(dma_g + st + (uint32_t)(u * 1024)), 16,
+          (int)g_off[u], 0, 0, 0);
+    }
+    if (wave_u < 2) {  // wave 0: log-sum-exp, wave 1: D, 4 bytes per lane
+      const float* src = (wave_u == 0 ? p.lse : p.delta) + (int64_t)bh * T + q0;
+      const __amdgpu_buffer_rsrc_t rl = scalar_rsrc(uniform(src), (uint32_t)(rows * 4));
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(
+          rl, (__attribute__((address_space(3))) void*)(uintptr_t)(dma_l + st), 4, lane * 4, 0, 0, 0);
+    }
+  };
+  Rd rd;
+  rd.init(lane);
+
+  f32x16_t dk[NC], dv[NC];
+#pragma unroll
+  for (int c = 0; c < NC; ++c)
+#pragma unroll
+    for (int e = 0; e < 16; ++e) dk[c][e] = dv[c][e] = 0.0f;
+  const float sl2 = p.scale_log2;
+
+  auto block = [&](const int q0, const uint32_t st, auto MASK_c) __attribute__((always_inline)) {
+    constexpr bool MASK = decltype(MASK_c)::value;
+    const uint32_t tq = st, tg = st + Tl::BYTES, tl = st + 2 * Tl::BYTES, td = tl + QT * 4;
+    f32x16_t sacc[2], pacc[2];
+#pragma unroll
+    for (int qh = 0; qh < 2; ++qh)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) sacc[qh][e] = pacc[qh][e] = 0.0f;
+#pragma unroll
+    for (int s = 0; s < NS; ++s)
+#pragma unroll
+      for (int qh = 0; qh < 2; ++qh) {
+        const u32x4_t qr = rd.row(tq, qh, s, h32);
+        const u32x4_t gr = rd.row(tg, qh, s, h32);
+        sacc[qh] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, qr),
+                                                          __builtin_bit_cast(bf16x8_t, kf[s]),
+                                                          sacc[qh], 0, 0, 0);
+        pacc[qh] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, gr),
+                                                          __builtin_bit_cast(bf16x8_t, vf[s]),
+                                                          pacc[qh], 0, 0, 0);
+      }
+    // register i of half qh: query q0 + 32qh + 8*h32 + 16((i>>2)>>1) + 4((i>>2)&1) + (i&3)
+    u32x4_t pf[4], df[4];
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) {
+      const int qh = ks >> 1, base = 8 * (ks & 1);
+      const int tix = 32 * qh + 8 * h32 + 16 * (ks & 1);  // tile index of register `base`
+      // registers base..base+3 and base+4..base+7 hold 4 consecutive queries each
+      const f32x4_t l0 = *(const __attribute__((address_space(3))) f32x4_t*)(uintptr_t)(tl + 4 * tix);
+      const f32x4_t l1 = *(const __attribute__((address_space(3))) f32x4_t*)(uintptr_t)(tl + 4 * (tix + 4));
+      const f32x4_t d0 = *(const __attribute__((address_space(3))) f32x4_t*)(uintptr_t)(td + 4 * tix);
+      const f32x4_t d1 = *(const __attribute__((address_space(3))) f32x4_t*)(uintptr_t)(td + 4 * (tix + 4));
+      const int need = key - (q0 + tix);  // register base + r is visible iff its offset >= need
+#pragma unroll
+      for (int w2 = 0; w2 < 4; ++w2) {
+        float pv[2], dsv[2];
+#pragma unroll
+        for (int u = 0; u < 2; ++u) {
+          const int r = 2 * w2 + u;  // 0..7 within the run: offsets 0..3, then 4..7
+          const float lse2 = (r < 4 ? l0[r] : l1[r - 4]) * 1.4426950408889634f;
+          const float dl = r < 4 ? d0[r] : d1[r - 4];
+          float x = __builtin_fmaf(sacc[qh][base + r], sl2, -lse2);
+          if constexpr (MASK) x = r >= need ? x : -INFINITY;
+          pv[u] = __builtin_amdgcn_exp2f(x);
+          dsv[u] = pv[u] * (pacc[qh][base + r] - dl);
+        }
+        pf[ks][w2] = pack_bf16x2(pv[0], pv[1]);
+        df[ks][w2] = pack_bf16x2(dsv[0], dsv[1]);
+      }
+    }
+    // dV += P^T dO (first operand dO^T), dK += dS^T Q (first operand Q^T)
+    static_for<4>([&](auto ks_c) __attribute__((always_inline)) {
+      constexpr int KS = decltype(ks_c)::value;
+      u32x4_t gt[NC], qt[NC];
+#pragma unroll
+      for (int c = 0; c < NC; ++c) {
+        gt[c] = fa_tr_frag<D, KS>(tg, rd.tr[c]);
+        qt[c] = fa_tr_frag<D, KS>(tq, rd.tr[c]);
+      }
+      fa_lds_fence();
+#pragma unroll
+      for (int c = 0; c < NC; ++c) {
+        dv[c] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, gt[c]),
+                                                        __builtin_bit_cast(bf16x8_t, pf[KS]), dv[c],
+                                                        0, 0, 0);
+        dk[c] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, qt[c]),
+                                                        __builtin_bit_cast(bf16x8_t, df[KS]), dk[c],
+                                                        0, 0, 0);
+      }
+    });
+  };
+
+  if (total > 0) issue(0);
+  for (int it = 0; it < total; ++it) {
+    wait_vmcnt<0>();
+    lds_ring_barrier();
+    if (it + 1 < total) issue(it + 1);
+    int h, q0;
+    tile_of(it, h, q0);
+    (void)h;
+    q0 = uniform(q0);
+    if (p.causal && q0 + QT - 1 < kw) continue;  // every query of the tile precedes every key
+    const uint32_t st = lds0 + (uint32_t)((it & 1) * STAGE);
+    if (p.causal && q0 < kw + 31)
+      block(q0, st, std::true_type{});
+    else
+      block(q0, st, std::false_type{});
+  }
+
+  if (live) {
+    uint16_t* ok = (uint16_t*)p.dK + ((int64_t)bkv * T + key) * D;
+    uint16_t* ov = (uint16_t*)p.dV + ((int64_t)bkv * T + key) * D;
+#pragma unroll
+    for (int c = 0; c < NC; ++c)
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const int d = 32 * c + 8 * q + 4 * h32;
+        *(u32x2_t*)(ok + d) = u32x2_t{pack_bf16x2(dk[c][4 * q] * p.scale, dk[c][4 * q + 1] * p.scale),
+                                      pack_bf16x2(dk[c][4 * q + 2] * p.scale, dk[c][4 * q + 3] * p.scale)};
+        *(u32x2_t*)(ov + d) = u32x2_t{pack_bf16x2(dv[c][4 * q], dv[c][4 * q + 1]),
+                                      pack_bf16x2(dv[c][4 * q + 2], dv[c][4 * q + 3])};
+      }
+  }
+}
+
 }  // namespace
 
 int flash_fwd_blocks(int T) { return (T + FA_BQ - 1) / FA_BQ; }
+
+hipError_t launch_flash_bwd(const FbParams& p, int head_dim, hipStream_t stream) {
+  if (head_dim != 128) return hipErrorInvalidValue;
+  // dQ (and D) first: the dK/dV kernel reads D.
+  const int64_t nq = (int64_t)p.B * p.nH * p.q_blocks;
+  hipLaunchKernelGGL(flash_bwd_dq_kernel<128>, dim3((unsigned)nq), dim3(256), 0, stream, p);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  const int64_t nk = (int64_t)p.B * p.nKV * p.k_blocks;
+  hipLaunchKernelGGL(flash_bwd_dkdv_kernel<128>, dim3((unsigned)nk), dim3(256), 0, stream, p);
+  return hipGetLastError();
+}
+
+int flash_bwd_key_blocks(int T) { return (T + 127) / 128; }
 
 hipError_t launch_flash_fwd(const FaParams& p, int head_dim, hipStream_t stream) {
   const int64_t n = (int64_t)p.B * p.nH * p.q_blocks;

@@ -603,6 +603,50 @@ int mi_flash_attn_fwd(void* stream, const void* Q, const void* K, const void* V,
   return e == hipSuccess ? MI_OK : fail(MI_ERR_HIP, "flash attention launch: %s", hipGetErrorString(e));
 }
 
+int mi_flash_attn_bwd(void* stream, const void* Q, const void* K, const void* V, const void* O,
+                      const void* dO, const float* lse, void* dQ, void* dK, void* dV, float* delta,
+                      int64_t batch, int64_t n_heads, int64_t n_kv, int64_t seq_len,
+                      int64_t head_dim, int32_t causal, int32_t o_layout) {
+  if (batch < 0 || n_heads < 0 || n_kv < 0 || seq_len < 0)
+    return fail(MI_ERR_SHAPE, "negative size");
+  if (batch == 0 || n_heads == 0 || seq_len == 0) return MI_OK;
+  if (!Q || !K || !V || !O || !dO || !lse || !dQ || !dK || !dV || !delta)
+    return fail(MI_ERR_NULL, "an operand of the attention backward is NULL");
+  if (n_kv <= 0 || n_heads % n_kv != 0)
+    return fail(MI_ERR_SHAPE, "n_heads=%lld is not a multiple of n_kv=%lld", (long long)n_heads,
+                (long long)n_kv);
+  if (head_dim != 128)
+    return fail(MI_ERR_UNSUPPORTED, "flash attention supports head_dim 128 (got %lld)",
+                (long long)head_dim);
+  if (o_layout != MI_ATTN_O_BHTD && o_layout != MI_ATTN_O_BTHD)
+    return fail(MI_ERR_SHAPE, "unknown output layout %d", o_layout);
+  const void* a16[] = {Q, K, V, O, dO};
+  for (const void* q : a16)
+    if (!aligned16(q)) return fail(MI_ERR_UNSUPPORTED, "Q, K, V, O, dO must be 16-byte aligned");
+  if (((uintptr_t)dQ & 7u) || ((uintptr_t)dK & 7u) || ((uintptr_t)dV & 7u) || ((uintptr_t)lse & 15u) ||
+      ((uintptr_t)delta & 15u))
+    return fail(MI_ERR_UNSUPPORTED, "dQ, dK, dV must be 8-byte aligned, lse and delta 16-byte");
+  if (seq_len * head_dim * 2 * (o_layout == MI_ATTN_O_BTHD ? n_heads : 1) >= ((int64_t)1 << 31) ||
+      batch * n_heads * seq_len > INT32_MAX)
+    return fail(MI_ERR_SHAPE, "sequence too long");
+  int st = init_devices();
+  if (st != MI_OK) return st;
+  FbParams p;
+  p.Q = Q; p.K = K; p.V = V; p.O = O; p.dO = dO; p.lse = lse;
+  p.dQ = dQ; p.dK = dK; p.dV = dV; p.delta = delta;
+  p.B = (int)batch; p.nH = (int)n_heads; p.nKV = (int)n_kv; p.T = (int)seq_len;
+  p.group = (int)(n_heads / n_kv);
+  p.causal = causal != 0;
+  p.o_bthd = o_layout == MI_ATTN_O_BTHD;
+  p.q_blocks = flash_fwd_blocks(p.T);
+  p.k_blocks = flash_bwd_key_blocks(p.T);
+  p.scale = (float)(1.0 / std::sqrt((double)head_dim));
+  p.scale_log2 = (float)(1.4426950408889634 / std::sqrt((double)head_dim));
+  hipError_t e = launch_flash_bwd(p, (int)head_dim, (hipStream_t)stream);
+  return e == hipSuccess ? MI_OK : fail(MI_ERR_HIP, "flash attention backward launch: %s",
+                                        hipGetErrorString(e));
+}
+
 int mi_gemm_describe(int transA, int transB, int64_t M, int64_t N, int64_t K, int32_t dtype_in,
                      int64_t batch, int32_t epi_mode, size_t workspace_bytes, char* buf,
                      size_t buf_len) {

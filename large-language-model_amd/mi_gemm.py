@@ -33,7 +33,7 @@ MI_CAUSAL_NONE, MI_CAUSAL_OUT_LOWER, MI_CAUSAL_A_LOWER, MI_CAUSAL_A_UPPER = 0, 1
 C_SYMBOLS = (
     "mi_init", "mi_last_error", "mi_version", "mi_gemm_workspace_size", "mi_gemm",
     "mi_gemm_batched", "mi_residual_add", "mi_softmax_causal", "mi_softmax_bwd",
-    "mi_gemm_describe", "mi_stream_sync", "mi_flash_attn_fwd",
+    "mi_gemm_describe", "mi_stream_sync", "mi_flash_attn_fwd", "mi_flash_attn_bwd",
 )
 MI_ATTN_O_BHTD, MI_ATTN_O_BTHD = 0, 1
 
@@ -110,6 +110,9 @@ def load_library():
     L.mi_stream_sync.argtypes = [vp]
     L.mi_flash_attn_fwd.restype = ctypes.c_int
     L.mi_flash_attn_fwd.argtypes = [vp, vp, vp, vp, vp, vp, i64, i64, i64, i64, i64, i32, i32]
+    L.mi_flash_attn_bwd.restype = ctypes.c_int
+    L.mi_flash_attn_bwd.argtypes = [vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, i64, i64, i64, i64,
+                                    i64, i32, i32]
     _lib = L
     return L
 
@@ -433,6 +436,31 @@ def flash_attn_fwd(Q4, K4, V4, O=None, lse=None, causal=True, layout="bthd", syn
     else:
         _check("mi_flash_attn_fwd", st)
     return O
+
+
+def flash_attn_bwd(Q4, K4, V4, O, dO, lse, causal=True, layout="bthd", sync=None):
+    """Fused backward (metal_bridge::fused_attn_bwd, MetalBridge.hpp:54-57; Attention.cpp:292-348)
+    from the forward's O and lse: returns (dQ [B,nH,T,d], dK, dV [B,nKV,T,d]), bf16, dK/dV
+    summed over the query heads of each KV head. O and dO in `layout` ("bthd" or "bhtd")."""
+    torch = _torch()
+    Bn, nH, T, d = Q4.shape
+    nKV = K4.shape[1]
+    for t in (Q4, K4, V4, O, dO):
+        if t.dtype != torch.bfloat16 or not t.is_contiguous():
+            raise ValueError("Q, K, V, O, dO must be contiguous bf16 tensors")
+    dQ = torch.empty_like(Q4)
+    dK = torch.empty_like(K4)
+    dV = torch.empty_like(V4)
+    delta = torch.empty((Bn, nH, T), dtype=torch.float32, device=Q4.device)
+    code = MI_ATTN_O_BTHD if layout == "bthd" else MI_ATTN_O_BHTD
+    st = load_library().mi_flash_attn_bwd(_stream(), _ptr(Q4), _ptr(K4), _ptr(V4), _ptr(O),
+                                          _ptr(dO), _ptr(lse), _ptr(dQ), _ptr(dK), _ptr(dV),
+                                          _ptr(delta), Bn, nH, nKV, T, d, int(bool(causal)), code)
+    if sync is None:
+        _finish("mi_flash_attn_bwd", st)
+    else:
+        _check("mi_flash_attn_bwd", st)
+    return dQ, dK, dV
 
 
 def attention_backward(Q4, K4, V4, dO, P, grad_dtype=None):

@@ -117,6 +117,10 @@ def test_aux_validation(mi):
     assert fa(None, p16, p16, p16, p16, None, 1, 4, 2, 64, 96, 1, 1) == 5        # head_dim 96
     assert fa(None, p16, p16, p16, p16, None, 1, 4, 2, 64, 128, 1, 7) == 1       # layout
     assert fa(None, ctypes.c_void_p(18), p16, p16, p16, None, 1, 4, 2, 64, 128, 1, 1) == 5
+    fb = lib.mi_flash_attn_bwd
+    assert fb(None, *([None] * 10), 0, 4, 2, 64, 128, 1, 1) == 0                  # empty batch
+    assert fb(None, *([p16] * 9), None, 1, 4, 2, 64, 128, 1, 1) == 3              # delta NULL
+    assert fb(None, *([p16] * 10), 1, 4, 2, 64, 64, 1, 1) == 5                    # head_dim 64
 
 
 def test_matmul_shape_rules(mi):

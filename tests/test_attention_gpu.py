@@ -161,3 +161,61 @@ def test_flash_forward_config4(mi, dev, oracle):
     for b in (0, 7):
         sl = slice(b, b + 1)
         check(O[sl], oracle.attention_fwd(q[sl], k[sl], v[sl]), TOL_BF16, f"O[{b}]")
+
+
+@pytest.mark.parametrize("Bn,nH,nKV,T", [(2, 16, 4, 256), (1, 4, 2, 300), (1, 2, 1, 64),
+                                         (1, 4, 4, 520)])
+def test_flash_backward(mi, dev, oracle, Bn, nH, nKV, T):
+    """Fused backward vs the oracle (Attention.cpp:292-348: dV = P^T dO, dS = P (dP - rowsum),
+    dQ = scale dS K, dK = scale dS^T Q summed over the query heads of a KV head)."""
+    import torch
+
+    d = 128
+    q, k, v, do = _qkv(oracle, Bn, nH, nKV, T, d, 1900 + T)
+    Q, K, V, dO = (to_dev(x, dev, True) for x in (q, k, v, do))
+    lse = torch.empty((Bn, nH, T), dtype=torch.float32, device=dev)
+    O = mi.flash_attn_fwd(Q, K, V, lse=lse)
+    dQ, dK, dV = mi.flash_attn_bwd(Q, K, V, O, dO, lse)
+    dQ_ref, dK_ref, dV_ref = oracle.attention_bwd(q, k, v, do)
+    check(host(dV), dV_ref, TOL_BF16, "dV")
+    check(host(dK), dK_ref, TOL_BF16, "dK")
+    check(host(dQ), dQ_ref, TOL_BF16, "dQ")
+
+
+def test_flash_backward_layouts_and_determinism(mi, dev, oracle):
+    """O/dO in [B,nH,T,d] give the same gradients as [B,T,nH*d], bit for bit, and two
+    launches agree bit for bit (no atomics)."""
+    import torch
+
+    Bn, nH, nKV, T, d = 1, 8, 2, 384, 128
+    q, k, v, do = _qkv(oracle, Bn, nH, nKV, T, d, 2100)
+    Q, K, V, dO = (to_dev(x, dev, True) for x in (q, k, v, do))
+    lse = torch.empty((Bn, nH, T), dtype=torch.float32, device=dev)
+    O = mi.flash_attn_fwd(Q, K, V, lse=lse)
+    g1 = mi.flash_attn_bwd(Q, K, V, O, dO, lse)
+    g2 = mi.flash_attn_bwd(Q, K, V, O, dO, lse)
+    O4 = O.view(Bn, T, nH, d).transpose(1, 2).contiguous()
+    dO4 = dO.view(Bn, T, nH, d).transpose(1, 2).contiguous()
+    g3 = mi.flash_attn_bwd(Q, K, V, O4, dO4, lse, layout="bhtd")
+    for a, b_, c in zip(g1, g2, g3):
+        assert torch.equal(a, b_), "backward differs between launches"
+        assert torch.equal(a, c), "backward differs between output layouts"
+
+
+def test_flash_backward_config4(mi, dev, oracle):
+    """Benchmark configuration 4 backward (B=8, 16/4 heads, T=1024, d=128) vs the oracle on
+    batch elements 0 and 7."""
+    import torch
+
+    Bn, nH, nKV, T, d = 8, 16, 4, 1024, 128
+    q, k, v, do = _qkv(oracle, Bn, nH, nKV, T, d, 4000)
+    Q, K, V, dO = (to_dev(x, dev, True) for x in (q, k, v, do))
+    lse = torch.empty((Bn, nH, T), dtype=torch.float32, device=dev)
+    O = mi.flash_attn_fwd(Q, K, V, lse=lse)
+    dQ, dK, dV = (host(t) for t in mi.flash_attn_bwd(Q, K, V, O, dO, lse))
+    for b in (0, 7):
+        sl = slice(b, b + 1)
+        dQ_ref, dK_ref, dV_ref = oracle.attention_bwd(q[sl], k[sl], v[sl], do[sl])
+        check(dQ[sl], dQ_ref, TOL_BF16, f"dQ[{b}]")
+        check(dK[sl], dK_ref, TOL_BF16, f"dK[{b}]")
+        check(dV[sl], dV_ref, TOL_BF16, f"dV[{b}]")
