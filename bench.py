@@ -72,6 +72,9 @@ def parse():
     ap.add_argument("--cpu-rows", type=int, default=2048, help="token rows of the CPU sample")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="also launch a 1 GiB device copy (for PMC byte-counter scaling)")
+    ap.add_argument("--workload", choices=("block", "attention"), default="block",
+                    help="block: the configuration-3 GEMM set (the headline metric); attention: "
+                         "configuration 4, fused GQA attention forward + backward")
     return ap.parse_args()
 
 
@@ -102,12 +105,107 @@ def cpu_baseline(m_rows: int) -> dict:
                       f"{t_total:.2f} s"}
 
 
+ATT = dict(B=8, nH=16, nKV=4, T=1024, d=128)   # benchmark configuration 4
+ATT_PRODUCT_FLOPS = 17_196_646_400                # one causal product: 2*B*nH*d*T(T+1)/2
+
+
+def cpu_attention_baseline() -> dict:
+    """The oracle's attention forward + backward (oracle/mi_oracle.c, Attention.cpp:236-348,
+    float64, OpenMP) on batch element 0 and 4 query heads (one KV group)."""
+    import numpy as np
+
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import oracle
+
+    T, d = ATT["T"], ATT["d"]
+    rng = np.random.default_rng(0)
+    q = rng.standard_normal((1, 4, T, d), dtype=np.float32)
+    k = rng.standard_normal((1, 1, T, d), dtype=np.float32)
+    v = rng.standard_normal((1, 1, T, d), dtype=np.float32)
+    do = rng.standard_normal((1, T, 4 * d), dtype=np.float32) * 1e-2
+    t0 = time.perf_counter()
+    oracle.attention_fwd(q, k, v)
+    oracle.attention_bwd(q, k, v, do)
+    dt = time.perf_counter() - t0
+    flops = 6 * ATT_PRODUCT_FLOPS * 4 / (ATT["B"] * ATT["nH"])
+    return {"value": round(flops / dt / 1e12, 5), "unit": "TFLOP/s", "cores": oracle.num_threads(),
+            "kind": "port",
+            "sample": f"batch element 0, 4 query heads / 1 KV head of configuration 4, float64, "
+                      f"{flops / 1e9:.1f} GFLOP, {dt:.2f} s"}
+
+
+def attention_main(args):
+    """Configuration 4: one step = fused attention forward (S, PV) + backward (dQ kernel: S, dP,
+    dQ; dK/dV kernel: S, dP, dV, dK) on Q/K/V/dO resident in HBM. value counts the 6 algorithmic
+    causal products (forward 2, backward 4), not the recomputed ones."""
+    import torch
+
+    import mi_gemm as mi
+
+    dev = torch.device("cuda:0")
+    mi.init()
+    B, nH, nKV, T, d = (ATT[k] for k in ("B", "nH", "nKV", "T", "d"))
+    g = torch.Generator(device=dev)
+    g.manual_seed(4)
+    Q = torch.randn((B, nH, T, d), generator=g, device=dev).to(torch.bfloat16)
+    K = torch.randn((B, nKV, T, d), generator=g, device=dev).to(torch.bfloat16)
+    V = torch.randn((B, nKV, T, d), generator=g, device=dev).to(torch.bfloat16)
+    dO = (torch.randn((B, T, nH * d), generator=g, device=dev) * 1e-2).to(torch.bfloat16)
+    O = torch.empty((B, T, nH * d), dtype=torch.bfloat16, device=dev)
+    lse = torch.empty((B, nH, T), dtype=torch.float32, device=dev)
+
+    def step(ev=None):
+        mi.flash_attn_fwd(Q, K, V, O=O, lse=lse, sync=False)
+        if ev is not None:
+            ev[0].record()
+        mi.flash_attn_bwd(Q, K, V, O, dO, lse, sync=False)
+        if ev is not None:
+            ev[1].record()
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+           for _ in range(args.steps)]
+    t0 = time.perf_counter()
+    for s_ in range(args.steps):
+        step(evs[s_])
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - t0
+    flops = 6 * ATT_PRODUCT_FLOPS
+    value = flops * args.steps / elapsed / 1e12
+    # the backward pass (its two kernels, bracketed together) takes most of the step
+    ms_bwd = sum(a.elapsed_time(b) for a, b in evs) / args.steps
+    achieved = 4 * ATT_PRODUCT_FLOPS / (ms_bwd / 1e3) / 1e12
+    out = {
+        "metric": "GQA attention TFLOP/s (fused fwd+bwd, configuration 4)",
+        "value": round(value, 2), "unit": "TFLOP/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": round(elapsed / args.steps * 1e3, 4),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
+        "data": "synthetic (torch.randn on device; Q,K,V~N(0,1), dO~N(0,1e-2))",
+        "config": {"workload": "GQA attention B=8, 16 q / 4 kv heads, T=1024, d=128, causal: "
+                               "fused forward + backward (dQ, dK, dV)",
+                   "flops_per_step": flops, "flops_note": "6 causal products; the kernels "
+                   "also recompute S (twice) and dP (once) in the backward"},
+        "roofline": {"bound": "mfma", "achieved": round(achieved, 2), "peak": PEAK_BF16_TFLOPS,
+                     "unit": "TFLOP/s", "frac": round(achieved / PEAK_BF16_TFLOPS, 4),
+                     "traffic": None, "kernel": "flash_bwd_dq_kernel + flash_bwd_dkdv_kernel",
+                     "avg_launch_ms": round(ms_bwd, 4)},
+    }
+    if not args.no_cpu:
+        out["cpu_baseline"] = cpu_attention_baseline()
+    print(json.dumps(out))
+
+
 def main():
     args = parse()
     if args.gpus != 1:
         print(json.dumps({"error": "this build runs on one GPU only; --gpus must be 1 "
                                    "(the multi-GPU sharding is a design, not run)"}))
         sys.exit(2)
+    if args.workload == "attention":
+        attention_main(args)
+        return
     import torch
 
     import mi_gemm as mi
