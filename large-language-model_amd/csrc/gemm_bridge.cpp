@@ -36,6 +36,31 @@ void* workspace_for(int ta, int tb, size_t M, size_t N, size_t K, int dt_in, int
   return t_ws;
 }
 
+// Attention state for fused_attn_bwd (O, log-sum-exp, D), grown like the split-K
+// workspace; bytes = O bytes, floats = rows.
+thread_local void* t_att_o = nullptr;
+thread_local float* t_att_f = nullptr;
+thread_local size_t t_att_rows = 0, t_att_o_bytes = 0;
+
+hipStream_t get_stream();
+
+bool attention_state(size_t o_bytes, size_t rows) {
+  if (o_bytes <= t_att_o_bytes && rows <= t_att_rows) return true;
+  if (t_att_o || t_att_f) {
+    if (hipStreamSynchronize(get_stream()) != hipSuccess) return false;
+    (void)hipFree(t_att_o);
+    (void)hipFree(t_att_f);
+  }
+  t_att_o = nullptr;
+  t_att_f = nullptr;
+  t_att_o_bytes = t_att_rows = 0;
+  if (hipMalloc(&t_att_o, o_bytes) != hipSuccess) return false;
+  if (hipMalloc((void**)&t_att_f, 2 * rows * sizeof(float)) != hipSuccess) return false;
+  t_att_o_bytes = o_bytes;
+  t_att_rows = rows;
+  return true;
+}
+
 hipStream_t get_stream() {
   if (!t_stream) {
     if (hipStreamCreateWithFlags(&t_stream, hipStreamNonBlocking) != hipSuccess) t_stream = nullptr;
@@ -158,6 +183,37 @@ void gemm_proj_trans_b(const float* a, const float* b_transposed, float* c, size
   }
   finish("gemm_proj_trans_b",
          gemm(0, 1, M, N, K, 1.0f, a, b_transposed, MI_BF16, 0.0f, c, MI_BF16, nullptr));
+}
+
+void flash_attn_fwd(const void* Q, const void* K, const void* V, void* O, size_t batch,
+                    size_t n_heads, size_t n_kv, size_t seq_len, size_t head_dim) {
+  finish("flash_attn_fwd",
+         mi_flash_attn_fwd(get_stream(), Q, K, V, O, nullptr, (int64_t)batch, (int64_t)n_heads,
+                           (int64_t)n_kv, (int64_t)seq_len, (int64_t)head_dim, 1, MI_ATTN_O_BHTD));
+}
+
+void fused_attn_bwd(const void* Q, const void* K, const void* V, const void* dO, void* dQ,
+                    void* dK, void* dV, size_t batch, size_t n_heads, size_t n_kv,
+                    size_t seq_len, size_t head_dim) {
+  const size_t rows = batch * n_heads * seq_len;
+  if (rows == 0) {
+    t_status = MI_OK;
+    return;
+  }
+  if (!attention_state(rows * head_dim * 2, rows)) {
+    t_status = MI_ERR_HIP;
+    std::fprintf(stderr, "[mi_bridge] fused_attn_bwd: could not allocate the forward state\n");
+    return;
+  }
+  float* lse = t_att_f;
+  float* delta = t_att_f + t_att_rows;
+  int st = mi_flash_attn_fwd(get_stream(), Q, K, V, t_att_o, lse, (int64_t)batch, (int64_t)n_heads,
+                             (int64_t)n_kv, (int64_t)seq_len, (int64_t)head_dim, 1, MI_ATTN_O_BHTD);
+  if (st == MI_OK)
+    st = mi_flash_attn_bwd(get_stream(), Q, K, V, t_att_o, dO, lse, dQ, dK, dV, delta,
+                           (int64_t)batch, (int64_t)n_heads, (int64_t)n_kv, (int64_t)seq_len,
+                           (int64_t)head_dim, 1, MI_ATTN_O_BHTD);
+  finish("fused_attn_bwd", st);
 }
 
 void residual_add(float* a, const float* b, size_t n) {

@@ -244,6 +244,76 @@ int main() {
         std::to_string(err / mx));
     dfree(dA); dfree(dG); dfree(dU); dfree(dC);
   }
+  // flash_attn_fwd / fused_attn_bwd with Q = 0 (closed forms): every visible key gets
+  // P = 1/(q+1), so O[q] = mean(V[0..q]), dV[k] = sum_{q>=k} dO[q] / (q+1), dK = 0
+  // (dK = scale dS^T Q), dQ[q] = scale sum_{k<=q} dS[q,k] K[k] with dS = P (dP - rowsum(P dP)).
+  {
+    const size_t B = 1, nH = 2, nKV = 1, T = 96, d = 128, g = nH / nKV;
+    const double scale = 1.0 / std::sqrt((double)d);
+    auto kv = ints(T * d, 21), vv = ints(T * d, 22), go = ints(nH * T * d, 23);
+    for (auto& x : kv) x *= 0.25f;
+    for (auto& x : go) x *= 0.125f;
+    std::vector<uint16_t> hq(nH * T * d, 0), hk(T * d), hv(T * d), hg(nH * T * d);
+    for (size_t i = 0; i < T * d; ++i) { hk[i] = bf(kv[i]); hv[i] = bf(vv[i]); }
+    for (size_t i = 0; i < nH * T * d; ++i) hg[i] = bf(go[i]);
+    uint16_t *dq_in = dev(hq), *dk_in = dev(hk), *dv_in = dev(hv), *dgo = dev(hg);
+    uint16_t *dO_out = dev(std::vector<uint16_t>(nH * T * d, 0));
+    uint16_t *dQg = dev(std::vector<uint16_t>(nH * T * d, 0));
+    uint16_t *dKg = dev(std::vector<uint16_t>(T * d, 0)), *dVg = dev(std::vector<uint16_t>(T * d, 0));
+    mi_bridge::flash_attn_fwd(dq_in, dk_in, dv_in, dO_out, B, nH, nKV, T, d);
+    bool ok = mi_bridge::last_status() == MI_OK;
+    auto ho = host(dO_out, nH * T * d);
+    double mx = 0, err = 0;
+    for (size_t h = 0; h < nH && ok; ++h)
+      for (size_t t = 0; t < T; ++t)
+        for (size_t c = 0; c < d; ++c) {
+          double ref = 0;
+          for (size_t k = 0; k <= t; ++k) ref += vv[k * d + c];
+          ref /= (double)(t + 1);
+          mx = std::fmax(mx, std::fabs(ref));
+          err = std::fmax(err, std::fabs(ref - fb(ho[(h * T + t) * d + c])));
+        }
+    row("GB-11", "flash_attn_fwd, Q = 0: O[q] = mean(V[0..q]), max rel <= 1e-2",
+        ok && err <= 1e-2 * mx, std::to_string(err / mx));
+    mi_bridge::fused_attn_bwd(dq_in, dk_in, dv_in, dgo, dQg, dKg, dVg, B, nH, nKV, T, d);
+    ok = mi_bridge::last_status() == MI_OK;
+    auto hdq = host(dQg, nH * T * d), hdk = host(dKg, T * d), hdv = host(dVg, T * d);
+    std::vector<double> rdv(T * d, 0.0), rdq(nH * T * d, 0.0);
+    for (size_t h = 0; h < nH; ++h)
+      for (size_t t = 0; t < T; ++t) {
+        const double p = 1.0 / (double)(t + 1);
+        std::vector<double> dp(t + 1, 0.0);
+        double rs = 0;
+        for (size_t k = 0; k <= t; ++k) {
+          for (size_t c = 0; c < d; ++c) dp[k] += (double)go[(h * T + t) * d + c] * vv[k * d + c];
+          rs += p * dp[k];
+        }
+        for (size_t k = 0; k <= t; ++k) {
+          const double ds = p * (dp[k] - rs);
+          for (size_t c = 0; c < d; ++c) {
+            rdv[k * d + c] += p * go[(h * T + t) * d + c];
+            rdq[(h * T + t) * d + c] += scale * ds * kv[k * d + c];
+          }
+        }
+      }
+    (void)g;
+    auto rel = [](const std::vector<double>& ref, const std::vector<uint16_t>& got) {
+      double m = 0, e = 0;
+      for (size_t i = 0; i < ref.size(); ++i) {
+        m = std::fmax(m, std::fabs(ref[i]));
+        e = std::fmax(e, std::fabs(ref[i] - fb(got[i])));
+      }
+      return m > 0 ? e / m : e;
+    };
+    bool dk_zero = true;
+    for (auto x : hdk) dk_zero = dk_zero && fb(x) == 0.0f;
+    const double edv = rel(rdv, hdv), edq = rel(rdq, hdq);
+    row("GB-12", "fused_attn_bwd, Q = 0: dV, dQ closed forms (1e-2), dK = 0",
+        ok && edv <= 1e-2 && edq <= 1e-2 && dk_zero,
+        std::to_string(edv) + " " + std::to_string(edq));
+    dfree(dq_in); dfree(dk_in); dfree(dv_in); dfree(dgo); dfree(dO_out);
+    dfree(dQg); dfree(dKg); dfree(dVg);
+  }
   std::printf("%d/%d checks passed\n", g_passed, g_total);
   return g_passed == g_total ? 0 : 1;
 }
