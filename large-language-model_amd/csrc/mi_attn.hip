@@ -764,21 +764,29 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1)))
     });
   };
 
-  if (total > 0) issue(0);
-  for (int it = 0; it < total; ++it) {
+  // Per head: the first n_diag tiles may hold queries before some of this wave's keys
+  // (causal mask, or skipped when every query precedes every key); the rest are
+  // visible whole.  Separate loops keep the accumulators in place across iterations.
+  const int n_diag = uniform(p.causal ? (per_h < 2 ? per_h : 2) : 0);
+  auto ring_step = [&](int it) __attribute__((always_inline)) {
     wait_vmcnt<0>();
     lds_ring_barrier();
     if (it + 1 < total) issue(it + 1);
-    int h, q0;
-    tile_of(it, h, q0);
-    (void)h;
-    q0 = uniform(q0);
-    if (p.causal && q0 + QT - 1 < kw) continue;  // every query of the tile precedes every key
-    const uint32_t st = lds0 + (uint32_t)((it & 1) * STAGE);
-    if (p.causal && q0 < kw + 31)
+    return lds0 + (uint32_t)((it & 1) * STAGE);
+  };
+  if (total > 0) issue(0);
+  int it = 0;
+  for (int hh = 0; hh < p.group; ++hh) {
+    for (int t = 0; t < n_diag; ++t, ++it) {
+      const uint32_t st = ring_step(it);
+      const int q0 = uniform((qt0 + t) * QT);
+      if (q0 + QT - 1 < kw) continue;  // every query of the tile precedes every key
       block(q0, st, std::true_type{});
-    else
-      block(q0, st, std::false_type{});
+    }
+    for (int t = n_diag; t < per_h; ++t, ++it) {
+      const uint32_t st = ring_step(it);
+      block(uniform((qt0 + t) * QT), st, std::false_type{});
+    }
   }
 
   if (live) {
