@@ -87,6 +87,15 @@ void fused_attn_bwd(const void* Q, const void* K, const void* V, const void* dO,
                     void* dK, void* dV, size_t batch, size_t n_heads, size_t n_kv,
                     size_t seq_len, size_t head_dim);
 
+// MetalBridge.hpp:89-91: fused softmax cross-entropy (cross_entropy.metal) over
+// total_tokens rows of vocab_size bf16 logits.  grad_logits (fp32, device) receives
+// (softmax - onehot) / total_tokens; *loss_out (host) the mean of
+// -log(max(p_target, 1e-15)), written when the work has run: on return outside a
+// scope, at end_scope() inside one (the reference's copy-back).  targets are device
+// memory.
+void cross_entropy(const void* logits, const uint32_t* targets, float* loss_out,
+                   float* grad_logits, size_t total_tokens, size_t vocab_size);
+
 // MetalBridge.hpp:78: a[i] += b[i] on bf16 storage (residual_add.metal:15-28).
 void residual_add(float* a, const float* b, size_t n);
 // fp32 storage variant.

@@ -189,6 +189,28 @@ int mi_flash_attn_bwd(void* stream, const void* Q, const void* K, const void* V,
                       int64_t head_dim, int32_t causal, int32_t o_layout);
 
 /*
+ * Softmax cross-entropy over rows of logits, the loss after the LM head.  For
+ * row r (a token) with target y = targets[r]:
+ *   p[v] = exp(x[v] - max x) / sum_v exp(x[v] - max x)
+ *   row_loss[r] = -log(max(p[y], 1e-15))
+ *   grad[r, v]  = scale * (p[v] - [v == y])           (if grad is not NULL)
+ *   *loss_out   = scale * sum_r row_loss[r]            (if loss_out is not NULL)
+ * logits [rows, ld_logits] and grad [rows, ld_grad] are MI_BF16 or MI_F32 (fp32
+ * arithmetic either way); grad may be the logits array itself (same dtype and
+ * leading dimension: the gradient overwrites the logits) but must not
+ * otherwise overlap it.  targets, row_loss [rows] and loss_out [1] are device
+ * memory; row_loss is required.  The reference's scale is 1 / rows.  A target
+ * outside [0, vocab) gives a NaN row loss.  Deterministic (fixed-order
+ * reductions, no atomics); rows == 0 or vocab == 0 is a no-op.  Replaces
+ * metal_bridge::cross_entropy (MetalBridge.hpp:89-91, cross_entropy.metal) and
+ * CrossEntropyLoss::forward / backward (Loss.hpp, Loss.cpp:43-195).
+ */
+int mi_cross_entropy(void* stream, const void* logits, int32_t logits_dtype, int64_t ld_logits,
+                     const uint32_t* targets, int64_t rows, int64_t vocab, float scale,
+                     float* row_loss, float* loss_out, void* grad, int32_t grad_dtype,
+                     int64_t ld_grad);
+
+/*
  * Describe the kernel mi_gemm_batched would launch for this problem (tile,
  * loader, split-K factor) as text into buf (always NUL-terminated).  For
  * measurement and logging; no reference counterpart.  epi_mode: 0 plain,

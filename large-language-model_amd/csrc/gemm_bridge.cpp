@@ -61,6 +61,39 @@ bool attention_state(size_t o_bytes, size_t rows) {
   return true;
 }
 
+// cross_entropy state: per-row losses and the loss scalar on the device, and the
+// host copies a scope still owes its callers (the reference's copy-back tasks,
+// MetalBridge.mm:1846-1900: loss_out is written once the work has run).
+thread_local float* t_ce_dev = nullptr;  // [rows + 1]: row losses, then the loss
+thread_local size_t t_ce_rows = 0;
+thread_local float* t_ce_host = nullptr;  // pinned staging, CE_PENDING entries
+constexpr int CE_PENDING = 64;
+thread_local float* t_ce_dst[CE_PENDING];
+thread_local int t_ce_n = 0;
+
+bool ce_state(size_t rows) {
+  if (!t_ce_host && hipHostMalloc((void**)&t_ce_host, CE_PENDING * sizeof(float)) != hipSuccess) {
+    t_ce_host = nullptr;
+    return false;
+  }
+  if (rows <= t_ce_rows) return true;
+  if (t_ce_dev) {
+    if (hipStreamSynchronize(get_stream()) != hipSuccess) return false;
+    (void)hipFree(t_ce_dev);
+  }
+  t_ce_dev = nullptr;
+  t_ce_rows = 0;
+  if (hipMalloc((void**)&t_ce_dev, (rows + 1) * sizeof(float)) != hipSuccess) return false;
+  t_ce_rows = rows;
+  return true;
+}
+
+// Write the staged losses to their callers (after the stream has drained).
+void ce_flush() {
+  for (int i = 0; i < t_ce_n; ++i) *t_ce_dst[i] = t_ce_host[i];
+  t_ce_n = 0;
+}
+
 hipStream_t get_stream() {
   if (!t_stream) {
     if (hipStreamCreateWithFlags(&t_stream, hipStreamNonBlocking) != hipSuccess) t_stream = nullptr;
@@ -107,6 +140,7 @@ void end_scope() {
   t_in_scope = false;
   t_status = mi_stream_sync(get_stream());
   if (t_status != MI_OK) std::fprintf(stderr, "[mi_bridge] end_scope: %s\n", mi_last_error());
+  else ce_flush();
 }
 
 void* stream() { return (void*)get_stream(); }
@@ -190,6 +224,42 @@ void flash_attn_fwd(const void* Q, const void* K, const void* V, void* O, size_t
   finish("flash_attn_fwd",
          mi_flash_attn_fwd(get_stream(), Q, K, V, O, nullptr, (int64_t)batch, (int64_t)n_heads,
                            (int64_t)n_kv, (int64_t)seq_len, (int64_t)head_dim, 1, MI_ATTN_O_BHTD));
+}
+
+void cross_entropy(const void* logits, const uint32_t* targets, float* loss_out,
+                   float* grad_logits, size_t total_tokens, size_t vocab_size) {
+  if (total_tokens == 0 || vocab_size == 0) {  // MetalBridge.mm:1848
+    t_status = MI_OK;
+    return;
+  }
+  if (!ce_state(total_tokens)) {
+    t_status = MI_ERR_HIP;
+    std::fprintf(stderr, "[mi_bridge] cross_entropy: could not allocate the loss buffers\n");
+    return;
+  }
+  if (t_in_scope && t_ce_n == CE_PENDING) {  // staging full: drain the scope's work once
+    if (mi_stream_sync(get_stream()) != MI_OK) {
+      finish("cross_entropy", MI_ERR_HIP);
+      return;
+    }
+    ce_flush();
+  }
+  float* dev_loss = t_ce_dev + t_ce_rows;
+  int st = mi_cross_entropy(get_stream(), logits, MI_BF16, (int64_t)vocab_size, targets,
+                            (int64_t)total_tokens, (int64_t)vocab_size,
+                            (float)(1.0 / (double)total_tokens), t_ce_dev, dev_loss, grad_logits,
+                            MI_F32, (int64_t)vocab_size);
+  if (st == MI_OK && loss_out) {
+    if (hipMemcpyAsync(&t_ce_host[t_ce_n], dev_loss, sizeof(float), hipMemcpyDeviceToHost,
+                       get_stream()) != hipSuccess) {
+      t_status = MI_ERR_HIP;
+      std::fprintf(stderr, "[mi_bridge] cross_entropy: loss copy failed\n");
+      return;
+    }
+    t_ce_dst[t_ce_n++] = loss_out;
+  }
+  finish("cross_entropy", st);
+  if (!t_in_scope && t_status == MI_OK) ce_flush();
 }
 
 void fused_attn_bwd(const void* Q, const void* K, const void* V, const void* dO, void* dQ,

@@ -19,6 +19,7 @@
 
 #include "../../include/mi_gemm.h"
 #include "mi_attn.hpp"
+#include "mi_xent.hpp"
 #include "mi_gemm_kernels.hpp"
 
 using namespace mig;
@@ -645,6 +646,52 @@ int mi_flash_attn_bwd(void* stream, const void* Q, const void* K, const void* V,
   hipError_t e = launch_flash_bwd(p, (int)head_dim, (hipStream_t)stream);
   return e == hipSuccess ? MI_OK : fail(MI_ERR_HIP, "flash attention backward launch: %s",
                                         hipGetErrorString(e));
+}
+
+int mi_cross_entropy(void* stream, const void* logits, int32_t logits_dtype, int64_t ld_logits,
+                     const uint32_t* targets, int64_t rows, int64_t vocab, float scale,
+                     float* row_loss, float* loss_out, void* grad, int32_t grad_dtype,
+                     int64_t ld_grad) {
+  if (rows < 0 || vocab < 0) return fail(MI_ERR_SHAPE, "negative size");
+  if (rows == 0 || vocab == 0) return MI_OK;
+  if (rows > INT32_MAX || vocab > INT32_MAX) return fail(MI_ERR_SHAPE, "size exceeds 2^31-1");
+  if (logits_dtype != MI_F32 && logits_dtype != MI_BF16)
+    return fail(MI_ERR_DTYPE, "logits dtype %d", logits_dtype);
+  if (grad && grad_dtype != MI_F32 && grad_dtype != MI_BF16)
+    return fail(MI_ERR_DTYPE, "grad dtype %d", grad_dtype);
+  if (!logits || !targets || !row_loss) return fail(MI_ERR_NULL, "logits, targets or row_loss is NULL");
+  if (ld_logits < vocab) return fail(MI_ERR_LD, "ld_logits=%lld < vocab=%lld", (long long)ld_logits,
+                                     (long long)vocab);
+  if (grad && ld_grad < vocab)
+    return fail(MI_ERR_LD, "ld_grad=%lld < vocab=%lld", (long long)ld_grad, (long long)vocab);
+  const int64_t in_es = logits_dtype == MI_BF16 ? 2 : 4, out_es = grad_dtype == MI_BF16 ? 2 : 4;
+  if (((uintptr_t)logits % in_es) || ((uintptr_t)targets & 3u) || ((uintptr_t)row_loss & 3u) ||
+      ((uintptr_t)loss_out & 3u) || (grad && ((uintptr_t)grad % out_es)))
+    return fail(MI_ERR_UNSUPPORTED, "pointers must be aligned to their element size");
+  if (grad) {  // in place only as an exact alias of the logits
+    const uintptr_t l0 = (uintptr_t)logits, l1 = l0 + (uintptr_t)(((rows - 1) * ld_logits + vocab) * in_es);
+    const uintptr_t g0 = (uintptr_t)grad, g1 = g0 + (uintptr_t)(((rows - 1) * ld_grad + vocab) * out_es);
+    if (g0 < l1 && l0 < g1 &&
+        !(g0 == l0 && grad_dtype == logits_dtype && ld_grad == ld_logits))
+      return fail(MI_ERR_UNSUPPORTED, "grad overlaps logits without being the same array");
+  }
+  const int64_t ev = 16 / in_es;
+  const int64_t out_vec = ev * out_es;  // bytes one vector's gradient occupies
+  const int64_t out_align = out_vec < 16 ? out_vec : 16;
+  const bool vector_path = vocab % ev == 0 && aligned16(logits) && (ld_logits * in_es) % 16 == 0 &&
+                           vocab / ev <= (int64_t)XENT_THREADS * XENT_MAX_VEC_PER_THREAD &&
+                           (!grad || ((uintptr_t)grad % out_align == 0 && (ld_grad * out_es) % out_align == 0));
+  int st = init_devices();
+  if (st != MI_OK) return st;
+  XentParams p;
+  p.logits = logits; p.targets = targets; p.row_loss = row_loss; p.grad = grad;
+  p.ld = ld_logits; p.ldg = grad ? ld_grad : 0;
+  p.rows = (int)rows; p.vocab = (int)vocab;
+  p.scale = scale;
+  hipError_t e = launch_xent(p, logits_dtype == MI_BF16, grad && grad_dtype == MI_BF16, vector_path,
+                             (hipStream_t)stream);
+  if (e == hipSuccess && loss_out) e = launch_xent_mean(row_loss, (int)rows, scale, loss_out, (hipStream_t)stream);
+  return e == hipSuccess ? MI_OK : fail(MI_ERR_HIP, "cross_entropy launch: %s", hipGetErrorString(e));
 }
 
 int mi_gemm_describe(int transA, int transB, int64_t M, int64_t N, int64_t K, int32_t dtype_in,

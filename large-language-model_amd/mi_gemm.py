@@ -34,6 +34,7 @@ C_SYMBOLS = (
     "mi_init", "mi_last_error", "mi_version", "mi_gemm_workspace_size", "mi_gemm",
     "mi_gemm_batched", "mi_residual_add", "mi_softmax_causal", "mi_softmax_bwd",
     "mi_gemm_describe", "mi_stream_sync", "mi_flash_attn_fwd", "mi_flash_attn_bwd",
+    "mi_cross_entropy",
 )
 MI_ATTN_O_BHTD, MI_ATTN_O_BTHD = 0, 1
 
@@ -113,6 +114,9 @@ def load_library():
     L.mi_flash_attn_bwd.restype = ctypes.c_int
     L.mi_flash_attn_bwd.argtypes = [vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, i64, i64, i64, i64,
                                     i64, i32, i32]
+    L.mi_cross_entropy.restype = ctypes.c_int
+    L.mi_cross_entropy.argtypes = [vp, vp, i32, i64, vp, i64, i64, ctypes.c_float, vp, vp, vp,
+                                   i32, i64]
     _lib = L
     return L
 
@@ -502,3 +506,73 @@ def attention_backward(Q4, K4, V4, dO, P, grad_dtype=None):
     gemm_batched(dP, Q4, dK, T, d, T, bt, transA=True, sync=False)
     _finish("attention_backward", 0)
     return dQ, dK, dV
+
+
+# ---- loss ---------------------------------------------------------------------
+
+def cross_entropy(logits, targets, grad="new", grad_dtype=None, scale=None, sync=None):
+    """Softmax cross-entropy over the rows of logits [..., V] (metal_bridge::cross_entropy,
+    MetalBridge.hpp:89-91; CrossEntropyLoss, Loss.cpp:43-195).
+
+    logits: bf16 or fp32, last dimension contiguous. targets: integer tensor of the
+    leading shape (a value outside [0, V) gives a NaN row loss). Returns (loss, row_loss,
+    grad): loss a 1-element fp32 device tensor = scale * sum(row_loss), row_loss fp32
+    [rows] = -log(max(p_target, 1e-15)), grad = scale * (softmax - onehot) shaped like
+    logits. grad: "new" allocates it in grad_dtype (default fp32, the reference's),
+    "inplace" overwrites the logits, None skips it, or a tensor to write into.
+    scale defaults to 1 / rows, the reference's mean."""
+    torch = _torch()
+    V = logits.shape[-1]
+    rows = logits.numel() // V if V else 0
+    if logits.stride(-1) != 1:
+        raise ValueError("logits must have a contiguous last dimension")
+    L2 = logits.reshape(rows, V)
+    ld = L2.stride(0) if rows > 1 else V
+    tg = targets.reshape(-1).to(torch.int32).contiguous()
+    if tg.numel() != rows:
+        raise ValueError(f"targets has {tg.numel()} entries for {rows} rows")
+    if scale is None:
+        scale = 1.0 / rows if rows else 0.0
+    row_loss = torch.empty((rows,), dtype=torch.float32, device=logits.device)
+    loss = torch.zeros((1,), dtype=torch.float32, device=logits.device)
+    if isinstance(grad, str) and grad == "new":
+        g = torch.empty(logits.shape, dtype=grad_dtype or torch.float32, device=logits.device)
+    elif isinstance(grad, str) and grad == "inplace":
+        g = logits
+    elif grad is None:
+        g = None
+    else:
+        g = grad
+    if g is not None:
+        if g.stride(-1) != 1 or g.shape != logits.shape:
+            raise ValueError("grad must match the logits' shape with a contiguous last dimension")
+        ldg = g.reshape(rows, V).stride(0) if rows > 1 else V
+    else:
+        ldg = 0
+    st = load_library().mi_cross_entropy(
+        _stream(), _ptr(L2), _dt(logits), ld, _ptr(tg), rows, V, float(scale), _ptr(row_loss),
+        _ptr(loss), _ptr(g), _dt(g) if g is not None else MI_F32, ldg)
+    if sync is None:
+        _finish("mi_cross_entropy", st)
+    else:
+        _check("mi_cross_entropy", st)
+    return loss, row_loss, g
+
+
+class CrossEntropyLoss:
+    """Mirror of the reference's CrossEntropyLoss (Loss.hpp; Loss.cpp:43-195, GPU branch):
+    forward(logits [B,S,V], targets [B,S]) returns the mean loss as a Python float and
+    keeps the logits gradient; backward(targets) returns it ([B,S,V] fp32, scaled by
+    1 / (B*S))."""
+
+    def __init__(self):
+        self._grad = None
+
+    def forward(self, logits, targets) -> float:
+        loss, _, self._grad = cross_entropy(logits, targets)
+        return float(loss.item())
+
+    def backward(self, targets=None):
+        if self._grad is None:
+            raise RuntimeError("CrossEntropyLoss.backward before forward")
+        return self._grad

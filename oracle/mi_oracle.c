@@ -31,6 +31,10 @@
  *   mo_attention_fwd / mo_attention_bwd
  *                  Attention.cpp:236-280 (forward, causal, stable softmax, GQA map
  *                  kv_h = h / (nH/nKV)) and Attention.cpp:292-348 (backward).
+ *   mo_cross_entropy
+ *                  Loss.cpp:43-195 (CrossEntropyLoss forward and backward): softmax
+ *                  with max subtraction, -log(max(p_target, 1e-15)), the logits
+ *                  gradient (p - onehot) * scale and the mean loss.
  *   mo_sgemm_omp   fp32 cache-blocked OpenMP SGEMM with cblas_sgemm row-major
  *                  semantics -- the CPU baseline timed next to the GPU.
  *   bf16 helpers   Tensor.hpp:16-27 (truncating fp32->bf16, bf16->fp32) plus RNE.
@@ -277,6 +281,44 @@ void mo_attention_bwd(int64_t Bn, int64_t nH, int64_t nKV, int64_t T, int64_t d,
       free(p);
       free(dp);
     }
+}
+
+/*
+ * Loss.cpp:43-195 in float64.  Per row r (token) with target y = targets[r]:
+ * m = max_v x[v] (Loss.cpp:95-101), s = sum_v exp(x[v] - m) (:103-107),
+ * p[v] = exp(x[v] - m) / s (:109-112), row_loss[r] = -log(max(p[y], 1e-15f))
+ * (:114-116), grad[r*vocab + v] = (p[v] - [v == y]) * scale (:160, :182-186;
+ * the reference's scale is 1 / (batch*seq_len)).  Returns scale * sum_r
+ * row_loss[r] (:128-132).  grad may be NULL.  A target outside [0, vocab)
+ * gives a NaN row loss and no one-hot term.
+ */
+double mo_cross_entropy(const float* logits, int64_t ld, const int64_t* targets, int64_t rows,
+                        int64_t vocab, double scale, double* row_loss, double* grad) {
+  const double floor_p = (double)1e-15f;
+#pragma omp parallel for schedule(static)
+  for (int64_t r = 0; r < rows; ++r) {
+    const float* x = logits + r * ld;
+    double m = -INFINITY;
+    for (int64_t v = 0; v < vocab; ++v)
+      if ((double)x[v] > m) m = (double)x[v];
+    double sum = 0.0;
+    for (int64_t v = 0; v < vocab; ++v) sum += exp((double)x[v] - m);
+    const int64_t y = targets[r];
+    const int valid = y >= 0 && y < vocab;
+    if (valid) {
+      const double py = exp((double)x[y] - m) / sum;
+      row_loss[r] = -log(py > floor_p ? py : floor_p);
+      if (py != py) row_loss[r] = py;  /* NaN stays NaN, as std::max keeps it */
+    } else {
+      row_loss[r] = NAN;
+    }
+    if (grad)
+      for (int64_t v = 0; v < vocab; ++v)
+        grad[r * vocab + v] = (exp((double)x[v] - m) / sum - (valid && v == y ? 1.0 : 0.0)) * scale;
+  }
+  double total = 0.0;
+  for (int64_t r = 0; r < rows; ++r) total += row_loss[r];
+  return total * scale;
 }
 
 /* ---- fp32 CPU SGEMM baseline (cblas_sgemm semantics, MetalBridge.mm:695-697) -- */

@@ -7,7 +7,7 @@ Every function here forwards to mi_oracle.c, whose header lists the reference
 file:line each routine restates (Tensor.hpp:16-27, MetalBridge.mm:691-701,
 gemm_bf16.metal:45,63, gemm_backward.metal:104-115, gemm_ffn.metal:160-181,
 fused_swiglu_gemm.metal:48-77, Activations.cpp:31-75, residual_add.metal:27,
-Attention.cpp:236-348).
+Attention.cpp:236-348, Loss.cpp:43-195).
 """
 from __future__ import annotations
 
@@ -53,6 +53,8 @@ def lib():
                                  _vp, _vp, _i64, ctypes.c_int, _vp, _i64, _vp, _i64]
         L.mo_attention_fwd.argtypes = [_i64] * 5 + [_vp] * 5
         L.mo_attention_bwd.argtypes = [_i64] * 5 + [_vp] * 7
+        L.mo_cross_entropy.restype = _dbl
+        L.mo_cross_entropy.argtypes = [_vp, _i64, _vp, _i64, _i64, _dbl, _vp, _vp]
         L.mo_sgemm_omp.argtypes = [ctypes.c_int, ctypes.c_int, _i64, _i64, _i64, ctypes.c_float,
                                    _vp, _i64, _vp, _i64, ctypes.c_float, _vp, _i64]
         L.mo_num_threads.restype = ctypes.c_int
@@ -146,6 +148,20 @@ def attention_bwd(Q4, K4, V4, dO):
     lib().mo_attention_bwd(Bn, nH, nKV, T, d, _p(Q4), _p(K4), _p(V4), _p(dO),
                            _p(dQ), _p(dK), _p(dV))
     return dQ, dK, dV
+
+
+def cross_entropy(logits, targets, scale=None, want_grad=True):
+    """Loss.cpp:43-195. logits [rows, V] (fp32 values), targets [rows] integers ->
+    (loss, row_loss [rows], grad [rows, V] or None), float64; scale defaults to 1/rows."""
+    x = _f32(logits)
+    rows, V = x.shape
+    t = np.ascontiguousarray(targets, dtype=np.int64).reshape(-1)
+    if scale is None:
+        scale = 1.0 / rows
+    row_loss = np.empty((rows,), dtype=np.float64)
+    grad = np.empty((rows, V), dtype=np.float64) if want_grad else None
+    loss = lib().mo_cross_entropy(_p(x), V, _p(t), rows, V, float(scale), _p(row_loss), _p(grad))
+    return loss, row_loss, grad
 
 
 def sgemm_omp(tA, tB, M, N, K, A, B, C=None, alpha=1.0, beta=0.0, lda=None, ldb=None):

@@ -314,6 +314,32 @@ int main() {
     dfree(dq_in); dfree(dk_in); dfree(dv_in); dfree(dgo); dfree(dO_out);
     dfree(dQg); dfree(dKg); dfree(dVg);
   }
+  {  // GB-13: cross_entropy with the known answers of test_loss.cpp:56-87 (TC-01, TC-02):
+     // uniform logits over 4 classes, target 2 -> loss log 4, grad [.25 .25 -.75 .25]; two
+     // rows (scale 1/2).  Inside a scope the loss arrives at end_scope().
+    std::vector<uint16_t> hl(8, bf(0.0f));
+    std::vector<uint32_t> ht = {2, 2};
+    uint16_t* dl = dev(hl);
+    uint32_t* dt = dev(ht);
+    float* dg = nullptr;
+    (void)hipMalloc((void**)&dg, 8 * sizeof(float));
+    float loss = -1.0f;
+    mi_bridge::cross_entropy(dl, dt, &loss, dg, 2, 4);
+    bool ok = mi_bridge::last_status() == MI_OK;
+    std::vector<float> hg = host(dg, 8);
+    const float want[4] = {0.125f, 0.125f, -0.375f, 0.125f};
+    double e = std::fabs(loss - std::log(4.0));
+    for (int i = 0; i < 8; ++i) e = std::fmax(e, std::fabs(hg[i] - want[i % 4]));
+    float loss2 = -1.0f;
+    mi_bridge::begin_scope();
+    mi_bridge::cross_entropy(dl, dt, &loss2, dg, 2, 4);
+    mi_bridge::end_scope();
+    ok = ok && mi_bridge::last_status() == MI_OK;
+    e = std::fmax(e, std::fabs(loss2 - std::log(4.0)));
+    row("GB-13", "cross_entropy TC-01/TC-02: loss log 4, grad (p - onehot)/2, <= 1e-5",
+        ok && e <= 1e-5, std::to_string(e));
+    dfree(dl); dfree(dt); dfree(dg);
+  }
   std::printf("%d/%d checks passed\n", g_passed, g_total);
   return g_passed == g_total ? 0 : 1;
 }

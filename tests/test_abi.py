@@ -143,3 +143,30 @@ def test_workspace_query(mi):
     assert mi.workspace_size(1, 0, 1024, 1024, 65536) > 0
     assert mi.workspace_size(0, 0, 8192, 5632, 2048) == 0
     assert mi.workspace_size(0, 0, 0, 5, 5) == 0
+
+
+def test_cross_entropy_validation(mi):
+    # mi_cross_entropy rejects bad arguments before any device work.
+    lib = mi.load_library()
+    vp = ctypes.c_void_p
+
+    def ce(rows=4, vocab=64, ld=64, L=4096, T=8192, RL=12288, LO=16384, G=None, gdt=0, ldg=64, dt=1):
+        st = lib.mi_cross_entropy(None, vp(L) if L else None, dt, ld, vp(T) if T else None, rows,
+                                  vocab, 0.25, vp(RL) if RL else None, vp(LO) if LO else None,
+                                  vp(G) if G else None, gdt, ldg)
+        return st, lib.mi_last_error().decode()
+
+    assert ce(rows=0)[0] == 0 and ce(vocab=0)[0] == 0    # no-op, as the reference
+    assert ce(rows=-1)[0] == 1                           # MI_ERR_SHAPE
+    st, msg = ce(ld=10)
+    assert st == 2 and "ld_logits" in msg                # MI_ERR_LD
+    st, msg = ce(G=65536, ldg=10)
+    assert st == 2 and "ld_grad" in msg
+    assert ce(L=0)[0] == 3 and ce(T=0)[0] == 3 and ce(RL=0)[0] == 3   # MI_ERR_NULL
+    assert ce(dt=7)[0] == 4                              # MI_ERR_DTYPE
+    assert ce(G=65536, gdt=9)[0] == 4
+    # a gradient that overlaps the logits without being the same array
+    st, msg = ce(G=4096 + 64, gdt=1, ldg=64)
+    assert st == 5 and "overlaps" in msg                 # MI_ERR_UNSUPPORTED
+    st, msg = ce(L=4097)
+    assert st == 5 and "aligned" in msg
