@@ -72,9 +72,10 @@ def parse():
     ap.add_argument("--cpu-rows", type=int, default=2048, help="token rows of the CPU sample")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="also launch a 1 GiB device copy (for PMC byte-counter scaling)")
-    ap.add_argument("--workload", choices=("block", "attention"), default="block",
+    ap.add_argument("--workload", choices=("block", "attention", "lm_head"), default="block",
                     help="block: the configuration-3 GEMM set (the headline metric); attention: "
-                         "configuration 4, fused GQA attention forward + backward")
+                         "configuration 4, fused GQA attention forward + backward; lm_head: "
+                         "configuration 5, LM-head GEMMs with the fused cross-entropy between")
     return ap.parse_args()
 
 
@@ -197,6 +198,143 @@ def attention_main(args):
     print(json.dumps(out))
 
 
+LMH = dict(M=8192, H=2048, V=32000)               # benchmark configuration 5
+LMH_GEMM_FLOPS = 2 * 8192 * 2048 * 32000            # one of the three LM-head GEMMs
+
+
+def cpu_lm_head_baseline(m_rows: int = 1024) -> dict:
+    """The oracle's fp32 OpenMP SGEMM for the three LM-head GEMMs and its float64
+    cross-entropy (Loss.cpp:43-195), on m_rows token rows of configuration 5."""
+    import numpy as np
+
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import oracle
+
+    H, V = LMH["H"], LMH["V"]
+    rng = np.random.default_rng(0)
+    x = rng.standard_normal((m_rows, H), dtype=np.float32)
+    e = rng.standard_normal((V, H), dtype=np.float32) * 0.02
+    t = rng.integers(0, V, m_rows)
+    de = np.zeros((V, H), np.float32)
+    t0 = time.perf_counter()
+    logits = oracle.sgemm_omp(0, 1, m_rows, V, H, x, e)                        # X E^T
+    _, _, dl = oracle.cross_entropy(logits, t)
+    dl = dl.astype(np.float32)
+    oracle.sgemm_omp(0, 0, m_rows, H, V, dl, e)                                # dX = dL E
+    oracle.sgemm_omp(1, 0, V, H, m_rows, dl, x, C=de, beta=1.0)                # dE += dL^T X
+    dt = time.perf_counter() - t0
+    flops = 3 * 2 * m_rows * H * V
+    return {"value": round(flops / dt / 1e12, 4), "unit": "TFLOP/s", "cores": oracle.num_threads(),
+            "kind": "port",
+            "sample": f"configuration 5 at M={m_rows} token rows instead of {LMH['M']}: fp32 SGEMMs "
+                      f"+ float64 cross-entropy, {flops / 1e9:.1f} GFLOP, {dt:.2f} s"}
+
+
+def lm_head_main(args):
+    """Configuration 5: one step = logits = X E^T (NT, bf16 out), the fused cross-entropy
+    overwriting the logits with dL = (softmax - onehot) / M (bf16), dX = dL E (NN, bf16) and
+    dE += dL^T X (TN, fp32 accumulate), all operands resident in HBM. value counts the three
+    GEMMs' FLOPs over the whole step's time (the cross-entropy included)."""
+    import torch
+
+    import mi_gemm as mi
+
+    dev = torch.device("cuda:0")
+    mi.init()
+    M, H, V = LMH["M"], LMH["H"], LMH["V"]
+    g = torch.Generator(device=dev)
+    g.manual_seed(5)
+    ws = torch.empty(WS_BYTES // 4, dtype=torch.float32, device=dev)
+    X = torch.randn((M, H), generator=g, device=dev).to(torch.bfloat16)
+    E = (torch.randn((V, H), generator=g, device=dev) * 0.02).to(torch.bfloat16)
+    T = torch.randint(0, V, (M,), generator=g, device=dev).to(torch.int32)
+    logits = torch.empty((M, V), dtype=torch.bfloat16, device=dev)
+    dX = torch.empty((M, H), dtype=torch.bfloat16, device=dev)
+    dE = torch.zeros((V, H), dtype=torch.float32, device=dev)
+    row_loss = torch.empty((M,), dtype=torch.float32, device=dev)
+    loss = torch.empty((1,), dtype=torch.float32, device=dev)
+    ops = [
+        ("logits NT", LMH_GEMM_FLOPS, mi.describe(0, 1, M, V, H, workspace_bytes=WS_BYTES),
+         lambda: mi.gemm(X, E, logits, M, V, H, transB=True, workspace=ws, sync=False)),
+        ("cross-entropy", 0, "xent_vec_kernel bf16 in place",
+         lambda: mi.cross_entropy(logits, T, grad="inplace", sync=False, row_loss=row_loss,
+                                  loss=loss)),
+        ("dX NN", LMH_GEMM_FLOPS, mi.describe(0, 0, M, H, V, workspace_bytes=WS_BYTES),
+         lambda: mi.gemm(logits, E, dX, M, H, V, workspace=ws, sync=False)),
+        ("dE TN", LMH_GEMM_FLOPS, mi.describe(1, 0, V, H, M, workspace_bytes=WS_BYTES),
+         lambda: mi.gemm(logits, X, dE, V, H, M, transA=True, beta=1.0, workspace=ws, sync=False)),
+    ]
+
+    def step():
+        for op in ops:
+            op[3]()
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    # attribution pass: events around every launch
+    n_attr = 3
+    evs = [[(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+            for _ in ops] for _ in range(n_attr)]
+    for s_ in range(n_attr):
+        for i, op in enumerate(ops):
+            evs[s_][i][0].record()
+            op[3]()
+            evs[s_][i][1].record()
+    torch.cuda.synchronize()
+    per_ms = [sum(evs[s_][i][0].elapsed_time(evs[s_][i][1]) for s_ in range(n_attr)) / n_attr
+              for i in range(len(ops))]
+    dom = max((i for i in range(len(ops)) if ops[i][1]), key=lambda i: per_ms[i])
+    xi = 1
+    # timed region: back to back, events around the dominant GEMM and the cross-entropy only
+    tev = [[(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+            for _ in range(2)] for _ in range(args.steps)]
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for s_ in range(args.steps):
+        for i, op in enumerate(ops):
+            k = 0 if i == dom else (1 if i == xi else None)
+            if k is not None:
+                tev[s_][k][0].record()
+            op[3]()
+            if k is not None:
+                tev[s_][k][1].record()
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - t0
+    ms_dom = sum(a.elapsed_time(b) for (a, b), _ in tev) / args.steps
+    ms_x = sum(a.elapsed_time(b) for _, (a, b) in tev) / args.steps
+    flops = 3 * LMH_GEMM_FLOPS
+    value = flops * args.steps / elapsed / 1e12
+    achieved = LMH_GEMM_FLOPS / (ms_dom / 1e3) / 1e12
+    x_bytes = M * V * 2 * 2 + M * 4 * 2           # logits read + gradient written, targets, row losses
+    x_gbs = x_bytes / (ms_x / 1e3) / 1e9
+    out = {
+        "metric": "LM head + cross-entropy TFLOP/s (configuration 5: logits NT, dX NN, dE TN)",
+        "value": round(value, 2), "unit": "TFLOP/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": round(elapsed / args.steps * 1e3, 4),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
+        "data": "synthetic (torch.randn on device; X~N(0,1), E~N(0,0.02), uniform targets)",
+        "config": {"workload": "LM head M=8192 tokens, H=2048, V=32000: logits = X E^T (bf16), "
+                               "fused softmax cross-entropy in place (dL bf16, scale 1/M), "
+                               "dX = dL E (bf16), dE += dL^T X (fp32)",
+                   "flops_per_step": flops,
+                   "per_op_ms": {op[0]: round(t, 4) for op, t in zip(ops, per_ms)},
+                   "per_gemm_tflops": {op[0]: round(op[1] / (t / 1e3) / 1e12, 1)
+                                       for op, t in zip(ops, per_ms) if op[1]},
+                   "kernels": {op[0]: op[2] for op in ops},
+                   "cross_entropy": {"ms": round(ms_x, 4), "bytes": x_bytes,
+                                     "achieved_GBs": round(x_gbs, 1), "peak_GBs": PEAK_HBM_GBS,
+                                     "frac": round(x_gbs / PEAK_HBM_GBS, 4)}},
+        "roofline": {"bound": "mfma", "achieved": round(achieved, 2), "peak": PEAK_BF16_TFLOPS,
+                     "unit": "TFLOP/s", "frac": round(achieved / PEAK_BF16_TFLOPS, 4),
+                     "traffic": None, "kernel": ops[dom][2], "gemms": [ops[dom][0]],
+                     "avg_launch_ms": round(ms_dom, 4)},
+    }
+    if not args.no_cpu:
+        out["cpu_baseline"] = cpu_lm_head_baseline()
+    print(json.dumps(out))
+
+
 def main():
     args = parse()
     if args.gpus != 1:
@@ -205,6 +343,9 @@ def main():
         sys.exit(2)
     if args.workload == "attention":
         attention_main(args)
+        return
+    if args.workload == "lm_head":
+        lm_head_main(args)
         return
     import torch
 

@@ -510,7 +510,8 @@ def attention_backward(Q4, K4, V4, dO, P, grad_dtype=None):
 
 # ---- loss ---------------------------------------------------------------------
 
-def cross_entropy(logits, targets, grad="new", grad_dtype=None, scale=None, sync=None):
+def cross_entropy(logits, targets, grad="new", grad_dtype=None, scale=None, sync=None,
+                  row_loss=None, loss=None):
     """Softmax cross-entropy over the rows of logits [..., V] (metal_bridge::cross_entropy,
     MetalBridge.hpp:89-91; CrossEntropyLoss, Loss.cpp:43-195).
 
@@ -520,7 +521,8 @@ def cross_entropy(logits, targets, grad="new", grad_dtype=None, scale=None, sync
     [rows] = -log(max(p_target, 1e-15)), grad = scale * (softmax - onehot) shaped like
     logits. grad: "new" allocates it in grad_dtype (default fp32, the reference's),
     "inplace" overwrites the logits, None skips it, or a tensor to write into.
-    scale defaults to 1 / rows, the reference's mean."""
+    scale defaults to 1 / rows, the reference's mean. row_loss ([rows] fp32) and loss ([1]
+    fp32) may be given to reuse device buffers."""
     torch = _torch()
     V = logits.shape[-1]
     rows = logits.numel() // V if V else 0
@@ -533,8 +535,12 @@ def cross_entropy(logits, targets, grad="new", grad_dtype=None, scale=None, sync
         raise ValueError(f"targets has {tg.numel()} entries for {rows} rows")
     if scale is None:
         scale = 1.0 / rows if rows else 0.0
-    row_loss = torch.empty((rows,), dtype=torch.float32, device=logits.device)
-    loss = torch.zeros((1,), dtype=torch.float32, device=logits.device)
+    if row_loss is None:
+        row_loss = torch.empty((rows,), dtype=torch.float32, device=logits.device)
+    if loss is None:
+        loss = torch.empty((1,), dtype=torch.float32, device=logits.device)
+    if row_loss.numel() < rows or row_loss.dtype != torch.float32 or loss.dtype != torch.float32:
+        raise ValueError("row_loss must hold rows fp32 values and loss one fp32 value")
     if isinstance(grad, str) and grad == "new":
         g = torch.empty(logits.shape, dtype=grad_dtype or torch.float32, device=logits.device)
     elif isinstance(grad, str) and grad == "inplace":
