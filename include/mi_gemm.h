@@ -211,6 +211,42 @@ int mi_cross_entropy(void* stream, const void* logits, int32_t logits_dtype, int
                      int64_t ld_grad);
 
 /*
+ * RMSNorm forward over rows of dims values: with residual != NULL, first
+ * x += residual (x updated in place, in its own dtype), then
+ *   y = x / sqrt(sum(x^2)/dims + eps) * weight
+ * computed in fp32.  x, residual, y are [rows, ld] of `dtype` (MI_BF16 or
+ * MI_F32), weight [dims] of w_dtype; rstd (optional, fp32 [rows]) receives
+ * 1/rms per row.  y may be x itself; arrays must otherwise not overlap.
+ * Replaces metal_bridge::rms_norm_forward (MetalBridge.hpp:60-61,
+ * rms_norm_forward.metal; RMSNorm::forward, RMSNorm.cpp:48-75) and
+ * metal_bridge::fused_add_norm (MetalBridge.hpp:79-81, fused_add_norm.metal;
+ * h += out; ffn_in = rmsnorm(h), Transformer.cpp:150-158).
+ */
+int mi_rmsnorm_fwd(void* stream, void* x, const void* residual, const void* weight, int32_t w_dtype,
+                   void* y, float* rstd, int64_t rows, int64_t dims, int64_t ld, int32_t dtype,
+                   float eps);
+
+/* Workspace bytes mi_rmsnorm_bwd needs when it computes dw. */
+size_t mi_rmsnorm_bwd_workspace_size(int64_t rows, int64_t dims);
+
+/*
+ * RMSNorm backward: with xhat = x / rms and rms = sqrt(sum(x^2)/dims + eps),
+ *   dx = (dy*w - xhat * mean(dy*w*xhat)) / rms  [+ residual_grad]
+ *   dw = dw_beta * dw + sum over rows of dy * xhat     (if dw is not NULL)
+ * dy, x, residual_grad, dx are [rows, ld] of `dtype`; weight [dims] of
+ * w_dtype; dw [dims] of dw_dtype.  dx may be dy, x or residual_grad itself.
+ * dw needs workspace of mi_rmsnorm_bwd_workspace_size bytes; it is summed in
+ * a fixed order (bit-identical across launches).  Replaces
+ * metal_bridge::rms_norm_backward (MetalBridge.hpp:62-64, rms_norm_backward.metal;
+ * RMSNorm::backward, RMSNorm.cpp:77-180) and metal_bridge::fused_backward_add_norm
+ * (MetalBridge.hpp:82-85, fused_backward_add_norm.metal, Transformer.cpp:441-466).
+ */
+int mi_rmsnorm_bwd(void* stream, const void* dy, const void* x, const void* weight, int32_t w_dtype,
+                   const void* residual_grad, void* dx, void* dw, int32_t dw_dtype, float dw_beta,
+                   int64_t rows, int64_t dims, int64_t ld, int32_t dtype, float eps,
+                   void* workspace, size_t workspace_bytes);
+
+/*
  * Describe the kernel mi_gemm_batched would launch for this problem (tile,
  * loader, split-K factor) as text into buf (always NUL-terminated).  For
  * measurement and logging; no reference counterpart.  epi_mode: 0 plain,

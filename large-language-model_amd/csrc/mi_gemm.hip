@@ -20,6 +20,7 @@
 #include "../../include/mi_gemm.h"
 #include "mi_attn.hpp"
 #include "mi_xent.hpp"
+#include "mi_norm.hpp"
 #include "mi_gemm_kernels.hpp"
 
 using namespace mig;
@@ -197,6 +198,13 @@ Plan make_plan(int dtype_in, int64_t M, int64_t N, int64_t Ktot, int64_t batch, 
 }
 
 bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
+
+// Two row arrays of `bytes` bytes each that share memory without being the same array.
+bool rows_overlap(const void* a, const void* b, int64_t bytes) {
+  if (!a || !b || a == b) return false;
+  const uintptr_t a0 = (uintptr_t)a, b0 = (uintptr_t)b;
+  return a0 < b0 + (uintptr_t)bytes && b0 < a0 + (uintptr_t)bytes;
+}
 
 struct Problem {
   int transA, transB;
@@ -646,6 +654,85 @@ int mi_flash_attn_bwd(void* stream, const void* Q, const void* K, const void* V,
   hipError_t e = launch_flash_bwd(p, (int)head_dim, (hipStream_t)stream);
   return e == hipSuccess ? MI_OK : fail(MI_ERR_HIP, "flash attention backward launch: %s",
                                         hipGetErrorString(e));
+}
+
+size_t mi_rmsnorm_bwd_workspace_size(int64_t rows, int64_t dims) {
+  if (rows <= 0 || dims <= 0 || rows > INT32_MAX || dims > INT32_MAX) return 0;
+  return (size_t)norm_bwd_grid((int)rows) * (size_t)dims * sizeof(float);
+}
+
+int mi_rmsnorm_fwd(void* stream, void* x, const void* residual, const void* weight, int32_t w_dtype,
+                   void* y, float* rstd, int64_t rows, int64_t dims, int64_t ld, int32_t dtype,
+                   float eps) {
+  if (rows < 0 || dims < 0) return fail(MI_ERR_SHAPE, "negative size");
+  if (rows == 0 || dims == 0) return MI_OK;
+  if (rows > INT32_MAX || dims > INT32_MAX) return fail(MI_ERR_SHAPE, "size exceeds 2^31-1");
+  if ((dtype != MI_F32 && dtype != MI_BF16) || (w_dtype != MI_F32 && w_dtype != MI_BF16))
+    return fail(MI_ERR_DTYPE, "dtype %d / weight dtype %d", dtype, w_dtype);
+  if (!x || !weight || !y) return fail(MI_ERR_NULL, "x, weight or y is NULL");
+  if (ld < dims) return fail(MI_ERR_LD, "ld=%lld < dims=%lld", (long long)ld, (long long)dims);
+  const int64_t es = dtype == MI_BF16 ? 2 : 4, wes = w_dtype == MI_BF16 ? 2 : 4;
+  const void* rows_arr[] = {x, y, residual};
+  for (const void* q : rows_arr)
+    if ((uintptr_t)q % es) return fail(MI_ERR_UNSUPPORTED, "row arrays must be aligned to their element size");
+  if ((uintptr_t)weight % wes || ((uintptr_t)rstd & 3u))
+    return fail(MI_ERR_UNSUPPORTED, "weight and rstd must be aligned to their element size");
+  const int64_t extent = ((rows - 1) * ld + dims) * es;
+  if (rows_overlap(y, x, extent) || rows_overlap(y, residual, extent) || rows_overlap(x, residual, extent))
+    return fail(MI_ERR_UNSUPPORTED, "x, residual and y must each be the same array or disjoint");
+  const int64_t ev = 16 / es;
+  const bool vector_path = dims % ev == 0 && (ld * es) % 16 == 0 && aligned16(x) && aligned16(y) &&
+                           (!residual || aligned16(residual)) &&
+                           (uintptr_t)weight % (w_dtype == MI_BF16 && ev == 4 ? 8 : 16) == 0 &&
+                           dims / ev <= 64 * NORM_MAX_VEC_PER_LANE;
+  int st = init_devices();
+  if (st != MI_OK) return st;
+  NormParams p{};
+  p.x = x; p.r = residual; p.w = weight; p.y = y; p.rstd = rstd;
+  p.ld = ld; p.rows = (int)rows; p.dims = (int)dims; p.eps = eps;
+  hipError_t e = launch_norm_fwd(p, dtype == MI_BF16, w_dtype == MI_BF16, vector_path, (hipStream_t)stream);
+  return e == hipSuccess ? MI_OK : fail(MI_ERR_HIP, "rmsnorm_fwd launch: %s", hipGetErrorString(e));
+}
+
+int mi_rmsnorm_bwd(void* stream, const void* dy, const void* x, const void* weight, int32_t w_dtype,
+                   const void* residual_grad, void* dx, void* dw, int32_t dw_dtype, float dw_beta,
+                   int64_t rows, int64_t dims, int64_t ld, int32_t dtype, float eps,
+                   void* workspace, size_t workspace_bytes) {
+  if (rows < 0 || dims < 0) return fail(MI_ERR_SHAPE, "negative size");
+  if (rows == 0 || dims == 0) return MI_OK;
+  if (rows > INT32_MAX || dims > INT32_MAX) return fail(MI_ERR_SHAPE, "size exceeds 2^31-1");
+  if ((dtype != MI_F32 && dtype != MI_BF16) || (w_dtype != MI_F32 && w_dtype != MI_BF16) ||
+      (dw && dw_dtype != MI_F32 && dw_dtype != MI_BF16))
+    return fail(MI_ERR_DTYPE, "dtype %d / weight dtype %d / dw dtype %d", dtype, w_dtype, dw_dtype);
+  if (!dy || !x || !weight || !dx) return fail(MI_ERR_NULL, "dy, x, weight or dx is NULL");
+  if (ld < dims) return fail(MI_ERR_LD, "ld=%lld < dims=%lld", (long long)ld, (long long)dims);
+  const size_t need = mi_rmsnorm_bwd_workspace_size(rows, dims);
+  if (dw && (!workspace || workspace_bytes < need))
+    return fail(MI_ERR_WORKSPACE, "dw needs %zu workspace bytes (got %zu)", need, workspace ? workspace_bytes : 0);
+  const int64_t es = dtype == MI_BF16 ? 2 : 4, wes = w_dtype == MI_BF16 ? 2 : 4;
+  const void* rows_arr[] = {dy, x, dx, residual_grad};
+  for (const void* q : rows_arr)
+    if ((uintptr_t)q % es) return fail(MI_ERR_UNSUPPORTED, "row arrays must be aligned to their element size");
+  if ((uintptr_t)weight % wes || (dw && (uintptr_t)dw % (dw_dtype == MI_BF16 ? 2 : 4)) ||
+      ((uintptr_t)workspace & 3u))
+    return fail(MI_ERR_UNSUPPORTED, "weight, dw and workspace must be aligned to their element size");
+  const int64_t extent = ((rows - 1) * ld + dims) * es;
+  if (rows_overlap(dx, dy, extent) || rows_overlap(dx, x, extent) || rows_overlap(dx, residual_grad, extent))
+    return fail(MI_ERR_UNSUPPORTED, "dx and each input must be the same array or disjoint");
+  const int64_t ev = 16 / es;
+  const bool vector_path = dims % ev == 0 && (ld * es) % 16 == 0 && aligned16(dy) && aligned16(x) &&
+                           aligned16(dx) && (!residual_grad || aligned16(residual_grad)) &&
+                           (uintptr_t)weight % (w_dtype == MI_BF16 && ev == 4 ? 8 : 16) == 0 &&
+                           dims / ev <= 64 * NORM_MAX_VEC_PER_LANE;
+  int st = init_devices();
+  if (st != MI_OK) return st;
+  NormParams p{};
+  p.x = (void*)x; p.r = residual_grad; p.w = weight; p.dy = dy; p.dx = dx; p.dw = dw;
+  p.ws = (float*)workspace;
+  p.ld = ld; p.rows = (int)rows; p.dims = (int)dims; p.eps = eps; p.dw_beta = dw_beta;
+  hipError_t e = launch_norm_bwd(p, dtype == MI_BF16, w_dtype == MI_BF16, dw_dtype == MI_BF16,
+                                 vector_path, (hipStream_t)stream);
+  return e == hipSuccess ? MI_OK : fail(MI_ERR_HIP, "rmsnorm_bwd launch: %s", hipGetErrorString(e));
 }
 
 int mi_cross_entropy(void* stream, const void* logits, int32_t logits_dtype, int64_t ld_logits,

@@ -1,0 +1,384 @@
+// mi_norm.hip -- RMSNorm forward (optionally after a residual add) and backward
+// (optionally plus a residual gradient, optionally with the weight gradient),
+// gfx950.
+//
+// Reference (cpp/ of the engine): RMSNorm::forward / backward (src/RMSNorm.cpp:48-180),
+// GPU kernels rms_norm_forward.metal, rms_norm_backward.metal, and the fused forms
+// the decoder layer calls: fused_add_norm (h += r; y = rmsnorm(h), Transformer.cpp:150-158)
+// and fused_backward_add_norm (dx = rmsnorm_backward(dy) + residual gradient,
+// Transformer.cpp:441-466).  Per row of dims values, in fp32:
+//   rms = sqrt(sum x^2 / dims + eps)
+//   y   = (x / rms) * w                                   (RMSNorm.cpp:40-47)
+//   dx  = (1/rms) * (dy*w - xhat * mean(dy*w*xhat)) [+ r], xhat = x / rms  (RMSNorm.cpp:137-160)
+//   dw  = sum over rows of dy * xhat                       (RMSNorm.cpp:163-176)
+// With a residual in the forward, x is first replaced by x + r in its own dtype (as
+// the reference writes h back for the backward) and the norm uses the stored value.
+//
+// HBM-bound row kernels.  Register path: one wave per row, each lane holding up to
+// 8 16-byte vectors of the row (4096 bf16 / 2048 fp32 values), reductions by
+// butterflies inside the wave, no LDS and no barriers in the forward.  The backward
+// runs a fixed grid of 4-wave workgroups over the rows, each lane accumulating the
+// weight gradient of its own columns in registers; the waves of a workgroup add
+// their partials in wave order through LDS into one workspace row, and a second
+// kernel sums the workspace rows in order: dw is bit-identical across launches.
+// Generic path (rows that are not whole aligned 16-byte vectors, or longer): one
+// 256-thread workgroup per row, strided passes over global memory.
+#include <hip/hip_runtime.h>
+#include <math.h>
+
+#include "mi_gemm_device.hpp"
+#include "mi_norm.hpp"
+
+namespace mig {
+namespace {
+
+typedef uint32_t nu32x4_t __attribute__((ext_vector_type(4)));
+typedef uint32_t nu32x2_t __attribute__((ext_vector_type(2)));
+
+__device__ __forceinline__ float nwave_sum(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+  return v;  // commutative steps: every lane holds the same bits
+}
+
+__device__ __forceinline__ float bf16_round(float v) { return bf16_bits_to_f32(f32_to_bf16_rne(v)); }
+
+// One 16-byte vector of activations: 8 bf16 or 4 fp32 values at element e0.
+template <bool BF16>
+__device__ __forceinline__ void load_act(const char* row, int e0, float* v) {
+  if constexpr (BF16) {
+    const nu32x4_t q = *(const nu32x4_t*)(row + (int64_t)e0 * 2);
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      v[2 * k] = __uint_as_float(q[k] << 16);
+      v[2 * k + 1] = __uint_as_float(q[k] & 0xffff0000u);
+    }
+  } else {
+    const nu32x4_t q = *(const nu32x4_t*)(row + (int64_t)e0 * 4);
+#pragma unroll
+    for (int k = 0; k < 4; ++k) v[k] = __uint_as_float(q[k]);
+  }
+}
+
+template <bool BF16>
+__device__ __forceinline__ void store_act(char* row, int e0, const float* v) {
+  if constexpr (BF16)
+    *(nu32x4_t*)(row + (int64_t)e0 * 2) = nu32x4_t{pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3]),
+                                                    pack_bf16x2(v[4], v[5]), pack_bf16x2(v[6], v[7])};
+  else
+    *(nu32x4_t*)(row + (int64_t)e0 * 4) = nu32x4_t{__float_as_uint(v[0]), __float_as_uint(v[1]),
+                                                   __float_as_uint(v[2]), __float_as_uint(v[3])};
+}
+
+// EV weight values at element e0 (EV = 8 for bf16 activations, 4 for fp32).
+template <bool W_BF16, int EV>
+__device__ __forceinline__ void load_w(const void* w, int e0, float* v) {
+  if constexpr (W_BF16 && EV == 8) {
+    load_act<true>((const char*)w, e0, v);
+  } else if constexpr (W_BF16) {
+    const nu32x2_t q = *(const nu32x2_t*)((const char*)w + (int64_t)e0 * 2);
+    v[0] = __uint_as_float(q[0] << 16);
+    v[1] = __uint_as_float(q[0] & 0xffff0000u);
+    v[2] = __uint_as_float(q[1] << 16);
+    v[3] = __uint_as_float(q[1] & 0xffff0000u);
+  } else {
+#pragma unroll
+    for (int h = 0; h < EV / 4; ++h) load_act<false>((const char*)w, e0 + 4 * h, v + 4 * h);
+  }
+}
+
+template <bool BF16>
+__device__ __forceinline__ float ld_elem(const void* row, int c) {
+  if constexpr (BF16) return bf16_bits_to_f32(((const uint16_t*)row)[c]);
+  else return ((const float*)row)[c];
+}
+
+// Stores v at element c and returns the value as stored.
+template <bool BF16>
+__device__ __forceinline__ float st_elem(void* row, int c, float v) {
+  if constexpr (BF16) {
+    const uint32_t h = f32_to_bf16_rne(v);
+    ((uint16_t*)row)[c] = (uint16_t)h;
+    return bf16_bits_to_f32(h);
+  } else {
+    ((float*)row)[c] = v;
+    return v;
+  }
+}
+
+// Sum over a 256-thread workgroup, combined in wave order; red holds 4 floats.
+__device__ __forceinline__ float block_sum256(float v, float* red) {
+  v = nwave_sum(v);
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
+  __syncthreads();
+  const float t = (red[0] + red[1]) + (red[2] + red[3]);
+  __syncthreads();  // red is reused by the next reduction
+  return t;
+}
+
+// ---- forward ----------------------------------------------------------------
+
+template <bool BF16, bool W_BF16, int NV>
+__global__ void __launch_bounds__(256) norm_fwd_vec(NormParams p) {
+  constexpr int EV = BF16 ? 8 : 4, ES = BF16 ? 2 : 4;
+  const int lane = threadIdx.x & 63;
+  const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (row >= p.rows) return;  // no barriers in this kernel
+  const int nvec = p.dims / EV;
+  char* xr = (char*)p.x + (int64_t)row * p.ld * ES;
+  float v[NV][EV];
+  float ss = 0.0f;
+#pragma unroll
+  for (int i = 0; i < NV; ++i) {
+    const int j = lane + 64 * i;
+    if (j < nvec) {
+      load_act<BF16>(xr, j * EV, v[i]);
+      if (p.r) {
+        float rv[EV];
+        load_act<BF16>((const char*)p.r + (int64_t)row * p.ld * ES, j * EV, rv);
+#pragma unroll
+        for (int e = 0; e < EV; ++e) v[i][e] += rv[e];
+        store_act<BF16>(xr, j * EV, v[i]);
+        if constexpr (BF16) {
+#pragma unroll
+          for (int e = 0; e < EV; ++e) v[i][e] = bf16_round(v[i][e]);  // the value stored
+        }
+      }
+#pragma unroll
+      for (int e = 0; e < EV; ++e) ss = __builtin_fmaf(v[i][e], v[i][e], ss);
+    }
+  }
+  ss = nwave_sum(ss);
+  const float rs = 1.0f / sqrtf(ss / (float)p.dims + p.eps);
+  if (p.rstd && lane == 0) p.rstd[row] = rs;
+  char* yr = (char*)p.y + (int64_t)row * p.ld * ES;
+#pragma unroll
+  for (int i = 0; i < NV; ++i) {
+    const int j = lane + 64 * i;
+    if (j < nvec) {
+      float wv[EV], o[EV];
+      load_w<W_BF16, EV>(p.w, j * EV, wv);
+#pragma unroll
+      for (int e = 0; e < EV; ++e) o[e] = v[i][e] * rs * wv[e];
+      store_act<BF16>(yr, j * EV, o);
+    }
+  }
+}
+
+template <bool BF16, bool W_BF16>
+__global__ void __launch_bounds__(256) norm_fwd_gen(NormParams p) {
+  constexpr int ES = BF16 ? 2 : 4;
+  __shared__ float red[4];
+  const int row = blockIdx.x;
+  char* xr = (char*)p.x + (int64_t)row * p.ld * ES;
+  const char* rr = p.r ? (const char*)p.r + (int64_t)row * p.ld * ES : nullptr;
+  char* yr = (char*)p.y + (int64_t)row * p.ld * ES;
+  float ss = 0.0f;
+  for (int c = threadIdx.x; c < p.dims; c += 256) {
+    float v = ld_elem<BF16>(xr, c);
+    if (rr) v = st_elem<BF16>(xr, c, v + ld_elem<BF16>(rr, c));
+    ss = __builtin_fmaf(v, v, ss);
+  }
+  ss = block_sum256(ss, red);
+  const float rs = 1.0f / sqrtf(ss / (float)p.dims + p.eps);
+  if (p.rstd && threadIdx.x == 0) p.rstd[row] = rs;
+  for (int c = threadIdx.x; c < p.dims; c += 256)  // each thread re-reads what it wrote
+    st_elem<BF16>(yr, c, ld_elem<BF16>(xr, c) * rs * ld_elem<W_BF16>(p.w, c));
+}
+
+// ---- backward ---------------------------------------------------------------
+
+template <bool BF16, bool W_BF16, int NV>
+__global__ void __launch_bounds__(256) norm_bwd_vec(NormParams p) {
+  constexpr int EV = BF16 ? 8 : 4, ES = BF16 ? 2 : 4;
+  extern __shared__ float red_dw[];  // dims floats when p.dw
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int nvec = p.dims / EV;
+  float wv[NV][EV], acc[NV][EV];
+#pragma unroll
+  for (int i = 0; i < NV; ++i) {
+    const int j = lane + 64 * i;
+#pragma unroll
+    for (int e = 0; e < EV; ++e) wv[i][e] = acc[i][e] = 0.0f;
+    if (j < nvec) load_w<W_BF16, EV>(p.w, j * EV, wv[i]);
+  }
+  for (int row = blockIdx.x * 4 + wave; row < p.rows; row += gridDim.x * 4) {
+    const char* xr = (const char*)p.x + (int64_t)row * p.ld * ES;
+    const char* gr = (const char*)p.dy + (int64_t)row * p.ld * ES;
+    float xv[NV][EV], gv[NV][EV];
+    float ss = 0.0f;
+#pragma unroll
+    for (int i = 0; i < NV; ++i) {
+      const int j = lane + 64 * i;
+      if (j < nvec) {
+        load_act<BF16>(xr, j * EV, xv[i]);
+        load_act<BF16>(gr, j * EV, gv[i]);
+      } else {
+#pragma unroll
+        for (int e = 0; e < EV; ++e) xv[i][e] = gv[i][e] = 0.0f;
+      }
+#pragma unroll
+      for (int e = 0; e < EV; ++e) ss = __builtin_fmaf(xv[i][e], xv[i][e], ss);
+    }
+    ss = nwave_sum(ss);
+    const float rms = sqrtf(ss / (float)p.dims + p.eps);
+    const float rinv = 1.0f / rms;
+    float s2 = 0.0f;
+#pragma unroll
+    for (int i = 0; i < NV; ++i)
+#pragma unroll
+      for (int e = 0; e < EV; ++e) s2 = __builtin_fmaf(gv[i][e] * wv[i][e], xv[i][e] / rms, s2);
+    s2 = nwave_sum(s2) / (float)p.dims;
+    char* dxr = (char*)p.dx + (int64_t)row * p.ld * ES;
+    const char* rr = p.r ? (const char*)p.r + (int64_t)row * p.ld * ES : nullptr;
+#pragma unroll
+    for (int i = 0; i < NV; ++i) {
+      const int j = lane + 64 * i;
+      if (j < nvec) {
+        float o[EV], rv[EV];
+        if (rr) load_act<BF16>(rr, j * EV, rv);
+#pragma unroll
+        for (int e = 0; e < EV; ++e) {
+          const float xhat = xv[i][e] / rms;
+          o[e] = rinv * (gv[i][e] * wv[i][e] - xhat * s2) + (rr ? rv[e] : 0.0f);
+          acc[i][e] = __builtin_fmaf(gv[i][e], xhat, acc[i][e]);
+        }
+        store_act<BF16>(dxr, j * EV, o);
+      }
+    }
+  }
+  if (p.dw) {  // uniform: every thread takes it
+    for (int w = 0; w < 4; ++w) {
+      if (wave == w) {
+#pragma unroll
+        for (int i = 0; i < NV; ++i) {
+          const int j = lane + 64 * i;
+          if (j < nvec) {
+#pragma unroll
+            for (int e = 0; e < EV; ++e) {
+              const int c = j * EV + e;
+              red_dw[c] = (w == 0 ? 0.0f : red_dw[c]) + acc[i][e];
+            }
+          }
+        }
+      }
+      __syncthreads();
+    }
+    float* wsr = p.ws + (int64_t)blockIdx.x * p.dims;
+    for (int c = threadIdx.x; c < p.dims; c += 256) wsr[c] = red_dw[c];
+  }
+}
+
+template <bool BF16, bool W_BF16>
+__global__ void __launch_bounds__(256) norm_bwd_gen(NormParams p) {
+  constexpr int ES = BF16 ? 2 : 4;
+  __shared__ float red[4];
+  float* wsr = p.dw ? p.ws + (int64_t)blockIdx.x * p.dims : nullptr;
+  if (wsr)  // each thread owns columns tid + 256k of this workspace row
+    for (int c = threadIdx.x; c < p.dims; c += 256) wsr[c] = 0.0f;
+  for (int row = blockIdx.x; row < p.rows; row += gridDim.x) {
+    const char* xr = (const char*)p.x + (int64_t)row * p.ld * ES;
+    const char* gr = (const char*)p.dy + (int64_t)row * p.ld * ES;
+    const char* rr = p.r ? (const char*)p.r + (int64_t)row * p.ld * ES : nullptr;
+    char* dxr = (char*)p.dx + (int64_t)row * p.ld * ES;
+    float ss = 0.0f;
+    for (int c = threadIdx.x; c < p.dims; c += 256) {
+      const float x = ld_elem<BF16>(xr, c);
+      ss = __builtin_fmaf(x, x, ss);
+    }
+    ss = block_sum256(ss, red);
+    const float rms = sqrtf(ss / (float)p.dims + p.eps);
+    const float rinv = 1.0f / rms;
+    float s2 = 0.0f;
+    for (int c = threadIdx.x; c < p.dims; c += 256)
+      s2 = __builtin_fmaf(ld_elem<BF16>(gr, c) * ld_elem<W_BF16>(p.w, c), ld_elem<BF16>(xr, c) / rms, s2);
+    s2 = block_sum256(s2, red) / (float)p.dims;  // its barriers order every read above before the writes below
+    for (int c = threadIdx.x; c < p.dims; c += 256) {
+      const float x = ld_elem<BF16>(xr, c), g = ld_elem<BF16>(gr, c);
+      const float xhat = x / rms;
+      float o = rinv * (g * ld_elem<W_BF16>(p.w, c) - xhat * s2);
+      if (rr) o += ld_elem<BF16>(rr, c);
+      st_elem<BF16>(dxr, c, o);
+      if (wsr) wsr[c] = __builtin_fmaf(g, xhat, wsr[c]);
+    }
+    __syncthreads();  // dx may alias dy or x: the next row's reads follow this row's writes
+  }
+}
+
+template <bool DW_BF16>
+__global__ void __launch_bounds__(256) norm_dw_reduce(const float* ws, int G, int dims, float beta,
+                                                      void* dw) {
+  const int c = blockIdx.x * 256 + threadIdx.x;
+  if (c >= dims) return;
+  float s = 0.0f;
+  for (int g = 0; g < G; ++g) s += ws[(int64_t)g * dims + c];
+  if (beta != 0.0f) s = __builtin_fmaf(beta, ld_elem<DW_BF16>(dw, c), s);
+  st_elem<DW_BF16>(dw, c, s);
+}
+
+int vec_per_lane(int dims, bool bf16) {
+  const int per = (dims / (bf16 ? 8 : 4) + 63) / 64;
+  return per <= 1 ? 1 : per <= 2 ? 2 : per <= 4 ? 4 : 8;
+}
+
+template <bool BF16, bool W_BF16>
+hipError_t fwd_one(const NormParams& p, bool vector_path, hipStream_t st) {
+  if (!vector_path) {
+    hipLaunchKernelGGL((norm_fwd_gen<BF16, W_BF16>), dim3((unsigned)p.rows), dim3(256), 0, st, p);
+    return hipGetLastError();
+  }
+  const dim3 grid((unsigned)((p.rows + 3) / 4)), block(256);
+  switch (vec_per_lane(p.dims, BF16)) {
+    case 1: hipLaunchKernelGGL((norm_fwd_vec<BF16, W_BF16, 1>), grid, block, 0, st, p); break;
+    case 2: hipLaunchKernelGGL((norm_fwd_vec<BF16, W_BF16, 2>), grid, block, 0, st, p); break;
+    case 4: hipLaunchKernelGGL((norm_fwd_vec<BF16, W_BF16, 4>), grid, block, 0, st, p); break;
+    default: hipLaunchKernelGGL((norm_fwd_vec<BF16, W_BF16, 8>), grid, block, 0, st, p); break;
+  }
+  return hipGetLastError();
+}
+
+template <bool BF16, bool W_BF16>
+hipError_t bwd_one(const NormParams& p, bool vector_path, hipStream_t st) {
+  const int G = norm_bwd_grid(p.rows);
+  if (!vector_path) {
+    hipLaunchKernelGGL((norm_bwd_gen<BF16, W_BF16>), dim3((unsigned)G), dim3(256), 0, st, p);
+  } else {
+    const dim3 grid((unsigned)G), block(256);
+    const size_t lds = p.dw ? (size_t)p.dims * sizeof(float) : 0;
+    switch (vec_per_lane(p.dims, BF16)) {
+      case 1: hipLaunchKernelGGL((norm_bwd_vec<BF16, W_BF16, 1>), grid, block, lds, st, p); break;
+      case 2: hipLaunchKernelGGL((norm_bwd_vec<BF16, W_BF16, 2>), grid, block, lds, st, p); break;
+      case 4: hipLaunchKernelGGL((norm_bwd_vec<BF16, W_BF16, 4>), grid, block, lds, st, p); break;
+      default: hipLaunchKernelGGL((norm_bwd_vec<BF16, W_BF16, 8>), grid, block, lds, st, p); break;
+    }
+  }
+  return hipGetLastError();
+}
+
+}  // namespace
+
+hipError_t launch_norm_fwd(const NormParams& p, bool bf16, bool w_bf16, bool vector_path,
+                           hipStream_t stream) {
+  if (bf16) return w_bf16 ? fwd_one<true, true>(p, vector_path, stream)
+                          : fwd_one<true, false>(p, vector_path, stream);
+  return w_bf16 ? fwd_one<false, true>(p, vector_path, stream)
+                : fwd_one<false, false>(p, vector_path, stream);
+}
+
+hipError_t launch_norm_bwd(const NormParams& p, bool bf16, bool w_bf16, bool dw_bf16,
+                           bool vector_path, hipStream_t stream) {
+  hipError_t e = bf16 ? (w_bf16 ? bwd_one<true, true>(p, vector_path, stream)
+                                : bwd_one<true, false>(p, vector_path, stream))
+                      : (w_bf16 ? bwd_one<false, true>(p, vector_path, stream)
+                                : bwd_one<false, false>(p, vector_path, stream));
+  if (e != hipSuccess || !p.dw) return e;
+  const dim3 grid((unsigned)((p.dims + 255) / 256)), block(256);
+  const int G = norm_bwd_grid(p.rows);
+  if (dw_bf16)
+    hipLaunchKernelGGL(norm_dw_reduce<true>, grid, block, 0, stream, p.ws, G, p.dims, p.dw_beta, p.dw);
+  else
+    hipLaunchKernelGGL(norm_dw_reduce<false>, grid, block, 0, stream, p.ws, G, p.dims, p.dw_beta, p.dw);
+  return hipGetLastError();
+}
+
+}  // namespace mig

@@ -34,7 +34,7 @@ C_SYMBOLS = (
     "mi_init", "mi_last_error", "mi_version", "mi_gemm_workspace_size", "mi_gemm",
     "mi_gemm_batched", "mi_residual_add", "mi_softmax_causal", "mi_softmax_bwd",
     "mi_gemm_describe", "mi_stream_sync", "mi_flash_attn_fwd", "mi_flash_attn_bwd",
-    "mi_cross_entropy",
+    "mi_cross_entropy", "mi_rmsnorm_fwd", "mi_rmsnorm_bwd", "mi_rmsnorm_bwd_workspace_size",
 )
 MI_ATTN_O_BHTD, MI_ATTN_O_BTHD = 0, 1
 
@@ -117,6 +117,13 @@ def load_library():
     L.mi_cross_entropy.restype = ctypes.c_int
     L.mi_cross_entropy.argtypes = [vp, vp, i32, i64, vp, i64, i64, ctypes.c_float, vp, vp, vp,
                                    i32, i64]
+    L.mi_rmsnorm_fwd.restype = ctypes.c_int
+    L.mi_rmsnorm_fwd.argtypes = [vp, vp, vp, vp, i32, vp, vp, i64, i64, i64, i32, ctypes.c_float]
+    L.mi_rmsnorm_bwd_workspace_size.restype = ctypes.c_size_t
+    L.mi_rmsnorm_bwd_workspace_size.argtypes = [i64, i64]
+    L.mi_rmsnorm_bwd.restype = ctypes.c_int
+    L.mi_rmsnorm_bwd.argtypes = [vp, vp, vp, vp, i32, vp, vp, vp, i32, ctypes.c_float, i64, i64, i64,
+                                 i32, ctypes.c_float, vp, ctypes.c_size_t]
     _lib = L
     return L
 
@@ -582,3 +589,96 @@ class CrossEntropyLoss:
         if self._grad is None:
             raise RuntimeError("CrossEntropyLoss.backward before forward")
         return self._grad
+
+
+# ---- RMSNorm ------------------------------------------------------------------
+
+def _rows_of(t, what):
+    """(rows, dims, ld) of a row-major [..., dims] tensor whose rows share one stride."""
+    dims = t.shape[-1]
+    if t.stride(-1) != 1:
+        raise ValueError(f"{what} must have a contiguous last dimension")
+    if t.dim() == 2:
+        return t.shape[0], dims, (t.stride(0) if t.shape[0] > 1 else dims)
+    if not t.is_contiguous():
+        raise ValueError(f"{what} must be contiguous (or 2-D with a row stride)")
+    return t.numel() // dims if dims else 0, dims, dims
+
+
+def rms_norm_forward(x, weight, eps=1e-5, residual=None, out=None, rstd=None, sync=None):
+    """RMSNorm forward (metal_bridge::rms_norm_forward, MetalBridge.hpp:60-61; RMSNorm.cpp:48-75):
+    y = x / sqrt(mean(x^2) + eps) * weight over the last dimension. With residual, first
+    x += residual in place (metal_bridge::fused_add_norm, Transformer.cpp:150-158). x, residual,
+    out: bf16 or fp32 with one row stride; weight [dims] bf16 or fp32; rstd: optional fp32 [rows]
+    tensor receiving 1/rms. out may be x. Returns y."""
+    torch = _torch()
+    rows, dims, ld = _rows_of(x, "x")
+    if out is None:
+        out = torch.empty_strided(x.shape, x.stride(), dtype=x.dtype, device=x.device)
+    for t, n in ((out, "out"), (residual, "residual")):
+        if t is not None and (t.dtype != x.dtype or _rows_of(t, n) != (rows, dims, ld)):
+            raise ValueError(f"{n} must match x's dtype, shape and row stride")
+    st = load_library().mi_rmsnorm_fwd(_stream(), _ptr(x), _ptr(residual), _ptr(weight), _dt(weight),
+                                       _ptr(out), _ptr(rstd), rows, dims, ld, _dt(x), float(eps))
+    if sync is None:
+        _finish("mi_rmsnorm_fwd", st)
+    else:
+        _check("mi_rmsnorm_fwd", st)
+    return out
+
+
+def rms_norm_backward(dy, x, weight, eps=1e-5, residual_grad=None, dx=None, dw=None, dw_beta=0.0,
+                      want_dw=True, sync=None):
+    """RMSNorm backward (metal_bridge::rms_norm_backward, MetalBridge.hpp:62-64; RMSNorm.cpp:77-180):
+    dx = (dy*w - xhat*mean(dy*w*xhat)) / rms [+ residual_grad] (metal_bridge::fused_backward_add_norm,
+    Transformer.cpp:441-466), dw = dw_beta*dw + sum over rows of dy*xhat. dw (fp32 [dims] unless
+    given) is allocated when want_dw; dx may be dy. Returns (dx, dw or None)."""
+    torch = _torch()
+    rows, dims, ld = _rows_of(x, "x")
+    if dx is None:
+        dx = torch.empty_strided(x.shape, x.stride(), dtype=x.dtype, device=x.device)
+    for t, n in ((dy, "dy"), (dx, "dx"), (residual_grad, "residual_grad")):
+        if t is not None and (t.dtype != x.dtype or _rows_of(t, n) != (rows, dims, ld)):
+            raise ValueError(f"{n} must match x's dtype, shape and row stride")
+    ws = None
+    if want_dw or dw is not None:
+        if dw is None:
+            dw = torch.zeros((dims,), dtype=torch.float32, device=x.device)
+        nbytes = load_library().mi_rmsnorm_bwd_workspace_size(rows, dims)
+        ws = torch.empty((max(nbytes, 4) // 4,), dtype=torch.float32, device=x.device)
+    st = load_library().mi_rmsnorm_bwd(
+        _stream(), _ptr(dy), _ptr(x), _ptr(weight), _dt(weight), _ptr(residual_grad), _ptr(dx),
+        _ptr(dw), _dt(dw) if dw is not None else MI_F32, float(dw_beta), rows, dims, ld, _dt(x),
+        float(eps), _ptr(ws), 0 if ws is None else ws.numel() * 4)
+    if sync is None:
+        _finish("mi_rmsnorm_bwd", st)
+    else:
+        _check("mi_rmsnorm_bwd", st)
+    return dx, dw
+
+
+class RMSNorm:
+    """Mirror of the reference's RMSNorm (RMSNorm.hpp; RMSNorm.cpp:31-180): weight [dims]
+    (bf16, initialised to 1 as RMSNorm.cpp:31), forward(x) -> y, backward(grad_output, input,
+    grad_weight) -> grad_input with grad_weight (fp32 [dims]) accumulated, as the CPU path does."""
+
+    def __init__(self, dims, eps=1e-5, device="cuda", dtype=None):
+        torch = _torch()
+        self.eps = float(eps)
+        self.weight = torch.ones((dims,), dtype=dtype or torch.bfloat16, device=device)
+
+    def forward(self, x):
+        if x.dim() < 2:
+            raise ValueError("Input tensor must have at least 2 dimensions")
+        if x.shape[-1] != self.weight.shape[0]:
+            raise ValueError("Input tensor last dimension must match RMSNorm dims")
+        return rms_norm_forward(x, self.weight, self.eps)
+
+    def backward(self, grad_output, input, grad_weight):
+        if tuple(grad_output.shape) != tuple(input.shape):
+            raise ValueError("grad_output and input shapes must match in RMSNorm::backward")
+        if tuple(grad_weight.shape) != tuple(self.weight.shape):
+            raise ValueError("grad_weight must match RMSNorm weight dimensions")
+        dx, _ = rms_norm_backward(grad_output, input, self.weight, self.eps, dw=grad_weight,
+                                  dw_beta=1.0)
+        return dx

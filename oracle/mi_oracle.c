@@ -35,6 +35,11 @@
  *                  Loss.cpp:43-195 (CrossEntropyLoss forward and backward): softmax
  *                  with max subtraction, -log(max(p_target, 1e-15)), the logits
  *                  gradient (p - onehot) * scale and the mean loss.
+ *   mo_rmsnorm_fwd / mo_rmsnorm_bwd
+ *                  RMSNorm.cpp:40-180 (forward, backward with the weight gradient)
+ *                  and the decoder layer's fused forms: residual add before the
+ *                  norm (fused_add_norm, Transformer.cpp:150-158) and the residual
+ *                  gradient added to dx (fused_backward_add_norm, Transformer.cpp:441-466).
  *   mo_sgemm_omp   fp32 cache-blocked OpenMP SGEMM with cblas_sgemm row-major
  *                  semantics -- the CPU baseline timed next to the GPU.
  *   bf16 helpers   Tensor.hpp:16-27 (truncating fp32->bf16, bf16->fp32) plus RNE.
@@ -319,6 +324,58 @@ double mo_cross_entropy(const float* logits, int64_t ld, const int64_t* targets,
   double total = 0.0;
   for (int64_t r = 0; r < rows; ++r) total += row_loss[r];
   return total * scale;
+}
+
+/*
+ * RMSNorm forward in float64 (RMSNorm.cpp:40-75): per row, with r given, first
+ * x := x + r stored back in x's dtype (round_bf16: RNE to bf16, the storage of
+ * the bf16 path; Transformer.cpp:150-158 writes h back for the backward), then
+ * rms = sqrt(sum x^2 / dims + eps), y = x / rms * w, rstd[row] = 1 / rms.
+ */
+void mo_rmsnorm_fwd(float* x, const float* r, const float* w, int64_t rows, int64_t dims,
+                    double eps, int round_bf16, double* y, double* rstd) {
+#pragma omp parallel for schedule(static)
+  for (int64_t i = 0; i < rows; ++i) {
+    float* xr = x + i * dims;
+    double ss = 0.0;
+    for (int64_t c = 0; c < dims; ++c) {
+      if (r) {
+        float v = xr[c] + r[i * dims + c];
+        if (round_bf16) v = mo_bf16_to_f32(mo_f32_to_bf16_rne(v));
+        xr[c] = v;
+      }
+      ss += (double)xr[c] * (double)xr[c];
+    }
+    const double rms = sqrt(ss / (double)dims + eps);
+    for (int64_t c = 0; c < dims; ++c) y[i * dims + c] = (double)xr[c] / rms * (double)w[c];
+    if (rstd) rstd[i] = 1.0 / rms;
+  }
+}
+
+/*
+ * RMSNorm backward in float64 (RMSNorm.cpp:77-180): xhat = x / rms,
+ * dx = (1/rms) * (dy*w - xhat * mean(dy*w*xhat)) (:137-160), plus rg when given
+ * (fused_backward_add_norm.metal, Transformer.cpp:449-452: grad_h += grad_output);
+ * dw += sum over rows of dy * xhat (:163-176, accumulated as the CPU path does).
+ */
+void mo_rmsnorm_bwd(const float* dy, const float* x, const float* w, const float* rg,
+                    int64_t rows, int64_t dims, double eps, double* dx, double* dw) {
+  for (int64_t i = 0; i < rows; ++i) {
+    const float* xr = x + i * dims;
+    const float* gr = dy + i * dims;
+    double ss = 0.0;
+    for (int64_t c = 0; c < dims; ++c) ss += (double)xr[c] * (double)xr[c];
+    const double rms = sqrt(ss / (double)dims + eps);
+    double s = 0.0;
+    for (int64_t c = 0; c < dims; ++c) s += (double)gr[c] * (double)w[c] * ((double)xr[c] / rms);
+    s /= (double)dims;
+    for (int64_t c = 0; c < dims; ++c) {
+      const double xhat = (double)xr[c] / rms;
+      dx[i * dims + c] = (1.0 / rms) * ((double)gr[c] * (double)w[c] - xhat * s) +
+                         (rg ? (double)rg[i * dims + c] : 0.0);
+      if (dw) dw[c] += (double)gr[c] * xhat;
+    }
+  }
 }
 
 /* ---- fp32 CPU SGEMM baseline (cblas_sgemm semantics, MetalBridge.mm:695-697) -- */

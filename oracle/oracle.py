@@ -7,7 +7,7 @@ Every function here forwards to mi_oracle.c, whose header lists the reference
 file:line each routine restates (Tensor.hpp:16-27, MetalBridge.mm:691-701,
 gemm_bf16.metal:45,63, gemm_backward.metal:104-115, gemm_ffn.metal:160-181,
 fused_swiglu_gemm.metal:48-77, Activations.cpp:31-75, residual_add.metal:27,
-Attention.cpp:236-348, Loss.cpp:43-195).
+Attention.cpp:236-348, Loss.cpp:43-195, RMSNorm.cpp:40-180).
 """
 from __future__ import annotations
 
@@ -55,6 +55,8 @@ def lib():
         L.mo_attention_bwd.argtypes = [_i64] * 5 + [_vp] * 7
         L.mo_cross_entropy.restype = _dbl
         L.mo_cross_entropy.argtypes = [_vp, _i64, _vp, _i64, _i64, _dbl, _vp, _vp]
+        L.mo_rmsnorm_fwd.argtypes = [_vp, _vp, _vp, _i64, _i64, _dbl, ctypes.c_int, _vp, _vp]
+        L.mo_rmsnorm_bwd.argtypes = [_vp, _vp, _vp, _vp, _i64, _i64, _dbl, _vp, _vp]
         L.mo_sgemm_omp.argtypes = [ctypes.c_int, ctypes.c_int, _i64, _i64, _i64, ctypes.c_float,
                                    _vp, _i64, _vp, _i64, ctypes.c_float, _vp, _i64]
         L.mo_num_threads.restype = ctypes.c_int
@@ -162,6 +164,31 @@ def cross_entropy(logits, targets, scale=None, want_grad=True):
     grad = np.empty((rows, V), dtype=np.float64) if want_grad else None
     loss = lib().mo_cross_entropy(_p(x), V, _p(t), rows, V, float(scale), _p(row_loss), _p(grad))
     return loss, row_loss, grad
+
+
+def rmsnorm_fwd(x, w, eps=1e-5, residual=None, round_bf16=False):
+    """RMSNorm.cpp:40-75 (+ the residual add of fused_add_norm). x [rows, dims] ->
+    (y float64, rstd float64 [rows], x_after (x + residual as stored, float32))."""
+    xs = np.array(x, dtype=np.float32, order="C", copy=True)
+    rows, dims = xs.shape
+    r = _f32(residual)
+    y = np.empty((rows, dims), dtype=np.float64)
+    rstd = np.empty((rows,), dtype=np.float64)
+    lib().mo_rmsnorm_fwd(_p(xs), _p(r), _p(_f32(w)), rows, dims, float(eps), int(bool(round_bf16)),
+                         _p(y), _p(rstd))
+    return y, rstd, xs
+
+
+def rmsnorm_bwd(dy, x, w, eps=1e-5, residual_grad=None, dw0=None):
+    """RMSNorm.cpp:77-180 (+ the residual gradient of fused_backward_add_norm).
+    -> (dx float64 [rows, dims], dw float64 [dims] = dw0 + sum_rows dy * xhat)."""
+    dy, x = _f32(dy), _f32(x)
+    rows, dims = x.shape
+    dx = np.empty((rows, dims), dtype=np.float64)
+    dw = np.zeros((dims,), dtype=np.float64) if dw0 is None else np.array(dw0, dtype=np.float64)
+    lib().mo_rmsnorm_bwd(_p(dy), _p(x), _p(_f32(w)), _p(_f32(residual_grad)), rows, dims, float(eps),
+                         _p(dx), _p(dw))
+    return dx, dw
 
 
 def sgemm_omp(tA, tB, M, N, K, A, B, C=None, alpha=1.0, beta=0.0, lda=None, ldb=None):

@@ -170,3 +170,40 @@ def test_cross_entropy_validation(mi):
     assert st == 5 and "overlaps" in msg                 # MI_ERR_UNSUPPORTED
     st, msg = ce(L=4097)
     assert st == 5 and "aligned" in msg
+
+
+def test_rmsnorm_validation(mi):
+    # mi_rmsnorm_fwd / _bwd reject bad arguments before any device work.
+    lib = mi.load_library()
+    vp = ctypes.c_void_p
+
+    def fwd(rows=4, dims=64, ld=64, X=4096, R=None, W=65536, Y=131072, dt=1, wdt=1):
+        st = lib.mi_rmsnorm_fwd(None, vp(X) if X else None, vp(R) if R else None,
+                                vp(W) if W else None, wdt, vp(Y) if Y else None, None, rows, dims,
+                                ld, dt, 1e-5)
+        return st, lib.mi_last_error().decode()
+
+    assert fwd(rows=0)[0] == 0 and fwd(dims=0)[0] == 0
+    assert fwd(rows=-1)[0] == 1
+    st, msg = fwd(ld=10)
+    assert st == 2 and "ld" in msg
+    assert fwd(X=0)[0] == 3 and fwd(W=0)[0] == 3 and fwd(Y=0)[0] == 3
+    assert fwd(dt=5)[0] == 4 and fwd(wdt=5)[0] == 4
+    st, msg = fwd(Y=4096 + 64)                      # y overlaps x without being x
+    assert st == 5 and "disjoint" in msg
+    assert fwd(X=4097)[0] == 5
+
+    def bwd(DY=4096, X=131072, W=65536, DX=262144, DW=None, ws=None, wsb=0, dims=64, rows=4):
+        st = lib.mi_rmsnorm_bwd(None, vp(DY) if DY else None, vp(X), vp(W), 1, None,
+                                vp(DX) if DX else None, vp(DW) if DW else None, 0, 0.0, rows, dims,
+                                dims, 1, 1e-5, vp(ws) if ws else None, wsb)
+        return st, lib.mi_last_error().decode()
+
+    need = lib.mi_rmsnorm_bwd_workspace_size(4, 64)
+    assert need == 1 * 64 * 4                       # one workgroup for 4 rows
+    st, msg = bwd(DW=8192)
+    assert st == 6 and "workspace" in msg           # MI_ERR_WORKSPACE
+    assert bwd(DW=8192, ws=16384, wsb=need - 4)[0] == 6
+    assert bwd(DY=0)[0] == 3 and bwd(DX=0)[0] == 3
+    st, msg = bwd(DX=131072 + 2)                    # dx overlaps x without being x
+    assert st == 5
