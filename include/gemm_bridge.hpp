@@ -96,6 +96,30 @@ void fused_attn_bwd(const void* Q, const void* K, const void* V, const void* dO,
 void cross_entropy(const void* logits, const uint32_t* targets, float* loss_out,
                    float* grad_logits, size_t total_tokens, size_t vocab_size);
 
+// MetalBridge.hpp:60-61: y = x / sqrt(mean(x^2) + eps) * w per row of dims values,
+// bf16 storage behind the float pointers (rms_norm_forward.metal; RMSNorm.cpp:48-75).
+void rms_norm_forward(const float* input, float* output, const float* weight, float eps,
+                      size_t num_rows, size_t dims);
+
+// MetalBridge.hpp:62-64: dx and the weight gradient (written, as
+// rms_norm_backward.metal does), bf16 storage (RMSNorm.cpp:77-180).  grad_weight may
+// be NULL.  The weight-gradient workspace is bridge-owned.
+void rms_norm_backward(const float* grad_output, const float* input, const float* weight,
+                       float* grad_input, float* grad_weight, float eps, size_t num_rows,
+                       size_t dims);
+
+// MetalBridge.hpp:79-81: x_residual += residual; output = rmsnorm(x_residual) * weight,
+// fp32 (fused_add_norm.metal; the decoder layer's h += out, ffn_in = norm(h),
+// Transformer.cpp:150-158).
+void fused_add_norm(float* x_residual, const float* residual, const float* weight, float* output,
+                    size_t num_rows, size_t D, float eps);
+
+// MetalBridge.hpp:82-85: grad_input = rmsnorm_backward(grad_output, input) + residual,
+// bf16 activations, fp32 weight (fused_backward_add_norm.metal, Transformer.cpp:441-466).
+void fused_backward_add_norm(const void* grad_output, const void* input, const void* weight,
+                             const void* residual, void* grad_input, size_t num_rows, size_t D,
+                             float eps);
+
 // MetalBridge.hpp:78: a[i] += b[i] on bf16 storage (residual_add.metal:15-28).
 void residual_add(float* a, const float* b, size_t n);
 // fp32 storage variant.

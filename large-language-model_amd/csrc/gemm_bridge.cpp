@@ -18,9 +18,7 @@ thread_local hipStream_t t_stream = nullptr;
 thread_local void* t_ws = nullptr;
 thread_local size_t t_ws_bytes = 0;
 
-void* workspace_for(int ta, int tb, size_t M, size_t N, size_t K, int dt_in, int dt_c,
-                    size_t* bytes) {
-  const size_t need = mi_gemm_workspace_size(ta, tb, (int64_t)M, (int64_t)N, (int64_t)K, dt_in, dt_c, 1);
+void* grow_workspace(size_t need, size_t* bytes) {
   if (need > t_ws_bytes) {
     if (t_ws) {
       // the stream may still use the old buffer
@@ -34,6 +32,12 @@ void* workspace_for(int ta, int tb, size_t M, size_t N, size_t K, int dt_in, int
   }
   *bytes = t_ws_bytes;
   return t_ws;
+}
+
+void* workspace_for(int ta, int tb, size_t M, size_t N, size_t K, int dt_in, int dt_c,
+                    size_t* bytes) {
+  return grow_workspace(
+      mi_gemm_workspace_size(ta, tb, (int64_t)M, (int64_t)N, (int64_t)K, dt_in, dt_c, 1), bytes);
 }
 
 // Attention state for fused_attn_bwd (O, log-sum-exp, D), grown like the split-K
@@ -260,6 +264,42 @@ void cross_entropy(const void* logits, const uint32_t* targets, float* loss_out,
   }
   finish("cross_entropy", st);
   if (!t_in_scope && t_status == MI_OK) ce_flush();
+}
+
+void rms_norm_forward(const float* input, float* output, const float* weight, float eps,
+                      size_t num_rows, size_t dims) {
+  finish("rms_norm_forward",
+         mi_rmsnorm_fwd(get_stream(), (void*)input, nullptr, weight, MI_BF16, output, nullptr,
+                        (int64_t)num_rows, (int64_t)dims, (int64_t)dims, MI_BF16, eps));
+}
+
+void rms_norm_backward(const float* grad_output, const float* input, const float* weight,
+                       float* grad_input, float* grad_weight, float eps, size_t num_rows,
+                       size_t dims) {
+  size_t ws_bytes = 0;
+  void* ws = grad_weight ? grow_workspace(mi_rmsnorm_bwd_workspace_size((int64_t)num_rows, (int64_t)dims),
+                                          &ws_bytes)
+                         : nullptr;
+  finish("rms_norm_backward",
+         mi_rmsnorm_bwd(get_stream(), grad_output, input, weight, MI_BF16, nullptr, grad_input,
+                        grad_weight, MI_BF16, 0.0f, (int64_t)num_rows, (int64_t)dims, (int64_t)dims,
+                        MI_BF16, eps, ws, ws_bytes));
+}
+
+void fused_add_norm(float* x_residual, const float* residual, const float* weight, float* output,
+                    size_t num_rows, size_t D, float eps) {
+  finish("fused_add_norm",
+         mi_rmsnorm_fwd(get_stream(), x_residual, residual, weight, MI_F32, output, nullptr,
+                        (int64_t)num_rows, (int64_t)D, (int64_t)D, MI_F32, eps));
+}
+
+void fused_backward_add_norm(const void* grad_output, const void* input, const void* weight,
+                             const void* residual, void* grad_input, size_t num_rows, size_t D,
+                             float eps) {
+  finish("fused_backward_add_norm",
+         mi_rmsnorm_bwd(get_stream(), grad_output, input, weight, MI_F32, residual, grad_input,
+                        nullptr, MI_F32, 0.0f, (int64_t)num_rows, (int64_t)D, (int64_t)D, MI_BF16,
+                        eps, nullptr, 0));
 }
 
 void fused_attn_bwd(const void* Q, const void* K, const void* V, const void* dO, void* dQ,

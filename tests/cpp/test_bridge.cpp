@@ -340,6 +340,77 @@ int main() {
         ok && e <= 1e-5, std::to_string(e));
     dfree(dl); dfree(dt); dfree(dg);
   }
+  {  // GB-14: the norm functions on closed forms.  A constant row c normalises to
+     // w * c / sqrt(c^2 + eps); fused_add_norm adds the residual into x first (fp32);
+     // the backward of a constant row with dy = w is 0 (dy*w - xhat*mean(dy*w*xhat) = 0 when
+     // xhat = 1 and w = 1), so fused_backward_add_norm returns the residual gradient.
+    const size_t R = 4, D = 64;
+    const float eps = 1e-2f;
+    std::vector<float> hx(R * D), hr(R * D), hw(D, 1.0f);
+    for (size_t i = 0; i < R; ++i)
+      for (size_t c = 0; c < D; ++c) {
+        hx[i * D + c] = (float)(i + 1);
+        hr[i * D + c] = (float)(i + 1);  // x + r = 2 (i + 1)
+      }
+    float* dx = dev(hx);
+    float* dr = dev(hr);
+    float* dwt = dev(hw);
+    float* dout = nullptr;
+    (void)hipMalloc((void**)&dout, R * D * sizeof(float));
+    mi_bridge::fused_add_norm(dx, dr, dwt, dout, R, D, eps);
+    bool ok = mi_bridge::last_status() == MI_OK;
+    std::vector<float> hy = host(dout, R * D), hx2 = host(dx, R * D);
+    double e = 0;
+    for (size_t i = 0; i < R; ++i) {
+      const double c = 2.0 * (i + 1);
+      for (size_t k = 0; k < D; ++k) {
+        e = std::fmax(e, std::fabs(hy[i * D + k] - c / std::sqrt(c * c + eps)));
+        e = std::fmax(e, std::fabs(hx2[i * D + k] - c));
+      }
+    }
+    // bf16 forward / backward on the same constant rows
+    std::vector<uint16_t> bx(R * D), bg(R * D, bf(1.0f)), bres(R * D), bw(D, bf(1.0f));
+    for (size_t i = 0; i < R * D; ++i) {
+      bx[i] = bf(3.0f);
+      bres[i] = bf((float)(i % 7));
+    }
+    uint16_t* dbx = dev(bx);
+    uint16_t* dbg = dev(bg);
+    uint16_t* dbres = dev(bres);
+    uint16_t* dbw = dev(bw);
+    uint16_t* dby = nullptr;
+    uint16_t* dbgi = nullptr;
+    uint16_t* dbgw = nullptr;
+    (void)hipMalloc((void**)&dby, R * D * 2);
+    (void)hipMalloc((void**)&dbgi, R * D * 2);
+    (void)hipMalloc((void**)&dbgw, D * 2);
+    mi_bridge::rms_norm_forward((const float*)dbx, (float*)dby, (const float*)dbw, eps, R, D);
+    ok = ok && mi_bridge::last_status() == MI_OK;
+    std::vector<uint16_t> hby = host(dby, R * D);
+    const double want = 3.0 / std::sqrt(9.0 + eps);
+    double e16 = 0;  // bf16 outputs: relative error
+    for (size_t i = 0; i < R * D; ++i) e16 = std::fmax(e16, std::fabs(fb(hby[i]) - want) / want);
+    mi_bridge::rms_norm_backward((const float*)dbg, (const float*)dbx, (const float*)dbw,
+                                 (float*)dbgi, (float*)dbgw, eps, R, D);
+    ok = ok && mi_bridge::last_status() == MI_OK;
+    std::vector<uint16_t> hgi = host(dbgi, R * D), hgw = host(dbgw, D);
+    // constant x: xhat = 3/rms for every column, dy = 1: dw[c] = R * 3/rms, and
+    // dx = (1 - xhat^2) / rms, which eps makes small but not zero
+    const double rms = std::sqrt(9.0 + eps), xh = 3.0 / rms;
+    const double dxw = (1.0 - xh * xh) / rms;
+    for (size_t c = 0; c < D; ++c) e16 = std::fmax(e16, std::fabs(fb(hgw[c]) - R * xh) / (R * xh));
+    for (size_t i = 0; i < R * D; ++i) e16 = std::fmax(e16, std::fabs(fb(hgi[i]) - dxw) / dxw);
+    std::vector<float> hw32(D, 1.0f);
+    float* dw32 = dev(hw32);
+    mi_bridge::fused_backward_add_norm(dbg, dbx, dw32, dbres, dbgi, R, D, 0.0f);
+    ok = ok && mi_bridge::last_status() == MI_OK;
+    hgi = host(dbgi, R * D);
+    for (size_t i = 0; i < R * D; ++i) e = std::fmax(e, std::fabs(fb(hgi[i]) - (float)(i % 7)));
+    row("GB-14", "norm closed forms: fp32 / exact <= 1e-5, bf16 rel <= 1e-2",
+        ok && e <= 1e-5 && e16 <= 1e-2, std::to_string(e) + " " + std::to_string(e16));
+    dfree(dx); dfree(dr); dfree(dwt); dfree(dout); dfree(dbx); dfree(dbg); dfree(dbres); dfree(dbw);
+    dfree(dby); dfree(dbgi); dfree(dbgw); dfree(dw32);
+  }
   std::printf("%d/%d checks passed\n", g_passed, g_total);
   return g_passed == g_total ? 0 : 1;
 }
