@@ -72,10 +72,11 @@ def parse():
     ap.add_argument("--cpu-rows", type=int, default=2048, help="token rows of the CPU sample")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="also launch a 1 GiB device copy (for PMC byte-counter scaling)")
-    ap.add_argument("--workload", choices=("block", "attention", "lm_head"), default="block",
+    ap.add_argument("--workload", choices=("block", "attention", "lm_head", "norm"), default="block",
                     help="block: the configuration-3 GEMM set (the headline metric); attention: "
                          "configuration 4, fused GQA attention forward + backward; lm_head: "
-                         "configuration 5, LM-head GEMMs with the fused cross-entropy between")
+                         "configuration 5, LM-head GEMMs with the fused cross-entropy between; "
+                         "norm: configuration 3's residual add + RMSNorm forward and backward")
     return ap.parse_args()
 
 
@@ -335,6 +336,93 @@ def lm_head_main(args):
     print(json.dumps(out))
 
 
+def norm_main(args):
+    """The RMSNorm around configuration 3's GEMMs (8192 tokens x 2048, bf16): forward
+    h += a; y = rmsnorm(h) * w (Transformer.cpp:150-158), backward dx = rmsnorm_bwd(dy, h) + rg
+    with the weight gradient (RMSNorm.cpp:77-180, Transformer.cpp:441-466). HBM-bound: value is
+    algorithmic bytes per step / step time, in GB/s."""
+    import torch
+
+    import mi_gemm as mi
+
+    dev = torch.device("cuda:0")
+    mi.init()
+    rows, dims = M_TOKENS, 2048
+    g = torch.Generator(device=dev)
+    g.manual_seed(3)
+    mk = lambda s=1.0: (torch.randn((rows, dims), generator=g, device=dev) * s).to(torch.bfloat16)
+    h, a, dy, rg = mk(), mk(), mk(1e-2), mk(1e-2)
+    w = (1.0 + 0.1 * torch.randn((dims,), generator=g, device=dev)).to(torch.bfloat16)
+    y = torch.empty_like(h)
+    dx = torch.empty_like(h)
+    dw = torch.zeros((dims,), dtype=torch.float32, device=dev)
+    lib = mi.load_library()
+    ws = torch.empty((lib.mi_rmsnorm_bwd_workspace_size(rows, dims) // 4,), dtype=torch.float32,
+                     device=dev)
+
+    # C ABI calls with prepared arguments: the launch cost stays below the kernels' time
+    stream = mi._stream()
+    args_f = (stream, mi._ptr(h), mi._ptr(a), mi._ptr(w), mi.MI_BF16, mi._ptr(y), None, rows, dims,
+              dims, mi.MI_BF16, 1e-5)
+    args_b = (stream, mi._ptr(dy), mi._ptr(h), mi._ptr(w), mi.MI_BF16, mi._ptr(rg), mi._ptr(dx),
+              mi._ptr(dw), mi.MI_F32, 1.0, rows, dims, dims, mi.MI_BF16, 1e-5, mi._ptr(ws),
+              ws.numel() * 4)
+
+    def fwd():
+        mi._check("mi_rmsnorm_fwd", lib.mi_rmsnorm_fwd(*args_f))
+
+    def bwd():
+        mi._check("mi_rmsnorm_bwd", lib.mi_rmsnorm_bwd(*args_b))
+
+    for _ in range(args.warmup):
+        fwd()
+        bwd()
+    torch.cuda.synchronize()
+
+    def per_call(fn, n=50):  # back to back, two events: the kernel time, not the launch gaps
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(n):
+            fn()
+        e1.record()
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) / n
+
+    ms_f = per_call(fwd)
+    ms_b = per_call(bwd)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        fwd()
+        bwd()
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - t0
+    act = rows * dims * 2
+    fwd_bytes = 4 * act                      # read h, a; write h, y
+    bwd_bytes = 4 * act + 2 * dims * 4       # read dy, h, rg; write dx; dw read + written
+    value = (fwd_bytes + bwd_bytes) * args.steps / elapsed / 1e9
+    dom_ms, dom_bytes, dom = max((ms_f, fwd_bytes, "norm_fwd_vec (residual add + RMSNorm)"),
+                                 (ms_b, bwd_bytes, "norm_bwd_vec + norm_dw_reduce"))
+    achieved = dom_bytes / (dom_ms / 1e3) / 1e9
+    out = {
+        "metric": "RMSNorm HBM throughput GB/s (configuration 3 norms: fused add + norm fwd, bwd with dw)",
+        "value": round(value, 1), "unit": "GB/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": round(elapsed / args.steps * 1e3, 4),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
+        "data": "synthetic (torch.randn on device)",
+        "config": {"workload": "8192 tokens x 2048, bf16: h += a; y = rmsnorm(h) w; dx = "
+                               "rmsnorm_bwd(dy, h) + rg; dw += sum dy xhat",
+                   "bytes_per_step": fwd_bytes + bwd_bytes,
+                   "fwd_ms": round(ms_f, 4), "bwd_ms": round(ms_b, 4),
+                   "fwd_GBs": round(fwd_bytes / (ms_f / 1e3) / 1e9, 1),
+                   "bwd_GBs": round(bwd_bytes / (ms_b / 1e3) / 1e9, 1)},
+        "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": PEAK_HBM_GBS,
+                     "unit": "GB/s", "frac": round(achieved / PEAK_HBM_GBS, 4), "traffic": None,
+                     "kernel": dom, "avg_launch_ms": round(dom_ms, 4)},
+    }
+    print(json.dumps(out))
+
+
 def main():
     args = parse()
     if args.gpus != 1:
@@ -346,6 +434,9 @@ def main():
         return
     if args.workload == "lm_head":
         lm_head_main(args)
+        return
+    if args.workload == "norm":
+        norm_main(args)
         return
     import torch
 

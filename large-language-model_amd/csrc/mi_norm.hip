@@ -22,7 +22,9 @@
 // their partials in wave order through LDS into one workspace row, and a second
 // kernel sums the workspace rows in order: dw is bit-identical across launches.
 // Generic path (rows that are not whole aligned 16-byte vectors, or longer): one
-// 256-thread workgroup per row, strided passes over global memory.
+// 256-thread workgroup per row, strided passes over global memory.  xhat is formed as
+// x * (1/rms): one reciprocal per row instead of a division per element (the divide
+// sequence made the backward VALU-bound).
 #include <hip/hip_runtime.h>
 #include <math.h>
 
@@ -188,63 +190,110 @@ __global__ void __launch_bounds__(256) norm_fwd_gen(NormParams p) {
 
 // ---- backward ---------------------------------------------------------------
 
+template <bool BF16>
+__device__ __forceinline__ void unpack_act(nu32x4_t q, float* v) {
+  if constexpr (BF16) {
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      v[2 * k] = __uint_as_float(q[k] << 16);
+      v[2 * k + 1] = __uint_as_float(q[k] & 0xffff0000u);
+    }
+  } else {
+#pragma unroll
+    for (int k = 0; k < 4; ++k) v[k] = __uint_as_float(q[k]);
+  }
+}
+
+// Each wave walks its rows with the next row's x, dy and residual gradient loaded
+// (packed, 16-byte vectors) while the current row is computed; the current row is
+// unpacked again in each pass from a copy the compiler cannot see through, so the
+// unpacked values are not kept live across passes, and the weight is re-read (L1).
 template <bool BF16, bool W_BF16, int NV>
-__global__ void __launch_bounds__(256) norm_bwd_vec(NormParams p) {
+__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(NV <= 4 ? 2 : 1)))
+    norm_bwd_vec(NormParams p) {
   constexpr int EV = BF16 ? 8 : 4, ES = BF16 ? 2 : 4;
   extern __shared__ float red_dw[];  // dims floats when p.dw
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int nvec = p.dims / EV;
-  float wv[NV][EV], acc[NV][EV];
+  const bool has_r = p.r != nullptr;
+  float acc[NV][EV];
 #pragma unroll
-  for (int i = 0; i < NV; ++i) {
-    const int j = lane + 64 * i;
+  for (int i = 0; i < NV; ++i)
 #pragma unroll
-    for (int e = 0; e < EV; ++e) wv[i][e] = acc[i][e] = 0.0f;
-    if (j < nvec) load_w<W_BF16, EV>(p.w, j * EV, wv[i]);
-  }
-  for (int row = blockIdx.x * 4 + wave; row < p.rows; row += gridDim.x * 4) {
-    const char* xr = (const char*)p.x + (int64_t)row * p.ld * ES;
-    const char* gr = (const char*)p.dy + (int64_t)row * p.ld * ES;
-    float xv[NV][EV], gv[NV][EV];
-    float ss = 0.0f;
+    for (int e = 0; e < EV; ++e) acc[i][e] = 0.0f;
+  const int stride = gridDim.x * 4;
+  auto load_row = [&](int row, nu32x4_t* xq, nu32x4_t* gq, nu32x4_t* rq) __attribute__((always_inline)) {
+    const int64_t off = (int64_t)row * p.ld * ES;
 #pragma unroll
     for (int i = 0; i < NV; ++i) {
       const int j = lane + 64 * i;
+      xq[i] = gq[i] = rq[i] = nu32x4_t{0u, 0u, 0u, 0u};
       if (j < nvec) {
-        load_act<BF16>(xr, j * EV, xv[i]);
-        load_act<BF16>(gr, j * EV, gv[i]);
-      } else {
-#pragma unroll
-        for (int e = 0; e < EV; ++e) xv[i][e] = gv[i][e] = 0.0f;
+        xq[i] = *(const nu32x4_t*)((const char*)p.x + off + (int64_t)j * 16);
+        gq[i] = *(const nu32x4_t*)((const char*)p.dy + off + (int64_t)j * 16);
+        if (has_r) rq[i] = *(const nu32x4_t*)((const char*)p.r + off + (int64_t)j * 16);
       }
+    }
+  };
+  nu32x4_t xq[NV], gq[NV], rq[NV];
+  int row = blockIdx.x * 4 + wave;
+  if (row < p.rows) load_row(row, xq, gq, rq);
+  for (; row < p.rows; row += stride) {
+    nu32x4_t xn[NV], gn[NV], rn[NV];
+    if (row + stride < p.rows) load_row(row + stride, xn, gn, rn);
+    float ss = 0.0f;
 #pragma unroll
-      for (int e = 0; e < EV; ++e) ss = __builtin_fmaf(xv[i][e], xv[i][e], ss);
+    for (int i = 0; i < NV; ++i) {
+      float xv[EV];
+      unpack_act<BF16>(xq[i], xv);
+#pragma unroll
+      for (int e = 0; e < EV; ++e) ss = __builtin_fmaf(xv[e], xv[e], ss);
     }
     ss = nwave_sum(ss);
     const float rms = sqrtf(ss / (float)p.dims + p.eps);
     const float rinv = 1.0f / rms;
     float s2 = 0.0f;
 #pragma unroll
-    for (int i = 0; i < NV; ++i)
+    for (int i = 0; i < NV; ++i) {
+      const int j = lane + 64 * i;
+      if (j < nvec) {
+        nu32x4_t a = xq[i], b = gq[i];
+        __asm__ volatile("" : "+v"(a), "+v"(b));
+        float xv[EV], gv[EV], wv[EV];
+        unpack_act<BF16>(a, xv);
+        unpack_act<BF16>(b, gv);
+        load_w<W_BF16, EV>(p.w, j * EV, wv);
 #pragma unroll
-      for (int e = 0; e < EV; ++e) s2 = __builtin_fmaf(gv[i][e] * wv[i][e], xv[i][e] / rms, s2);
+        for (int e = 0; e < EV; ++e) s2 = __builtin_fmaf(gv[e] * wv[e], xv[e] * rinv, s2);
+      }
+    }
     s2 = nwave_sum(s2) / (float)p.dims;
     char* dxr = (char*)p.dx + (int64_t)row * p.ld * ES;
-    const char* rr = p.r ? (const char*)p.r + (int64_t)row * p.ld * ES : nullptr;
 #pragma unroll
     for (int i = 0; i < NV; ++i) {
       const int j = lane + 64 * i;
       if (j < nvec) {
-        float o[EV], rv[EV];
-        if (rr) load_act<BF16>(rr, j * EV, rv);
+        nu32x4_t a = xq[i], b = gq[i];
+        __asm__ volatile("" : "+v"(a), "+v"(b));
+        float xv[EV], gv[EV], wv[EV], o[EV], rv[EV];
+        unpack_act<BF16>(a, xv);
+        unpack_act<BF16>(b, gv);
+        unpack_act<BF16>(rq[i], rv);  // zeros without a residual gradient
+        load_w<W_BF16, EV>(p.w, j * EV, wv);
 #pragma unroll
         for (int e = 0; e < EV; ++e) {
-          const float xhat = xv[i][e] / rms;
-          o[e] = rinv * (gv[i][e] * wv[i][e] - xhat * s2) + (rr ? rv[e] : 0.0f);
-          acc[i][e] = __builtin_fmaf(gv[i][e], xhat, acc[i][e]);
+          const float xhat = xv[e] * rinv;
+          o[e] = rinv * (gv[e] * wv[e] - xhat * s2) + rv[e];
+          acc[i][e] = __builtin_fmaf(gv[e], xhat, acc[i][e]);
         }
         store_act<BF16>(dxr, j * EV, o);
       }
+    }
+#pragma unroll
+    for (int i = 0; i < NV; ++i) {
+      xq[i] = xn[i];
+      gq[i] = gn[i];
+      rq[i] = rn[i];
     }
   }
   if (p.dw) {  // uniform: every thread takes it
@@ -291,11 +340,11 @@ __global__ void __launch_bounds__(256) norm_bwd_gen(NormParams p) {
     const float rinv = 1.0f / rms;
     float s2 = 0.0f;
     for (int c = threadIdx.x; c < p.dims; c += 256)
-      s2 = __builtin_fmaf(ld_elem<BF16>(gr, c) * ld_elem<W_BF16>(p.w, c), ld_elem<BF16>(xr, c) / rms, s2);
+      s2 = __builtin_fmaf(ld_elem<BF16>(gr, c) * ld_elem<W_BF16>(p.w, c), ld_elem<BF16>(xr, c) * rinv, s2);
     s2 = block_sum256(s2, red) / (float)p.dims;  // its barriers order every read above before the writes below
     for (int c = threadIdx.x; c < p.dims; c += 256) {
       const float x = ld_elem<BF16>(xr, c), g = ld_elem<BF16>(gr, c);
-      const float xhat = x / rms;
+      const float xhat = x * rinv;
       float o = rinv * (g * ld_elem<W_BF16>(p.w, c) - xhat * s2);
       if (rr) o += ld_elem<BF16>(rr, c);
       st_elem<BF16>(dxr, c, o);
@@ -305,15 +354,36 @@ __global__ void __launch_bounds__(256) norm_bwd_gen(NormParams p) {
   }
 }
 
+// dw[c] = beta*dw[c] + sum_g ws[g][c].  One 1024-thread workgroup per 64 columns:
+// lane = column, wave w sums rows w, w+16, ... (coalesced 256-byte rows, few
+// loads per thread), then wave 0 adds the 16 wave sums in wave order.
 template <bool DW_BF16>
-__global__ void __launch_bounds__(256) norm_dw_reduce(const float* ws, int G, int dims, float beta,
-                                                      void* dw) {
-  const int c = blockIdx.x * 256 + threadIdx.x;
-  if (c >= dims) return;
+__global__ void __launch_bounds__(1024) norm_dw_reduce(const float* ws, int G, int dims, float beta,
+                                                       void* dw) {
+  __shared__ float red[16][64];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int c = blockIdx.x * 64 + lane;
   float s = 0.0f;
-  for (int g = 0; g < G; ++g) s += ws[(int64_t)g * dims + c];
-  if (beta != 0.0f) s = __builtin_fmaf(beta, ld_elem<DW_BF16>(dw, c), s);
-  st_elem<DW_BF16>(dw, c, s);
+  if (c < dims)
+    for (int g0 = wave; g0 < G; g0 += 16 * 8) {  // 8 loads in flight, summed in g order
+      float v[8];
+#pragma unroll
+      for (int k = 0; k < 8; ++k) {
+        const int g = g0 + 16 * k;
+        v[k] = g < G ? ws[(int64_t)g * dims + c] : 0.0f;
+      }
+#pragma unroll
+      for (int k = 0; k < 8; ++k) s += v[k];
+    }
+  red[wave][lane] = s;
+  __syncthreads();
+  if (wave == 0 && c < dims) {
+    float t = red[0][lane];
+#pragma unroll
+    for (int w = 1; w < 16; ++w) t += red[w][lane];
+    if (beta != 0.0f) t = __builtin_fmaf(beta, ld_elem<DW_BF16>(dw, c), t);
+    st_elem<DW_BF16>(dw, c, t);
+  }
 }
 
 int vec_per_lane(int dims, bool bf16) {
@@ -372,7 +442,7 @@ hipError_t launch_norm_bwd(const NormParams& p, bool bf16, bool w_bf16, bool dw_
                       : (w_bf16 ? bwd_one<false, true>(p, vector_path, stream)
                                 : bwd_one<false, false>(p, vector_path, stream));
   if (e != hipSuccess || !p.dw) return e;
-  const dim3 grid((unsigned)((p.dims + 255) / 256)), block(256);
+  const dim3 grid((unsigned)((p.dims + 63) / 64)), block(1024);
   const int G = norm_bwd_grid(p.rows);
   if (dw_bf16)
     hipLaunchKernelGGL(norm_dw_reduce<true>, grid, block, 0, stream, p.ws, G, p.dims, p.dw_beta, p.dw);
