@@ -147,3 +147,28 @@ def test_config3_size(mi, dev, oracle):
     dx_ref, dw_ref = oracle.rmsnorm_bwd(_np(dy), _np(h), wv, 1e-5, residual_grad=_np(rg))
     check(host(dx[pick]), dx_ref[pick], TOL_BF16, "dx")
     check(host(dw), dw_ref, 1e-3, "dw")
+
+
+def test_reference_kats(mi, dev):
+    """test_rmsnorm.cpp:48-130 (TC-01 .. TC-10) through the RMSNorm mirror, fp32."""
+    import json
+    import os
+
+    import torch
+
+    k = json.load(open(os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden",
+                                    "reference_kats.json")))
+    c = k["rmsnorm_tc03_06"]
+    norm = mi.RMSNorm(2, eps=c["eps"], device=dev, dtype=torch.float32)
+    assert tuple(norm.weight.shape) == (2,) and torch.all(norm.weight == 1.0)      # TC-01, TC-02
+    x = torch.tensor(c["x"], dtype=torch.float32, device=dev)
+    y = norm.forward(x).cpu().numpy()
+    assert np.max(np.abs(y - np.array(c["expected"]))) < c["tol"]                  # TC-03 .. 06
+    c = k["rmsnorm_tc07_08"]
+    norm.weight.copy_(torch.tensor(c["weight"], device=dev))
+    y = norm.forward(x).cpu().numpy()
+    assert np.max(np.abs(y[0] - np.array(c["expected_row0"]))) < c["tol"]          # TC-07, 08
+    with pytest.raises(ValueError):                                                # TC-09
+        norm.forward(torch.ones((4,), dtype=torch.float32, device=dev))
+    with pytest.raises(ValueError):                                                # TC-10
+        norm.forward(torch.ones((2, 3), dtype=torch.float32, device=dev))

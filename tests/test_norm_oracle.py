@@ -98,3 +98,18 @@ def test_residual_forms(oracle):
     dx, dw = oracle.rmsnorm_bwd(dy, x, w, 1e-5, residual_grad=g, dw0=np.ones(16))
     dx0, dw0 = oracle.rmsnorm_bwd(dy, x, w, 1e-5)
     assert np.allclose(dx, dx0 + g, rtol=1e-12) and np.allclose(dw, dw0 + 1.0, rtol=1e-12)
+
+
+def test_reference_kats(oracle):
+    """test_rmsnorm.cpp:48-130: x = [[0.3, 0.9], [-0.7, 0.4]], eps 1e-5, unit and [2, 0.5] weights."""
+    import json
+    import os
+
+    k = json.load(open(os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden",
+                                    "reference_kats.json")))
+    c = k["rmsnorm_tc03_06"]
+    y, _, _ = oracle.rmsnorm_fwd(np.array(c["x"], np.float32), np.array(c["weight"], np.float32), c["eps"])
+    assert np.max(np.abs(y - np.array(c["expected"]))) < c["tol"]
+    c = k["rmsnorm_tc07_08"]
+    y, _, _ = oracle.rmsnorm_fwd(np.array(c["x"], np.float32), np.array(c["weight"], np.float32), c["eps"])
+    assert np.max(np.abs(y[0] - np.array(c["expected_row0"]))) < c["tol"]
