@@ -17,6 +17,7 @@
 #include <cstddef>
 #include <cstdint>
 #include <stdexcept>
+#include <string>
 #include <vector>
 
 #include "mi_gemm.h"
@@ -150,5 +151,68 @@ std::vector<size_t> matmul_shape(const DeviceTensor& a, const DeviceTensor& b);
 // launch for all batch slices; out.dtype = a.dtype, out.data preallocated with
 // matmul_shape(a, b) elements.  a and b must share a dtype.
 void matmul(const DeviceTensor& a, const DeviceTensor& b, DeviceTensor& out);
+
+// ---- checkpoint weights (Checkpoint.cpp) ---------------------------------------
+
+// One entry of a safetensors header: dtype "F32" / "BF16" / "F16" (others are listed
+// but not loadable), shape, and byte range within the payload.
+struct TensorInfo {
+  std::string name, dtype;
+  std::vector<size_t> shape;
+  size_t begin = 0, end = 0;
+};
+
+// A memory-mapped safetensors file (8-byte header length, JSON header, payload;
+// Checkpoint.cpp:301-400).  open() checks the header (at most 10 MiB, as the
+// reference) and that every tensor's byte range lies in the payload and matches its
+// shape; on failure it returns false and error() says why.
+class SafetensorsFile {
+ public:
+  SafetensorsFile() = default;
+  ~SafetensorsFile();
+  SafetensorsFile(const SafetensorsFile&) = delete;
+  SafetensorsFile& operator=(const SafetensorsFile&) = delete;
+  bool open(const std::string& path);
+  void close();
+  const std::string& error() const { return err_; }
+  const std::vector<TensorInfo>& tensors() const { return tensors_; }
+  const TensorInfo* find(const std::string& name) const;
+  const uint8_t* data(const TensorInfo& t) const;  // host pointer into the mapping
+  // A Python/MLX checkpoint holds "tok_embeddings.weight" (Checkpoint.cpp:404-406).
+  bool is_python_format() const;
+
+ private:
+  uint8_t* map_ = nullptr;
+  size_t size_ = 0, payload_ = 0;
+  std::vector<TensorInfo> tensors_;
+  std::string err_;
+};
+
+// Model dimensions (the reference's TransformerConfig fields the weights depend on).
+struct ModelConfig {
+  size_t n_layers = 0, hidden_dim = 0, n_heads = 0, n_kv_heads = 0, head_dim = 0;
+  size_t intermediate_dim = 0, vocab_size = 0;
+};
+
+// Caller-allocated device buffers in the engine layout: Wq [H, nH*hd], Wk/Wv
+// [H, nKV*hd], Wo [nH*hd, H], w_gate/w_up [H, I], w_down [I, H], norms [H],
+// token_embeddings [V, H], output_projection [H, V]; all of `dtype`.
+struct LayerWeights {
+  void *attn_norm = nullptr, *ffn_norm = nullptr;
+  void *Wq = nullptr, *Wk = nullptr, *Wv = nullptr, *Wo = nullptr;
+  void *w_gate = nullptr, *w_up = nullptr, *w_down = nullptr;
+};
+struct ModelWeights {
+  DType dtype = DType::BF16;
+  void *token_embeddings = nullptr, *output_projection = nullptr, *final_norm = nullptr;
+  std::vector<LayerWeights> layers;
+};
+
+// The model part of Checkpoint::load (Checkpoint.cpp:331-388, 532-570): reads a
+// Python/MLX file (nn.Linear [out, in] matrices, fused wqkv and w12, transposed and
+// cut into the engine's matrices) or an engine file (engine names and layout) into
+// `w`, widening or rounding to w.dtype on the GPU.  Fails (false, message on stderr)
+// on a bad file, a missing tensor or a shape mismatch.
+bool load_weights(const std::string& path, const ModelConfig& cfg, const ModelWeights& w);
 
 }  // namespace mi_bridge

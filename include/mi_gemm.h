@@ -35,7 +35,7 @@
 extern "C" {
 #endif
 
-typedef enum mi_dtype { MI_F32 = 0, MI_BF16 = 1 } mi_dtype;
+typedef enum mi_dtype { MI_F32 = 0, MI_BF16 = 1, MI_F16 = 2 /* checkpoint sources only */ } mi_dtype;
 
 typedef enum mi_status {
   MI_OK = 0,
@@ -245,6 +245,22 @@ int mi_rmsnorm_bwd(void* stream, const void* dy, const void* x, const void* weig
                    const void* residual_grad, void* dx, void* dw, int32_t dw_dtype, float dw_beta,
                    int64_t rows, int64_t dims, int64_t ld, int32_t dtype, float eps,
                    void* workspace, size_t workspace_bytes);
+
+/*
+ * Weight conversion for checkpoint loading: rows [row0, row0 + rows) x columns
+ * [0, cols) of a row-major source matrix (leading dimension src_ld, dtype MI_F32,
+ * MI_BF16 or MI_F16) into dst (MI_F32, or MI_BF16 rounded to nearest even):
+ *   dst[r*dst_ld + c] = src[(row0 + r)*src_ld + c]      transpose == 0
+ *   dst[c*dst_ld + r] = src[(row0 + r)*src_ld + c]      transpose != 0
+ * Both pointers are device memory and must not overlap.  One launch covers the
+ * slice + transpose + widening the reference loader does on the CPU for a
+ * Python/MLX checkpoint: [out, in] -> [in, out] and the row ranges of the fused
+ * wqkv / w12 matrices (Checkpoint.cpp:28-75 bf16_to_f32 / f16_to_f32, :77-83
+ * transpose_matrix, :407-530 load_python_tensor / load_python_fused_tensor).
+ */
+int mi_convert_matrix(void* stream, const void* src, int32_t src_dtype, int64_t src_ld, int64_t row0,
+                      int64_t rows, int64_t cols, int32_t transpose, void* dst, int32_t dst_dtype,
+                      int64_t dst_ld);
 
 /*
  * Describe the kernel mi_gemm_batched would launch for this problem (tile,

@@ -21,6 +21,7 @@
 #include "mi_attn.hpp"
 #include "mi_xent.hpp"
 #include "mi_norm.hpp"
+#include "mi_convert.hpp"
 #include "mi_gemm_kernels.hpp"
 
 using namespace mig;
@@ -733,6 +734,37 @@ int mi_rmsnorm_bwd(void* stream, const void* dy, const void* x, const void* weig
   hipError_t e = launch_norm_bwd(p, dtype == MI_BF16, w_dtype == MI_BF16, dw_dtype == MI_BF16,
                                  vector_path, (hipStream_t)stream);
   return e == hipSuccess ? MI_OK : fail(MI_ERR_HIP, "rmsnorm_bwd launch: %s", hipGetErrorString(e));
+}
+
+int mi_convert_matrix(void* stream, const void* src, int32_t src_dtype, int64_t src_ld, int64_t row0,
+                      int64_t rows, int64_t cols, int32_t transpose, void* dst, int32_t dst_dtype,
+                      int64_t dst_ld) {
+  if (rows < 0 || cols < 0 || row0 < 0) return fail(MI_ERR_SHAPE, "negative size or row offset");
+  if (rows == 0 || cols == 0) return MI_OK;
+  if (src_dtype != MI_F32 && src_dtype != MI_BF16 && src_dtype != MI_F16)
+    return fail(MI_ERR_DTYPE, "source dtype %d", src_dtype);
+  if (dst_dtype != MI_F32 && dst_dtype != MI_BF16) return fail(MI_ERR_DTYPE, "destination dtype %d", dst_dtype);
+  if (!src || !dst) return fail(MI_ERR_NULL, "src or dst is NULL");
+  if (src_ld < cols) return fail(MI_ERR_LD, "src_ld=%lld < cols=%lld", (long long)src_ld, (long long)cols);
+  if (dst_ld < (transpose ? rows : cols))
+    return fail(MI_ERR_LD, "dst_ld=%lld < %lld", (long long)dst_ld, (long long)(transpose ? rows : cols));
+  if (transpose && (rows + 63) / 64 > 65535) return fail(MI_ERR_SHAPE, "too many rows to transpose");
+  const int64_t ses = src_dtype == MI_F32 ? 4 : 2, des = dst_dtype == MI_F32 ? 4 : 2;
+  if ((uintptr_t)src % ses || (uintptr_t)dst % des)
+    return fail(MI_ERR_UNSUPPORTED, "src and dst must be aligned to their element size");
+  const uintptr_t s0 = (uintptr_t)src + (uintptr_t)(row0 * src_ld * ses);
+  const uintptr_t s1 = (uintptr_t)src + (uintptr_t)(((row0 + rows - 1) * src_ld + cols) * ses);
+  const int64_t drows = transpose ? cols : rows, dcols = transpose ? rows : cols;
+  const uintptr_t d0 = (uintptr_t)dst, d1 = d0 + (uintptr_t)(((drows - 1) * dst_ld + dcols) * des);
+  if (d0 < s1 && s0 < d1) return fail(MI_ERR_UNSUPPORTED, "dst overlaps the source rows");
+  int st = init_devices();
+  if (st != MI_OK) return st;
+  ConvParams p;
+  p.src = src; p.dst = dst; p.src_ld = src_ld; p.dst_ld = dst_ld;
+  p.row0 = row0; p.rows = rows; p.cols = cols;
+  p.src_dtype = src_dtype; p.dst_dtype = dst_dtype;
+  hipError_t e = launch_convert(p, transpose != 0, current_cus(), (hipStream_t)stream);
+  return e == hipSuccess ? MI_OK : fail(MI_ERR_HIP, "convert launch: %s", hipGetErrorString(e));
 }
 
 int mi_cross_entropy(void* stream, const void* logits, int32_t logits_dtype, int64_t ld_logits,

@@ -26,7 +26,7 @@ import os
 _HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(_HERE, "libmi_gemm.so")
 
-MI_F32, MI_BF16 = 0, 1
+MI_F32, MI_BF16, MI_F16 = 0, 1, 2
 MI_CAUSAL_NONE, MI_CAUSAL_OUT_LOWER, MI_CAUSAL_A_LOWER, MI_CAUSAL_A_UPPER = 0, 1, 2, 3
 
 # Exported C-ABI symbols (include/mi_gemm.h).
@@ -35,6 +35,7 @@ C_SYMBOLS = (
     "mi_gemm_batched", "mi_residual_add", "mi_softmax_causal", "mi_softmax_bwd",
     "mi_gemm_describe", "mi_stream_sync", "mi_flash_attn_fwd", "mi_flash_attn_bwd",
     "mi_cross_entropy", "mi_rmsnorm_fwd", "mi_rmsnorm_bwd", "mi_rmsnorm_bwd_workspace_size",
+    "mi_convert_matrix",
 )
 MI_ATTN_O_BHTD, MI_ATTN_O_BTHD = 0, 1
 
@@ -124,6 +125,8 @@ def load_library():
     L.mi_rmsnorm_bwd.restype = ctypes.c_int
     L.mi_rmsnorm_bwd.argtypes = [vp, vp, vp, vp, i32, vp, vp, vp, i32, ctypes.c_float, i64, i64, i64,
                                  i32, ctypes.c_float, vp, ctypes.c_size_t]
+    L.mi_convert_matrix.restype = ctypes.c_int
+    L.mi_convert_matrix.argtypes = [vp, vp, i32, i64, i64, i64, i64, i32, vp, i32, i64]
     _lib = L
     return L
 
@@ -682,3 +685,120 @@ class RMSNorm:
         dx, _ = rms_norm_backward(grad_output, input, self.weight, self.eps, dw=grad_weight,
                                   dw_beta=1.0)
         return dx
+
+
+# ---- checkpoint weights ---------------------------------------------------------
+
+_ST_DTYPES = {"F32": (MI_F32, 4), "BF16": (MI_BF16, 2), "F16": (MI_F16, 2)}
+
+
+def read_safetensors_header(path):
+    """(header dict, payload offset) of a safetensors file (Checkpoint.cpp:390-400): 8-byte
+    little-endian length (at most 10 MiB, as the reference), then the JSON header."""
+    import json
+    import struct
+
+    with open(path, "rb") as f:
+        raw = f.read(8)
+        if len(raw) != 8:
+            raise ValueError(f"{path}: shorter than 8 bytes")
+        (n,) = struct.unpack("<Q", raw)
+        if n == 0 or n > (10 << 20):
+            raise ValueError(f"{path}: bad header length {n}")
+        head = json.loads(f.read(n).decode("utf-8"))
+    return head, 8 + n
+
+
+def convert_matrix(src, src_dtype, src_ld, row0, rows, cols, transpose, dst, sync=None):
+    """mi_convert_matrix: rows [row0, row0+rows) x [0, cols) of a device source matrix
+    (raw bytes of dtype MI_F32 / MI_BF16 / MI_F16, leading dimension src_ld) into dst
+    (fp32 or bf16 tensor), transposed or not (Checkpoint.cpp:77-83, 407-530)."""
+    ld_dst = rows if transpose else cols
+    st = load_library().mi_convert_matrix(_stream(), _ptr(src), src_dtype, src_ld, row0, rows, cols,
+                                          int(bool(transpose)), _ptr(dst), _dt(dst), ld_dst)
+    if sync is None:
+        _finish("mi_convert_matrix", st)
+    else:
+        _check("mi_convert_matrix", st)
+    return dst
+
+
+def engine_weight_shapes(cfg):
+    """Engine names and [in, out] shapes of a model's weights (Checkpoint.cpp:147-174).
+    cfg: dict with n_layers, hidden_dim, n_heads, n_kv_heads, head_dim, intermediate_dim,
+    vocab_size."""
+    H, V, I = cfg["hidden_dim"], cfg["vocab_size"], cfg["intermediate_dim"]
+    q, kv = cfg["n_heads"] * cfg["head_dim"], cfg["n_kv_heads"] * cfg["head_dim"]
+    shapes = {"token_embeddings": (V, H), "output_projection": (H, V), "final_norm.weight": (H,)}
+    for l in range(cfg["n_layers"]):
+        p = f"layers.{l}."
+        shapes.update({p + "attn_norm.weight": (H,), p + "attn.Wq": (H, q), p + "attn.Wk": (H, kv),
+                       p + "attn.Wv": (H, kv), p + "attn.Wo": (q, H), p + "ffn_norm.weight": (H,),
+                       p + "w_gate": (H, I), p + "w_up": (H, I), p + "w_down": (I, H)})
+    return shapes
+
+
+def weight_sources(cfg, python_format):
+    """For every engine tensor: (file tensor, file shape, row0, rows, transpose). The
+    Python/MLX layout is nn.Linear [out, in] with fused attention.wqkv and feed_forward.w12
+    (Checkpoint.cpp:532-570); the engine layout is the engine's own (:147-174)."""
+    H, V, I = cfg["hidden_dim"], cfg["vocab_size"], cfg["intermediate_dim"]
+    q, kv = cfg["n_heads"] * cfg["head_dim"], cfg["n_kv_heads"] * cfg["head_dim"]
+    src = {}
+    if python_format:
+        src["token_embeddings"] = ("tok_embeddings.weight", (V, H), 0, V, False)
+        src["output_projection"] = ("output.weight", (V, H), 0, V, True)
+        src["final_norm.weight"] = ("norm.weight", (H,), 0, 1, False)
+        for l in range(cfg["n_layers"]):
+            p = f"layers.{l}."
+            src[p + "attn_norm.weight"] = (p + "attention_norm.weight", (H,), 0, 1, False)
+            src[p + "ffn_norm.weight"] = (p + "ffn_norm.weight", (H,), 0, 1, False)
+            src[p + "attn.Wo"] = (p + "attention.wo.weight", (H, q), 0, H, True)
+            src[p + "w_down"] = (p + "feed_forward.w3.weight", (H, I), 0, H, True)
+            fq = (q + 2 * kv, H)
+            src[p + "attn.Wq"] = (p + "attention.wqkv.weight", fq, 0, q, True)
+            src[p + "attn.Wk"] = (p + "attention.wqkv.weight", fq, q, kv, True)
+            src[p + "attn.Wv"] = (p + "attention.wqkv.weight", fq, q + kv, kv, True)
+            src[p + "w_gate"] = (p + "feed_forward.w12.weight", (2 * I, H), 0, I, True)
+            src[p + "w_up"] = (p + "feed_forward.w12.weight", (2 * I, H), I, I, True)
+    else:
+        for name, shape in engine_weight_shapes(cfg).items():
+            src[name] = (name, shape, 0, shape[0] if len(shape) == 2 else 1, False)
+    return src
+
+
+def load_weights(path, cfg, dtype=None, device="cuda"):
+    """Mirror of the model part of Checkpoint::load (Checkpoint.cpp:331-388, 532-570): reads a
+    Python/MLX or an engine safetensors file into new device tensors in the engine layout
+    (dict keyed by the engine names), dtype bf16 (default) or fp32. Each file tensor's bytes
+    go to the device once; slicing, transposing and widening run in mi_convert_matrix."""
+    import numpy as np
+    torch = _torch()
+
+    dtype = dtype or torch.bfloat16
+    head, payload = read_safetensors_header(path)
+    python_format = "tok_embeddings.weight" in head
+    mm = np.memmap(path, dtype=np.uint8, mode="r")
+    staged = {}
+    out = {}
+    for name, shape in engine_weight_shapes(cfg).items():
+        fname, fshape, row0, rows, transpose = weight_sources(cfg, python_format)[name]
+        ent = head.get(fname)
+        if ent is None:
+            raise KeyError(f"tensor '{fname}' not found in {path}")
+        if tuple(ent["shape"]) != tuple(fshape):
+            raise ValueError(f"tensor '{fname}' has shape {ent['shape']}, expected {list(fshape)}")
+        if ent["dtype"] not in _ST_DTYPES:
+            raise ValueError(f"tensor '{fname}' has dtype {ent['dtype']}")
+        code, es = _ST_DTYPES[ent["dtype"]]
+        b, e = ent["data_offsets"]
+        if e - b != int(np.prod(fshape)) * es or payload + e > mm.size:
+            raise ValueError(f"tensor '{fname}' has a byte range that does not match its shape")
+        if fname not in staged:
+            staged = {fname: torch.from_numpy(np.array(mm[payload + b: payload + e])).to(device)}
+        cols = fshape[-1]
+        dst = torch.empty(shape, dtype=dtype, device=device)
+        convert_matrix(staged[fname], code, cols, row0, rows, cols, transpose, dst, sync=False)
+        out[name] = dst
+    _finish("load_weights", 0)
+    return out

@@ -7,7 +7,8 @@ Every function here forwards to mi_oracle.c, whose header lists the reference
 file:line each routine restates (Tensor.hpp:16-27, MetalBridge.mm:691-701,
 gemm_bf16.metal:45,63, gemm_backward.metal:104-115, gemm_ffn.metal:160-181,
 fused_swiglu_gemm.metal:48-77, Activations.cpp:31-75, residual_add.metal:27,
-Attention.cpp:236-348, Loss.cpp:43-195, RMSNorm.cpp:40-180).
+Attention.cpp:236-348, Loss.cpp:43-195, RMSNorm.cpp:40-180), except
+checkpoint_weights, which restates the checkpoint loader (Checkpoint.cpp) in numpy.
 """
 from __future__ import annotations
 
@@ -189,6 +190,64 @@ def rmsnorm_bwd(dy, x, w, eps=1e-5, residual_grad=None, dw0=None):
     lib().mo_rmsnorm_bwd(_p(dy), _p(x), _p(_f32(w)), _p(_f32(residual_grad)), rows, dims, float(eps),
                          _p(dx), _p(dw))
     return dx, dw
+
+
+def checkpoint_weights(path, cfg):
+    """Checkpoint.cpp:28-83, 390-570 in numpy: the model tensors of a safetensors file (a
+    Python/MLX file holding "tok_embeddings.weight", or an engine file) as float32 arrays in
+    the engine layout, keyed by the engine names. bf16 and f16 widen exactly (bf16_to_f32:
+    the 16 bits as the high half of an fp32; f16_to_f32); [out, in] matrices are transposed
+    (transpose_matrix) and the fused wqkv / w12 are cut into row ranges first
+    (load_python_fused_tensor)."""
+    import json
+    import struct
+
+    raw = np.fromfile(path, dtype=np.uint8)
+    (n,) = struct.unpack("<Q", raw[:8].tobytes())
+    head = json.loads(raw[8:8 + n].tobytes().decode("utf-8"))
+    payload = 8 + n
+
+    def tensor(name):
+        ent = head[name]
+        b, e = ent["data_offsets"]
+        byts = raw[payload + b: payload + e]
+        if ent["dtype"] == "BF16":
+            v = (byts.view(np.uint16).astype(np.uint32) << 16).view(np.float32)
+        elif ent["dtype"] == "F16":
+            v = byts.view(np.float16).astype(np.float32)
+        else:
+            v = byts.view(np.float32).copy()
+        return v.reshape(ent["shape"])
+
+    H, V, I = cfg["hidden_dim"], cfg["vocab_size"], cfg["intermediate_dim"]
+    q, kv = cfg["n_heads"] * cfg["head_dim"], cfg["n_kv_heads"] * cfg["head_dim"]
+    out = {}
+    if "tok_embeddings.weight" in head:
+        out["token_embeddings"] = tensor("tok_embeddings.weight")
+        out["output_projection"] = tensor("output.weight").T.copy()
+        out["final_norm.weight"] = tensor("norm.weight")
+        for l in range(cfg["n_layers"]):
+            p = f"layers.{l}."
+            out[p + "attn_norm.weight"] = tensor(p + "attention_norm.weight")
+            out[p + "ffn_norm.weight"] = tensor(p + "ffn_norm.weight")
+            out[p + "attn.Wo"] = tensor(p + "attention.wo.weight").T.copy()
+            out[p + "w_down"] = tensor(p + "feed_forward.w3.weight").T.copy()
+            wqkv = tensor(p + "attention.wqkv.weight")
+            out[p + "attn.Wq"] = wqkv[:q].T.copy()
+            out[p + "attn.Wk"] = wqkv[q:q + kv].T.copy()
+            out[p + "attn.Wv"] = wqkv[q + kv:q + 2 * kv].T.copy()
+            w12 = tensor(p + "feed_forward.w12.weight")
+            out[p + "w_gate"] = w12[:I].T.copy()
+            out[p + "w_up"] = w12[I:2 * I].T.copy()
+    else:
+        names = ["token_embeddings", "output_projection", "final_norm.weight"]
+        for l in range(cfg["n_layers"]):
+            p = f"layers.{l}."
+            names += [p + k for k in ("attn_norm.weight", "attn.Wq", "attn.Wk", "attn.Wv", "attn.Wo",
+                                      "ffn_norm.weight", "w_gate", "w_up", "w_down")]
+        for k in names:
+            out[k] = tensor(k)
+    return out
 
 
 def sgemm_omp(tA, tB, M, N, K, A, B, C=None, alpha=1.0, beta=0.0, lda=None, ldb=None):

@@ -411,6 +411,78 @@ int main() {
     dfree(dx); dfree(dr); dfree(dwt); dfree(dout); dfree(dbx); dfree(dbg); dfree(dbres); dfree(dbw);
     dfree(dby); dfree(dbgi); dfree(dbgw); dfree(dw32);
   }
+  {  // GB-15: load_weights of a Python/MLX file written here (fp32 values i*31 + t*1000 +
+     // small, exact in fp32): engine matrices are the transposed row ranges of the file's.
+    mi_bridge::ModelConfig c;
+    c.n_layers = 1; c.hidden_dim = 8; c.n_heads = 2; c.n_kv_heads = 1; c.head_dim = 4;
+    c.intermediate_dim = 12; c.vocab_size = 10;
+    const size_t H = 8, V = 10, I = 12, q = 8, kv = 4;
+    struct T { const char* name; std::vector<size_t> shape; };
+    const std::vector<T> ts = {{"tok_embeddings.weight", {V, H}}, {"output.weight", {V, H}},
+                               {"norm.weight", {H}}, {"layers.0.attention_norm.weight", {H}},
+                               {"layers.0.ffn_norm.weight", {H}}, {"layers.0.attention.wo.weight", {H, q}},
+                               {"layers.0.feed_forward.w3.weight", {H, I}},
+                               {"layers.0.attention.wqkv.weight", {q + 2 * kv, H}},
+                               {"layers.0.feed_forward.w12.weight", {2 * I, H}}};
+    auto val = [](size_t t, size_t i) { return (float)(t * 1000 + i * 31 % 997); };
+    std::string json = "{\"__metadata__\":{\"format\":\"mlx\"}";
+    std::vector<float> payload;
+    for (size_t t = 0; t < ts.size(); ++t) {
+      size_t n = 1;
+      for (size_t d : ts[t].shape) n *= d;
+      const size_t b = payload.size() * 4;
+      for (size_t i = 0; i < n; ++i) payload.push_back(val(t, i));
+      json += std::string(",\"") + ts[t].name + "\":{\"dtype\":\"F32\",\"shape\":[";
+      for (size_t k = 0; k < ts[t].shape.size(); ++k) json += (k ? "," : "") + std::to_string(ts[t].shape[k]);
+      json += "],\"data_offsets\":[" + std::to_string(b) + "," + std::to_string(payload.size() * 4) + "]}";
+    }
+    json += "}";
+    const std::string path = "/tmp/mi_bridge_gb15.safetensors";
+    FILE* fp = std::fopen(path.c_str(), "wb");
+    const uint64_t hl = json.size();
+    bool ok = fp && std::fwrite(&hl, 8, 1, fp) == 1 && std::fwrite(json.data(), 1, hl, fp) == hl &&
+              std::fwrite(payload.data(), 4, payload.size(), fp) == payload.size();
+    if (fp) std::fclose(fp);
+    mi_bridge::ModelWeights w;
+    w.dtype = mi_bridge::DType::FP32;
+    std::vector<void*> bufs;
+    auto alloc = [&](size_t n) {
+      void* p = nullptr;
+      (void)hipMalloc(&p, n * 4);
+      bufs.push_back(p);
+      return p;
+    };
+    w.token_embeddings = alloc(V * H);
+    w.output_projection = alloc(H * V);
+    w.final_norm = alloc(H);
+    mi_bridge::LayerWeights lw;
+    lw.attn_norm = alloc(H); lw.ffn_norm = alloc(H); lw.Wq = alloc(H * q); lw.Wk = alloc(H * kv);
+    lw.Wv = alloc(H * kv); lw.Wo = alloc(q * H); lw.w_gate = alloc(H * I); lw.w_up = alloc(H * I);
+    lw.w_down = alloc(I * H);
+    w.layers.push_back(lw);
+    ok = ok && mi_bridge::load_weights(path, c, w);
+    size_t bad = 0;
+    auto chk = [&](void* d, size_t rows, size_t cols, auto ref) {
+      std::vector<float> h = host((float*)d, rows * cols);
+      for (size_t r = 0; r < rows; ++r)
+        for (size_t k = 0; k < cols; ++k) bad += h[r * cols + k] != ref(r, k);
+    };
+    // engine [in, out] element (r, k) = file element (row range offset + k, r) of the file matrix
+    chk(w.token_embeddings, V, H, [&](size_t r, size_t k) { return val(0, r * H + k); });
+    chk(w.output_projection, H, V, [&](size_t r, size_t k) { return val(1, k * H + r); });
+    chk(lw.Wo, q, H, [&](size_t r, size_t k) { return val(5, k * q + r); });
+    chk(lw.w_down, I, H, [&](size_t r, size_t k) { return val(6, k * I + r); });
+    chk(lw.Wq, H, q, [&](size_t r, size_t k) { return val(7, k * H + r); });
+    chk(lw.Wk, H, kv, [&](size_t r, size_t k) { return val(7, (q + k) * H + r); });
+    chk(lw.Wv, H, kv, [&](size_t r, size_t k) { return val(7, (q + kv + k) * H + r); });
+    chk(lw.w_gate, H, I, [&](size_t r, size_t k) { return val(8, k * H + r); });
+    chk(lw.w_up, H, I, [&](size_t r, size_t k) { return val(8, (I + k) * H + r); });
+    chk(lw.ffn_norm, 1, H, [&](size_t, size_t k) { return val(4, k); });
+    row("GB-15", "load_weights: Python/MLX file, transposed and de-fused, exact", ok && bad == 0,
+        std::to_string(bad) + " mismatches");
+    for (void* p : bufs) dfree(p);
+    std::remove(path.c_str());
+  }
   std::printf("%d/%d checks passed\n", g_passed, g_total);
   return g_passed == g_total ? 0 : 1;
 }

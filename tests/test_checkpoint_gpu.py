@@ -1,0 +1,66 @@
+"""Checkpoint weights loaded onto the GPU (mi_gemm.load_weights over mi_convert_matrix) vs
+the oracle's restatement of the reference loader (Checkpoint.cpp:28-83, 390-570): a
+Python/MLX file with bf16, f16 and fp32 tensors (transposed [out, in] matrices, de-fused
+wqkv and w12) and engine files, into fp32 (exact) and bf16 (round to nearest even of the
+exact value) buffers; odd-shaped slices and transposes; missing and mismatched tensors."""
+import numpy as np
+import pytest
+
+from checkpoint_files import CFG, write_engine_file, write_python_file
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.mark.parametrize("fmt", ["python", "engine_f32", "engine_bf16"])
+@pytest.mark.parametrize("dst", ["f32", "bf16"])
+def test_load_weights(mi, dev, oracle, tmp_path, fmt, dst):
+    import torch
+
+    path = str(tmp_path / f"{fmt}.safetensors")
+    if fmt == "python":
+        write_python_file(path)
+    else:
+        write_engine_file(path, dtype=torch.float32 if fmt == "engine_f32" else torch.bfloat16)
+    print(f"load_weights {fmt} -> {dst}", flush=True)
+    w = mi.load_weights(path, CFG, dtype=torch.float32 if dst == "f32" else torch.bfloat16, device=dev)
+    ref = oracle.checkpoint_weights(path, CFG)
+    assert set(w) == set(ref)
+    for k, v in ref.items():
+        got = w[k].float().cpu().numpy()
+        want = v if dst == "f32" else oracle.round_bf16(v)
+        assert got.shape == want.shape and np.array_equal(got, want), k
+
+
+@pytest.mark.parametrize("src_dt", ["f32", "bf16", "f16"])
+@pytest.mark.parametrize("transpose", [False, True])
+def test_convert_matrix_slices(mi, dev, src_dt, transpose):
+    import torch
+
+    tdt = {"f32": torch.float32, "bf16": torch.bfloat16, "f16": torch.float16}[src_dt]
+    code = {"f32": mi.MI_F32, "bf16": mi.MI_BF16, "f16": mi.MI_F16}[src_dt]
+    R, C, row0, rows = 130, 77, 5, 100
+    src = torch.randn((R, C), device=dev).to(tdt)
+    for out_dt in (torch.float32, torch.bfloat16):
+        dst = torch.full((C, rows) if transpose else (rows, C), 7.0, dtype=out_dt, device=dev)
+        mi.convert_matrix(src, code, C, row0, rows, C, transpose, dst)
+        want = src[row0:row0 + rows].float()
+        want = (want.t() if transpose else want).to(out_dt)
+        assert torch.equal(dst, want)
+
+
+def test_missing_and_mismatched(mi, dev, tmp_path):
+    import torch
+    from safetensors.torch import save_file
+
+    path = str(tmp_path / "mlx.safetensors")
+    tensors = write_python_file(path)
+    del tensors["layers.1.feed_forward.w12.weight"]
+    p2 = str(tmp_path / "missing.safetensors")
+    save_file(tensors, p2)
+    with pytest.raises(KeyError):
+        mi.load_weights(p2, CFG, device=dev)
+    tensors["layers.1.feed_forward.w12.weight"] = torch.zeros((10, 64))
+    p3 = str(tmp_path / "shape.safetensors")
+    save_file(tensors, p3)
+    with pytest.raises(ValueError):
+        mi.load_weights(p3, CFG, device=dev)
