@@ -72,11 +72,14 @@ def parse():
     ap.add_argument("--cpu-rows", type=int, default=2048, help="token rows of the CPU sample")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="also launch a 1 GiB device copy (for PMC byte-counter scaling)")
-    ap.add_argument("--workload", choices=("block", "attention", "lm_head", "norm"), default="block",
+    ap.add_argument("--workload", choices=("block", "attention", "lm_head", "norm", "convert"),
+                    default="block",
                     help="block: the configuration-3 GEMM set (the headline metric); attention: "
                          "configuration 4, fused GQA attention forward + backward; lm_head: "
                          "configuration 5, LM-head GEMMs with the fused cross-entropy between; "
-                         "norm: configuration 3's residual add + RMSNorm forward and backward")
+                         "norm: configuration 3's residual add + RMSNorm forward and backward; "
+                         "convert: checkpoint weight conversion of one configuration-3 layer and "
+                         "the LM head (Python/MLX layout -> engine layout)")
     return ap.parse_args()
 
 
@@ -423,6 +426,74 @@ def norm_main(args):
     print(json.dumps(out))
 
 
+def convert_main(args):
+    """Checkpoint conversion on the GPU (Checkpoint.cpp:407-570 restated as mi_convert_matrix):
+    one configuration-3 layer and the LM head from the Python/MLX layout ([out, in], fused
+    wqkv [3072, 2048] and w12 [11264, 2048], wo [2048, 2048], w3 [2048, 5632], output
+    [32000, 2048], bf16) into the engine's [in, out] bf16 matrices. HBM-bound: value =
+    bytes read + written per step / step time."""
+    import torch
+
+    import mi_gemm as mi
+
+    dev = torch.device("cuda:0")
+    mi.init()
+    H, I, V, q, kv = 2048, 5632, 32000, 2048, 512
+    g = torch.Generator(device=dev)
+    g.manual_seed(8)
+    src = {n: torch.randn(s, generator=g, device=dev).to(torch.bfloat16) for n, s in
+           (("wqkv", (q + 2 * kv, H)), ("w12", (2 * I, H)), ("wo", (H, q)), ("w3", (H, I)),
+            ("output", (V, H)))}
+    # (source, row0, rows, destination shape): every engine matrix is a transposed row range
+    jobs = [("wqkv", 0, q, (H, q)), ("wqkv", q, kv, (H, kv)), ("wqkv", q + kv, kv, (H, kv)),
+            ("w12", 0, I, (H, I)), ("w12", I, I, (H, I)), ("wo", 0, H, (q, H)), ("w3", 0, H, (I, H)),
+            ("output", 0, V, (H, V))]
+    dst = [torch.empty(shape, dtype=torch.bfloat16, device=dev) for _, _, _, shape in jobs]
+    lib = mi.load_library()
+    stream = mi._stream()
+    calls = [(stream, mi._ptr(src[n]), mi.MI_BF16, src[n].shape[1], r0, rows, src[n].shape[1], 1,
+              mi._ptr(d), mi.MI_BF16, rows) for (n, r0, rows, _), d in zip(jobs, dst)]
+
+    def step():
+        for c in calls:
+            mi._check("mi_convert_matrix", lib.mi_convert_matrix(*c))
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    ev = [torch.cuda.Event(enable_timing=True) for _ in range(2)]
+    ev[0].record()
+    for c in calls[-1:] * 20:  # the LM-head matrix alone, back to back
+        lib.mi_convert_matrix(*c)
+    ev[1].record()
+    torch.cuda.synchronize()
+    ms_out = ev[0].elapsed_time(ev[1]) / 20
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        step()
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - t0
+    nbytes = sum(2 * 2 * rows * src[n].shape[1] for n, _, rows, _ in jobs)   # bf16 read + write
+    out_bytes = 2 * 2 * V * H
+    value = nbytes * args.steps / elapsed / 1e9
+    achieved = out_bytes / (ms_out / 1e3) / 1e9
+    print(json.dumps({
+        "metric": "checkpoint conversion GB/s (Python/MLX layout -> engine layout, one "
+                  "configuration-3 layer + LM head, bf16)",
+        "value": round(value, 1), "unit": "GB/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": round(elapsed / args.steps * 1e3, 4),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
+        "data": "synthetic (torch.randn on device)",
+        "config": {"workload": "8 transposed row-range conversions: wqkv -> Wq, Wk, Wv; w12 -> "
+                               "w_gate, w_up; wo; w3; output [32000, 2048]",
+                   "bytes_per_step": nbytes},
+        "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": PEAK_HBM_GBS,
+                     "unit": "GB/s", "frac": round(achieved / PEAK_HBM_GBS, 4), "traffic": None,
+                     "kernel": "convert_transpose_kernel (output [32000, 2048] -> [2048, 32000])",
+                     "avg_launch_ms": round(ms_out, 4)},
+    }))
+
+
 def main():
     args = parse()
     if args.gpus != 1:
@@ -437,6 +508,9 @@ def main():
         return
     if args.workload == "norm":
         norm_main(args)
+        return
+    if args.workload == "convert":
+        convert_main(args)
         return
     import torch
 
