@@ -76,14 +76,17 @@ void gemm_proj_trans_b(const float* a, const float* b_transposed, float* c, size
 
 // MetalBridge.hpp:49-51: causal GQA attention forward, bf16.  Q [B,nH,S,d], K/V
 // [B,nKV,S,d], O [B,nH,S,d] (the output layout of flash_attn_fwd.metal); query
-// head h reads KV head h / (nH/nKV); head_dim 128.
+// head h reads KV head h / (nH/nKV).  head_dim 128 runs the fused kernel; any other
+// head_dim (the reference kernel's is 64) runs the materialised form: S and P in a
+// bridge-owned [B,nH,S,S] bf16 buffer, batched GEMMs and the softmax kernel.
 void flash_attn_fwd(const void* Q, const void* K, const void* V, void* O, size_t batch,
                     size_t n_heads, size_t n_kv, size_t seq_len, size_t head_dim);
 
 // MetalBridge.hpp:54-57: gradients of the causal GQA attention, bf16, dO and dQ
 // [B,nH,S,d], dK/dV [B,nKV,S,d] summed over each KV group's query heads.  Like
 // the reference kernel it takes no forward state: the forward's O and row
-// log-sum-exp are recomputed into bridge-owned device buffers first.
+// log-sum-exp are recomputed into bridge-owned device buffers first.  head_dim
+// other than 128: the materialised backward (P and dP in bridge-owned buffers).
 void fused_attn_bwd(const void* Q, const void* K, const void* V, const void* dO, void* dQ,
                     void* dK, void* dV, size_t batch, size_t n_heads, size_t n_kv,
                     size_t seq_len, size_t head_dim);

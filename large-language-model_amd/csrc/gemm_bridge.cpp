@@ -4,6 +4,7 @@
 
 #include <hip/hip_runtime.h>
 
+#include <cmath>
 #include <cstdio>
 #include <cstring>
 
@@ -223,8 +224,120 @@ void gemm_proj_trans_b(const float* a, const float* b_transposed, float* c, size
          gemm(0, 1, M, N, K, 1.0f, a, b_transposed, MI_BF16, 0.0f, c, MI_BF16, nullptr));
 }
 
+namespace {
+
+// Head dimensions other than 128 run the materialised form: S and P [B, nH, T, T]
+// (and dP in the backward) in bridge-owned bf16 buffers, batched GEMMs with the
+// KV-head map and causal skipping, and the row softmax kernels (Attention.cpp:236-348).
+thread_local void* t_sp = nullptr;
+thread_local size_t t_sp_bytes = 0;
+
+bool sp_state(size_t bytes) {
+  if (bytes <= t_sp_bytes) return true;
+  if (t_sp) {
+    if (hipStreamSynchronize(get_stream()) != hipSuccess) return false;
+    (void)hipFree(t_sp);
+  }
+  t_sp = nullptr;
+  t_sp_bytes = 0;
+  if (hipMalloc(&t_sp, bytes) != hipSuccess) return false;
+  t_sp_bytes = bytes;
+  return true;
+}
+
+mi_batch attn_batch(int64_t batch, int64_t heads, int64_t ao, int64_t ai, int64_t ag, int64_t bo,
+                    int64_t bi, int64_t bg, int64_t co, int64_t ci, int32_t causal, float mask) {
+  mi_batch b;
+  std::memset(&b, 0, sizeof(b));
+  b.batch = batch; b.heads = heads;
+  b.a_outer = ao; b.a_inner = ai; b.a_group = ag;
+  b.b_outer = bo; b.b_inner = bi; b.b_group = bg;
+  b.c_outer = co; b.c_inner = ci; b.c_group = 1;
+  b.k_segments = 1;
+  b.causal = causal;
+  b.mask_value = mask;
+  return b;
+}
+
+// P = softmax(Q K^T / sqrt(d)), causal, into P [B, nH, T, T]; O (BHTD) = P V when O is set.
+int materialised_fwd(const void* Q, const void* K, const void* V, void* O, void* P, int64_t B,
+                     int64_t nH, int64_t nKV, int64_t T, int64_t d) {
+  const int64_t g = nH / nKV;
+  hipStream_t st = get_stream();
+  mi_batch bs = attn_batch(B * nH, nH, nH * T * d, T * d, 1, nKV * T * d, T * d, g, nH * T * T, T * T,
+                           MI_CAUSAL_OUT_LOWER, -INFINITY);
+  int s = mi_gemm_batched(st, 0, 1, T, T, d, (float)(1.0 / std::sqrt((double)d)), Q, d, K, d, MI_BF16,
+                          0.0f, P, T, MI_BF16, &bs, nullptr, nullptr, 0);
+  if (s == MI_OK) s = mi_softmax_causal(st, P, B * nH * T, T, T, MI_BF16);
+  if (s == MI_OK && O) {
+    mi_batch bo = attn_batch(B * nH, nH, nH * T * T, T * T, 1, nKV * T * d, T * d, g, nH * T * d, T * d,
+                             MI_CAUSAL_A_LOWER, 0.0f);
+    s = mi_gemm_batched(st, 0, 0, T, d, T, 1.0f, P, T, V, d, MI_BF16, 0.0f, O, d, MI_BF16, &bo,
+                        nullptr, nullptr, 0);
+  }
+  return s;
+}
+
+int materialised_bwd(const void* Q, const void* K, const void* V, const void* dO, void* dQ, void* dK,
+                     void* dV, int64_t B, int64_t nH, int64_t nKV, int64_t T, int64_t d) {
+  const int64_t g = nH / nKV;
+  const size_t sp = (size_t)(B * nH * T * T) * 2;
+  if (!sp_state(2 * sp)) return MI_ERR_HIP;
+  void* P = t_sp;
+  void* dP = (char*)t_sp + sp;
+  hipStream_t st = get_stream();
+  int s = materialised_fwd(Q, K, V, nullptr, P, B, nH, nKV, T, d);
+  // dV[b,kv] = sum over the group's heads of P^T dO   (TN, K = g segments of T)
+  mi_batch b1 = attn_batch(B * nKV, nKV, nH * T * T, g * T * T, 1, nH * T * d, g * T * d, 1, nKV * T * d,
+                           T * d, MI_CAUSAL_A_UPPER, 0.0f);
+  b1.k_segments = g; b1.seg_a = T * T; b1.seg_b = T * d;
+  if (s == MI_OK)
+    s = mi_gemm_batched(st, 1, 0, T, d, T, 1.0f, P, T, dO, d, MI_BF16, 0.0f, dV, d, MI_BF16, &b1,
+                        nullptr, nullptr, 0);
+  // dP = dO V^T   (NT, KV map, causal output)
+  mi_batch b2 = attn_batch(B * nH, nH, nH * T * d, T * d, 1, nKV * T * d, T * d, g, nH * T * T, T * T,
+                           MI_CAUSAL_OUT_LOWER, 0.0f);
+  if (s == MI_OK)
+    s = mi_gemm_batched(st, 0, 1, T, T, d, 1.0f, dO, d, V, d, MI_BF16, 0.0f, dP, T, MI_BF16, &b2,
+                        nullptr, nullptr, 0);
+  // dS = P (dP - rowsum(P dP)) / sqrt(d), over dP
+  if (s == MI_OK)
+    s = mi_softmax_bwd(st, P, dP, B * nH * T, T, T, (float)(1.0 / std::sqrt((double)d)), MI_BF16);
+  // dQ = dS K   (NN, KV map, causal K skipping)
+  mi_batch b3 = attn_batch(B * nH, nH, nH * T * T, T * T, 1, nKV * T * d, T * d, g, nH * T * d, T * d,
+                           MI_CAUSAL_A_LOWER, 0.0f);
+  if (s == MI_OK)
+    s = mi_gemm_batched(st, 0, 0, T, d, T, 1.0f, dP, T, K, d, MI_BF16, 0.0f, dQ, d, MI_BF16, &b3,
+                        nullptr, nullptr, 0);
+  // dK[b,kv] = sum over the group's heads of dS^T Q   (TN, K = g segments of T)
+  mi_batch b4 = attn_batch(B * nKV, nKV, nH * T * T, g * T * T, 1, nH * T * d, g * T * d, 1, nKV * T * d,
+                           T * d, MI_CAUSAL_A_UPPER, 0.0f);
+  b4.k_segments = g; b4.seg_a = T * T; b4.seg_b = T * d;
+  if (s == MI_OK)
+    s = mi_gemm_batched(st, 1, 0, T, d, T, 1.0f, dP, T, Q, d, MI_BF16, 0.0f, dK, d, MI_BF16, &b4,
+                        nullptr, nullptr, 0);
+  return s;
+}
+
+}  // namespace
+
 void flash_attn_fwd(const void* Q, const void* K, const void* V, void* O, size_t batch,
                     size_t n_heads, size_t n_kv, size_t seq_len, size_t head_dim) {
+  if (head_dim != 128 && batch && n_heads && seq_len && head_dim) {
+    if (n_kv == 0 || n_heads % n_kv) {
+      finish("flash_attn_fwd", MI_ERR_SHAPE);
+      return;
+    }
+    const size_t sp = batch * n_heads * seq_len * seq_len * 2;
+    if (!sp_state(sp)) {
+      t_status = MI_ERR_HIP;
+      std::fprintf(stderr, "[mi_bridge] flash_attn_fwd: could not allocate S/P\n");
+      return;
+    }
+    finish("flash_attn_fwd", materialised_fwd(Q, K, V, O, t_sp, (int64_t)batch, (int64_t)n_heads,
+                                              (int64_t)n_kv, (int64_t)seq_len, (int64_t)head_dim));
+    return;
+  }
   finish("flash_attn_fwd",
          mi_flash_attn_fwd(get_stream(), Q, K, V, O, nullptr, (int64_t)batch, (int64_t)n_heads,
                            (int64_t)n_kv, (int64_t)seq_len, (int64_t)head_dim, 1, MI_ATTN_O_BHTD));
@@ -306,8 +419,17 @@ void fused_attn_bwd(const void* Q, const void* K, const void* V, const void* dO,
                     void* dK, void* dV, size_t batch, size_t n_heads, size_t n_kv,
                     size_t seq_len, size_t head_dim) {
   const size_t rows = batch * n_heads * seq_len;
-  if (rows == 0) {
+  if (rows == 0 || head_dim == 0) {
     t_status = MI_OK;
+    return;
+  }
+  if (head_dim != 128) {
+    if (n_kv == 0 || n_heads % n_kv) {
+      finish("fused_attn_bwd", MI_ERR_SHAPE);
+      return;
+    }
+    finish("fused_attn_bwd", materialised_bwd(Q, K, V, dO, dQ, dK, dV, (int64_t)batch, (int64_t)n_heads,
+                                              (int64_t)n_kv, (int64_t)seq_len, (int64_t)head_dim));
     return;
   }
   if (!attention_state(rows * head_dim * 2, rows)) {
