@@ -177,16 +177,25 @@ int mi_flash_attn_fwd(void* stream, const void* Q, const void* K, const void* V,
  * computes dQ [batch, n_heads, seq_len, d] and dK, dV [batch, n_kv, seq_len, d]
  * (bf16), dK/dV summed over the n_heads/n_kv query heads of each KV head.  O
  * and dO use o_layout; delta is caller workspace of batch*n_heads*seq_len fp32
- * (receives rowsum(dO * O)).  Two kernels on `stream`, deterministic (no
- * atomics).  head_dim must be 128.  Replaces metal_bridge::fused_attn_bwd
- * (MetalBridge.hpp:54-57; that kernel recomputes the forward itself, this one
- * takes the forward's O and lse) and the backward of Attention::backward
- * (Attention.cpp:292-348).
+ * (receives rowsum(dO * O)).  Deterministic (no atomics).  head_dim must be 128.
+ * With workspace of mi_flash_attn_bwd_workspace_size bytes (16-byte aligned;
+ * seq_len a multiple of 8, at most 32767) the dK/dV kernel also writes dS^T there and dQ is
+ * one batched GEMM (5 MFMA products); with NULL / too little workspace a dQ
+ * kernel recomputes S and dP instead (7 products).  Replaces
+ * metal_bridge::fused_attn_bwd (MetalBridge.hpp:54-57; that kernel recomputes
+ * the forward itself, this one takes the forward's O and lse) and the backward
+ * of Attention::backward (Attention.cpp:292-348).
  */
 int mi_flash_attn_bwd(void* stream, const void* Q, const void* K, const void* V, const void* O,
                       const void* dO, const float* lse, void* dQ, void* dK, void* dV, float* delta,
                       int64_t batch, int64_t n_heads, int64_t n_kv, int64_t seq_len,
-                      int64_t head_dim, int32_t causal, int32_t o_layout);
+                      int64_t head_dim, int32_t causal, int32_t o_layout, void* workspace,
+                      size_t workspace_bytes);
+
+/* Workspace bytes for the dS^T form of mi_flash_attn_bwd (batch*n_heads*seq_len^2
+ * bf16), or 0 when that form does not apply (seq_len not a multiple of 8, or
+ * above 32767). */
+size_t mi_flash_attn_bwd_workspace_size(int64_t batch, int64_t n_heads, int64_t seq_len);
 
 /*
  * Softmax cross-entropy over rows of logits, the loss after the LM head.  For

@@ -441,10 +441,14 @@ void fused_attn_bwd(const void* Q, const void* K, const void* V, const void* dO,
   float* delta = t_att_f + t_att_rows;
   int st = mi_flash_attn_fwd(get_stream(), Q, K, V, t_att_o, lse, (int64_t)batch, (int64_t)n_heads,
                              (int64_t)n_kv, (int64_t)seq_len, (int64_t)head_dim, 1, MI_ATTN_O_BHTD);
+  // dS^T workspace (bridge-owned, shared with the materialised path's S/P buffer)
+  const size_t ws = mi_flash_attn_bwd_workspace_size((int64_t)batch, (int64_t)n_heads, (int64_t)seq_len);
+  const bool have_ws = ws && sp_state(ws);
   if (st == MI_OK)
     st = mi_flash_attn_bwd(get_stream(), Q, K, V, t_att_o, dO, lse, dQ, dK, dV, delta,
                            (int64_t)batch, (int64_t)n_heads, (int64_t)n_kv, (int64_t)seq_len,
-                           (int64_t)head_dim, 1, MI_ATTN_O_BHTD);
+                           (int64_t)head_dim, 1, MI_ATTN_O_BHTD, have_ws ? t_sp : nullptr,
+                           have_ws ? t_sp_bytes : 0);
   finish("fused_attn_bwd", st);
 }
 

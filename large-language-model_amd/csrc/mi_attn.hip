@@ -593,8 +593,9 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2)))
 // and dK / dV accumulators in registers, computes S^T = K Q^T and dP^T = V dO^T
 // with one lane per key, P^T and dS^T = P^T (dP^T - D) in registers, and
 // accumulates dV += P^T dO and dK += scale * dS^T Q.  The KV-group reduction
-// (Attention.cpp:332,344-345) is the loop over the group's heads.
-template <int D>
+// (Attention.cpp:332,344-345) is the loop over the group's heads.  DS: also store
+// dS^T (bf16, [B, nH, key, query]) for dQ = scale * dS K as a batched GEMM.
+template <int D, bool DS>
 __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1)))
     flash_bwd_dkdv_kernel(FbParams p) {
   using Tl = FaTile<D>;
@@ -692,7 +693,27 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1)))
     for (int e = 0; e < 16; ++e) dk[c][e] = dv[c][e] = 0.0f;
   const float sl2 = p.scale_log2;
 
-  auto block = [&](const int q0, const uint32_t st, auto MASK_c) __attribute__((always_inline)) {
+  // dS^T rows of this lane's key: registers base..base+7 of a run hold 8 consecutive
+  // queries, stored as one 16-byte buffer store, 4 per tile.  Lanes l and l + 32 hold
+  // the same key, so each key's 64 queries of a tile fill one 128-byte line.  Lanes
+  // past the last key, and runs past the last query (T % 8 == 0, so a run is all in or
+  // all out), get an offset beyond the tile descriptor's range, which the hardware
+  // drops: every wave issues exactly 4 stores per tile, and ring_step's wait counts
+  // them (vmcnt retires in issue order on gfx9-family parts).
+  const uint32_t ds_lane = live ? (uint32_t)(key * T + 8 * h32) * 2u : 0x80000000u;
+  auto store_ds = [&](int bh, int q0, auto&& run) __attribute__((always_inline)) {
+    const __amdgpu_buffer_rsrc_t rs =
+        scalar_rsrc(uniform((const uint16_t*)p.dsT + (int64_t)bh * T * T + q0),
+                    (uint32_t)(((int64_t)T * T - q0) * 2));
+    const int lim = T - q0 - 8 * h32;  // runs starting below lim exist
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) {
+      const int c = 32 * (ks >> 1) + 16 * (ks & 1);
+      const uint32_t off = c < lim ? ds_lane : 0x80000000u;
+      __builtin_amdgcn_raw_buffer_store_b128(run(ks), rs, off + 2 * c, 0, 0);
+    }
+  };
+  auto block = [&](const int q0, const int bh, const uint32_t st, auto MASK_c) __attribute__((always_inline)) {
     constexpr bool MASK = decltype(MASK_c)::value;
     const uint32_t tq = st, tg = st + Tl::BYTES, tl = st + 2 * Tl::BYTES, td = tl + QT * 4;
     f32x16_t sacc[2], pacc[2];
@@ -742,6 +763,7 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1)))
         df[ks][w2] = pack_bf16x2(dsv[0], dsv[1]);
       }
     }
+    if constexpr (DS) store_ds(bh, q0, [&](int ks) __attribute__((always_inline)) { return df[ks]; });
     // dV += P^T dO (first operand dO^T), dK += dS^T Q (first operand Q^T)
     static_for<4>([&](auto ks_c) __attribute__((always_inline)) {
       constexpr int KS = decltype(ks_c)::value;
@@ -769,7 +791,8 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1)))
   // visible whole.  Separate loops keep the accumulators in place across iterations.
   const int n_diag = uniform(p.causal ? (per_h < 2 ? per_h : 2) : 0);
   auto ring_step = [&](int it) __attribute__((always_inline)) {
-    wait_vmcnt<0>();
+    if (DS && it > 0) wait_vmcnt<4>();  // the last tile's dS^T stores stay in flight
+    else wait_vmcnt<0>();
     lds_ring_barrier();
     if (it + 1 < total) issue(it + 1);
     return lds0 + (uint32_t)((it & 1) * STAGE);
@@ -777,15 +800,20 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1)))
   if (total > 0) issue(0);
   int it = 0;
   for (int hh = 0; hh < p.group; ++hh) {
+    const int bh = uniform(b * p.nH + kvh * p.group + hh);
     for (int t = 0; t < n_diag; ++t, ++it) {
       const uint32_t st = ring_step(it);
       const int q0 = uniform((qt0 + t) * QT);
-      if (q0 + QT - 1 < kw) continue;  // every query of the tile precedes every key
-      block(q0, st, std::true_type{});
+      if (q0 + QT - 1 < kw) {  // every query of the tile precedes every key
+        if constexpr (DS)  // zeros: the dQ GEMM reads whole K tiles around the diagonal
+          store_ds(bh, q0, [](int) __attribute__((always_inline)) { return u32x4_t{0u, 0u, 0u, 0u}; });
+        continue;
+      }
+      block(q0, bh, st, std::true_type{});
     }
     for (int t = n_diag; t < per_h; ++t, ++it) {
       const uint32_t st = ring_step(it);
-      block(uniform((qt0 + t) * QT), st, std::false_type{});
+      block(uniform((qt0 + t) * QT), bh, st, std::false_type{});
     }
   }
 
@@ -805,19 +833,60 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1)))
   }
 }
 
+// D = rowsum(dO * O) for the dS^T path (the dQ kernel computes it otherwise), with the
+// dQ kernel's lane layout and summation order: lane l32 of a wave is a row, lanes l
+// and l + 32 sum alternate 8-column chunks, then add their halves.
+template <int D>
+__global__ void __launch_bounds__(256) flash_bwd_delta_kernel(FbParams p) {
+  constexpr int NS = D / 16;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int h32 = lane >> 5, l32 = lane & 31;
+  const int64_t r = (int64_t)blockIdx.x * 128 + wave * 32 + l32;  // row of [B, nH, T]
+  const int64_t rows = (int64_t)p.B * p.nH * p.T;
+  const bool live = r < rows;
+  const int64_t bh = live ? r / p.T : 0, t = live ? r - bh * p.T : 0;
+  const int64_t b = bh / p.nH, h = bh - b * p.nH;
+  const int64_t orow = p.o_bthd ? ((b * p.T + t) * p.nH + h) * D : (bh * p.T + t) * D;
+  float dsum = 0.0f;
+  if (live) {
+#pragma unroll
+    for (int s = 0; s < NS; ++s) {
+      const int dd = 16 * s + 8 * h32;
+      const u32x4_t gf = *(const u32x4_t*)((const __bf16*)p.dO + orow + dd);
+      const u32x4_t of = *(const u32x4_t*)((const __bf16*)p.O + orow + dd);
+#pragma unroll
+      for (int w2 = 0; w2 < 4; ++w2)
+        dsum += bf16_bits_to_f32(gf[w2] & 0xffffu) * bf16_bits_to_f32(of[w2] & 0xffffu) +
+                bf16_bits_to_f32(gf[w2] >> 16) * bf16_bits_to_f32(of[w2] >> 16);
+    }
+  }
+  dsum += __shfl_xor(dsum, 32, 64);
+  if (live && h32 == 0) p.delta[r] = dsum;
+}
+
 }  // namespace
 
 int flash_fwd_blocks(int T) { return (T + FA_BQ - 1) / FA_BQ; }
 
 hipError_t launch_flash_bwd(const FbParams& p, int head_dim, hipStream_t stream) {
   if (head_dim != 128) return hipErrorInvalidValue;
-  // dQ (and D) first: the dK/dV kernel reads D.
-  const int64_t nq = (int64_t)p.B * p.nH * p.q_blocks;
-  hipLaunchKernelGGL(flash_bwd_dq_kernel<128>, dim3((unsigned)nq), dim3(256), 0, stream, p);
+  // dQ (and D) first: the dK/dV kernel reads D.  With the dS^T workspace only D here;
+  // the dK/dV kernel then writes dS^T and the caller runs dQ = scale * dS K.
+  if (p.dsT) {
+    const int64_t rows = (int64_t)p.B * p.nH * p.T;
+    hipLaunchKernelGGL(flash_bwd_delta_kernel<128>, dim3((unsigned)((rows + 127) / 128)), dim3(256), 0,
+                       stream, p);
+  } else {
+    const int64_t nq = (int64_t)p.B * p.nH * p.q_blocks;
+    hipLaunchKernelGGL(flash_bwd_dq_kernel<128>, dim3((unsigned)nq), dim3(256), 0, stream, p);
+  }
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
   const int64_t nk = (int64_t)p.B * p.nKV * p.k_blocks;
-  hipLaunchKernelGGL(flash_bwd_dkdv_kernel<128>, dim3((unsigned)nk), dim3(256), 0, stream, p);
+  if (p.dsT)
+    hipLaunchKernelGGL((flash_bwd_dkdv_kernel<128, true>), dim3((unsigned)nk), dim3(256), 0, stream, p);
+  else
+    hipLaunchKernelGGL((flash_bwd_dkdv_kernel<128, false>), dim3((unsigned)nk), dim3(256), 0, stream, p);
   return hipGetLastError();
 }
 

@@ -29,6 +29,8 @@ struct FbParams {
   void* dK;        // [B, nKV, T, d] bf16
   void* dV;        // [B, nKV, T, d] bf16
   float* delta;    // [B, nH, T] workspace: rowsum(dO * O)
+  void* dsT;       // null, or [B, nH, T, T] bf16 workspace receiving dS^T (key-major):
+                   // then dQ is left to a batched GEMM dQ = scale * dS K by the caller
   int B, nH, nKV, T, group;
   int causal, o_bthd;
   int q_blocks;    // flash_fwd_blocks(T)

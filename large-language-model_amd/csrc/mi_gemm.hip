@@ -613,10 +613,17 @@ int mi_flash_attn_fwd(void* stream, const void* Q, const void* K, const void* V,
   return e == hipSuccess ? MI_OK : fail(MI_ERR_HIP, "flash attention launch: %s", hipGetErrorString(e));
 }
 
+size_t mi_flash_attn_bwd_workspace_size(int64_t batch, int64_t n_heads, int64_t seq_len) {
+  // The dK/dV kernel stores dS^T in runs of 8 queries through 32-bit buffer offsets.
+  if (batch <= 0 || n_heads <= 0 || seq_len <= 0 || seq_len % 8 || seq_len > 32767) return 0;
+  return (size_t)batch * (size_t)n_heads * (size_t)seq_len * (size_t)seq_len * 2;
+}
+
 int mi_flash_attn_bwd(void* stream, const void* Q, const void* K, const void* V, const void* O,
                       const void* dO, const float* lse, void* dQ, void* dK, void* dV, float* delta,
                       int64_t batch, int64_t n_heads, int64_t n_kv, int64_t seq_len,
-                      int64_t head_dim, int32_t causal, int32_t o_layout) {
+                      int64_t head_dim, int32_t causal, int32_t o_layout, void* workspace,
+                      size_t workspace_bytes) {
   if (batch < 0 || n_heads < 0 || n_kv < 0 || seq_len < 0)
     return fail(MI_ERR_SHAPE, "negative size");
   if (batch == 0 || n_heads == 0 || seq_len == 0) return MI_OK;
@@ -652,9 +659,33 @@ int mi_flash_attn_bwd(void* stream, const void* Q, const void* K, const void* V,
   p.k_blocks = flash_bwd_key_blocks(p.T);
   p.scale = (float)(1.0 / std::sqrt((double)head_dim));
   p.scale_log2 = (float)(1.4426950408889634 / std::sqrt((double)head_dim));
+  // With room for dS^T the dK/dV kernel writes it and dQ = scale * dS K is one batched
+  // GEMM (5 MFMA products instead of 7); otherwise the dQ kernel recomputes S and dP.
+  const size_t need = mi_flash_attn_bwd_workspace_size(batch, n_heads, seq_len);
+  p.dsT = (workspace && need && workspace_bytes >= need && aligned16(workspace)) ? workspace : nullptr;
+  if (p.dsT && causal) {
+    // Causal skipping in the dQ GEMM works on whole K tiles up to the end of a
+    // 128-row output tile; the dK/dV kernel writes dS^T (zeros included) for every
+    // key below that bound, and not beyond it, so taller tiles take the dQ kernel.
+    const Plan pl = make_plan(MI_BF16, seq_len, head_dim, seq_len, batch * n_heads, MODE_PLAIN, false, 0,
+                              current_cus(), true);
+    if (shape_of(MI_BF16, pl.cfg).bm != 128) p.dsT = nullptr;
+  }
   hipError_t e = launch_flash_bwd(p, (int)head_dim, (hipStream_t)stream);
-  return e == hipSuccess ? MI_OK : fail(MI_ERR_HIP, "flash attention backward launch: %s",
-                                        hipGetErrorString(e));
+  if (e != hipSuccess)
+    return fail(MI_ERR_HIP, "flash attention backward launch: %s", hipGetErrorString(e));
+  if (!p.dsT) return MI_OK;
+  const int64_t T = seq_len, d = head_dim, g = n_heads / n_kv;
+  mi_batch bt;
+  std::memset(&bt, 0, sizeof(bt));
+  bt.batch = batch * n_heads; bt.heads = n_heads;
+  bt.a_outer = n_heads * T * T; bt.a_inner = T * T; bt.a_group = 1;   // dS^T [b][h][key][query]
+  bt.b_outer = n_kv * T * d; bt.b_inner = T * d; bt.b_group = g;      // K of the head's KV head
+  bt.c_outer = n_heads * T * d; bt.c_inner = T * d; bt.c_group = 1;   // dQ [b][h][query][d]
+  bt.k_segments = 1;
+  bt.causal = causal ? MI_CAUSAL_A_LOWER : MI_CAUSAL_NONE;            // dS[q][k] = 0 for k > q
+  return mi_gemm_batched(stream, 1, 0, T, d, T, p.scale, p.dsT, T, K, d, MI_BF16, 0.0f, dQ, d, MI_BF16,
+                         &bt, nullptr, nullptr, 0);
 }
 
 size_t mi_rmsnorm_bwd_workspace_size(int64_t rows, int64_t dims) {

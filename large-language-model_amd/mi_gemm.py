@@ -35,7 +35,7 @@ C_SYMBOLS = (
     "mi_gemm_batched", "mi_residual_add", "mi_softmax_causal", "mi_softmax_bwd",
     "mi_gemm_describe", "mi_stream_sync", "mi_flash_attn_fwd", "mi_flash_attn_bwd",
     "mi_cross_entropy", "mi_rmsnorm_fwd", "mi_rmsnorm_bwd", "mi_rmsnorm_bwd_workspace_size",
-    "mi_convert_matrix",
+    "mi_convert_matrix", "mi_flash_attn_bwd_workspace_size",
 )
 MI_ATTN_O_BHTD, MI_ATTN_O_BTHD = 0, 1
 
@@ -114,7 +114,9 @@ def load_library():
     L.mi_flash_attn_fwd.argtypes = [vp, vp, vp, vp, vp, vp, i64, i64, i64, i64, i64, i32, i32]
     L.mi_flash_attn_bwd.restype = ctypes.c_int
     L.mi_flash_attn_bwd.argtypes = [vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, i64, i64, i64, i64,
-                                    i64, i32, i32]
+                                    i64, i32, i32, vp, ctypes.c_size_t]
+    L.mi_flash_attn_bwd_workspace_size.restype = ctypes.c_size_t
+    L.mi_flash_attn_bwd_workspace_size.argtypes = [i64, i64, i64]
     L.mi_cross_entropy.restype = ctypes.c_int
     L.mi_cross_entropy.argtypes = [vp, vp, i32, i64, vp, i64, i64, ctypes.c_float, vp, vp, vp,
                                    i32, i64]
@@ -452,10 +454,12 @@ def flash_attn_fwd(Q4, K4, V4, O=None, lse=None, causal=True, layout="bthd", syn
     return O
 
 
-def flash_attn_bwd(Q4, K4, V4, O, dO, lse, causal=True, layout="bthd", sync=None):
+def flash_attn_bwd(Q4, K4, V4, O, dO, lse, causal=True, layout="bthd", sync=None, workspace="auto"):
     """Fused backward (metal_bridge::fused_attn_bwd, MetalBridge.hpp:54-57; Attention.cpp:292-348)
     from the forward's O and lse: returns (dQ [B,nH,T,d], dK, dV [B,nKV,T,d]), bf16, dK/dV
-    summed over the query heads of each KV head. O and dO in `layout` ("bthd" or "bhtd")."""
+    summed over the query heads of each KV head. O and dO in `layout` ("bthd" or "bhtd").
+    workspace: "auto" allocates the dS^T workspace (dQ as one batched GEMM), None runs the
+    dQ kernel instead, or a device tensor of at least mi_flash_attn_bwd_workspace_size bytes."""
     torch = _torch()
     Bn, nH, T, d = Q4.shape
     nKV = K4.shape[1]
@@ -467,9 +471,14 @@ def flash_attn_bwd(Q4, K4, V4, O, dO, lse, causal=True, layout="bthd", sync=None
     dV = torch.empty_like(V4)
     delta = torch.empty((Bn, nH, T), dtype=torch.float32, device=Q4.device)
     code = MI_ATTN_O_BTHD if layout == "bthd" else MI_ATTN_O_BHTD
+    if isinstance(workspace, str) and workspace == "auto":
+        nbytes = load_library().mi_flash_attn_bwd_workspace_size(Bn, nH, T)
+        workspace = torch.empty((nbytes // 2,), dtype=torch.bfloat16, device=Q4.device) if nbytes else None
+    ws_bytes = 0 if workspace is None else workspace.numel() * workspace.element_size()
     st = load_library().mi_flash_attn_bwd(_stream(), _ptr(Q4), _ptr(K4), _ptr(V4), _ptr(O),
                                           _ptr(dO), _ptr(lse), _ptr(dQ), _ptr(dK), _ptr(dV),
-                                          _ptr(delta), Bn, nH, nKV, T, d, int(bool(causal)), code)
+                                          _ptr(delta), Bn, nH, nKV, T, d, int(bool(causal)), code,
+                                          _ptr(workspace), ws_bytes)
     if sync is None:
         _finish("mi_flash_attn_bwd", st)
     else:

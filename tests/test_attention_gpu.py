@@ -163,11 +163,14 @@ def test_flash_forward_config4(mi, dev, oracle):
         check(O[sl], oracle.attention_fwd(q[sl], k[sl], v[sl]), TOL_BF16, f"O[{b}]")
 
 
+@pytest.mark.parametrize("ws", ["auto", None])
 @pytest.mark.parametrize("Bn,nH,nKV,T", [(2, 16, 4, 256), (1, 4, 2, 300), (1, 2, 1, 64),
-                                         (1, 4, 4, 520)])
-def test_flash_backward(mi, dev, oracle, Bn, nH, nKV, T):
+                                         (1, 4, 4, 520), (1, 2, 1, 130), (2, 4, 1, 200)])
+def test_flash_backward(mi, dev, oracle, Bn, nH, nKV, T, ws):
     """Fused backward vs the oracle (Attention.cpp:292-348: dV = P^T dO, dS = P (dP - rowsum),
-    dQ = scale dS K, dK = scale dS^T Q summed over the query heads of a KV head)."""
+    dQ = scale dS K, dK = scale dS^T Q summed over the query heads of a KV head), in both
+    forms: dS^T workspace + batched dQ GEMM ("auto"; T = 300 and 130 are not multiples of 8
+    and fall back; 520 and 200 end in a partial query tile) and the dQ kernel (None)."""
     import torch
 
     d = 128
@@ -175,11 +178,57 @@ def test_flash_backward(mi, dev, oracle, Bn, nH, nKV, T):
     Q, K, V, dO = (to_dev(x, dev, True) for x in (q, k, v, do))
     lse = torch.empty((Bn, nH, T), dtype=torch.float32, device=dev)
     O = mi.flash_attn_fwd(Q, K, V, lse=lse)
-    dQ, dK, dV = mi.flash_attn_bwd(Q, K, V, O, dO, lse)
+    print(f"flash backward B={Bn} nH={nH} nKV={nKV} T={T} workspace={ws}", flush=True)
+    dQ, dK, dV = mi.flash_attn_bwd(Q, K, V, O, dO, lse, workspace=ws)
     dQ_ref, dK_ref, dV_ref = oracle.attention_bwd(q, k, v, do)
     check(host(dV), dV_ref, TOL_BF16, "dV")
     check(host(dK), dK_ref, TOL_BF16, "dK")
     check(host(dQ), dQ_ref, TOL_BF16, "dQ")
+
+
+def _dense_attention_bwd(q, k, v, do, causal):
+    """float64 closed form of the backward: dV = P^T dO, dS = P (dO V^T - rowsum(dO O)),
+    dQ = dS K / sqrt(d), dK = dS^T Q / sqrt(d), dK and dV summed over a KV head's query
+    heads.  do is [B, T, nH*d]."""
+    Bn, nH, T, d = q.shape
+    nKV = k.shape[1]
+    g = nH // nKV
+    qq = q.astype(np.float64)
+    kk = np.repeat(k.astype(np.float64), g, axis=1)
+    vv = np.repeat(v.astype(np.float64), g, axis=1)
+    s = np.matmul(qq, kk.transpose(0, 1, 3, 2)) / np.sqrt(d)
+    if causal:
+        s = np.where(np.tril(np.ones((T, T), bool)), s, -np.inf)
+    p = np.exp(s - s.max(axis=-1, keepdims=True))
+    p /= p.sum(axis=-1, keepdims=True)
+    o = np.matmul(p, vv)
+    g4 = do.astype(np.float64).reshape(Bn, T, nH, d).transpose(0, 2, 1, 3)
+    ds = p * (np.matmul(g4, vv.transpose(0, 1, 3, 2)) - (g4 * o).sum(axis=-1, keepdims=True))
+    dq = np.matmul(ds, kk) / np.sqrt(d)
+    dk = (np.matmul(ds.transpose(0, 1, 3, 2), qq) / np.sqrt(d)).reshape(Bn, nKV, g, T, d).sum(2)
+    dv = np.matmul(p.transpose(0, 1, 3, 2), g4).reshape(Bn, nKV, g, T, d).sum(2)
+    return dq, dk, dv
+
+
+@pytest.mark.parametrize("ws", ["auto", None])
+def test_flash_backward_noncausal(mi, dev, oracle, ws):
+    """causal = 0: gradients over every key (T % 64 != 0: a partial last query tile and key
+    block) vs the closed form, which is itself pinned to the oracle on the causal case."""
+    import torch
+
+    d, Bn, nH, nKV, T = 128, 1, 4, 2, 200
+    q, k, v, do = _qkv(oracle, Bn, nH, nKV, T, d, 2300)
+    for ref, got in zip(_dense_attention_bwd(q, k, v, do, True), oracle.attention_bwd(q, k, v, do)):
+        assert np.abs(ref - got).max() <= 1e-9 * max(1.0, np.abs(got).max())
+    Q, K, V, dO = (to_dev(x, dev, True) for x in (q, k, v, do))
+    lse = torch.empty((Bn, nH, T), dtype=torch.float32, device=dev)
+    O = mi.flash_attn_fwd(Q, K, V, causal=False, lse=lse)
+    print(f"flash backward non-causal T={T} workspace={ws}", flush=True)
+    dQ, dK, dV = mi.flash_attn_bwd(Q, K, V, O, dO, lse, causal=False, workspace=ws)
+    dq_ref, dk_ref, dv_ref = _dense_attention_bwd(q, k, v, do, False)
+    check(host(dV), dv_ref, TOL_BF16, "dV")
+    check(host(dK), dk_ref, TOL_BF16, "dK")
+    check(host(dQ), dq_ref, TOL_BF16, "dQ")
 
 
 def test_flash_backward_layouts_and_determinism(mi, dev, oracle):
@@ -192,14 +241,19 @@ def test_flash_backward_layouts_and_determinism(mi, dev, oracle):
     Q, K, V, dO = (to_dev(x, dev, True) for x in (q, k, v, do))
     lse = torch.empty((Bn, nH, T), dtype=torch.float32, device=dev)
     O = mi.flash_attn_fwd(Q, K, V, lse=lse)
-    g1 = mi.flash_attn_bwd(Q, K, V, O, dO, lse)
-    g2 = mi.flash_attn_bwd(Q, K, V, O, dO, lse)
-    O4 = O.view(Bn, T, nH, d).transpose(1, 2).contiguous()
-    dO4 = dO.view(Bn, T, nH, d).transpose(1, 2).contiguous()
-    g3 = mi.flash_attn_bwd(Q, K, V, O4, dO4, lse, layout="bhtd")
-    for a, b_, c in zip(g1, g2, g3):
-        assert torch.equal(a, b_), "backward differs between launches"
-        assert torch.equal(a, c), "backward differs between output layouts"
+    for ws in ("auto", None):
+        g1 = mi.flash_attn_bwd(Q, K, V, O, dO, lse, workspace=ws)
+        g2 = mi.flash_attn_bwd(Q, K, V, O, dO, lse, workspace=ws)
+        O4 = O.view(Bn, T, nH, d).transpose(1, 2).contiguous()
+        dO4 = dO.view(Bn, T, nH, d).transpose(1, 2).contiguous()
+        g3 = mi.flash_attn_bwd(Q, K, V, O4, dO4, lse, layout="bhtd", workspace=ws)
+        for a, b_, c in zip(g1, g2, g3):
+            assert torch.equal(a, b_), "backward differs between launches"
+            assert torch.equal(a, c), "backward differs between output layouts"
+        if ws is None:  # the two forms share the dK / dV kernel: identical dK and dV
+            assert torch.equal(g1[1], g_auto[1]) and torch.equal(g1[2], g_auto[2])
+        else:
+            g_auto = g1
 
 
 def test_flash_backward_config4(mi, dev, oracle):
