@@ -701,18 +701,23 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1)))
   // drops: every wave issues exactly 4 stores per tile, and ring_step's wait counts
   // them (vmcnt retires in issue order on gfx9-family parts).
   const uint32_t ds_lane = live ? (uint32_t)(key * T + 8 * h32) * 2u : 0x80000000u;
-  auto store_ds = [&](int bh, int q0, auto&& run) __attribute__((always_inline)) {
+  // The runs of half qh (k-steps 2qh and 2qh + 1); both halves: the 4 stores.
+  auto store_ds = [&](int bh, int q0, int qh, auto&& run) __attribute__((always_inline)) {
     const __amdgpu_buffer_rsrc_t rs =
         scalar_rsrc(uniform((const uint16_t*)p.dsT + (int64_t)bh * T * T + q0),
                     (uint32_t)(((int64_t)T * T - q0) * 2));
     const int lim = T - q0 - 8 * h32;  // runs starting below lim exist
 #pragma unroll
-    for (int ks = 0; ks < 4; ++ks) {
+    for (int ks = 2 * qh; ks < 2 * qh + 2; ++ks) {
       const int c = 32 * (ks >> 1) + 16 * (ks & 1);
       const uint32_t off = c < lim ? ds_lane : 0x80000000u;
       __builtin_amdgcn_raw_buffer_store_b128(run(ks), rs, off + 2 * c, 0, 0);
     }
   };
+  // One query tile in two 32-query halves, so that each half's softmax (VALU) runs
+  // between MFMAs of the other half: S and dP of half 0; S and dP of half 1 with the
+  // softmax of half 0; dV and dK of half 0 with the softmax of half 1; dV and dK of
+  // half 1.  A wave is alone on its SIMD (488 VGPRs), so nothing else hides the VALU.
   auto block = [&](const int q0, const int bh, const uint32_t st, auto MASK_c) __attribute__((always_inline)) {
     constexpr bool MASK = decltype(MASK_c)::value;
     const uint32_t tq = st, tg = st + Tl::BYTES, tl = st + 2 * Tl::BYTES, td = tl + QT * 4;
@@ -721,51 +726,46 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1)))
     for (int qh = 0; qh < 2; ++qh)
 #pragma unroll
       for (int e = 0; e < 16; ++e) sacc[qh][e] = pacc[qh][e] = 0.0f;
-#pragma unroll
-    for (int s = 0; s < NS; ++s)
-#pragma unroll
-      for (int qh = 0; qh < 2; ++qh) {
-        const u32x4_t qr = rd.row(tq, qh, s, h32);
-        const u32x4_t gr = rd.row(tg, qh, s, h32);
-        sacc[qh] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, qr),
-                                                          __builtin_bit_cast(bf16x8_t, kf[s]),
-                                                          sacc[qh], 0, 0, 0);
-        pacc[qh] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, gr),
-                                                          __builtin_bit_cast(bf16x8_t, vf[s]),
-                                                          pacc[qh], 0, 0, 0);
-      }
     // register i of half qh: query q0 + 32qh + 8*h32 + 16((i>>2)>>1) + 4((i>>2)&1) + (i&3)
     u32x4_t pf[4], df[4];
-#pragma unroll
-    for (int ks = 0; ks < 4; ++ks) {
+    f32x4_t lv[2], dv4[2];  // log-sum-exp and D of the 8 queries of the current run
+    // Softmax of k-step ks (half ks >> 1), registers base + 2*w2 .. +1 of that half
+    // (base = 8 (ks & 1)): P and dS = P (dP - D) as bf16 pairs.
+    auto soft = [&](const int ks, const int w2) __attribute__((always_inline)) {
       const int qh = ks >> 1, base = 8 * (ks & 1);
       const int tix = 32 * qh + 8 * h32 + 16 * (ks & 1);  // tile index of register `base`
-      // registers base..base+3 and base+4..base+7 hold 4 consecutive queries each
-      const f32x4_t l0 = *(const __attribute__((address_space(3))) f32x4_t*)(uintptr_t)(tl + 4 * tix);
-      const f32x4_t l1 = *(const __attribute__((address_space(3))) f32x4_t*)(uintptr_t)(tl + 4 * (tix + 4));
-      const f32x4_t d0 = *(const __attribute__((address_space(3))) f32x4_t*)(uintptr_t)(td + 4 * tix);
-      const f32x4_t d1 = *(const __attribute__((address_space(3))) f32x4_t*)(uintptr_t)(td + 4 * (tix + 4));
-      const int need = key - (q0 + tix);  // register base + r is visible iff its offset >= need
-#pragma unroll
-      for (int w2 = 0; w2 < 4; ++w2) {
-        float pv[2], dsv[2];
-#pragma unroll
-        for (int u = 0; u < 2; ++u) {
-          const int r = 2 * w2 + u;  // 0..7 within the run: offsets 0..3, then 4..7
-          const float lse2 = (r < 4 ? l0[r] : l1[r - 4]) * 1.4426950408889634f;
-          const float dl = r < 4 ? d0[r] : d1[r - 4];
-          float x = __builtin_fmaf(sacc[qh][base + r], sl2, -lse2);
-          if constexpr (MASK) x = r >= need ? x : -INFINITY;
-          pv[u] = __builtin_amdgcn_exp2f(x);
-          dsv[u] = pv[u] * (pacc[qh][base + r] - dl);
-        }
-        pf[ks][w2] = pack_bf16x2(pv[0], pv[1]);
-        df[ks][w2] = pack_bf16x2(dsv[0], dsv[1]);
+      if (w2 == 0) {  // registers base..base+3 and base+4..base+7: 4 consecutive queries each
+        lv[0] = *(const __attribute__((address_space(3))) f32x4_t*)(uintptr_t)(tl + 4 * tix);
+        lv[1] = *(const __attribute__((address_space(3))) f32x4_t*)(uintptr_t)(tl + 4 * (tix + 4));
+        dv4[0] = *(const __attribute__((address_space(3))) f32x4_t*)(uintptr_t)(td + 4 * tix);
+        dv4[1] = *(const __attribute__((address_space(3))) f32x4_t*)(uintptr_t)(td + 4 * (tix + 4));
       }
-    }
-    if constexpr (DS) store_ds(bh, q0, [&](int ks) __attribute__((always_inline)) { return df[ks]; });
-    // dV += P^T dO (first operand dO^T), dK += dS^T Q (first operand Q^T)
-    static_for<4>([&](auto ks_c) __attribute__((always_inline)) {
+      const int need = key - (q0 + tix);  // register base + r is visible iff its offset >= need
+      float pv[2], dsv[2];
+#pragma unroll
+      for (int u = 0; u < 2; ++u) {
+        const int r = 2 * w2 + u;  // 0..7 within the run: offsets 0..3, then 4..7
+        const float lse2 = lv[r >> 2][r & 3] * 1.4426950408889634f;
+        float x = __builtin_fmaf(sacc[qh][base + r], sl2, -lse2);
+        if constexpr (MASK) x = r >= need ? x : -INFINITY;
+        pv[u] = __builtin_amdgcn_exp2f(x);
+        dsv[u] = pv[u] * (pacc[qh][base + r] - dv4[r >> 2][r & 3]);
+      }
+      pf[ks][w2] = pack_bf16x2(pv[0], pv[1]);
+      df[ks][w2] = pack_bf16x2(dsv[0], dsv[1]);
+    };
+    // S^T = K Q^T and dP^T = V dO^T of half qh at k-step s
+    auto sdp = [&](const int qh, const int s) __attribute__((always_inline)) {
+      const u32x4_t qr = rd.row(tq, qh, s, h32);
+      const u32x4_t gr = rd.row(tg, qh, s, h32);
+      sacc[qh] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, qr),
+                                                        __builtin_bit_cast(bf16x8_t, kf[s]), sacc[qh], 0, 0, 0);
+      pacc[qh] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, gr),
+                                                        __builtin_bit_cast(bf16x8_t, vf[s]), pacc[qh], 0, 0, 0);
+    };
+    // dV += P^T dO (first operand dO^T), dK += dS^T Q (first operand Q^T) at k-step KS,
+    // with softmax steps of k-step KS + 2 between the MFMAs when KS < 2
+    auto dvdk = [&](auto ks_c) __attribute__((always_inline)) {
       constexpr int KS = decltype(ks_c)::value;
       u32x4_t gt[NC], qt[NC];
 #pragma unroll
@@ -777,13 +777,27 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1)))
 #pragma unroll
       for (int c = 0; c < NC; ++c) {
         dv[c] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, gt[c]),
-                                                        __builtin_bit_cast(bf16x8_t, pf[KS]), dv[c],
-                                                        0, 0, 0);
+                                                        __builtin_bit_cast(bf16x8_t, pf[KS]), dv[c], 0, 0, 0);
         dk[c] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, qt[c]),
-                                                        __builtin_bit_cast(bf16x8_t, df[KS]), dk[c],
-                                                        0, 0, 0);
+                                                        __builtin_bit_cast(bf16x8_t, df[KS]), dk[c], 0, 0, 0);
+        if constexpr (KS < 2) soft(KS + 2, c);
       }
-    });
+    };
+    static_assert(NS == 8 && NC == 4, "the interleave below assumes d = 128");
+    auto dsrun = [&](int ks) __attribute__((always_inline)) { return df[ks]; };
+#pragma unroll
+    for (int s = 0; s < NS; ++s) sdp(0, s);
+#pragma unroll
+    for (int s = 0; s < NS; ++s) {
+      sdp(1, s);
+      soft(s >> 2, s & 3);  // k-steps 0 and 1: half 0
+    }
+    if constexpr (DS) store_ds(bh, q0, 0, dsrun);
+    dvdk(ic<0>{});
+    dvdk(ic<1>{});
+    if constexpr (DS) store_ds(bh, q0, 1, dsrun);
+    dvdk(ic<2>{});
+    dvdk(ic<3>{});
   };
 
   // Per head: the first n_diag tiles may hold queries before some of this wave's keys
@@ -805,8 +819,11 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1)))
       const uint32_t st = ring_step(it);
       const int q0 = uniform((qt0 + t) * QT);
       if (q0 + QT - 1 < kw) {  // every query of the tile precedes every key
-        if constexpr (DS)  // zeros: the dQ GEMM reads whole K tiles around the diagonal
-          store_ds(bh, q0, [](int) __attribute__((always_inline)) { return u32x4_t{0u, 0u, 0u, 0u}; });
+        if constexpr (DS) {  // zeros: the dQ GEMM reads whole K tiles around the diagonal
+          auto zero = [](int) __attribute__((always_inline)) { return u32x4_t{0u, 0u, 0u, 0u}; };
+          store_ds(bh, q0, 0, zero);
+          store_ds(bh, q0, 1, zero);
+        }
         continue;
       }
       block(q0, bh, st, std::true_type{});
