@@ -430,7 +430,66 @@ def norm_main(args):
                      "unit": "GB/s", "frac": round(achieved / PEAK_HBM_GBS, 4), "traffic": None,
                      "kernel": dom, "avg_launch_ms": round(dom_ms, 4)},
     }
+    if not args.no_cpu:
+        out["cpu_baseline"] = cpu_norm_baseline()
     print(json.dumps(out))
+
+
+def cpu_norm_baseline(rows: int = 8192, min_seconds: float = 2.0) -> dict:
+    """The oracle's RMSNorm forward (residual add, bf16-rounded sum) and backward (residual
+    gradient, weight gradient) over the same 8192 x 2048 rows (RMSNorm.cpp:40-180, float64
+    arithmetic on fp32 copies of the inputs), repeated for at least min_seconds."""
+    import numpy as np
+
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import oracle
+
+    dims = 2048
+    rng = np.random.default_rng(3)
+    h = rng.standard_normal((rows, dims), dtype=np.float32)
+    a = rng.standard_normal((rows, dims), dtype=np.float32)
+    dy = rng.standard_normal((rows, dims), dtype=np.float32) * 1e-2
+    rg = rng.standard_normal((rows, dims), dtype=np.float32) * 1e-2
+    w = (1.0 + 0.1 * rng.standard_normal(dims)).astype(np.float32)
+    reps, t0 = 0, time.perf_counter()
+    while True:
+        _, _, h2 = oracle.rmsnorm_fwd(h, w, 1e-5, residual=a, round_bf16=True)
+        oracle.rmsnorm_bwd(dy, h2, w, 1e-5, residual_grad=rg, dw0=np.zeros(dims))
+        reps += 1
+        dt = time.perf_counter() - t0
+        if dt >= min_seconds:
+            break
+    nbytes = 8 * rows * dims * 2 * reps   # the GPU step's algorithmic bf16 bytes
+    return {"value": round(nbytes / dt / 1e9, 3), "unit": "GB/s", "cores": oracle.num_threads(),
+            "kind": "port",
+            "sample": f"the whole workload ({rows} x {dims}), {reps} passes in {dt:.2f} s; bytes "
+                      f"counted as the GPU step's bf16 bytes"}
+
+
+def cpu_convert_baseline(jobs, shapes, min_seconds: float = 2.0) -> dict:
+    """The oracle's conversion (Checkpoint.cpp:28-33, 407-535: row range, bf16 -> fp32, [out, in]
+    -> [in, out]) of the same eight matrices from host copies, repeated for at least
+    min_seconds."""
+    import numpy as np
+
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import oracle
+
+    rng = np.random.default_rng(8)
+    src = {n: rng.integers(0x3000, 0x4000, size=shape, dtype=np.uint16) for n, shape in shapes.items()}
+    reps, t0 = 0, time.perf_counter()
+    while True:
+        for n, r0, rows, _ in jobs:
+            oracle.engine_matrix(src[n], r0, rows)
+        reps += 1
+        dt = time.perf_counter() - t0
+        if dt >= min_seconds:
+            break
+    nbytes = sum(2 * 2 * rows * shapes[n][1] for n, _, rows, _ in jobs) * reps
+    return {"value": round(nbytes / dt / 1e9, 3), "unit": "GB/s", "cores": 1, "kind": "port",
+            "sample": f"the eight matrices, {reps} passes in {dt:.2f} s (numpy, one thread; writes "
+                      f"fp32 as the reference loader does, bytes counted as the GPU's bf16 "
+                      f"read + write)"}
 
 
 def convert_main(args):
@@ -484,7 +543,7 @@ def convert_main(args):
     out_bytes = 2 * 2 * V * H
     value = nbytes * args.steps / elapsed / 1e9
     achieved = out_bytes / (ms_out / 1e3) / 1e9
-    print(json.dumps({
+    out = {
         "metric": "checkpoint conversion GB/s (Python/MLX layout -> engine layout, one "
                   "configuration-3 layer + LM head, bf16)",
         "value": round(value, 1), "unit": "GB/s", "n_gpus": 1, "steps": args.steps,
@@ -498,7 +557,10 @@ def convert_main(args):
                      "unit": "GB/s", "frac": round(achieved / PEAK_HBM_GBS, 4), "traffic": None,
                      "kernel": "convert_transpose_kernel (output [32000, 2048] -> [2048, 32000])",
                      "avg_launch_ms": round(ms_out, 4)},
-    }))
+    }
+    if not args.no_cpu:
+        out["cpu_baseline"] = cpu_convert_baseline(jobs, {n: tuple(t.shape) for n, t in src.items()})
+    print(json.dumps(out))
 
 
 def main():

@@ -204,11 +204,38 @@ __device__ __forceinline__ void unpack_act(nu32x4_t q, float* v) {
   }
 }
 
+// Sums of v and u over the 64 lanes of a wave, both chains interleaved.  Each step
+// adds a lane's value to its partner's under an involution of the lane index (DPP
+// swaps within a quad, the half-row and row mirrors, then lanes 16 and 32 apart), so
+// partners add the same two values and every lane ends with the same bits.
+template <int CTRL>
+__device__ __forceinline__ float dpp_partner(float v) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL,
+                                                               0xF, 0xF, false));
+}
+__device__ __forceinline__ void nwave_sum2(float& v, float& u) {
+  v += dpp_partner<0xB1>(v);   // quad_perm [1,0,3,2]: lane ^ 1
+  u += dpp_partner<0xB1>(u);
+  v += dpp_partner<0x4E>(v);   // quad_perm [2,3,0,1]: lane ^ 2
+  u += dpp_partner<0x4E>(u);
+  v += dpp_partner<0x141>(v);  // row_half_mirror: lane 7 - i within 8
+  u += dpp_partner<0x141>(u);
+  v += dpp_partner<0x140>(v);  // row_mirror: lane 15 - i within 16
+  u += dpp_partner<0x140>(u);
+  v += __shfl_xor(v, 16, 64);
+  u += __shfl_xor(u, 16, 64);
+  v += __shfl_xor(v, 32, 64);
+  u += __shfl_xor(u, 32, 64);
+}
+
 // Each wave walks its rows with the next row's x, dy and residual gradient loaded
-// (packed, 16-byte vectors) while the current row is computed; the current row is
-// unpacked again in each pass from a copy the compiler cannot see through, so the
-// unpacked values are not kept live across passes, and the weight is re-read (L1).
-template <bool BF16, bool W_BF16, int NV>
+// (packed, 16-byte vectors) while the current row is computed, in two passes: (1)
+// sum x^2 and dy*w*x, both reduced together; (2) dx = rinv*(dy*w) - rinv^3*t/dims*x
+// + rg and the weight-gradient term dy*x*rinv.  The second pass unpacks the row again
+// from a copy the compiler cannot see through, so the unpacked values of the first
+// are not kept live.  The weight is unpacked once per kernel.  FULL: every lane owns
+// NV whole vectors of each row (no bounds tests).
+template <bool BF16, bool W_BF16, int NV, bool FULL>
 __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(NV <= 4 ? 2 : 1)))
     norm_bwd_vec(NormParams p) {
   constexpr int EV = BF16 ? 8 : 4, ES = BF16 ? 2 : 4;
@@ -216,11 +243,14 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(NV <= 
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int nvec = p.dims / EV;
   const bool has_r = p.r != nullptr;
-  float acc[NV][EV];
+  auto live = [&](int i) __attribute__((always_inline)) { return FULL || lane + 64 * i < nvec; };
+  float acc[NV][EV], wr[NV][EV];
 #pragma unroll
-  for (int i = 0; i < NV; ++i)
+  for (int i = 0; i < NV; ++i) {
 #pragma unroll
-    for (int e = 0; e < EV; ++e) acc[i][e] = 0.0f;
+    for (int e = 0; e < EV; ++e) acc[i][e] = wr[i][e] = 0.0f;
+    if (live(i)) load_w<W_BF16, EV>(p.w, (lane + 64 * i) * EV, wr[i]);
+  }
   const int stride = gridDim.x * 4;
   auto load_row = [&](int row, nu32x4_t* xq, nu32x4_t* gq, nu32x4_t* rq) __attribute__((always_inline)) {
     const int64_t off = (int64_t)row * p.ld * ES;
@@ -228,7 +258,7 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(NV <= 
     for (int i = 0; i < NV; ++i) {
       const int j = lane + 64 * i;
       xq[i] = gq[i] = rq[i] = nu32x4_t{0u, 0u, 0u, 0u};
-      if (j < nvec) {
+      if (live(i)) {
         xq[i] = *(const nu32x4_t*)((const char*)p.x + off + (int64_t)j * 16);
         gq[i] = *(const nu32x4_t*)((const char*)p.dy + off + (int64_t)j * 16);
         if (has_r) rq[i] = *(const nu32x4_t*)((const char*)p.r + off + (int64_t)j * 16);
@@ -241,52 +271,38 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(NV <= 
   for (; row < p.rows; row += stride) {
     nu32x4_t xn[NV], gn[NV], rn[NV];
     if (row + stride < p.rows) load_row(row + stride, xn, gn, rn);
-    float ss = 0.0f;
+    float ss = 0.0f, t = 0.0f;  // sum x^2, sum dy*w*x (zeros past the row add nothing)
 #pragma unroll
     for (int i = 0; i < NV; ++i) {
-      float xv[EV];
+      float xv[EV], gv[EV];
       unpack_act<BF16>(xq[i], xv);
+      unpack_act<BF16>(gq[i], gv);
 #pragma unroll
-      for (int e = 0; e < EV; ++e) ss = __builtin_fmaf(xv[e], xv[e], ss);
-    }
-    ss = nwave_sum(ss);
-    const float rms = sqrtf(ss / (float)p.dims + p.eps);
-    const float rinv = 1.0f / rms;
-    float s2 = 0.0f;
-#pragma unroll
-    for (int i = 0; i < NV; ++i) {
-      const int j = lane + 64 * i;
-      if (j < nvec) {
-        nu32x4_t a = xq[i], b = gq[i];
-        __asm__ volatile("" : "+v"(a), "+v"(b));
-        float xv[EV], gv[EV], wv[EV];
-        unpack_act<BF16>(a, xv);
-        unpack_act<BF16>(b, gv);
-        load_w<W_BF16, EV>(p.w, j * EV, wv);
-#pragma unroll
-        for (int e = 0; e < EV; ++e) s2 = __builtin_fmaf(gv[e] * wv[e], xv[e] * rinv, s2);
+      for (int e = 0; e < EV; ++e) {
+        ss = __builtin_fmaf(xv[e], xv[e], ss);
+        t = __builtin_fmaf(gv[e] * wr[i][e], xv[e], t);
       }
     }
-    s2 = nwave_sum(s2) / (float)p.dims;
+    nwave_sum2(ss, t);
+    const float rms = sqrtf(ss / (float)p.dims + p.eps);
+    const float rinv = 1.0f / rms;
+    const float cx = rinv * rinv * rinv * (t / (float)p.dims);  // rinv * (sum dy*w*xhat) / dims * rinv
     char* dxr = (char*)p.dx + (int64_t)row * p.ld * ES;
 #pragma unroll
     for (int i = 0; i < NV; ++i) {
-      const int j = lane + 64 * i;
-      if (j < nvec) {
+      if (live(i)) {
         nu32x4_t a = xq[i], b = gq[i];
         __asm__ volatile("" : "+v"(a), "+v"(b));
-        float xv[EV], gv[EV], wv[EV], o[EV], rv[EV];
+        float xv[EV], gv[EV], o[EV], rv[EV];
         unpack_act<BF16>(a, xv);
         unpack_act<BF16>(b, gv);
         unpack_act<BF16>(rq[i], rv);  // zeros without a residual gradient
-        load_w<W_BF16, EV>(p.w, j * EV, wv);
 #pragma unroll
         for (int e = 0; e < EV; ++e) {
-          const float xhat = xv[e] * rinv;
-          o[e] = rinv * (gv[e] * wv[e] - xhat * s2) + rv[e];
-          acc[i][e] = __builtin_fmaf(gv[e], xhat, acc[i][e]);
+          o[e] = __builtin_fmaf(rinv, gv[e] * wr[i][e], __builtin_fmaf(-cx, xv[e], rv[e]));
+          acc[i][e] = __builtin_fmaf(gv[e] * rinv, xv[e], acc[i][e]);
         }
-        store_act<BF16>(dxr, j * EV, o);
+        store_act<BF16>(dxr, (lane + 64 * i) * EV, o);
       }
     }
 #pragma unroll
@@ -302,7 +318,7 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(NV <= 
 #pragma unroll
         for (int i = 0; i < NV; ++i) {
           const int j = lane + 64 * i;
-          if (j < nvec) {
+          if (live(i)) {
 #pragma unroll
             for (int e = 0; e < EV; ++e) {
               const int c = j * EV + e;
@@ -415,11 +431,14 @@ hipError_t bwd_one(const NormParams& p, bool vector_path, hipStream_t st) {
   } else {
     const dim3 grid((unsigned)G), block(256);
     const size_t lds = p.dw ? (size_t)p.dims * sizeof(float) : 0;
-    switch (vec_per_lane(p.dims, BF16)) {
-      case 1: hipLaunchKernelGGL((norm_bwd_vec<BF16, W_BF16, 1>), grid, block, lds, st, p); break;
-      case 2: hipLaunchKernelGGL((norm_bwd_vec<BF16, W_BF16, 2>), grid, block, lds, st, p); break;
-      case 4: hipLaunchKernelGGL((norm_bwd_vec<BF16, W_BF16, 4>), grid, block, lds, st, p); break;
-      default: hipLaunchKernelGGL((norm_bwd_vec<BF16, W_BF16, 8>), grid, block, lds, st, p); break;
+    const int nv = vec_per_lane(p.dims, BF16);
+    const bool full = p.dims == nv * 64 * (BF16 ? 8 : 4);  // every lane owns nv whole vectors
+    auto go = [&](auto kern) { hipLaunchKernelGGL(kern, grid, block, lds, st, p); };
+    switch (nv) {
+      case 1: full ? go(norm_bwd_vec<BF16, W_BF16, 1, true>) : go(norm_bwd_vec<BF16, W_BF16, 1, false>); break;
+      case 2: full ? go(norm_bwd_vec<BF16, W_BF16, 2, true>) : go(norm_bwd_vec<BF16, W_BF16, 2, false>); break;
+      case 4: full ? go(norm_bwd_vec<BF16, W_BF16, 4, true>) : go(norm_bwd_vec<BF16, W_BF16, 4, false>); break;
+      default: full ? go(norm_bwd_vec<BF16, W_BF16, 8, true>) : go(norm_bwd_vec<BF16, W_BF16, 8, false>); break;
     }
   }
   return hipGetLastError();

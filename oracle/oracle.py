@@ -192,6 +192,18 @@ def rmsnorm_bwd(dy, x, w, eps=1e-5, residual_grad=None, dw0=None):
     return dx, dw
 
 
+def bf16_bits_to_f32(bits):
+    """Checkpoint.cpp:28-33 (bf16_to_f32): the 16 bits as the high half of an fp32."""
+    return (np.asarray(bits, dtype=np.uint16).astype(np.uint32) << 16).view(np.float32)
+
+
+def engine_matrix(bits, row0, rows):
+    """Rows row0 .. row0+rows-1 of a bf16 [out, in] file matrix (as uint16 bits) in the
+    engine's [in, out] float32 layout (Checkpoint.cpp:407-535: load_python_fused_tensor's
+    row range, bf16_to_f32, transpose_matrix)."""
+    return bf16_bits_to_f32(bits[row0:row0 + rows]).T.copy()
+
+
 def checkpoint_weights(path, cfg):
     """Checkpoint.cpp:28-83, 390-570 in numpy: the model tensors of a safetensors file (a
     Python/MLX file holding "tok_embeddings.weight", or an engine file) as float32 arrays in
@@ -212,7 +224,7 @@ def checkpoint_weights(path, cfg):
         b, e = ent["data_offsets"]
         byts = raw[payload + b: payload + e]
         if ent["dtype"] == "BF16":
-            v = (byts.view(np.uint16).astype(np.uint32) << 16).view(np.float32)
+            v = bf16_bits_to_f32(byts.view(np.uint16))
         elif ent["dtype"] == "F16":
             v = byts.view(np.float16).astype(np.float32)
         else:
