@@ -468,8 +468,8 @@ def cpu_norm_baseline(rows: int = 8192, min_seconds: float = 2.0) -> dict:
 
 def cpu_convert_baseline(jobs, shapes, min_seconds: float = 2.0) -> dict:
     """The oracle's conversion (Checkpoint.cpp:28-33, 407-535: row range, bf16 -> fp32, [out, in]
-    -> [in, out]) of the same eight matrices from host copies, repeated for at least
-    min_seconds."""
+    -> [in, out] where the engine transposes) of the same nine matrices from host copies,
+    repeated for at least min_seconds."""
     import numpy as np
 
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
@@ -479,15 +479,18 @@ def cpu_convert_baseline(jobs, shapes, min_seconds: float = 2.0) -> dict:
     src = {n: rng.integers(0x3000, 0x4000, size=shape, dtype=np.uint16) for n, shape in shapes.items()}
     reps, t0 = 0, time.perf_counter()
     while True:
-        for n, r0, rows, _ in jobs:
-            oracle.engine_matrix(src[n], r0, rows)
+        for n, r0, rows, _, tr in jobs:
+            if tr:
+                oracle.engine_matrix(src[n], r0, rows)
+            else:
+                oracle.bf16_bits_to_f32(src[n][r0:r0 + rows])
         reps += 1
         dt = time.perf_counter() - t0
         if dt >= min_seconds:
             break
-    nbytes = sum(2 * 2 * rows * shapes[n][1] for n, _, rows, _ in jobs) * reps
+    nbytes = sum(2 * 2 * rows * shapes[n][1] for n, _, rows, _, _ in jobs) * reps
     return {"value": round(nbytes / dt / 1e9, 3), "unit": "GB/s", "cores": 1, "kind": "port",
-            "sample": f"the eight matrices, {reps} passes in {dt:.2f} s (numpy, one thread; writes "
+            "sample": f"the nine matrices, {reps} passes in {dt:.2f} s (numpy, one thread; writes "
                       f"fp32 as the reference loader does, bytes counted as the GPU's bf16 "
                       f"read + write)"}
 
@@ -496,8 +499,8 @@ def convert_main(args):
     """Checkpoint conversion on the GPU (Checkpoint.cpp:407-570 restated as mi_convert_matrix):
     one configuration-3 layer and the LM head from the Python/MLX layout ([out, in], fused
     wqkv [3072, 2048] and w12 [11264, 2048], wo [2048, 2048], w3 [2048, 5632], output
-    [32000, 2048], bf16) into the engine's [in, out] bf16 matrices. HBM-bound: value =
-    bytes read + written per step / step time."""
+    [32000, 2048], bf16) into the engine's [in, out] bf16 matrices, and the token embeddings
+    [32000, 2048] copied. HBM-bound: value = bytes read + written per step / step time."""
     import torch
 
     import mi_gemm as mi
@@ -510,15 +513,17 @@ def convert_main(args):
     src = {n: torch.randn(s, generator=g, device=dev).to(torch.bfloat16) for n, s in
            (("wqkv", (q + 2 * kv, H)), ("w12", (2 * I, H)), ("wo", (H, q)), ("w3", (H, I)),
             ("output", (V, H)))}
-    # (source, row0, rows, destination shape): every engine matrix is a transposed row range
-    jobs = [("wqkv", 0, q, (H, q)), ("wqkv", q, kv, (H, kv)), ("wqkv", q + kv, kv, (H, kv)),
-            ("w12", 0, I, (H, I)), ("w12", I, I, (H, I)), ("wo", 0, H, (q, H)), ("w3", 0, H, (I, H)),
-            ("output", 0, V, (H, V))]
-    dst = [torch.empty(shape, dtype=torch.bfloat16, device=dev) for _, _, _, shape in jobs]
+    src["tok_embeddings"] = torch.randn((V, H), generator=g, device=dev).to(torch.bfloat16)
+    # (source, row0, rows, destination shape, transpose): the engine's projection matrices
+    # are transposed row ranges, the token embeddings a plain copy
+    jobs = [("wqkv", 0, q, (H, q), 1), ("wqkv", q, kv, (H, kv), 1), ("wqkv", q + kv, kv, (H, kv), 1),
+            ("w12", 0, I, (H, I), 1), ("w12", I, I, (H, I), 1), ("wo", 0, H, (q, H), 1),
+            ("w3", 0, H, (I, H), 1), ("output", 0, V, (H, V), 1), ("tok_embeddings", 0, V, (V, H), 0)]
+    dst = [torch.empty(shape, dtype=torch.bfloat16, device=dev) for _, _, _, shape, _ in jobs]
     lib = mi.load_library()
     stream = mi._stream()
-    calls = [(stream, mi._ptr(src[n]), mi.MI_BF16, src[n].shape[1], r0, rows, src[n].shape[1], 1,
-              mi._ptr(d), mi.MI_BF16, rows) for (n, r0, rows, _), d in zip(jobs, dst)]
+    calls = [(stream, mi._ptr(src[n]), mi.MI_BF16, src[n].shape[1], r0, rows, src[n].shape[1], tr,
+              mi._ptr(d), mi.MI_BF16, shape[1]) for (n, r0, rows, shape, tr), d in zip(jobs, dst)]
 
     def step():
         for c in calls:
@@ -529,17 +534,23 @@ def convert_main(args):
     torch.cuda.synchronize()
     ev = [torch.cuda.Event(enable_timing=True) for _ in range(2)]
     ev[0].record()
-    for c in calls[-1:] * 20:  # the LM-head matrix alone, back to back
+    for c in calls[7:8] * 20:  # the LM-head matrix alone, back to back
         lib.mi_convert_matrix(*c)
     ev[1].record()
     torch.cuda.synchronize()
     ms_out = ev[0].elapsed_time(ev[1]) / 20
+    ev[0].record()
+    for c in calls[8:9] * 20:  # the embedding copy alone
+        lib.mi_convert_matrix(*c)
+    ev[1].record()
+    torch.cuda.synchronize()
+    ms_copy = ev[0].elapsed_time(ev[1]) / 20
     t0 = time.perf_counter()
     for _ in range(args.steps):
         step()
     torch.cuda.synchronize()
     elapsed = time.perf_counter() - t0
-    nbytes = sum(2 * 2 * rows * src[n].shape[1] for n, _, rows, _ in jobs)   # bf16 read + write
+    nbytes = sum(2 * 2 * rows * src[n].shape[1] for n, _, rows, _, _ in jobs)   # bf16 read + write
     out_bytes = 2 * 2 * V * H
     value = nbytes * args.steps / elapsed / 1e9
     achieved = out_bytes / (ms_out / 1e3) / 1e9
@@ -551,8 +562,10 @@ def convert_main(args):
         "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
         "data": "synthetic (torch.randn on device)",
         "config": {"workload": "8 transposed row-range conversions: wqkv -> Wq, Wk, Wv; w12 -> "
-                               "w_gate, w_up; wo; w3; output [32000, 2048]",
-                   "bytes_per_step": nbytes},
+                               "w_gate, w_up; wo; w3; output [32000, 2048]; and the token "
+                               "embeddings [32000, 2048] copied",
+                   "bytes_per_step": nbytes,
+                   "copy_GBs": round(out_bytes / (ms_copy / 1e3) / 1e9, 1)},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": PEAK_HBM_GBS,
                      "unit": "GB/s", "frac": round(achieved / PEAK_HBM_GBS, 4), "traffic": None,
                      "kernel": "convert_transpose_kernel (output [32000, 2048] -> [2048, 32000])",

@@ -122,6 +122,20 @@ __global__ void __launch_bounds__(256) convert_transpose_kernel(ConvParams p, in
   }
 }
 
+// Row-preserving copy, 4 elements (one 8- or 16-byte access each way) per thread: x
+// covers the columns, y the rows (strided past 65535).  Needs the alignment of the
+// transpose's vector path.
+template <int SRC, int DST>
+__global__ void __launch_bounds__(256) convert_copy_vec_kernel(ConvParams p) {
+  const int64_t c = ((int64_t)blockIdx.x * 256 + threadIdx.x) * 4;
+  if (c >= p.cols) return;
+  for (int64_t r = blockIdx.y; r < p.rows; r += gridDim.y) {
+    float v[4];
+    ld4<SRC>(p.src, (p.row0 + r) * p.src_ld + c, v);
+    st4<DST>(p.dst, r * p.dst_ld + c, v);
+  }
+}
+
 __global__ void __launch_bounds__(256) convert_copy_kernel(ConvParams p) {
   const int64_t n = p.rows * p.cols;
   for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (int64_t)gridDim.x * 256) {
@@ -134,11 +148,25 @@ __global__ void __launch_bounds__(256) convert_copy_kernel(ConvParams p) {
 }  // namespace
 
 hipError_t launch_convert(const ConvParams& p, bool transpose, int cus, hipStream_t stream) {
+  const int ses = p.src_dtype == 0 ? 4 : 2, des = p.dst_dtype == 0 ? 4 : 2;
+  const int vec = p.src_ld % 4 == 0 && p.dst_ld % 4 == 0 && (p.row0 * p.src_ld) % 4 == 0 &&
+                  (uintptr_t)p.src % (4 * ses) == 0 && (uintptr_t)p.dst % (4 * des) == 0;
+  if (!transpose && vec && p.cols % 4 == 0) {
+    const dim3 grid((unsigned)((p.cols + 1023) / 1024), (unsigned)std::min<int64_t>(p.rows, 65535));
+    auto go = [&](auto kern) { hipLaunchKernelGGL(kern, grid, dim3(256), 0, stream, p); };
+    if (p.dst_dtype == 1) {
+      if (p.src_dtype == 1) go(convert_copy_vec_kernel<1, 1>);
+      else if (p.src_dtype == 2) go(convert_copy_vec_kernel<2, 1>);
+      else go(convert_copy_vec_kernel<0, 1>);
+    } else {
+      if (p.src_dtype == 1) go(convert_copy_vec_kernel<1, 0>);
+      else if (p.src_dtype == 2) go(convert_copy_vec_kernel<2, 0>);
+      else go(convert_copy_vec_kernel<0, 0>);
+    }
+    return hipGetLastError();
+  }
   if (transpose) {
     const dim3 grid((unsigned)((p.cols + CT - 1) / CT), (unsigned)((p.rows + CT - 1) / CT));
-    const int ses = p.src_dtype == 0 ? 4 : 2, des = p.dst_dtype == 0 ? 4 : 2;
-    const int vec = p.src_ld % 4 == 0 && p.dst_ld % 4 == 0 && (p.row0 * p.src_ld) % 4 == 0 &&
-                    (uintptr_t)p.src % (4 * ses) == 0 && (uintptr_t)p.dst % (4 * des) == 0;
     auto go = [&](auto kern) { hipLaunchKernelGGL(kern, grid, dim3(256), 0, stream, p, vec); };
     if (p.dst_dtype == 1) {
       if (p.src_dtype == 1) go(convert_transpose_kernel<1, 1>);

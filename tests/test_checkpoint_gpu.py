@@ -33,12 +33,15 @@ def test_load_weights(mi, dev, oracle, tmp_path, fmt, dst):
 
 @pytest.mark.parametrize("src_dt", ["f32", "bf16", "f16"])
 @pytest.mark.parametrize("transpose", [False, True])
-def test_convert_matrix_slices(mi, dev, src_dt, transpose):
+@pytest.mark.parametrize("R,C,row0,rows", [(130, 77, 5, 100),     # element-wise paths
+                                          (130, 96, 4, 100),     # 4-element accesses
+                                          (70000, 8, 0, 70000)])  # more rows than a grid column
+def test_convert_matrix_slices(mi, dev, src_dt, transpose, R, C, row0, rows):
     import torch
 
     tdt = {"f32": torch.float32, "bf16": torch.bfloat16, "f16": torch.float16}[src_dt]
     code = {"f32": mi.MI_F32, "bf16": mi.MI_BF16, "f16": mi.MI_F16}[src_dt]
-    R, C, row0, rows = 130, 77, 5, 100
+    print(f"convert {src_dt} {R}x{C} rows {row0}+{rows} transpose={transpose}", flush=True)
     src = torch.randn((R, C), device=dev).to(tdt)
     for out_dt in (torch.float32, torch.bfloat16):
         dst = torch.full((C, rows) if transpose else (rows, C), 7.0, dtype=out_dt, device=dev)
