@@ -51,6 +51,26 @@ def test_convert_matrix_slices(mi, dev, src_dt, transpose, R, C, row0, rows):
         assert torch.equal(dst, want)
 
 
+@pytest.mark.parametrize("transpose", [False, True])
+def test_convert_matrix_padded_destination(mi, dev, transpose):
+    """A destination leading dimension above its row length (the 4-element copy and
+    transpose paths): the rows land at dst_ld apart and the pad columns keep their values."""
+    import torch
+
+    R, C = 64, 96
+    src = torch.randn((R, C), device=dev).to(torch.bfloat16)
+    drows, dcols = (C, R) if transpose else (R, C)
+    ld = dcols + 8
+    dst = torch.full((drows, ld), 7.0, dtype=torch.bfloat16, device=dev)
+    st = mi.load_library().mi_convert_matrix(mi._stream(), mi._ptr(src), mi.MI_BF16, C, 0, R, C,
+                                             int(transpose), mi._ptr(dst), mi.MI_BF16, ld)
+    torch.cuda.synchronize()
+    assert st == 0
+    want = src.t() if transpose else src
+    assert torch.equal(dst[:, :dcols], want)
+    assert torch.all(dst[:, dcols:] == 7.0)
+
+
 def test_missing_and_mismatched(mi, dev, tmp_path):
     import torch
     from safetensors.torch import save_file
