@@ -218,4 +218,39 @@ struct ModelWeights {
 // on a bad file, a missing tensor or a shape mismatch.
 bool load_weights(const std::string& path, const ModelConfig& cfg, const ModelWeights& w);
 
+// ---- GEMM profiler (gemm_profiler.hpp:18-117) -------------------------------------
+
+// One GEMM call: shape, transposes and its GPU time (HIP events around the call's
+// kernels on the bridge stream; the reference recorded host-side encoding time,
+// MetalBridge.mm:1408-1411), plus the plan that ran.
+struct GemmRecord {
+  size_t M, N, K;
+  bool transA, transB;
+  double elapsed_ms;
+  std::string kernel;
+  size_t batch = 1;
+};
+
+// Same methods as the reference's GemmProfiler singleton.  Recording is off until
+// enable(); it covers every GEMM issued through this bridge or the C ABI.
+class GemmProfiler {
+ public:
+  static GemmProfiler& instance();
+  void enable(bool on = true);
+  void begin_step();                            // drop the step's records
+  std::vector<GemmRecord> records() const;      // waits for the recorded kernels
+  void print_summary(double step_gpu_ms) const; // per (M,N,K,tA,tB): calls, GPU ms, TFLOP/s
+  static const char* op_name(size_t M, size_t N, size_t K, bool tA, bool tB);
+
+ private:
+  GemmProfiler() = default;
+};
+
+// MetalBridge.hpp:141-145 (there extern variables; here functions, because the GPU
+// times are read from events when asked for): GPU time and number of recorded GEMM
+// calls since the last reset_profile_stats().
+double accum_gpu_time_ms();
+size_t count_gpu_calls();
+void reset_profile_stats();
+
 }  // namespace mi_bridge

@@ -285,6 +285,38 @@ int mi_gemm_describe(int transA, int transB, int64_t M, int64_t N, int64_t K, in
  * (MetalBridge.hpp:29-30, MetalBridge.mm:2176-2225). */
 int mi_stream_sync(void* stream);
 
+/*
+ * Per-call GEMM profiler.  Replaces GemmProfiler (gemm_profiler.hpp:18-117, fed
+ * by MetalBridge.mm:1408-1411) and the bridge counters accum_gpu_time_ms /
+ * count_gpu_calls / reset_profile_stats (MetalBridge.hpp:141-145).  While
+ * enabled, every mi_gemm / mi_gemm_batched call records its problem, the plan
+ * it ran and the GPU time between two HIP events placed on its stream around
+ * its launches (the reference timed host-side encoding).  Off by default: the
+ * events cost a few microseconds per call.
+ */
+typedef struct mi_gemm_record {
+  int64_t M, N, K, batch;
+  int32_t transA, transB, dtype_in, dtype_c;
+  int32_t splits;       /* split-K factor of the plan (1 = none)                 */
+  double gpu_ms;        /* GPU time of the call's kernels                          */
+  char kernel[64];      /* the plan, in mi_gemm_describe's words                   */
+} mi_gemm_record;
+
+/* Turn recording on (on != 0) or off; returns the previous state. */
+int mi_profiler_enable(int on);
+/* GemmProfiler::begin_step: drop the records kept so far (their times stay in
+ * the totals). */
+int mi_profiler_begin_step(void);
+/* Number of records since the last begin_step. */
+int64_t mi_profiler_count(void);
+/* Record i (0-based, call order); waits for that call's kernels to finish. */
+int mi_profiler_record(int64_t i, mi_gemm_record* out);
+/* accum_gpu_time_ms / count_gpu_calls: GPU time and number of recorded calls
+ * since the last reset (waits for pending records). */
+int mi_profiler_totals(double* gpu_ms, int64_t* calls);
+/* reset_profile_stats: restart the totals from zero (records are kept). */
+int mi_profiler_reset(void);
+
 #ifdef __cplusplus
 }
 #endif

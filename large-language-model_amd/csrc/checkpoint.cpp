@@ -369,10 +369,11 @@ struct Loader {
     if (!dtype_bytes(t->dtype)) return err = "tensor '" + name + "' has dtype " + t->dtype, false;
     if (!dst) return err = "no destination for '" + name + "'", false;
     const size_t bytes = t->end - t->begin;
+    // The staging buffer is reused (and freed when it grows): the previous
+    // conversion, which reads it on `st`, must be done first.
+    if (hipStreamSynchronize(st) != hipSuccess) return err = "stream error before '" + name + "'", false;
     if (!stage(bytes)) return err = "cannot allocate the staging buffer", false;
-    // The staging buffer is reused: the previous conversion must be done before the copy.
-    if (hipStreamSynchronize(st) != hipSuccess ||
-        hipMemcpy(t_stage, f.data(*t), bytes, hipMemcpyHostToDevice) != hipSuccess)
+    if (hipMemcpy(t_stage, f.data(*t), bytes, hipMemcpyHostToDevice) != hipSuccess)
       return err = "copy of '" + name + "' to the device failed", false;
     const int64_t R = vec ? 1 : (int64_t)rows, C = (int64_t)cols;
     const int s = mi_convert_matrix(st, t_stage, dtype_code(t->dtype), C, vec ? 0 : (int64_t)row0, R, C,

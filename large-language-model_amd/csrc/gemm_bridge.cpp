@@ -4,6 +4,7 @@
 
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <cmath>
 #include <cstdio>
 #include <cstring>
@@ -493,8 +494,10 @@ void matmul(const DeviceTensor& a, const DeviceTensor& b, DeviceTensor& out) {
     size_t M = 1;
     for (size_t i = 0; i + 1 < ra; ++i) M *= a.shape[i];
     const size_t K = a.shape.back(), N = b.shape[1];
+    size_t ws_bytes = 0;
+    void* ws = workspace_for(0, 0, M, N, K, dt, dt, &ws_bytes);
     st = mi_gemm(get_stream(), 0, 0, (int64_t)M, (int64_t)N, (int64_t)K, 1.0f, a.data, (int64_t)K,
-                 b.data, (int64_t)N, dt, 0.0f, out.data, (int64_t)N, dt, nullptr, nullptr, 0);
+                 b.data, (int64_t)N, dt, 0.0f, out.data, (int64_t)N, dt, nullptr, ws, ws_bytes);
   } else {
     size_t nb = 1;
     for (size_t i = 0; i + 2 < ra; ++i) nb *= a.shape[i];
@@ -515,5 +518,95 @@ void matmul(const DeviceTensor& a, const DeviceTensor& b, DeviceTensor& out) {
   if (st != MI_OK) throw std::runtime_error(std::string("mi_gemm: ") + mi_last_error());
   finish("matmul", st);
 }
+
+// ---- GEMM profiler -------------------------------------------------------------
+
+GemmProfiler& GemmProfiler::instance() {
+  static GemmProfiler p;
+  return p;
+}
+
+void GemmProfiler::enable(bool on) { (void)mi_profiler_enable(on ? 1 : 0); }
+
+void GemmProfiler::begin_step() {
+  if (mi_profiler_begin_step() != MI_OK)
+    std::fprintf(stderr, "[mi_bridge] GemmProfiler::begin_step: %s\n", mi_last_error());
+}
+
+std::vector<GemmRecord> GemmProfiler::records() const {
+  std::vector<GemmRecord> out;
+  const int64_t n = mi_profiler_count();
+  for (int64_t i = 0; i < n; ++i) {
+    mi_gemm_record r;
+    if (mi_profiler_record(i, &r) != MI_OK) {
+      std::fprintf(stderr, "[mi_bridge] GemmProfiler::records: %s\n", mi_last_error());
+      break;
+    }
+    out.push_back(GemmRecord{(size_t)r.M, (size_t)r.N, (size_t)r.K, r.transA != 0, r.transB != 0,
+                             r.gpu_ms, r.kernel, (size_t)r.batch});
+  }
+  return out;
+}
+
+const char* GemmProfiler::op_name(size_t M, size_t N, size_t K, bool tA, bool tB) {
+  (void)M; (void)N; (void)K;
+  if (!tA && !tB) return "forward (NN)";
+  if (!tA && tB) return "input gradient (NT)";
+  if (tA && !tB) return "weight gradient (TN)";
+  return "TT";
+}
+
+void GemmProfiler::print_summary(double step_gpu_ms) const {
+  struct Agg {
+    size_t M, N, K;
+    bool tA, tB;
+    std::string kernel;
+    double ms = 0.0, flop = 0.0;
+    int calls = 0;
+  };
+  std::vector<Agg> agg;
+  const std::vector<GemmRecord> recs = records();
+  for (const GemmRecord& r : recs) {
+    Agg* a = nullptr;
+    for (Agg& x : agg)
+      if (x.M == r.M && x.N == r.N && x.K == r.K && x.tA == r.transA && x.tB == r.transB) a = &x;
+    if (!a) {
+      agg.push_back(Agg{r.M, r.N, r.K, r.transA, r.transB, r.kernel});
+      a = &agg.back();
+    }
+    a->ms += r.elapsed_ms;
+    a->flop += 2.0 * r.M * r.N * r.K * r.batch;
+    a->calls += 1;
+  }
+  std::sort(agg.begin(), agg.end(), [](const Agg& x, const Agg& y) { return x.ms > y.ms; });
+  double total = 0.0;
+  for (const Agg& a : agg) total += a.ms;
+  std::printf("GEMM PROFILER  (step GPU time %.3f ms, GEMM GPU time %.3f ms)\n", step_gpu_ms, total);
+  std::printf("%-22s %6s %6s %6s %5s %10s %9s  %s\n", "operation", "M", "N", "K", "calls", "GPU ms",
+              "TFLOP/s", "kernel");
+  for (const Agg& a : agg) {
+    const double tflops = a.ms > 0 ? a.flop / (a.ms * 1e-3) / 1e12 : 0.0;
+    std::printf("%-22s %6zu %6zu %6zu %5d %10.4f %9.1f  %s\n", op_name(a.M, a.N, a.K, a.tA, a.tB),
+                a.M, a.N, a.K, a.calls, a.ms, tflops, a.kernel.c_str());
+  }
+  std::printf("%-22s %6s %6s %6s %5zu %10.4f\n", "TOTAL", "", "", "", recs.size(), total);
+  std::fflush(stdout);
+}
+
+double accum_gpu_time_ms() {
+  double ms = 0.0;
+  int64_t n = 0;
+  (void)mi_profiler_totals(&ms, &n);
+  return ms;
+}
+
+size_t count_gpu_calls() {
+  double ms = 0.0;
+  int64_t n = 0;
+  (void)mi_profiler_totals(&ms, &n);
+  return (size_t)n;
+}
+
+void reset_profile_stats() { (void)mi_profiler_reset(); }
 
 }  // namespace mi_bridge

@@ -16,6 +16,7 @@
 #include <cstring>
 #include <mutex>
 #include <string>
+#include <vector>
 
 #include "../../include/mi_gemm.h"
 #include "mi_attn.hpp"
@@ -156,9 +157,11 @@ int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
 //     second workgroup on a CU hides the first one's C read-modify-write, which
 //     L tiles all do at once (in a hot-cache loop L1 leads, 1143 vs 1038);
 //   * when even S tiles leave half the CUs idle, K is split over S tiles, given
-//     a workspace;
+//     a workspace -- also for S tiles chosen by the fill rule and for the
+//     register-staged loader (unaligned operands);
 //   * fp32 (both configurations 128x128): fewer tiles than 5/8 of the CUs split
 //     K over L tiles, given a workspace.
+// Every split fits the workspace: splits * M * N * batch <= ws_limit_elems.
 Plan make_plan(int dtype_in, int64_t M, int64_t N, int64_t Ktot, int64_t batch, int mode,
                bool allow_split, int64_t ws_limit_elems, int cus, bool fast) {
   auto plan_for = [&](int cfg, int sp) {
@@ -167,38 +170,91 @@ Plan make_plan(int dtype_in, int64_t M, int64_t N, int64_t Ktot, int64_t batch, 
   };
   if (mode == MODE_DUAL) return plan_for(CFG_DUAL, 1);
   if (mode == MODE_PROLOGUE) return plan_for(CFG_PRO, 1);
-  if (!fast) return plan_for(CFG_S, 1);
   const CfgShape L = shape_of(dtype_in, CFG_L), S = shape_of(dtype_in, CFG_S);
   const int64_t tilesL = cdiv(M, L.bm) * cdiv(N, L.bn) * batch;
   const int64_t tilesS = cdiv(M, S.bm) * cdiv(N, S.bn) * batch;
   const double fillL = (double)(M * N * batch) / ((double)tilesL * L.bm * L.bn);
   const double fillS = (double)(M * N * batch) / ((double)tilesS * S.bm * S.bn);
-  if (fillL < 0.75 && fillS > fillL) return plan_for(CFG_S, 1);
-  if (tilesL >= cus) {
-    const double waves = (double)tilesL / cus;
-    const double frac = waves - std::floor(waves);
-    if (frac > 0.0 && frac <= 0.5 && tilesS >= cus) return plan_for(CFG_S, 1);
-    return plan_for(CFG_L, 1);
-  }
   // split K until the units cover the CUs once; each split keeps >= 8 K tiles
+  // of 32 and its partials fit the workspace
   auto split_of = [&](int64_t tiles, int kt) {
     int sp = (int)std::min<int64_t>(cus / std::max<int64_t>(tiles, 1), 8);
     while (sp > 1 && (cdiv(Ktot, kt) < 8 * sp || (int64_t)sp * M * N * batch > ws_limit_elems)) --sp;
     return sp;
   };
   if (dtype_in == MI_BF16) {
+    const bool sparse_L = fillL < 0.75 && fillS > fillL;
+    if (fast && !sparse_L && tilesL >= cus) {
+      const double waves = (double)tilesL / cus;
+      const double frac = waves - std::floor(waves);
+      if (frac > 0.0 && frac <= 0.5 && tilesS >= cus) return plan_for(CFG_S, 1);
+      return plan_for(CFG_L, 1);
+    }
     if (tilesS * 2 >= cus || !allow_split) return plan_for(CFG_S, 1);
     return plan_for(CFG_S, split_of(tilesS, 32));
   }
-  if (tilesL * 8 >= (int64_t)cus * 5) return plan_for(CFG_L, 1);
+  // fp32: L and S are the same 128x128 tile; only S has the element-granular loader
+  const int cfg = fast ? CFG_L : CFG_S;
+  if (tilesL * 8 >= (int64_t)cus * 5) return plan_for(cfg, 1);
   if (allow_split) {
     const int sp = split_of(tilesL, 32);
-    if (sp >= 2) return plan_for(CFG_L, sp);
+    if (sp >= 2) return plan_for(cfg, sp);
   }
-  return plan_for(tilesS > tilesL ? CFG_S : CFG_L, 1);
+  return plan_for(cfg, 1);
 }
 
 bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
+
+// Text of a plan, as mi_gemm_describe and the profiler records show it.
+void describe_plan(char* buf, size_t len, int dtype_in, bool fast, const Plan& pl, int transA,
+                   int transB, int64_t batch) {
+  const CfgShape sh = shape_of(dtype_in, pl.cfg);
+  const char* kind = (dtype_in == MI_BF16 && fast && pl.cfg != CFG_PRO) ? "dlds" : "regstage";
+  std::snprintf(buf, len, "%s %s %dx%d %s%s split%d tiles%lld", kind,
+                dtype_in == MI_BF16 ? "bf16" : "f32", sh.bm, sh.bn, transA ? "T" : "N",
+                transB ? "T" : "N", pl.splits, (long long)pl.tiles_m * pl.tiles_n * batch);
+}
+
+// ---- per-call GEMM profiler ----------------------------------------------------
+// When enabled, run() brackets each problem's launches (the GEMM and its split-K
+// reduction) with two HIP events on the caller's stream and keeps a record of the
+// problem, its plan and the events; the elapsed time is read when a record is
+// asked for.  Events are recycled per device.
+struct ProfEntry {
+  mi_gemm_record rec;
+  hipEvent_t e0, e1;
+  int dev;
+  bool resolved;
+};
+std::mutex g_prof_mu;
+bool g_prof_on = false;
+std::vector<ProfEntry> g_prof;
+std::vector<hipEvent_t> g_prof_free[64];
+double g_prof_total_ms = 0.0;
+int64_t g_prof_calls = 0;
+
+hipEvent_t prof_event(int dev) {
+  if (!g_prof_free[dev].empty()) {
+    hipEvent_t e = g_prof_free[dev].back();
+    g_prof_free[dev].pop_back();
+    return e;
+  }
+  hipEvent_t e = nullptr;
+  return hipEventCreate(&e) == hipSuccess ? e : nullptr;
+}
+
+// Wait for entry i's events and add its time to the totals (once).
+int prof_resolve(ProfEntry& en) {
+  if (en.resolved) return MI_OK;
+  float ms = 0.0f;
+  if (hipEventSynchronize(en.e1) != hipSuccess || hipEventElapsedTime(&ms, en.e0, en.e1) != hipSuccess)
+    return fail(MI_ERR_HIP, "profiler: event wait failed");
+  en.rec.gpu_ms = ms;
+  en.resolved = true;
+  g_prof_total_ms += ms;
+  g_prof_calls += 1;
+  return MI_OK;
+}
 
 // Two row arrays of `bytes` bytes each that share memory without being the same array.
 bool rows_overlap(const void* a, const void* b, int64_t bytes) {
@@ -221,6 +277,7 @@ struct Problem {
   mi_epilogue ep;
   void* ws;
   size_t ws_bytes;
+  bool noalloc = false;  // mi_gemm_noalloc: the library's static scratch is the workspace
 };
 
 int validate(const Problem& P) {
@@ -367,15 +424,51 @@ int run(const Problem& P, hipStream_t stream) {
 
   const int64_t nblocks = (int64_t)plan.tiles_m * plan.tiles_n * plan.splits * b.batch;
   if (nblocks > INT32_MAX) return fail(MI_ERR_SHAPE, "too many tiles");
+
+  // profiler: events around this problem's launches (never on the no-allocation path)
+  std::unique_lock<std::mutex> prof_lock(g_prof_mu, std::defer_lock);
+  ProfEntry pe;
+  bool prof = false;
+  if (!P.noalloc) {
+    prof_lock.lock();
+    if (g_prof_on && hipGetDevice(&pe.dev) == hipSuccess && pe.dev >= 0 && pe.dev < 64) {
+      pe.e0 = prof_event(pe.dev);
+      pe.e1 = prof_event(pe.dev);
+      prof = pe.e0 && pe.e1 && hipEventRecord(pe.e0, stream) == hipSuccess;
+    }
+    if (!prof) prof_lock.unlock();
+  }
+
+  auto drop_events = [&]() {
+    if (prof) {
+      g_prof_free[pe.dev].push_back(pe.e0);
+      g_prof_free[pe.dev].push_back(pe.e1);
+    }
+  };
   hipLaunchKernelGGL(fn, dim3((unsigned)nblocks), dim3(256), 0, stream, p);
   hipError_t e = hipGetLastError();
-  if (e != hipSuccess) return fail(MI_ERR_HIP, "gemm launch: %s", hipGetErrorString(e));
+  if (e != hipSuccess) return drop_events(), fail(MI_ERR_HIP, "gemm launch: %s", hipGetErrorString(e));
   if (plan.splits > 1) {
     const int64_t work = b.batch * P.M * ((P.N + 3) / 4);
     const int64_t grid = std::min<int64_t>(cdiv(work, 256), 8 * (int64_t)current_cus());
     hipLaunchKernelGGL(splitk_reduce_kernel, dim3((unsigned)grid), dim3(256), 0, stream, p);
     e = hipGetLastError();
-    if (e != hipSuccess) return fail(MI_ERR_HIP, "split-K reduce launch: %s", hipGetErrorString(e));
+    if (e != hipSuccess)
+      return drop_events(), fail(MI_ERR_HIP, "split-K reduce launch: %s", hipGetErrorString(e));
+  }
+  if (prof && hipEventRecord(pe.e1, stream) != hipSuccess) {
+    drop_events();
+  } else if (prof) {
+    std::memset(&pe.rec, 0, sizeof(pe.rec));
+    pe.rec.M = P.M; pe.rec.N = P.N; pe.rec.K = P.K; pe.rec.batch = b.batch;
+    pe.rec.transA = P.transA; pe.rec.transB = P.transB;
+    pe.rec.dtype_in = P.dtype_in; pe.rec.dtype_c = P.dtype_c;
+    pe.rec.splits = plan.splits;
+    pe.rec.gpu_ms = -1.0;
+    describe_plan(pe.rec.kernel, sizeof(pe.rec.kernel), P.dtype_in, fast, plan, P.transA, P.transB,
+                  b.batch);
+    pe.resolved = false;
+    g_prof.push_back(pe);
   }
   return MI_OK;
 }
@@ -855,12 +948,64 @@ int mi_gemm_describe(int transA, int transB, int64_t M, int64_t N, int64_t K, in
   const int mode = epi_mode == 1 ? MODE_DUAL : (epi_mode == 2 ? MODE_PROLOGUE : MODE_PLAIN);
   const int64_t ws = (int64_t)(workspace_bytes / sizeof(float));
   const Plan pl = make_plan(dtype_in, M, N, K, batch, mode, ws > 0, ws, cus, true);
-  const CfgShape sh = shape_of(dtype_in, pl.cfg);
-  const char* kind = (dtype_in == MI_BF16 && pl.cfg != CFG_PRO) ? "dlds" : "regstage";
-  std::snprintf(buf, buf_len, "%s %s %dx%d %s%s split%d tiles%d", kind,
-                dtype_in == MI_BF16 ? "bf16" : "f32", sh.bm, sh.bn, transA ? "T" : "N",
-                transB ? "T" : "N", pl.splits, pl.tiles_m * pl.tiles_n * (int)batch);
+  describe_plan(buf, buf_len, dtype_in, true, pl, transA, transB, batch);
   return MI_OK;
+}
+
+int mi_profiler_enable(int on) {
+  std::lock_guard<std::mutex> lk(g_prof_mu);
+  const int was = g_prof_on ? 1 : 0;
+  g_prof_on = on != 0;
+  return was;
+}
+
+int mi_profiler_begin_step(void) {
+  std::lock_guard<std::mutex> lk(g_prof_mu);
+  int st = MI_OK;
+  for (ProfEntry& en : g_prof) {
+    if (prof_resolve(en) != MI_OK) st = MI_ERR_HIP;
+    g_prof_free[en.dev].push_back(en.e0);
+    g_prof_free[en.dev].push_back(en.e1);
+  }
+  g_prof.clear();
+  return st;
+}
+
+int64_t mi_profiler_count(void) {
+  std::lock_guard<std::mutex> lk(g_prof_mu);
+  return (int64_t)g_prof.size();
+}
+
+int mi_profiler_record(int64_t i, mi_gemm_record* out) {
+  if (!out) return fail(MI_ERR_NULL, "out is NULL");
+  std::lock_guard<std::mutex> lk(g_prof_mu);
+  if (i < 0 || i >= (int64_t)g_prof.size())
+    return fail(MI_ERR_SHAPE, "record %lld of %zu", (long long)i, g_prof.size());
+  const int st = prof_resolve(g_prof[(size_t)i]);
+  if (st != MI_OK) return st;
+  *out = g_prof[(size_t)i].rec;
+  return MI_OK;
+}
+
+int mi_profiler_totals(double* gpu_ms, int64_t* calls) {
+  if (!gpu_ms || !calls) return fail(MI_ERR_NULL, "gpu_ms or calls is NULL");
+  std::lock_guard<std::mutex> lk(g_prof_mu);
+  int st = MI_OK;
+  for (ProfEntry& en : g_prof)
+    if (prof_resolve(en) != MI_OK) st = MI_ERR_HIP;
+  *gpu_ms = g_prof_total_ms;
+  *calls = g_prof_calls;
+  return st;
+}
+
+int mi_profiler_reset(void) {
+  std::lock_guard<std::mutex> lk(g_prof_mu);
+  int st = MI_OK;
+  for (ProfEntry& en : g_prof)  // records keep their times; the totals restart from zero
+    if (prof_resolve(en) != MI_OK) st = MI_ERR_HIP;
+  g_prof_total_ms = 0.0;
+  g_prof_calls = 0;
+  return st;
 }
 
 int mi_stream_sync(void* stream) {

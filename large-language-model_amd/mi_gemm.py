@@ -35,7 +35,9 @@ C_SYMBOLS = (
     "mi_gemm_batched", "mi_residual_add", "mi_softmax_causal", "mi_softmax_bwd",
     "mi_gemm_describe", "mi_stream_sync", "mi_flash_attn_fwd", "mi_flash_attn_bwd",
     "mi_cross_entropy", "mi_rmsnorm_fwd", "mi_rmsnorm_bwd", "mi_rmsnorm_bwd_workspace_size",
-    "mi_convert_matrix", "mi_flash_attn_bwd_workspace_size",
+    "mi_convert_matrix", "mi_flash_attn_bwd_workspace_size", "mi_profiler_enable",
+    "mi_profiler_begin_step", "mi_profiler_count", "mi_profiler_record", "mi_profiler_totals",
+    "mi_profiler_reset",
 )
 MI_ATTN_O_BHTD, MI_ATTN_O_BTHD = 0, 1
 
@@ -66,6 +68,17 @@ class MiBatch(ctypes.Structure):
         ("r_outer", ctypes.c_int64), ("r_inner", ctypes.c_int64),
         ("k_segments", ctypes.c_int64), ("seg_a", ctypes.c_int64), ("seg_b", ctypes.c_int64),
         ("causal", ctypes.c_int32), ("mask_value", ctypes.c_float),
+    ]
+
+
+class MiGemmRecord(ctypes.Structure):
+    _fields_ = [
+        ("M", ctypes.c_int64), ("N", ctypes.c_int64), ("K", ctypes.c_int64),
+        ("batch", ctypes.c_int64),
+        ("transA", ctypes.c_int32), ("transB", ctypes.c_int32),
+        ("dtype_in", ctypes.c_int32), ("dtype_c", ctypes.c_int32),
+        ("splits", ctypes.c_int32), ("gpu_ms", ctypes.c_double),
+        ("kernel", ctypes.c_char * 64),
     ]
 
 
@@ -129,6 +142,15 @@ def load_library():
                                  i32, ctypes.c_float, vp, ctypes.c_size_t]
     L.mi_convert_matrix.restype = ctypes.c_int
     L.mi_convert_matrix.argtypes = [vp, vp, i32, i64, i64, i64, i64, i32, vp, i32, i64]
+    L.mi_profiler_enable.restype = ctypes.c_int
+    L.mi_profiler_enable.argtypes = [ctypes.c_int]
+    L.mi_profiler_begin_step.restype = ctypes.c_int
+    L.mi_profiler_count.restype = i64
+    L.mi_profiler_record.restype = ctypes.c_int
+    L.mi_profiler_record.argtypes = [i64, ctypes.POINTER(MiGemmRecord)]
+    L.mi_profiler_totals.restype = ctypes.c_int
+    L.mi_profiler_totals.argtypes = [ctypes.POINTER(ctypes.c_double), ctypes.POINTER(i64)]
+    L.mi_profiler_reset.restype = ctypes.c_int
     _lib = L
     return L
 
@@ -346,6 +368,93 @@ def residual_add(a, b, n=None):
     n = a.numel() if n is None else n
     _finish("mi_residual_add", load_library().mi_residual_add(_stream(), _ptr(a), _ptr(b), n,
                                                               _dt(a)))
+
+
+# ---- GEMM profiler (gemm_profiler.hpp:18-117, MetalBridge.hpp:141-145) ----------
+
+class GemmProfiler:
+    """Per-call GEMM records with GPU times (HIP events around each call's kernels,
+    kept by the library); same methods as the reference's GemmProfiler singleton.
+    Recording is off until enable()."""
+
+    _inst = None
+
+    @classmethod
+    def instance(cls):
+        if cls._inst is None:
+            cls._inst = cls()
+        return cls._inst
+
+    def enable(self, on=True):
+        return bool(load_library().mi_profiler_enable(1 if on else 0))
+
+    def begin_step(self):
+        _check("mi_profiler_begin_step", load_library().mi_profiler_begin_step())
+
+    def records(self):
+        """[{M, N, K, transA, transB, batch, splits, elapsed_ms, kernel}] in call order."""
+        L = load_library()
+        out = []
+        for i in range(L.mi_profiler_count()):
+            r = MiGemmRecord()
+            _check("mi_profiler_record", L.mi_profiler_record(i, ctypes.byref(r)))
+            out.append(dict(M=r.M, N=r.N, K=r.K, transA=bool(r.transA), transB=bool(r.transB),
+                            batch=r.batch, splits=r.splits, elapsed_ms=r.gpu_ms,
+                            kernel=r.kernel.decode()))
+        return out
+
+    @staticmethod
+    def op_name(M, N, K, tA, tB):
+        return {(False, False): "forward (NN)", (False, True): "input gradient (NT)",
+                (True, False): "weight gradient (TN)"}.get((bool(tA), bool(tB)), "TT")
+
+    def summary(self):
+        """Records aggregated per (M, N, K, tA, tB), largest GPU time first."""
+        agg = {}
+        for r in self.records():
+            key = (r["M"], r["N"], r["K"], r["transA"], r["transB"])
+            a = agg.setdefault(key, dict(M=r["M"], N=r["N"], K=r["K"], transA=r["transA"],
+                                         transB=r["transB"], kernel=r["kernel"], calls=0, ms=0.0,
+                                         flop=0.0))
+            a["calls"] += 1
+            a["ms"] += r["elapsed_ms"]
+            a["flop"] += 2.0 * r["M"] * r["N"] * r["K"] * r["batch"]
+        rows = sorted(agg.values(), key=lambda a: -a["ms"])
+        for a in rows:
+            a["op"] = self.op_name(a["M"], a["N"], a["K"], a["transA"], a["transB"])
+            a["tflops"] = a["flop"] / (a["ms"] * 1e-3) / 1e12 if a["ms"] > 0 else 0.0
+        return rows
+
+    def print_summary(self, step_gpu_ms):
+        rows = self.summary()
+        total = sum(a["ms"] for a in rows)
+        print(f"GEMM PROFILER  (step GPU time {step_gpu_ms:.3f} ms, GEMM GPU time {total:.3f} ms)")
+        print(f"{'operation':22s} {'M':>6s} {'N':>6s} {'K':>6s} {'calls':>5s} {'GPU ms':>10s} "
+              f"{'TFLOP/s':>9s}  kernel")
+        for a in rows:
+            print(f"{a['op']:22s} {a['M']:6d} {a['N']:6d} {a['K']:6d} {a['calls']:5d} "
+                  f"{a['ms']:10.4f} {a['tflops']:9.1f}  {a['kernel']}")
+
+
+def _totals():
+    ms, n = ctypes.c_double(), ctypes.c_int64()
+    _check("mi_profiler_totals", load_library().mi_profiler_totals(ctypes.byref(ms), ctypes.byref(n)))
+    return ms.value, n.value
+
+
+def accum_gpu_time_ms():
+    """MetalBridge.hpp:141: GPU time of the recorded GEMM calls since the last reset."""
+    return _totals()[0]
+
+
+def count_gpu_calls():
+    """MetalBridge.hpp:143: number of recorded GEMM calls since the last reset."""
+    return _totals()[1]
+
+
+def reset_profile_stats():
+    """MetalBridge.hpp:145."""
+    _check("mi_profiler_reset", load_library().mi_profiler_reset())
 
 
 # ---- Tensor::matmul mirror ------------------------------------------------------

@@ -490,6 +490,45 @@ int main() {
     for (void* p : bufs) dfree(p);
     std::remove(path.c_str());
   }
+  {  // GB-18: GemmProfiler (gemm_profiler.hpp:18-117) records each bridge GEMM with its
+     // shape, transposes, plan and GPU time; the counters of MetalBridge.hpp:141-145 add up.
+    const size_t M = 512, N = 384, K = 256;
+    std::vector<uint16_t> ha(M * K, bf(1.0f)), hb(K * N, bf(1.0f));
+    uint16_t* A = dev(ha);
+    uint16_t* B = dev(hb);
+    uint16_t* C = dev(std::vector<uint16_t>(M * N, 0));
+    float* D = dev(std::vector<float>(K * N, 0.0f));
+    auto& prof = mi_bridge::GemmProfiler::instance();
+    prof.enable(true);
+    prof.begin_step();
+    mi_bridge::reset_profile_stats();
+    mi_bridge::gemm_bf16(A, B, C, M, N, K);                      // NN, every output = K
+    mi_bridge::gemm_backward_accumulate(A, C, D, K, N, M);       // TN, every output = M*K
+    const auto recs = prof.records();
+    bool ok = recs.size() == 2;
+    if (ok) {
+      ok = recs[0].M == M && recs[0].N == N && recs[0].K == K && !recs[0].transA && !recs[0].transB &&
+           recs[1].M == K && recs[1].N == N && recs[1].K == M && recs[1].transA && !recs[1].transB &&
+           recs[0].elapsed_ms > 0 && recs[1].elapsed_ms > 0 &&
+           recs[0].kernel.find("NN") != std::string::npos && recs[1].kernel.find("TN") != std::string::npos;
+      const double tot = mi_bridge::accum_gpu_time_ms();
+      ok = ok && mi_bridge::count_gpu_calls() == 2 &&
+           std::fabs(tot - recs[0].elapsed_ms - recs[1].elapsed_ms) <= 1e-6 * tot + 1e-9;
+    }
+    const auto d = host(D, K * N);
+    ok = ok && d[0] == (float)(M * K) && d[K * N - 1] == (float)(M * K);
+    prof.print_summary(mi_bridge::accum_gpu_time_ms());
+    prof.begin_step();
+    mi_bridge::reset_profile_stats();
+    ok = ok && prof.records().empty() && mi_bridge::count_gpu_calls() == 0;
+    prof.enable(false);
+    row("GB-18", "GemmProfiler records, counters, print_summary", ok,
+        std::to_string(recs.size()) + " records");
+    dfree(A);
+    dfree(B);
+    dfree(C);
+    dfree(D);
+  }
   std::printf("%d/%d checks passed\n", g_passed, g_total);
   return g_passed == g_total ? 0 : 1;
 }

@@ -147,6 +147,42 @@ def test_workspace_query(mi):
     assert mi.workspace_size(1, 0, 1024, 1024, 65536) > 0
     assert mi.workspace_size(0, 0, 8192, 5632, 2048) == 0
     assert mi.workspace_size(0, 0, 0, 5, 5) == 0
+    # a small output with a long K splits even where 256x256 tiles would sit mostly empty
+    assert "split8" in mi.describe(1, 0, 100, 60, 70000, workspace_bytes=64 << 20)
+
+
+def _planned_split(mi, *args, **kw):
+    text = mi.describe(*args, **kw)
+    m = re.search(r"split(\d+)", text)
+    assert m, text
+    return int(m.group(1))
+
+
+def test_split_plans_fit_the_workspace(mi):
+    """Planner invariant behind the MI_ERR_WORKSPACE guard in run(): a split-K plan
+    never writes more partials than the workspace holds, splits * M * N * batch * 4
+    <= workspace bytes, for every shape, dtype and workspace size; and the size
+    mi_gemm_workspace_size reports is exactly what its plan writes. Planner only:
+    no device, no kernel."""
+    shapes = [(100, 60, 70000, 1), (512, 768, 768, 1), (768, 768, 2048, 1), (2048, 768, 768, 1),
+              (1024, 1024, 65536, 1), (256, 384, 30000, 1), (2048, 2048, 8192, 1),
+              (8192, 32000, 2048, 1), (128, 128, 4096, 3), (64, 4096, 9000, 2), (1, 1, 100000, 1),
+              (300, 20, 513, 1), (2048, 5632, 8192, 1), (96, 96, 1 << 20, 1)]
+    seen_split = 0
+    for dt in (mi.MI_BF16, mi.MI_F32):
+        for M, N, K, batch in shapes:
+            full = mi.workspace_size(1, 0, M, N, K, dt, mi.MI_F32, batch)
+            sp_full = _planned_split(mi, 1, 0, M, N, K, dt, batch, 0, full)
+            assert full == (sp_full * M * N * batch * 4 if sp_full > 1 else 0), (M, N, K, dt)
+            for ws in sorted({0, 4, full // 2, full - 4 if full else 0, full, full * 3,
+                              M * N * batch * 4 * 2 - 4, M * N * batch * 4 * 2, 64 << 20, 1 << 34}):
+                if ws < 0:
+                    continue
+                sp = _planned_split(mi, 1, 0, M, N, K, dt, batch, 0, ws)
+                assert sp == 1 or sp * M * N * batch * 4 <= ws, (M, N, K, dt, batch, ws, sp)
+                assert sp <= max(sp_full, 1), (M, N, K, dt, ws)
+                seen_split = max(seen_split, sp)
+    assert seen_split >= 3
 
 
 def test_cross_entropy_validation(mi):
@@ -211,3 +247,27 @@ def test_rmsnorm_validation(mi):
     assert bwd(DY=0)[0] == 3 and bwd(DX=0)[0] == 3
     st, msg = bwd(DX=131072 + 2)                    # dx overlaps x without being x
     assert st == 5
+
+
+def test_profiler_api_without_device(mi):
+    """The profiler's C functions on the CPU: nothing is recorded (no call reaches a
+    launch without a device), out-of-range records are refused, totals are zero."""
+    import torch
+
+    if torch.cuda.is_available():
+        pytest.skip("a GPU is visible")
+    lib = mi.load_library()
+    prof = mi.GemmProfiler.instance()
+    assert prof is mi.GemmProfiler.instance()
+    was = prof.enable()
+    assert prof.enable() is True                       # previous state: on
+    assert _call(mi)[0] == 8                           # MI_ERR_NO_DEVICE: nothing recorded
+    assert lib.mi_profiler_count() == 0 and prof.records() == []
+    rec = mi.MiGemmRecord()
+    assert lib.mi_profiler_record(0, ctypes.byref(rec)) == 1   # MI_ERR_SHAPE
+    assert lib.mi_profiler_record(0, None) == 3                # MI_ERR_NULL
+    prof.begin_step()
+    mi.reset_profile_stats()
+    assert mi.accum_gpu_time_ms() == 0.0 and mi.count_gpu_calls() == 0
+    assert prof.enable(was) is True
+    assert mi.GemmProfiler.op_name(1, 1, 1, True, False) == "weight gradient (TN)"

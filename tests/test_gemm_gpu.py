@@ -135,9 +135,18 @@ def test_bf16_output_rounds_to_nearest_even(mi, dev, oracle):
 
 def test_config1_fp32_linear_bias(mi, dev, oracle):
     """Benchmark configuration 1: Y = X W^T + b, X [512x768], W [768x768] ~ N(0,0.02), fp32."""
+    import torch
+
     got, ref = _run(mi, dev, oracle, 512, 768, 768, 0, 1, False, seed=1, bias=True)
     check(got, ref, TOL_F32, "config 1")
     assert oracle.l2_rel_err(got, ref) < 1e-4  # test_gpu_kernels.cpp:87-116 metric
+    # with the workspace the bridges pass, the same problem runs as split-K 3
+    ws = torch.empty(mi.workspace_size(0, 1, 512, 768, 768, mi.MI_F32) // 4, dtype=torch.float32,
+                     device=dev)
+    assert _split_of(mi, 0, 1, 512, 768, 768, False, ws) == 3
+    got, ref = _run(mi, dev, oracle, 512, 768, 768, 0, 1, False, seed=1, bias=True, ws=ws)
+    check(got, ref, TOL_F32, "config 1, split-K")
+    assert oracle.l2_rel_err(got, ref) < 1e-4
 
 
 @pytest.mark.parametrize("bf16", [True, False], ids=["bf16", "f32"])
@@ -169,15 +178,53 @@ def test_prologue_silu_gate(mi, dev, oracle, bf16):
         check(got, ref, _tol(bf16), f"prologue {M}x{N}x{K}")
 
 
+def _split_of(mi, tA, tB, M, N, K, bf16, ws):
+    text = mi.describe(tA, tB, M, N, K, mi.MI_BF16 if bf16 else mi.MI_F32,
+                       workspace_bytes=ws.numel() * 4)
+    return int(text.split("split")[1].split()[0])
+
+
 def test_split_k(mi, dev, oracle):
+    """Split-K over the caller's workspace (partials + splitk_reduce_kernel): every case
+    must plan a split above 1. TN dW forms with fp32 beta = 0 / 1 output, NN and NT
+    forms, a register-staged case (leading dimensions that rule out 16-byte loads)
+    and the bias + beta epilogue, which the reduction applies."""
     import torch
 
     ws = torch.empty(64 << 20, dtype=torch.float32, device=dev)
-    for M, N, K, beta in [(1024, 1024, 65536, 0.0), (256, 384, 30000, 1.0), (100, 60, 70000, 0.0)]:
-        need = mi.workspace_size(1, 0, M, N, K)
-        got, ref = _run(mi, dev, oracle, M, N, K, 1, 0, True, seed=51, out_bf16=False, beta=beta,
-                        ws=ws)
-        check(got, ref, TOL_BF16, f"split-K {M}x{N}x{K} (ws {need} B)")
+    cases = [
+        dict(M=1024, N=1024, K=65536, tA=1, tB=0, beta=0.0),
+        dict(M=256, N=384, K=30000, tA=1, tB=0, beta=1.0),
+        dict(M=100, N=60, K=70000, tA=1, tB=0, beta=0.0),
+        dict(M=512, N=256, K=20000, tA=0, tB=0, beta=0.0, out_bf16=True),
+        dict(M=384, N=256, K=20000, tA=0, tB=1, beta=0.0, out_bf16=True),
+        dict(M=200, N=136, K=20000, tA=0, tB=0, beta=0.5, bias=True, pad=(3, 1, 4)),
+        dict(M=256, N=200, K=16384, tA=1, tB=0, beta=1.0, bias=True, alpha=0.5),
+    ]
+    for c in cases:
+        M, N, K, tA, tB = c.pop("M"), c.pop("N"), c.pop("K"), c.pop("tA"), c.pop("tB")
+        out_bf16 = c.pop("out_bf16", False)
+        assert _split_of(mi, tA, tB, M, N, K, True, ws) > 1, (M, N, K, tA, tB)
+        got, ref = _run(mi, dev, oracle, M, N, K, tA, tB, True, seed=51, out_bf16=out_bf16, ws=ws,
+                        **c)
+        check(got, ref, TOL_BF16, f"split-K {M}x{N}x{K} tA={tA} tB={tB} {c}")
+
+
+def test_fp32_split_k(mi, dev, oracle):
+    """fp32 split plans of configurations 1 and 2 (register-staged kernel writing
+    partials, then the reduction) against the oracle at the fp32 bar."""
+    import torch
+
+    ws = torch.empty(16 << 20, dtype=torch.float32, device=dev)
+    for (M, N, K), (tA, tB), kw in [((512, 768, 768), (0, 1), dict(bias=True)),
+                                    ((768, 768, 2048), (1, 0), dict(beta=1.0)),
+                                    ((2048, 768, 2304), (0, 1), {}),
+                                    ((768, 2304, 2048), (1, 0), dict(beta=1.0, bias=True)),
+                                    ((2048, 768, 768), (0, 0), dict(residual=True))]:
+        assert _split_of(mi, tA, tB, M, N, K, False, ws) > 1, (M, N, K)
+        got, ref = _run(mi, dev, oracle, M, N, K, tA, tB, False, seed=57, ws=ws, **kw)
+        check(got, ref, TOL_F32, f"fp32 split-K {M}x{N}x{K} tA={tA} tB={tB} {kw}")
+        assert oracle.l2_rel_err(got, ref) < 1e-4
 
 
 def test_zero_k(mi, dev, oracle):
@@ -187,12 +234,14 @@ def test_zero_k(mi, dev, oracle):
 
 # ---- decoder-block GEMM sets of the benchmark configurations ----------------------
 
-def _block_set(mi, dev, oracle, M, H, Nqkv, I, bf16, seed):
-    """Forward (NN), dX (NT) and dW (TN) for QKV, O, gate, up, down: engine layout W[in,out]."""
+def _block_set(mi, dev, oracle, M, H, Nqkv, I, bf16, seed, ws=None):
+    """Forward (NN), dX (NT) and dW (TN) for QKV, O, gate, up, down: engine layout W[in,out].
+    Returns the largest split-K factor the 15 products planned."""
     import torch
 
     shapes = {"qkv": (H, Nqkv), "o": (H, H), "gate": (H, I), "up": (H, I), "down": (I, H)}
     rows = sample_rows(M, 6, seed)
+    max_split = 1
     for name, (din, dout) in shapes.items():
         x = inputs(oracle, (M, din), seed + 1, 1.0, bf16)
         w = inputs(oracle, (din, dout), seed + 2, 0.02, bf16)
@@ -202,9 +251,13 @@ def _block_set(mi, dev, oracle, M, H, Nqkv, I, bf16, seed):
         Y = torch.empty((M, dout), dtype=odt, device=dev)
         dX = torch.empty((M, din), dtype=odt, device=dev)
         dW = torch.zeros((din, dout), dtype=torch.float32, device=dev)
-        mi.gemm(X, W, Y, M, dout, din)                                  # Y = X W
-        mi.gemm(dY, W, dX, M, din, dout, transB=True)                   # dX = dY W^T
-        mi.gemm(X, dY, dW, din, dout, M, transA=True, beta=1.0)         # dW += X^T dY
+        mi.gemm(X, W, Y, M, dout, din, workspace=ws)                    # Y = X W
+        mi.gemm(dY, W, dX, M, din, dout, transB=True, workspace=ws)     # dX = dY W^T
+        mi.gemm(X, dY, dW, din, dout, M, transA=True, beta=1.0, workspace=ws)  # dW += X^T dY
+        if ws is not None:
+            max_split = max([max_split] + [_split_of(mi, *f, bf16, ws) for f in
+                                           [(0, 0, M, dout, din), (0, 1, M, din, dout),
+                                            (1, 0, din, dout, M)]])
         torch.cuda.synchronize()
         tol = TOL_BF16 if bf16 else TOL_F32
         y, dx, dw = host(Y), host(dX), host(dW)
@@ -216,11 +269,18 @@ def _block_set(mi, dev, oracle, M, H, Nqkv, I, bf16, seed):
             col, row = checksums(a_op, b_op)
             check(got.sum(axis=0), col, tol, f"{name} column checksum")
             check(got.sum(axis=1), row, tol, f"{name} row checksum")
+    return max_split
 
 
-def test_config2_gpt_small_fp32(mi, dev, oracle):
-    """Benchmark configuration 2: d=768, 12 heads MHA (QKV 768->2304), SwiGLU 2048, M=2048, fp32."""
-    _block_set(mi, dev, oracle, 2048, 768, 2304, 2048, False, seed=200)
+@pytest.mark.parametrize("with_ws", [False, True], ids=["no_ws", "split_k"])
+def test_config2_gpt_small_fp32(mi, dev, oracle, with_ws):
+    """Benchmark configuration 2: d=768, 12 heads MHA (QKV 768->2304), SwiGLU 2048, M=2048, fp32.
+    With the workspace the bridges pass, 11 of the 15 products run split-K (2, and 7 for o dW)."""
+    import torch
+
+    ws = torch.empty(8 << 20, dtype=torch.float32, device=dev) if with_ws else None
+    max_split = _block_set(mi, dev, oracle, 2048, 768, 2304, 2048, False, seed=200, ws=ws)
+    assert max_split == (7 if with_ws else 1)
 
 
 def test_config3_1p6b_bf16(mi, dev, oracle):
@@ -254,6 +314,62 @@ def test_config5_lm_head(mi, dev, oracle):
         col, row = checksums(a_op, b_op)
         check(g.sum(axis=0), col, TOL_BF16, "column checksum")
         check(g.sum(axis=1), row, TOL_BF16, "row checksum")
+
+
+# ---- per-call GEMM profiler ---------------------------------------------------------
+
+def test_profiler_records_block_set(mi, dev, oracle):
+    """GemmProfiler over configuration 3's 15 GEMMs: one record per call, in call
+    order, with the call's shape and transposes, the plan mi_gemm_describe names for
+    it and a positive GPU time; the totals add up the records."""
+    import torch
+
+    M, H, Nqkv, I = 8192, 2048, 3072, 5632
+    shapes = [(H, Nqkv), (H, H), (H, I), (H, I), (I, H)]
+    prof = mi.GemmProfiler.instance()
+    prof.enable()
+    try:
+        prof.begin_step()
+        mi.reset_profile_stats()
+        want = []
+        for din, dout in shapes:
+            X = torch.randn((M, din), device=dev).to(torch.bfloat16)
+            W = (0.02 * torch.randn((din, dout), device=dev)).to(torch.bfloat16)
+            dY = (1e-2 * torch.randn((M, dout), device=dev)).to(torch.bfloat16)
+            Y = torch.empty((M, dout), dtype=torch.bfloat16, device=dev)
+            dX = torch.empty((M, din), dtype=torch.bfloat16, device=dev)
+            dW = torch.zeros((din, dout), dtype=torch.float32, device=dev)
+            mi.gemm(X, W, Y, M, dout, din, sync=False)
+            mi.gemm(dY, W, dX, M, din, dout, transB=True, sync=False)
+            mi.gemm(X, dY, dW, din, dout, M, transA=True, beta=1.0, sync=False)
+            want += [(M, dout, din, False, False), (M, din, dout, False, True),
+                     (din, dout, M, True, False)]
+        recs = prof.records()
+        assert len(recs) == 15
+        for r, (m, n, k, ta, tb) in zip(recs, want):
+            assert (r["M"], r["N"], r["K"], r["transA"], r["transB"]) == (m, n, k, ta, tb)
+            assert r["kernel"] == mi.describe(ta, tb, m, n, k), r
+            assert r["splits"] == 1 and r["batch"] == 1
+            assert 0.0 < r["elapsed_ms"] < 100.0, r
+        ms, calls = mi.accum_gpu_time_ms(), mi.count_gpu_calls()
+        assert calls == 15
+        assert abs(ms - sum(r["elapsed_ms"] for r in recs)) < 1e-6 * max(ms, 1.0) + 1e-9
+        rows = prof.summary()
+        assert sum(a["calls"] for a in rows) == 15
+        prof.print_summary(ms)
+        prof.begin_step()
+        assert prof.records() == []
+        assert mi.count_gpu_calls() == 15      # the totals survive begin_step
+        mi.reset_profile_stats()
+        assert mi.count_gpu_calls() == 0
+    finally:
+        prof.enable(False)
+        prof.begin_step()
+    # recording off: nothing is kept
+    A = torch.zeros((64, 64), dtype=torch.bfloat16, device=dev)
+    C = torch.empty((64, 64), dtype=torch.bfloat16, device=dev)
+    mi.gemm(A, A, C, 64, 64, 64)
+    assert prof.records() == []
 
 
 # ---- Tensor::matmul mirror --------------------------------------------------------
