@@ -27,6 +27,13 @@
 
 using namespace mig;
 
+// Split-K scratch of mi_gemm_noalloc: a file-scope device array, one copy per GPU
+// the library runs on, held until the process ends.  Host code never passes the
+// array's name to a kernel or copy (on the host it only stands in for the symbol):
+// its device address is looked up once per device with hipGetSymbolAddress
+// (scratch_of_current) and that address is what the kernels receive.
+static __device__ __align__(256) float scratch[MI_NOALLOC_SCRATCH_BYTES / sizeof(float)];
+
 namespace {
 
 thread_local std::string g_err;
@@ -71,6 +78,27 @@ int init_devices() {
   int d = 0;
   if (hipGetDevice(&d) != hipSuccess || d < 0 || d >= 64 || !g_dev[d].ok)
     return fail(MI_ERR_NO_DEVICE, "current device %d is not a gfx950", d);
+  return MI_OK;
+}
+
+constexpr size_t kScratchBytes = MI_NOALLOC_SCRATCH_BYTES;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[64];
+
+// Device address of `scratch` on the current device (looked up on first use).
+int scratch_of_current(void** out) {
+  int d = 0;
+  if (hipGetDevice(&d) != hipSuccess || d < 0 || d >= 64)
+    return fail(MI_ERR_NO_DEVICE, "no current device");
+  std::lock_guard<std::mutex> lk(g_scratch_mu);
+  if (!g_scratch_ptr[d]) {
+    void* ptr = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !ptr)
+      return fail(MI_ERR_HIP, "scratch symbol address on device %d: %s", d, hipGetErrorString(e));
+    g_scratch_ptr[d] = ptr;
+  }
+  *out = g_scratch_ptr[d];
   return MI_OK;
 }
 
@@ -363,8 +391,16 @@ int run(const Problem& P, hipStream_t stream) {
   const int64_t Ktot = P.K * b.k_segments;
   const int64_t ws_elems = P.ws ? (int64_t)(P.ws_bytes / sizeof(float)) : 0;
   const bool allow_split = ws_elems > 0 && aligned16(P.ws);
-  Plan plan = make_plan(P.dtype_in, P.M, P.N, Ktot, b.batch, mode, allow_split, ws_elems,
-                        current_cus(), fast);
+  // mi_gemm_noalloc: the plan mi_gemm makes with unlimited workspace, refused when
+  // its partials would not fit the scratch array (so both entry points run the same
+  // kernels on the same problem)
+  Plan plan = make_plan(P.dtype_in, P.M, P.N, Ktot, b.batch, mode, allow_split || P.noalloc,
+                        P.noalloc ? INT64_MAX / 8 : ws_elems, current_cus(), fast);
+  if (P.noalloc && plan.splits > 1 && (int64_t)plan.splits * P.M * P.N * b.batch > ws_elems)
+    return fail(MI_ERR_WORKSPACE,
+                "mi_gemm_noalloc: split-K by %d needs %lld bytes of scratch, above its %lld-byte "
+                "maximum (call mi_gemm with a workspace)",
+                plan.splits, (long long)plan.splits * P.M * P.N * b.batch * 4, (long long)ws_elems * 4);
 
   // The planner only splits within the workspace; checked again here because
   // an undersized workspace would take out-of-bounds partial-sum writes.
@@ -555,7 +591,12 @@ __global__ void __launch_bounds__(256) softmax_bwd_kernel(const void* P, void* d
 
 extern "C" {
 
-int mi_init(void) { return init_devices(); }
+int mi_init(void) {
+  const int st = init_devices();
+  if (st != MI_OK) return st;
+  void* ptr = nullptr;
+  return scratch_of_current(&ptr);  // set-up of mi_gemm_noalloc's scratch on this device
+}
 
 const char* mi_last_error(void) { return g_err.c_str(); }
 
@@ -588,6 +629,33 @@ int mi_gemm(void* stream, int transA, int transB, int64_t M, int64_t N, int64_t 
   else std::memset(&P.ep, 0, sizeof(P.ep));
   P.ws = workspace;
   P.ws_bytes = workspace_bytes;
+  return run(P, (hipStream_t)stream);
+}
+
+int mi_gemm_noalloc(void* stream, int transA, int transB, int64_t M, int64_t N, int64_t K,
+                    float alpha, const void* A, int64_t lda, const void* B, int64_t ldb,
+                    int32_t dtype_in, float beta, void* C, int64_t ldc, int32_t dtype_c,
+                    const mi_epilogue* epi) {
+  Problem P;
+  P.transA = transA;
+  P.transB = transB;
+  P.M = M; P.N = N; P.K = K;
+  P.alpha = alpha; P.beta = beta;
+  P.A = A; P.B = B; P.lda = lda; P.ldb = ldb;
+  P.dtype_in = dtype_in;
+  P.C = C; P.ldc = ldc; P.dtype_c = dtype_c;
+  P.bt = single_batch();
+  if (epi) P.ep = *epi;
+  else std::memset(&P.ep, 0, sizeof(P.ep));
+  P.noalloc = true;
+  P.ws = nullptr;
+  P.ws_bytes = 0;
+  int st = validate(P);
+  if (st != MI_OK) return st;
+  if (M == 0 || N == 0) return MI_OK;
+  if ((st = init_devices()) != MI_OK) return st;
+  if ((st = scratch_of_current(&P.ws)) != MI_OK) return st;
+  P.ws_bytes = kScratchBytes;
   return run(P, (hipStream_t)stream);
 }
 

@@ -37,7 +37,7 @@ C_SYMBOLS = (
     "mi_cross_entropy", "mi_rmsnorm_fwd", "mi_rmsnorm_bwd", "mi_rmsnorm_bwd_workspace_size",
     "mi_convert_matrix", "mi_flash_attn_bwd_workspace_size", "mi_profiler_enable",
     "mi_profiler_begin_step", "mi_profiler_count", "mi_profiler_record", "mi_profiler_totals",
-    "mi_profiler_reset",
+    "mi_profiler_reset", "mi_gemm_noalloc",
 )
 MI_ATTN_O_BHTD, MI_ATTN_O_BTHD = 0, 1
 
@@ -108,6 +108,9 @@ def load_library():
     L.mi_gemm.restype = ctypes.c_int
     L.mi_gemm.argtypes = [vp, ctypes.c_int, ctypes.c_int, i64, i64, i64, f32, vp, i64, vp, i64,
                           i32, f32, vp, i64, i32, ctypes.POINTER(MiEpilogue), vp, ctypes.c_size_t]
+    L.mi_gemm_noalloc.restype = ctypes.c_int
+    L.mi_gemm_noalloc.argtypes = [vp, ctypes.c_int, ctypes.c_int, i64, i64, i64, f32, vp, i64, vp,
+                                  i64, i32, f32, vp, i64, i32, ctypes.POINTER(MiEpilogue)]
     L.mi_gemm_batched.restype = ctypes.c_int
     L.mi_gemm_batched.argtypes = [vp, ctypes.c_int, ctypes.c_int, i64, i64, i64, f32, vp, i64,
                                   vp, i64, i32, f32, vp, i64, i32, ctypes.POINTER(MiBatch),

@@ -271,3 +271,18 @@ def test_profiler_api_without_device(mi):
     assert mi.accum_gpu_time_ms() == 0.0 and mi.count_gpu_calls() == 0
     assert prof.enable(was) is True
     assert mi.GemmProfiler.op_name(1, 1, 1, True, False) == "weight gradient (TN)"
+
+
+def test_noalloc_scratch_bound(mi):
+    """mi_gemm_noalloc's static scratch (16 MiB) holds the split-K partials of every
+    batch-1 problem on a 256-CU device: a split plan writes at most one 128x128 fp32
+    tile per CU (splits * tiles <= CUs). Planner only, no device."""
+    limit = 16 << 20
+    worst = 0
+    for dt in (mi.MI_BF16, mi.MI_F32):
+        for M in (1, 60, 100, 128, 129, 256, 384, 512, 768, 1000, 1024, 1536, 2048, 4096):
+            for N in (1, 64, 200, 256, 384, 768, 1024, 2000, 2048, 5632):
+                for K in (4096, 20000, 65536, 1 << 20):
+                    for tA, tB in ((0, 0), (1, 0), (0, 1)):
+                        worst = max(worst, mi.workspace_size(tA, tB, M, N, K, dt, mi.MI_F32))
+    assert 0 < worst <= limit, worst
