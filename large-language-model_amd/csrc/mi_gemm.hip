@@ -218,7 +218,24 @@ Plan make_plan(int dtype_in, int64_t M, int64_t N, int64_t Ktot, int64_t batch, 
       if (frac > 0.0 && frac <= 0.5 && tilesS >= cus) return plan_for(CFG_S, 1);
       return plan_for(CFG_L, 1);
     }
-    if (tilesS * 2 >= cus || !allow_split) return plan_for(CFG_S, 1);
+    // Below one wave of L tiles (long K): one partial round of L tiles, 128x128
+    // tiles two 4-wave workgroups per CU (S), or one 8-wave workgroup per CU that
+    // splits every K tile between two wave groups (W, wave-level split-K).  Cost
+    // in units of one W tile, measured on the dW shapes at K = 8192: an L tile
+    // (4x the work) takes 2.6, S tiles take 1.8 per round of two per CU and 1.1
+    // alone (2048x5632: L 170 us, W 184, S 189; 2048x3072: S 119, W 123, L 165;
+    // 2048x2048: W 66, S 73, L 153).
+    if (tilesS * 2 >= cus || !allow_split) {
+      if (fast && !sparse_L && Ktot >= 1024) {
+        const double cW = (double)cdiv(tilesS, cus);
+        const int64_t full2 = tilesS / (2 * cus), rem = tilesS - full2 * 2 * cus;
+        const double cS = 1.8 * (double)full2 + (rem > cus ? 1.8 : rem > 0 ? 1.1 : 0.0);
+        const double cL = 2.6 * (double)cdiv(tilesL, cus);
+        if (cL <= cW && cL <= cS) return plan_for(CFG_L, 1);
+        if (cW < cS) return plan_for(CFG_W, 1);
+      }
+      return plan_for(CFG_S, 1);
+    }
     return plan_for(CFG_S, split_of(tilesS, 32));
   }
   // fp32: L and S are the same 128x128 tile; only S has the element-granular loader
@@ -237,7 +254,9 @@ bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
 void describe_plan(char* buf, size_t len, int dtype_in, bool fast, const Plan& pl, int transA,
                    int transB, int64_t batch) {
   const CfgShape sh = shape_of(dtype_in, pl.cfg);
-  const char* kind = (dtype_in == MI_BF16 && fast && pl.cfg != CFG_PRO) ? "dlds" : "regstage";
+  const char* kind = (dtype_in == MI_BF16 && fast && pl.cfg != CFG_PRO)
+                         ? (pl.cfg == CFG_W ? "dlds-kg2" : "dlds")
+                         : "regstage";
   std::snprintf(buf, len, "%s %s %dx%d %s%s split%d tiles%lld", kind,
                 dtype_in == MI_BF16 ? "bf16" : "f32", sh.bm, sh.bn, transA ? "T" : "N",
                 transB ? "T" : "N", pl.splits, (long long)pl.tiles_m * pl.tiles_n * batch);
@@ -410,7 +429,8 @@ int run(const Problem& P, hipStream_t stream) {
   const CfgShape ts = shape_of(P.dtype_in, plan.cfg);
   const bool fast_epi = plan.splits == 1 && !P.ep.bias && !P.ep.residual && cvec &&
                         b.causal != MI_CAUSAL_OUT_LOWER && P.M % ts.bm == 0 && P.N % ts.bn == 0;
-  KernelFn fn = pick_kernel(P.dtype_in, P.transA, P.transB, plan.cfg, fast, P.K % 64 != 0, fast_epi);
+  const int64_t kstep = plan.cfg == CFG_W ? MI_W_BK : 64;
+  KernelFn fn = pick_kernel(P.dtype_in, P.transA, P.transB, plan.cfg, fast, P.K % kstep != 0, fast_epi);
   if (!fn) return fail(MI_ERR_UNSUPPORTED, "no kernel for this layout / mode");
 
   Params p;
@@ -481,7 +501,7 @@ int run(const Problem& P, hipStream_t stream) {
       g_prof_free[pe.dev].push_back(pe.e1);
     }
   };
-  hipLaunchKernelGGL(fn, dim3((unsigned)nblocks), dim3(256), 0, stream, p);
+  hipLaunchKernelGGL(fn, dim3((unsigned)nblocks), dim3((unsigned)ts.threads), 0, stream, p);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return drop_events(), fail(MI_ERR_HIP, "gemm launch: %s", hipGetErrorString(e));
   if (plan.splits > 1) {

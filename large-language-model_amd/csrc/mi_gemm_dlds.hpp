@@ -60,10 +60,32 @@ __device__ __forceinline__ int kc_swz(int r, int c) {
   else return c ^ ((r ^ (r >> 3)) & 7);
 }
 
-// Physical chunk of logical chunk q in k-row kr of a row-contiguous tile: the
-// four k-rows one transpose read touches land in four different 64-byte bank
-// groups.
-__device__ __forceinline__ int mc_swz(int kr, int q) { return q ^ ((kr & 3) << 2); }
+// Physical chunk of logical chunk q in k-row kr of a row-contiguous tile with
+// CPR chunks per k-row: the four k-rows one transpose read touches land in four
+// different 64-byte bank groups.  A power-of-two row XORs the chunk index; any
+// other row (e.g. 24 chunks for 192 columns) rotates it by 4 chunks per k-row,
+// which keeps the even/odd chunk pairs of a 16-column read adjacent.
+template <int CPR>
+__device__ __forceinline__ int mc_swz(int kr, int q) {
+  if constexpr ((CPR & (CPR - 1)) == 0) {
+    static_assert(CPR >= 16, "XOR swizzle needs 16 chunks per k-row");
+    return q ^ ((kr & 3) << 2);
+  } else {
+    static_assert(CPR % 2 == 0 && CPR > 12, "rotation swizzle needs an even row of > 12 chunks");
+    const int t = q + ((kr & 3) << 2);
+    return t >= CPR ? t - CPR : t;
+  }
+}
+// Inverse of mc_swz: the logical chunk stored at position p of k-row kr.
+template <int CPR>
+__device__ __forceinline__ int mc_unswz(int kr, int p) {
+  if constexpr ((CPR & (CPR - 1)) == 0) {
+    return p ^ ((kr & 3) << 2);
+  } else {
+    const int t = p - ((kr & 3) << 2);
+    return t < 0 ? t + CPR : t;
+  }
+}
 
 __device__ __forceinline__ uint32_t lds_addr(const void* p) {
   return (uint32_t)(uintptr_t)MIG_LDS_PTR(p);
@@ -91,20 +113,24 @@ __device__ __forceinline__ void static_for(F&& f) {
 
 // One operand of the direct-to-LDS pipeline.  R: tile rows (M or N extent),
 // BK: K extent of a stage, KC: K-contiguous in memory, WT: rows of the wave
-// tile (fragments of 32 rows each).
-template <int R, int BK, bool KC, int STAGES, int WT>
+// tile (fragments of 32 rows each), NW: waves sharing the DMA, NSUBW: K substeps
+// of 16 one wave computes per stage (BK/16, or half of it when two wave groups
+// split each stage's K range).
+template <int R, int BK, bool KC, int STAGES, int WT, int NW = 4, int NSUBW = BK / 16>
 struct DldsOperand {
   static constexpr int NCH = BK / 8;                  // KC: 16-byte chunks per row
+  static constexpr int CPR = R / 8;                   // !KC: 16-byte chunks per k-row
   static constexpr int BYTES = R * BK * 2;            // one stage of this operand
   static constexpr int NBLK = BYTES / 1024;           // 1 KB DMA blocks per stage
-  static constexpr int NU = NBLK / 4;                 // DMA instructions per wave
+  static constexpr int NU = NBLK / NW;                // DMA instructions per wave
   static constexpr int NSUB = BK / 16;
   static constexpr int NF = WT / 32;                  // fragments per wave
-  static constexpr int NRB = KC ? 2 * NSUB : NF;      // read base registers
-  static_assert(NBLK % 4 == 0, "tile must split into whole DMA blocks per wave");
+  static constexpr int NRB = KC ? 2 * NSUBW : NF;     // read base registers
+  static_assert(BYTES % 1024 == 0 && NBLK % NW == 0, "tile must split into whole DMA blocks per wave");
+  static_assert(NSUB % NSUBW == 0, "wave groups split the stage's substeps evenly");
   // largest immediate offset added to a read base must fit the 16-bit DS offset
   static constexpr int MAX_IMM = KC ? ((NF - 1) / 2) * 64 * BK * 2 + (STAGES - 1) * BYTES
-                                    : (16 * (NSUB - 1) + 4) * R * 2 + (STAGES - 1) * BYTES;
+                                    : (16 * (NSUBW - 1) + 4) * R * 2 + (STAGES - 1) * BYTES;
   static_assert(MAX_IMM < 65536, "LDS read offsets exceed the DS immediate");
 
   uint32_t voff[NU];  // byte offset of unit u from the tile's first K (kBufOOB: row outside)
@@ -126,9 +152,10 @@ struct DldsOperand {
         voff[u] = (uint32_t)((row0 + row) * ldb + c * 16);  // rows >= M lie past the extent
         klim[u] = kseg - c * 8;
       } else {
-        constexpr int CPR = R / 8;  // chunks per k-row
-        const int kr = b * (64 / CPR) + lane / CPR;
-        const int q = mc_swz(kr, lane % CPR);
+        // chunk q of the stage lands at LDS chunk q: k-row q / CPR, position q % CPR
+        const int qi = b * 64 + lane;
+        const int kr = qi / CPR;
+        const int q = mc_unswz<CPR>(kr, qi - kr * CPR);
         const int grow = row0 + q * 8;
         voff[u] = grow < rows ? (uint32_t)(kr * ldb + grow * 2) : kBufOOB;
         klim[u] = 0;
@@ -137,17 +164,18 @@ struct DldsOperand {
   }
 
   // LDS addresses.  region: LDS address of this operand's stage 0; w0: first row
-  // of the wave tile; wave_u: wave index held in a scalar register.
-  __device__ __forceinline__ void init_lds(uint32_t region, int w0, int wave_u) {
+  // of the wave tile; wave_u: wave index (among the NW) held in a scalar
+  // register; ks0: first of the NSUBW substeps this wave reads.
+  __device__ __forceinline__ void init_lds(uint32_t region, int w0, int wave_u, int ks0 = 0) {
     const int lane = threadIdx.x & 63;
     dma = region + (uint32_t)(wave_u * NU * 1024);
     if constexpr (KC) {
 #pragma unroll
-      for (int s = 0; s < NSUB; ++s)
+      for (int s = 0; s < NSUBW; ++s)
 #pragma unroll
         for (int par = 0; par < 2; ++par) {
           const int r = w0 + 32 * par + (lane & 31);
-          const int c = 2 * s + (lane >> 5);
+          const int c = 2 * (ks0 + s) + (lane >> 5);
           rb[2 * s + par] = region + (uint32_t)(r * (BK * 2) + 16 * kc_swz<NCH>(r, c));
         }
     } else {
@@ -157,7 +185,7 @@ struct DldsOperand {
         const int col = w0 + 32 * f + (g & 1) * 16 + 4 * (j & 3);
         const int q = col >> 3, sub = (col & 7) * 2;
         const int krb = 8 * (g >> 1) + (j >> 2);
-        rb[f] = region + (uint32_t)(krb * (R * 2) + 16 * mc_swz(krb, q) + sub);
+        rb[f] = region + (uint32_t)((krb + 16 * ks0) * (R * 2) + 16 * mc_swz<CPR>(krb, q) + sub);
       }
     }
   }
@@ -210,24 +238,35 @@ struct DldsOperand {
 // both epilogues would need the accumulators in two places at once.
 enum { DLDS_KTAIL = 1, DLDS_FAST_EPI = 2 };
 
-// bf16 GEMM, 4 waves (2 x 2), wave tile (BM/2) x (BN/2) of 32x32x16 MFMAs.
-template <int BM, int BN, int BK, int STAGES, bool AK, bool BKC, int MODE, int VAR>
-__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1)))
+// bf16 GEMM of WGM x WGN waves, wave tile (BM/WGM) x (BN/WGN) of 32x32x16 MFMAs.
+// KG = 2 (wave-level split-K): a second group of WGM x WGN waves computes the
+// same output tile over the other half of every LDS stage's K range (both
+// groups share the stage's DMA), so a workgroup keeps two waves per SIMD on one
+// output tile; the groups' accumulators are summed through LDS before the
+// epilogue, each group then storing half of the tile.
+template <int BM, int BN, int BK, int STAGES, bool AK, bool BKC, int MODE, int VAR, int WGM = 2,
+          int WGN = 2, int KG = 1>
+__global__ void __launch_bounds__(64 * WGM * WGN * KG)
+    __attribute__((amdgpu_waves_per_eu(WGM * WGN * KG / 4)))
     gemm_dlds_kernel(Params p) {
   constexpr bool KTAIL = (VAR & DLDS_KTAIL) != 0;
   constexpr bool FAST_EPI = (VAR & DLDS_FAST_EPI) != 0;
-  constexpr int WGM = 2, WGN = 2;
+  constexpr int NWG = WGM * WGN;          // waves of one K group
+  constexpr int NWAVE = NWG * KG;         // waves of the workgroup
   constexpr int WTM = BM / WGM, WTN = BN / WGN;
   constexpr int TM = WTM / 32, TN = WTN / 32;
   constexpr bool DUAL = (MODE == MODE_DUAL);
   constexpr int NB = DUAL ? 2 * TN : TN;
-  constexpr int NSUB = BK / 16;
+  constexpr int NSUBT = BK / 16;          // K substeps of a stage
+  constexpr int NSUB = NSUBT / KG;        // K substeps one wave computes per stage
   static_assert(MODE != MODE_PROLOGUE, "the SiLU-gate prologue needs register staging");
-  static_assert(NSUB == 2 || NSUB == 4, "BK must be 32 or 64");
+  static_assert(KG == 1 || KG == 2, "one or two K groups");
+  static_assert(KG == 1 || (MODE == MODE_PLAIN && TM == 2), "split-K groups: plain mode, two row blocks");
+  static_assert(NSUB == 2 || NSUB == 4, "each wave computes 2 or 4 substeps per stage");
   static_assert(STAGES >= 2 && STAGES <= 4, "2..4 stages");
-  static_assert(TN % 2 == 0, "epilogue stages 64-column halves");
-  using OpA = DldsOperand<BM, BK, AK, STAGES, WTM>;
-  using OpB = DldsOperand<BN, BK, BKC, STAGES, WTN>;
+  static_assert(TN % 2 == 0 || KG == 2, "epilogue stages 64-column halves");
+  using OpA = DldsOperand<BM, BK, AK, STAGES, WTM, NWAVE, NSUB>;
+  using OpB = DldsOperand<BN, BK, BKC, STAGES, WTN, NWAVE, NSUB>;
   constexpr int A_REG = 0;                                   // LDS regions (bytes)
   constexpr int B_REG = A_REG + STAGES * OpA::BYTES;
   constexpr int B2_REG = B_REG + STAGES * OpB::BYTES;
@@ -254,11 +293,13 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1)))
                        : nullptr;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int wave_u = uniform(wave);
-  const int wm = wave / WGN, wn = wave % WGN;
+  const int kg = uniform(wave / NWG);     // K group
+  const int wq = wave % NWG;              // wave within the group
+  const int wm = wq / WGN, wn = wq % WGN;
 
   if (p.causal == CAUSAL_OUT_LOWER && n0 > m0 + BM - 1) {
     if (p.splits > 1) return;  // the reduction kernel writes the mask
-    for (int idx = threadIdx.x; idx < BM * BN; idx += 256) {
+    for (int idx = threadIdx.x; idx < BM * BN; idx += 64 * NWAVE) {
       const int m = m0 + idx / BN, n = n0 + idx % BN;
       if (m < p.M && n < p.N) {
         const int64_t ci = (int64_t)m * p.ldc + n;
@@ -298,8 +339,8 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1)))
   OpB ob2;  // DUAL: LDS addresses of the second B (DMA offsets shared with ob)
   oa.init_dma(p.lda, p.M, m0, p.K);
   ob.init_dma(p.ldb, p.N, n0, p.K);
-  oa.init_lds(lds0 + A_REG, wm * WTM, wave_u);
-  ob.init_lds(lds0 + B_REG, wn * WTN, wave_u);
+  oa.init_lds(lds0 + A_REG, wm * WTM, wave_u, kg * NSUB);
+  ob.init_lds(lds0 + B_REG, wn * WTN, wave_u, kg * NSUB);
   if constexpr (DUAL) ob2.init_lds(lds0 + B2_REG, wn * WTN, wave_u);
 
   // Tile stream of the DMA.  Descriptors start at the tile (base + K offset,
@@ -539,6 +580,39 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1)))
 
   // acc[i][j][4q + e] holds C[m][n + e] with
   //   m = m0 + wm*WTM + i*32 + (lane & 31),  n = n0 + wn*WTN + j*32 + 8q + 4*(lane >> 5).
+  if constexpr (KG == 2) {
+    // Sum the K groups.  The wave of group g keeps row block i = g of its wave
+    // tile and sends the other block to its partner (same place in the other
+    // group) through LDS, in slots [sender group][wave][j][quad][lane] of 16
+    // bytes; the epilogue below then stores only row block kg.
+    __syncthreads();  // every wave is past its last fragment read
+    static_assert(2 * NWG * TN * 4 * 64 * 16 <= LDS_BYTES, "exchange fits the ring");
+    f32x4_t* xb = reinterpret_cast<f32x4_t*>(smem);
+    auto slot = [&](int g, int j, int q) __attribute__((always_inline)) {
+      return (((g * NWG + wq) * TN + j) * 4 + q) * 64 + lane;
+    };
+    auto quad = [](const f32x16_t& a, int q) __attribute__((always_inline)) {
+      return f32x4_t{a[4 * q], a[4 * q + 1], a[4 * q + 2], a[4 * q + 3]};
+    };
+    auto exchange = [&](auto KEEP_c) __attribute__((always_inline)) {
+      constexpr int KEEP = decltype(KEEP_c)::value, SEND = 1 - KEEP;
+#pragma unroll
+      for (int j = 0; j < TN; ++j)
+#pragma unroll
+        for (int q = 0; q < 4; ++q) xb[slot(KEEP, j, q)] = quad(acc[SEND][j], q);
+      __syncthreads();
+#pragma unroll
+      for (int j = 0; j < TN; ++j)
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const f32x4_t r = xb[slot(SEND, j, q)];
+#pragma unroll
+          for (int e = 0; e < 4; ++e) acc[KEEP][j][4 * q + e] += r[e];
+        }
+    };
+    if (kg == 0) exchange(ic<0>{});
+    else exchange(ic<1>{});
+  }
   auto value = [&](int i, int j, int q, int e) __attribute__((always_inline)) {
     if constexpr (DUAL)
       return silu_f(p.alpha * acc[i][j][4 * q + e]) * (p.alpha * acc[i][j + TN][4 * q + e]);
@@ -553,7 +627,7 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1)))
     // 16 bytes.  One barrier first: the patches reuse the ring's LDS.
     __syncthreads();
     constexpr int PP = 36;  // patch pitch (floats)
-    static_assert(4 * 32 * PP * 4 <= LDS_BYTES, "epilogue patches fit the ring");
+    static_assert(NWAVE * 32 * PP * 4 <= LDS_BYTES, "epilogue patches fit the ring");
     float* patch = reinterpret_cast<float*>(smem) + wave * (32 * PP);
     const float beta = p.beta;
     const int r_in = lane & 31, h_in = lane >> 5;
@@ -562,7 +636,8 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1)))
     auto store_tile = [&](auto BF_c, auto BETA_c) __attribute__((always_inline)) {
       constexpr bool BF = decltype(BF_c)::value, BETA = decltype(BETA_c)::value;
 #pragma unroll
-      for (int i = 0; i < TM; ++i)
+      for (int i = 0; i < TM; ++i) {
+        if (KG == 2 && i != kg) continue;
 #pragma unroll
         for (int j = 0; j < TN; ++j) {
 #pragma unroll
@@ -600,6 +675,7 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1)))
           }
           __builtin_amdgcn_sched_barrier(0);
         }
+      }
     };
     if (p.c_bf16) {
       if (beta != 0.0f) store_tile(std::true_type{}, std::true_type{});
@@ -617,7 +693,7 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1)))
   // of the ring's LDS needs every wave past its last fragment read.
   __syncthreads();
   constexpr int PITCH = WTN + 4;
-  static_assert(4 * 32 * PITCH * 4 <= LDS_BYTES, "epilogue staging fits the ring");
+  static_assert(NWAVE * 32 * PITCH * 4 <= LDS_BYTES, "epilogue staging fits the ring");
   float* stg = reinterpret_cast<float*>(smem) + wave * (32 * PITCH);
   float* W = (p.splits > 1) ? p.ws + ((int64_t)tc.z * p.splits + tc.split) * (int64_t)p.M * p.N
                             : nullptr;
@@ -625,6 +701,7 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1)))
   constexpr int C4 = WTN / 4;  // float4 groups per staged row
 #pragma unroll
   for (int i = 0; i < TM; ++i) {
+    if (KG == 2 && i != kg) continue;
 #pragma unroll
     for (int j = 0; j < TN; ++j)
 #pragma unroll

@@ -36,6 +36,11 @@ typedef float elem_t;
 #ifndef MI_S_STAGES
 #define MI_S_STAGES(ak) ((ak) ? 2 : 4)
 #endif
+// 128x128 with wave-level split-K (one workgroup of 8 waves per CU): K tile and
+// ring depth.
+#ifndef MI_W_STAGES
+#define MI_W_STAGES 4
+#endif
 
 #define MI_CAT5(a, b, c, d, e) a##b##c##d##e
 #define MI_PICK_NAME(dt, ta, tb) MI_CAT5(pick_, dt, _, ta, tb)
@@ -43,13 +48,19 @@ typedef float elem_t;
 #if MI_DT_BF16
 // bf16 direct-to-LDS kernels of one variant (K tile and LDS ring depth:
 // MI_DLDS_BK / MI_DLDS_STAGES for 256x256, MI_S_BK / MI_S_STAGES of the A layout for 128x128,
-// 32 / 4 for the dual-B 256x128).
+// 32 / 4 for the dual-B 256x128).  256x256 runs 8 waves (2 x 4, wave tiles 128x64): two
+// waves per SIMD, so one wave's MFMAs issue while the other waits on LDS or DMA issue
+// (8192x2048x5632 NT: 147 vs 161 us with 4 waves of 128x128; 8192x5632x2048 NN 157 vs
+// 166; 2048x5632x8192 TN 170 vs 180; bit-identical results).
 template <bool AK, bool BK, int V>
 KernelFn dlds_kernel(int cfg) {
   switch (cfg) {
-    case CFG_L: return gemm_dlds_kernel<256, 256, MI_DLDS_BK, MI_DLDS_STAGES, AK, BK, MODE_PLAIN, V>;
+    case CFG_L:
+      return gemm_dlds_kernel<256, 256, MI_DLDS_BK, MI_DLDS_STAGES, AK, BK, MODE_PLAIN, V, 2, 4, 1>;
     case CFG_S: return gemm_dlds_kernel<128, 128, MI_S_BK(AK), MI_S_STAGES(AK), AK, BK, MODE_PLAIN, V>;
     case CFG_DUAL: return gemm_dlds_kernel<256, 128, 32, 4, AK, BK, MODE_DUAL, V>;
+    case CFG_W:
+      return gemm_dlds_kernel<128, 128, MI_W_BK, MI_W_STAGES, AK, BK, MODE_PLAIN, V, 2, 2, 2>;
     default: return nullptr;
   }
 }

@@ -227,6 +227,31 @@ def test_fp32_split_k(mi, dev, oracle):
         assert oracle.l2_rel_err(got, ref) < 1e-4
 
 
+@pytest.mark.parametrize("tA,tB", [(0, 0), (0, 1), (1, 0), (1, 1)], ids=["NN", "NT", "TN", "TT"])
+def test_wave_split_k(mi, dev, oracle, tA, tB):
+    """128x128 tiles with wave-level split-K (two groups of 4 waves, each over half of
+    every K tile, summed through LDS): full tiles (direct epilogue), edge tiles with
+    bias + residual (general epilogue), a K tail, fp32 beta = 1 output, and
+    small-integer operands, whose outputs must be bit-exact."""
+    import torch
+
+    cases = [((256, 384, 2048), {}), ((384, 256, 1100), dict(beta=1.0, out_bf16=False)),
+             ((200, 136, 1536), dict(bias=True, residual=True, alpha=0.5)),
+             ((512, 512, 4096), dict(beta=-0.5, out_bf16=True))]
+    for (M, N, K), kw in cases:
+        assert "dlds-kg2" in mi.describe(tA, tB, M, N, K), (M, N, K)
+        got, ref = _run(mi, dev, oracle, M, N, K, tA, tB, True, seed=71 + K, **kw)
+        check(got, ref, TOL_BF16, f"wave split-K {M}x{N}x{K} tA={tA} tB={tB} {kw}")
+    rng = np.random.default_rng(7)
+    M, N, K = 384, 256, 2048
+    a = rng.integers(-4, 5, (M, K)).astype(np.float32)
+    b = rng.integers(-4, 5, (K, N)).astype(np.float32)
+    C = torch.zeros((M, N), dtype=torch.float32, device=dev)
+    mi.gemm(to_dev(layout(a, tA), dev, True), to_dev(layout(b, tB), dev, True), C, M, N, K,
+            transA=tA, transB=tB)
+    assert np.array_equal(C.cpu().numpy(), a.astype(np.int64) @ b.astype(np.int64))
+
+
 def test_zero_k(mi, dev, oracle):
     got, ref = _run(mi, dev, oracle, 70, 90, 0, 0, 0, False, seed=61, beta=0.5, bias=True)
     check(got, ref, TOL_F32, "K=0")
