@@ -264,7 +264,6 @@ __global__ void __launch_bounds__(64 * WGM * WGN * KG)
   static_assert(KG == 1 || (MODE == MODE_PLAIN && TM == 2), "split-K groups: plain mode, two row blocks");
   static_assert(NSUB == 2 || NSUB == 4, "each wave computes 2 or 4 substeps per stage");
   static_assert(STAGES >= 2 && STAGES <= 4, "2..4 stages");
-  static_assert(TN % 2 == 0 || KG == 2, "epilogue stages 64-column halves");
   using OpA = DldsOperand<BM, BK, AK, STAGES, WTM, NWAVE, NSUB>;
   using OpB = DldsOperand<BN, BK, BKC, STAGES, WTN, NWAVE, NSUB>;
   constexpr int A_REG = 0;                                   // LDS regions (bytes)
@@ -474,7 +473,9 @@ __global__ void __launch_bounds__(64 * WGM * WGN * KG)
                       const TileRef& t) __attribute__((always_inline)) {
     constexpr int S = decltype(S_c)::value, RSET = decltype(RSET_c)::value;
     constexpr int DPART = decltype(DPART_c)::value;
-    constexpr int H0 = DPART > 0 ? (DPART - 1) * NL / 2 : 0, HN = DPART > 0 ? NL / 2 : 0;
+    // first half NL/2 instructions, second half the rest (NL may be odd)
+    constexpr int H0 = DPART == 2 ? NL / 2 : 0;
+    constexpr int HN = DPART == 1 ? NL / 2 : DPART == 2 ? NL - NL / 2 : 0;
     if constexpr (!AK || !BKC) {
       // set S was read two substeps ago; the previous substep's LDS reads (one
       // set, READ_OPS instructions) may stay in flight: LDS returns in order

@@ -61,6 +61,8 @@ KernelFn dlds_kernel(int cfg) {
     case CFG_DUAL: return gemm_dlds_kernel<256, 128, 32, 4, AK, BK, MODE_DUAL, V>;
     case CFG_W:
       return gemm_dlds_kernel<128, 128, MI_W_BK, MI_W_STAGES, AK, BK, MODE_PLAIN, V, 2, 2, 2>;
+    case CFG_M:
+      return gemm_dlds_kernel<256, 192, MI_DLDS_BK, MI_DLDS_STAGES, AK, BK, MODE_PLAIN, V, 4, 2, 1>;
     default: return nullptr;
   }
 }

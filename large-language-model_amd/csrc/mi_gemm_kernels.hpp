@@ -12,9 +12,10 @@ typedef void (*KernelFn)(Params);
 //   bf16: L 256x256 (8 waves of 128x64, two per SIMD), S 128x128 (4 waves of 64x64),
 //         DUAL 256x128 (+ second B), PRO 256x256 with the SiLU-gate A prologue,
 //         W 128x128 with wave-level split-K (8 waves: two groups of 4 waves of
-//         64x64, each over half of every K tile, summed through LDS).
+//         64x64, each over half of every K tile, summed through LDS),
+//         M 256x192 (8 waves of 64x96).
 //   fp32: L = S = W 128x128, DUAL 128x64, PRO 128x128.
-enum Cfg { CFG_L = 0, CFG_S = 1, CFG_DUAL = 2, CFG_PRO = 3, CFG_W = 4, NCFG = 5 };
+enum Cfg { CFG_L = 0, CFG_S = 1, CFG_DUAL = 2, CFG_PRO = 3, CFG_W = 4, CFG_M = 5, NCFG = 6 };
 
 struct CfgShape {
   int bm, bn;
@@ -32,6 +33,7 @@ inline CfgShape cfg_shape(bool bf16, int cfg) {
     return cfg == CFG_L ? CfgShape{256, 256, 512}
          : cfg == CFG_S ? CfgShape{128, 128}
          : cfg == CFG_W ? CfgShape{128, 128, 512}
+         : cfg == CFG_M ? CfgShape{256, 192, 512}
          : cfg == CFG_DUAL ? CfgShape{256, 128}
                            : CfgShape{256, 256};
   return cfg == CFG_DUAL ? CfgShape{128, 64} : CfgShape{128, 128};

@@ -252,6 +252,37 @@ def test_wave_split_k(mi, dev, oracle, tA, tB):
     assert np.array_equal(C.cpu().numpy(), a.astype(np.int64) @ b.astype(np.int64))
 
 
+@pytest.mark.parametrize("tA,tB", [(0, 0), (0, 1), (1, 0), (1, 1)], ids=["NN", "NT", "TN", "TT"])
+def test_tile_256x192(mi, dev, oracle, tA, tB):
+    """256x192 tiles (8 waves of 64x96; 24 chunks per LDS k-row of a row-contiguous
+    B, placed by the rotation swizzle): the direct epilogue, a K tail, and the bias
+    epilogue. Sampled rows against the oracle, every element through checksums."""
+    import torch
+
+    M, N = 8192, 3072
+    for K, bias in [(2048, False), (2000, False), (512, True)]:
+        plan = mi.describe(tA, tB, M, N, K)
+        assert "256x192" in plan, plan
+        a = inputs(oracle, (M, K), 95 + K, 1.0)
+        b = inputs(oracle, (K, N), 96 + K, 0.02)
+        bv = inputs(oracle, (N,), 97, 0.02) if bias else None
+        C = torch.empty((M, N), dtype=torch.bfloat16, device=dev)
+        extra = {"bias": torch.from_numpy(bv).to(dev)} if bias else {}
+        mi.gemm(to_dev(layout(a, tA), dev, True), to_dev(layout(b, tB), dev, True), C, M, N, K,
+                transA=tA, transB=tB, **extra)
+        torch.cuda.synchronize()
+        got = host(C)
+        rows = sample_rows(M, 6, K)
+        check(got[rows], oracle.gemm(0, 0, M, N, K, a, b, rows=rows, bias=bv), TOL_BF16,
+              f"256x192 K={K} rows")
+        col, row = checksums(a, b)
+        if bias:
+            col = col + M * bv.astype(np.float64)
+            row = row + bv.astype(np.float64).sum()
+        check(got.sum(axis=0), col, TOL_BF16, f"256x192 K={K} column checksum")
+        check(got.sum(axis=1), row, TOL_BF16, f"256x192 K={K} row checksum")
+
+
 def test_zero_k(mi, dev, oracle):
     got, ref = _run(mi, dev, oracle, 70, 90, 0, 0, 0, False, seed=61, beta=0.5, bias=True)
     check(got, ref, TOL_F32, "K=0")
