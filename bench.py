@@ -38,19 +38,25 @@ PEAK_HBM_GBS = 8000.0
 BLOCK = [("qkv", 2048, 3072), ("o", 2048, 2048), ("gate", 2048, 5632), ("up", 2048, 5632),
          ("down", 5632, 2048)]
 M_TOKENS = 8192
+# benchmark configuration 2 (GPT-small, fp32): MHA 12 x 64 -> QKV 768->2304, SwiGLU 2048, M=4*512
+BLOCK_FP32 = [("qkv", 768, 2304), ("o", 768, 768), ("gate", 768, 2048), ("up", 768, 2048),
+              ("down", 2048, 768)]
+M_TOKENS_FP32 = 2048
+PEAK_FP32_TFLOPS = 157.3    # MI355X dense fp32 MFMA
 
 
 WS_BYTES = 512 << 20
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "gemm_block_set_bf16_m8192_hbm_bytes.md")
+TRAFFIC_FILE_FP32 = os.path.join(ROOT, "profiles", "gemm_block_set_f32_m2048_hbm_bytes.md")
 
 
-def hbm_bytes_per_launch(kernel: str):
+def hbm_bytes_per_launch(kernel: str, path: str = TRAFFIC_FILE):
     """HBM bytes per launch of `kernel` from the committed rocprofv3 --pmc summary
     (FETCH_SIZE and WRITE_SIZE per dispatch, scaled by the copy-kernel calibration),
     or None when the summary has no row for it."""
-    if not os.path.exists(TRAFFIC_FILE):
+    if not os.path.exists(path):
         return None
-    for line in open(TRAFFIC_FILE):
+    for line in open(path):
         cells = [c.strip() for c in line.strip().strip("|").split("|")]
         if len(cells) >= 5 and cells[0] == kernel:
             try:
@@ -60,8 +66,20 @@ def hbm_bytes_per_launch(kernel: str):
     return None
 
 
-def block_flops(M: int) -> int:
-    return sum(3 * 2 * M * din * dout for _, din, dout in BLOCK)
+def cpu_model() -> str:
+    """The host CPU's model name (first "model name" line of /proc/cpuinfo)."""
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def block_flops(M: int, block=BLOCK) -> int:
+    return sum(3 * 2 * M * din * dout for _, din, dout in block)
 
 
 def parse():
@@ -74,9 +92,11 @@ def parse():
                     help="token rows of the CPU sample (default: the whole set, M=8192)")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="also launch a 1 GiB device copy (for PMC byte-counter scaling)")
-    ap.add_argument("--workload", choices=("block", "attention", "lm_head", "norm", "convert"),
+    ap.add_argument("--workload",
+                    choices=("block", "block_fp32", "attention", "lm_head", "norm", "convert"),
                     default="block",
-                    help="block: the configuration-3 GEMM set (the headline metric); attention: "
+                    help="block: the configuration-3 GEMM set (the headline metric); block_fp32: "
+                         "configuration 2's fp32 GEMM set (GPT-small, M=2048); attention: "
                          "configuration 4, fused GQA attention forward + backward; lm_head: "
                          "configuration 5, LM-head GEMMs with the fused cross-entropy between; "
                          "norm: configuration 3's residual add + RMSNorm forward and backward; "
@@ -85,7 +105,8 @@ def parse():
     return ap.parse_args()
 
 
-def cpu_baseline(m_rows: int) -> dict:
+def cpu_baseline(m_rows: int, block=BLOCK, m_full: int = M_TOKENS, label: str = "config-3",
+                 inputs: str = "fp32 (bf16 inputs upcast)") -> dict:
     import numpy as np
 
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
@@ -94,7 +115,7 @@ def cpu_baseline(m_rows: int) -> dict:
     flops = 0
     t_total = 0.0
     rng = np.random.default_rng(0)
-    for _, din, dout in BLOCK:
+    for _, din, dout in block:
         x = rng.standard_normal((m_rows, din), dtype=np.float32)
         w = rng.standard_normal((din, dout), dtype=np.float32) * 0.02
         dy = rng.standard_normal((m_rows, dout), dtype=np.float32) * 1e-2
@@ -106,11 +127,11 @@ def cpu_baseline(m_rows: int) -> dict:
         t_total += time.perf_counter() - t0
         flops += 3 * 2 * m_rows * din * dout
     return {"value": round(flops / t_total / 1e12, 4), "unit": "TFLOP/s",
-            "cores": oracle.num_threads(), "kind": "port",
-            "sample": (f"the whole config-3 block set (15 GEMMs, M={m_rows})" if m_rows == M_TOKENS
-                       else f"config-3 block set (15 GEMMs) at M={m_rows} token rows instead of "
-                            f"{M_TOKENS}")
-                      + f", fp32 (bf16 inputs upcast), {flops / 1e9:.1f} GFLOP, {t_total:.2f} s"}
+            "cores": oracle.num_threads(), "cpu_model": cpu_model(), "kind": "port",
+            "sample": (f"the whole {label} block set (15 GEMMs, M={m_rows})" if m_rows == m_full
+                       else f"{label} block set (15 GEMMs) at M={m_rows} token rows instead of "
+                            f"{m_full}")
+                      + f", {inputs}, {flops / 1e9:.1f} GFLOP, {t_total:.2f} s"}
 
 
 ATT = dict(B=8, nH=16, nKV=4, T=1024, d=128)   # benchmark configuration 4
@@ -137,7 +158,7 @@ def cpu_attention_baseline() -> dict:
     dt = time.perf_counter() - t0
     flops = 6 * ATT_PRODUCT_FLOPS * 4 / (ATT["B"] * ATT["nH"])
     return {"value": round(flops / dt / 1e12, 5), "unit": "TFLOP/s", "cores": oracle.num_threads(),
-            "kind": "port",
+            "cpu_model": cpu_model(), "kind": "port",
             "sample": f"batch element 0, 4 query heads / 1 KV head of configuration 4, float64, "
                       f"{flops / 1e9:.1f} GFLOP, {dt:.2f} s"}
 
@@ -236,7 +257,7 @@ def cpu_lm_head_baseline(m_rows: int = 1024) -> dict:
     dt = time.perf_counter() - t0
     flops = 3 * 2 * m_rows * H * V
     return {"value": round(flops / dt / 1e12, 4), "unit": "TFLOP/s", "cores": oracle.num_threads(),
-            "kind": "port",
+            "cpu_model": cpu_model(), "kind": "port",
             "sample": f"configuration 5 at M={m_rows} token rows instead of {LMH['M']}: fp32 SGEMMs "
                       f"+ float64 cross-entropy, {flops / 1e9:.1f} GFLOP, {dt:.2f} s"}
 
@@ -461,7 +482,7 @@ def cpu_norm_baseline(rows: int = 8192, min_seconds: float = 2.0) -> dict:
             break
     nbytes = 8 * rows * dims * 2 * reps   # the GPU step's algorithmic bf16 bytes
     return {"value": round(nbytes / dt / 1e9, 3), "unit": "GB/s", "cores": oracle.num_threads(),
-            "kind": "port",
+            "cpu_model": cpu_model(), "kind": "port",
             "sample": f"the whole workload ({rows} x {dims}), {reps} passes in {dt:.2f} s; bytes "
                       f"counted as the GPU step's bf16 bytes"}
 
@@ -489,7 +510,8 @@ def cpu_convert_baseline(jobs, shapes, min_seconds: float = 2.0) -> dict:
         if dt >= min_seconds:
             break
     nbytes = sum(2 * 2 * rows * shapes[n][1] for n, _, rows, _, _ in jobs) * reps
-    return {"value": round(nbytes / dt / 1e9, 3), "unit": "GB/s", "cores": 1, "kind": "port",
+    return {"value": round(nbytes / dt / 1e9, 3), "unit": "GB/s", "cores": 1,
+            "cpu_model": cpu_model(), "kind": "port",
             "sample": f"the nine matrices, {reps} passes in {dt:.2f} s (numpy, one thread; writes "
                       f"fp32 as the reference loader does, bytes counted as the GPU's bf16 "
                       f"read + write)"}
@@ -594,35 +616,44 @@ def main():
     if args.workload == "convert":
         convert_main(args)
         return
+    gemm_set_main(args, fp32=args.workload == "block_fp32")
+
+
+def gemm_set_main(args, fp32: bool):
+    """Configuration 3 (bf16 in, bf16 Y/dX, fp32 dW +=) or, with fp32, configuration 2
+    (fp32 everywhere): the 15 GEMMs of one decoder block per step."""
     import torch
 
     import mi_gemm as mi
 
     dev = torch.device("cuda:0")
     mi.init()
-    M = M_TOKENS
+    block, M = (BLOCK_FP32, M_TOKENS_FP32) if fp32 else (BLOCK, M_TOKENS)
+    dt_in = torch.float32 if fp32 else torch.bfloat16
+    mi_dt = mi.MI_F32 if fp32 else mi.MI_BF16
+    peak = PEAK_FP32_TFLOPS if fp32 else PEAK_BF16_TFLOPS
     g = torch.Generator(device=dev)
     g.manual_seed(1234)
     # split-K workspace, as the bridge's pool provides it (the planner decides per GEMM)
     ws = torch.empty(WS_BYTES // 4, dtype=torch.float32, device=dev)
     ops = []
-    for name, din, dout in BLOCK:
-        X = torch.randn((M, din), generator=g, device=dev).to(torch.bfloat16)
-        W = (torch.randn((din, dout), generator=g, device=dev) * 0.02).to(torch.bfloat16)
-        dY = (torch.randn((M, dout), generator=g, device=dev) * 1e-2).to(torch.bfloat16)
-        Y = torch.empty((M, dout), dtype=torch.bfloat16, device=dev)
-        dX = torch.empty((M, din), dtype=torch.bfloat16, device=dev)
+    for name, din, dout in block:
+        X = torch.randn((M, din), generator=g, device=dev).to(dt_in)
+        W = (torch.randn((din, dout), generator=g, device=dev) * 0.02).to(dt_in)
+        dY = (torch.randn((M, dout), generator=g, device=dev) * 1e-2).to(dt_in)
+        Y = torch.empty((M, dout), dtype=dt_in, device=dev)
+        dX = torch.empty((M, din), dtype=dt_in, device=dev)
         dW = torch.zeros((din, dout), dtype=torch.float32, device=dev)
         ops.append((name, "fwd NN", 2 * M * din * dout,
-                    mi.describe(0, 0, M, dout, din, workspace_bytes=WS_BYTES),
+                    mi.describe(0, 0, M, dout, din, dtype_in=mi_dt, workspace_bytes=WS_BYTES),
                     lambda X=X, W=W, Y=Y, din=din, dout=dout:
                     mi.gemm(X, W, Y, M, dout, din, workspace=ws, sync=False)))
         ops.append((name, "dX NT", 2 * M * din * dout,
-                    mi.describe(0, 1, M, din, dout, workspace_bytes=WS_BYTES),
+                    mi.describe(0, 1, M, din, dout, dtype_in=mi_dt, workspace_bytes=WS_BYTES),
                     lambda dY=dY, W=W, dX=dX, din=din, dout=dout:
                     mi.gemm(dY, W, dX, M, din, dout, transB=True, workspace=ws, sync=False)))
         ops.append((name, "dW TN", 2 * M * din * dout,
-                    mi.describe(1, 0, din, dout, M, workspace_bytes=WS_BYTES),
+                    mi.describe(1, 0, din, dout, M, dtype_in=mi_dt, workspace_bytes=WS_BYTES),
                     lambda X=X, dY=dY, dW=dW, din=din, dout=dout:
                     mi.gemm(X, dY, dW, din, dout, M, transA=True, beta=1.0, workspace=ws,
                             sync=False)))
@@ -689,14 +720,14 @@ def main():
     torch.cuda.synchronize()
     t1 = time.perf_counter()
     elapsed = t1 - t0
-    flops = block_flops(M)
+    flops = block_flops(M, block)
     value = flops * args.steps / elapsed / 1e12
     ms_dom = sum(rev[s_][r][0].elapsed_time(rev[s_][r][1])
                  for s_ in range(args.steps) for r in range(len(runs)))
     n_dom = len(dom_idx) * args.steps
     fl_dom = sum(ops[k][2] for k in dom_idx) * args.steps
     achieved = fl_dom / (ms_dom / 1e3) / 1e12
-    traffic = hbm_bytes_per_launch(dom)
+    traffic = hbm_bytes_per_launch(dom, TRAFFIC_FILE_FP32 if fp32 else TRAFFIC_FILE)
     dom_ops = sorted(f"{ops[k][0]} {ops[k][1]}" for k in dom_idx)
 
     if args.copy_calibration:
@@ -705,8 +736,18 @@ def main():
         b.copy_(a)
         torch.cuda.synchronize()
 
+    if fp32:
+        metric = "GEMM TFLOP/s (fwd+bwd, GPT-small block fp32, M=2048) and % of MI355X fp32 MFMA peak"
+        workload = ("GPT-small decoder-block GEMM set (configuration 2): fwd NN + dX NT + dW TN "
+                    "(beta=1) for QKV 768->2304, O 768->768, gate/up 768->2048, down 2048->768; "
+                    "M=2048 tokens; fp32 in / fp32 acc / fp32 out")
+    else:
+        metric = "GEMM TFLOP/s (fwd+bwd, 1.6B block, M=8192) and % of MI355X MFMA peak"
+        workload = ("1.6B decoder-block GEMM set: fwd NN + dX NT + dW TN (beta=1, fp32) "
+                    "for QKV 2048->3072, O 2048->2048, gate/up 2048->5632, down "
+                    "5632->2048; M=8192 tokens; bf16 in / fp32 acc")
     out = {
-        "metric": "GEMM TFLOP/s (fwd+bwd, 1.6B block, M=8192) and % of MI355X MFMA peak",
+        "metric": metric,
         "value": round(value, 2),
         "unit": "TFLOP/s",
         "n_gpus": 1,
@@ -716,24 +757,24 @@ def main():
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "bf16",
+        "dtype": "f32" if fp32 else "bf16",
         "data": "synthetic (torch.randn on device; X~N(0,1), W~N(0,0.02), dY~N(0,1e-2))",
-        "config": {"workload": "1.6B decoder-block GEMM set: fwd NN + dX NT + dW TN (beta=1, fp32) "
-                               "for QKV 2048->3072, O 2048->2048, gate/up 2048->5632, down "
-                               "5632->2048; M=8192 tokens; bf16 in / fp32 acc",
-                   "M": M, "d_model": 2048, "gemms_per_step": len(ops),
-                   "flops_per_step": flops, "pct_of_peak": round(100 * value / PEAK_BF16_TFLOPS, 2),
+        "config": {"workload": workload,
+                   "M": M, "d_model": block[0][1], "gemms_per_step": len(ops),
+                   "flops_per_step": flops, "pct_of_peak": round(100 * value / peak, 2),
                    "order": "per projection: fwd, dX, dW",
                    "per_gemm_tflops": breakdown,
+                   "per_gemm_plan": {f"{op[0]} {op[1]}": op[3] for op in ops},
                    "per_gemm_source": f"attribution pass, {n_attr} steps, events around every launch"},
-        "roofline": {"bound": "mfma", "achieved": round(achieved, 2), "peak": PEAK_BF16_TFLOPS,
-                     "unit": "TFLOP/s", "frac": round(achieved / PEAK_BF16_TFLOPS, 4),
+        "roofline": {"bound": "mfma", "achieved": round(achieved, 2), "peak": peak,
+                     "unit": "TFLOP/s", "frac": round(achieved / peak, 4),
                      "traffic": traffic, "kernel": dom, "gemms": dom_ops,
                      "launches": n_dom, "avg_launch_ms": round(ms_dom / n_dom, 4),
                      "time_share": round(per_kernel[dom] / sum(per_kernel.values()), 3)},
     }
     if not args.no_cpu:
-        out["cpu_baseline"] = cpu_baseline(args.cpu_rows)
+        out["cpu_baseline"] = (cpu_baseline(M, BLOCK_FP32, M_TOKENS_FP32, "config-2", "fp32")
+                               if fp32 else cpu_baseline(args.cpu_rows))
     print(json.dumps(out))
 
 

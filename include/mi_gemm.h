@@ -125,15 +125,15 @@ int mi_gemm(void* stream, int transA, int transB, int64_t M, int64_t N, int64_t 
  * workspace of mi_gemm_workspace_size bytes, minus the workspace: split-K partials
  * go to a static device array of MI_NOALLOC_SCRATCH_BYTES that the library holds
  * on each GPU it runs on until the process ends (its address is set up by mi_init
- * or the first call on a device).  A split-K plan writes at most one 128x128 fp32
- * tile of partials per CU, 16 MiB on a 256-CU MI355X, so every problem fits; a
+ * or the first call on a device).  A split-K plan writes at most two 128x128 fp32
+ * tiles of partials per CU, 32 MiB on a 256-CU MI355X, so every problem fits; a
  * plan needing more (a larger device) fails with MI_ERR_WORKSPACE.  Calls no
  * allocating routine.  Every call on a
  * GPU shares that GPU's array: calls that overlap in time on one GPU (different
  * streams, or different host threads) race and must be serialised by the caller.
  * Not recorded by the profiler.
  */
-#define MI_NOALLOC_SCRATCH_BYTES ((size_t)16 << 20)
+#define MI_NOALLOC_SCRATCH_BYTES ((size_t)32 << 20)
 int mi_gemm_noalloc(void* stream, int transA, int transB, int64_t M, int64_t N, int64_t K,
                     float alpha, const void* A, int64_t lda, const void* B, int64_t ldb,
                     int32_t dtype_in, float beta, void* C, int64_t ldc, int32_t dtype_c,

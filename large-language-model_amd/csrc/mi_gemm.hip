@@ -188,7 +188,7 @@ int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
 //     a workspace -- also for S tiles chosen by the fill rule and for the
 //     register-staged loader (unaligned operands);
 //   * fp32 (both configurations 128x128): fewer tiles than 5/8 of the CUs split
-//     K over L tiles, given a workspace.
+//     K over L tiles, given a workspace (the rule at the fp32 branch).
 // Every split fits the workspace: splits * M * N * batch <= ws_limit_elems.
 Plan make_plan(int dtype_in, int64_t M, int64_t N, int64_t Ktot, int64_t batch, int mode,
                bool allow_split, int64_t ws_limit_elems, int cus, bool fast) {
@@ -242,14 +242,27 @@ Plan make_plan(int dtype_in, int64_t M, int64_t N, int64_t Ktot, int64_t batch, 
     }
     return plan_for(CFG_S, split_of(tilesS, 32));
   }
-  // fp32: L and S are the same 128x128 tile; only S has the element-granular loader
+  // fp32: L and S are the same 128x128 tile; only S has the element-granular loader.
+  // Below 5/8 of a wave, K is split so that the units (tiles x splits, at most two
+  // per CU) leave the fewest K tiles on the busiest CU: ceil(units / cus) / splits,
+  // ties to more splits; a split keeps >= 8 K tiles of 32, or >= 4 when the units
+  // fit one per CU.  Fitted to a forced-split sweep of configurations 1 and 2 (96
+  // tiles at K = 2048: splits 1..8 ran 43 71 59 74 83 66 69 76 TFLOP/s; 108 tiles:
+  // 47 78 67 83 65 73 76 71; 36 tiles: 16 28 37 44 49 52 54 41; 24 tiles at K = 768:
+  // 10 15 19 21 21 22 21 21; 96 tiles at K = 768: 37 49 43 46 49 41 41 43).
   const int cfg = fast ? CFG_L : CFG_S;
-  if (tilesL * 8 >= (int64_t)cus * 5) return plan_for(cfg, 1);
-  if (allow_split) {
-    const int sp = split_of(tilesL, 32);
-    if (sp >= 2) return plan_for(cfg, sp);
+  if (tilesL * 8 >= (int64_t)cus * 5 || !allow_split) return plan_for(cfg, 1);
+  const int64_t kts = cdiv(Ktot, 32);
+  int best = 1;
+  double best_score = 1.0;
+  for (int sp = 2; sp <= 8; ++sp) {
+    const int64_t units = tilesL * sp;
+    if (units > 2 * (int64_t)cus || (int64_t)sp * M * N * batch > ws_limit_elems) continue;
+    if (cdiv(kts, sp) < (units <= cus ? 4 : 8)) continue;
+    const double score = (double)cdiv(units, cus) / sp;
+    if (score <= best_score) best = sp, best_score = score;
   }
-  return plan_for(cfg, 1);
+  return plan_for(cfg, best);
 }
 
 bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }

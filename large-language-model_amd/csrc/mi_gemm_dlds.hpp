@@ -61,31 +61,29 @@ __device__ __forceinline__ int kc_swz(int r, int c) {
 }
 
 // Physical chunk of logical chunk q in k-row kr of a row-contiguous tile with
-// CPR chunks per k-row: the four k-rows one transpose read touches land in four
-// different 64-byte bank groups.  A power-of-two row XORs the chunk index; any
-// other row (e.g. 24 chunks for 192 columns) rotates it by 4 chunks per k-row,
-// which keeps the even/odd chunk pairs of a 16-column read adjacent.
+// CPR chunks per k-row (CPR a power of two >= 16): the four k-rows one transpose
+// read touches land in four different 64-byte bank groups.
 template <int CPR>
 __device__ __forceinline__ int mc_swz(int kr, int q) {
-  if constexpr ((CPR & (CPR - 1)) == 0) {
-    static_assert(CPR >= 16, "XOR swizzle needs 16 chunks per k-row");
-    return q ^ ((kr & 3) << 2);
-  } else {
-    static_assert(CPR % 2 == 0 && CPR > 12, "rotation swizzle needs an even row of > 12 chunks");
-    const int t = q + ((kr & 3) << 2);
-    return t >= CPR ? t - CPR : t;
-  }
+  static_assert((CPR & (CPR - 1)) == 0 && CPR >= 16, "XOR swizzle needs 2^n >= 16 chunks per k-row");
+  return q ^ ((kr & 3) << 2);
 }
 // Inverse of mc_swz: the logical chunk stored at position p of k-row kr.
 template <int CPR>
 __device__ __forceinline__ int mc_unswz(int kr, int p) {
-  if constexpr ((CPR & (CPR - 1)) == 0) {
-    return p ^ ((kr & 3) << 2);
-  } else {
-    const int t = p - ((kr & 3) << 2);
-    return t < 0 ? t + CPR : t;
-  }
+  return p ^ ((kr & 3) << 2);
 }
+
+// Row-contiguous tiles whose row is not a power of two (192 columns) are stored
+// in 128-byte granules, column block by column block: granule G holds k-row
+// G % BK of the 64-column block G / BK, so consecutive k-rows of one column block
+// are 128 bytes apart and any four of them cover both halves of a 256-byte bank
+// window; the two 64-byte halves of a granule swap on k-rows 2 and 3 (mod 4), so
+// the four k-rows one transpose read touches land in four different 64-byte bank
+// groups.  A k-row of R columns would instead start at R * 2 bytes (384: an odd
+// multiple of 128), and no chunk rotation of it avoids two k-rows meeting in one
+// bank group for every 32-column block.
+__device__ __forceinline__ int gran_half(int kr) { return ((kr >> 1) & 1) << 6; }
 
 __device__ __forceinline__ uint32_t lds_addr(const void* p) {
   return (uint32_t)(uintptr_t)MIG_LDS_PTR(p);
@@ -120,6 +118,9 @@ template <int R, int BK, bool KC, int STAGES, int WT, int NW = 4, int NSUBW = BK
 struct DldsOperand {
   static constexpr int NCH = BK / 8;                  // KC: 16-byte chunks per row
   static constexpr int CPR = R / 8;                   // !KC: 16-byte chunks per k-row
+  static constexpr bool GRAN = !KC && (CPR & (CPR - 1)) != 0;  // 128-byte granule layout
+  static constexpr int KRB = GRAN ? 128 : R * 2;      // !KC: LDS bytes between k-rows
+  static_assert(!GRAN || R % 64 == 0, "granule layout needs 64-column blocks");
   static constexpr int BYTES = R * BK * 2;            // one stage of this operand
   static constexpr int NBLK = BYTES / 1024;           // 1 KB DMA blocks per stage
   static constexpr int NU = NBLK / NW;                // DMA instructions per wave
@@ -130,7 +131,7 @@ struct DldsOperand {
   static_assert(NSUB % NSUBW == 0, "wave groups split the stage's substeps evenly");
   // largest immediate offset added to a read base must fit the 16-bit DS offset
   static constexpr int MAX_IMM = KC ? ((NF - 1) / 2) * 64 * BK * 2 + (STAGES - 1) * BYTES
-                                    : (16 * (NSUBW - 1) + 4) * R * 2 + (STAGES - 1) * BYTES;
+                                    : (16 * (NSUBW - 1) + 4) * KRB + (STAGES - 1) * BYTES;
   static_assert(MAX_IMM < 65536, "LDS read offsets exceed the DS immediate");
 
   uint32_t voff[NU];  // byte offset of unit u from the tile's first K (kBufOOB: row outside)
@@ -151,6 +152,14 @@ struct DldsOperand {
         const int c = kc_swz<NCH>(row, lane % NCH);
         voff[u] = (uint32_t)((row0 + row) * ldb + c * 16);  // rows >= M lie past the extent
         klim[u] = kseg - c * 8;
+      } else if constexpr (GRAN) {
+        // LDS chunk qi: granule qi / 8 = k-row kr of 64-column block qi / 8 / BK
+        const int qi = b * 64 + lane;
+        const int gi = qi >> 3, kr = gi % BK;
+        const int col = (gi / BK) * 64 + (((qi & 7) * 16) ^ gran_half(kr)) / 2;
+        const int grow = row0 + col;
+        voff[u] = grow < rows ? (uint32_t)(kr * ldb + grow * 2) : kBufOOB;
+        klim[u] = 0;
       } else {
         // chunk q of the stage lands at LDS chunk q: k-row q / CPR, position q % CPR
         const int qi = b * 64 + lane;
@@ -185,7 +194,11 @@ struct DldsOperand {
         const int col = w0 + 32 * f + (g & 1) * 16 + 4 * (j & 3);
         const int q = col >> 3, sub = (col & 7) * 2;
         const int krb = 8 * (g >> 1) + (j >> 2);
-        rb[f] = region + (uint32_t)((krb + 16 * ks0) * (R * 2) + 16 * mc_swz<CPR>(krb, q) + sub);
+        if constexpr (GRAN)
+          rb[f] = region + (uint32_t)(((col >> 6) * BK + krb + 16 * ks0) * 128 +
+                                      (((col & 63) * 2) ^ gran_half(krb)));
+        else
+          rb[f] = region + (uint32_t)((krb + 16 * ks0) * (R * 2) + 16 * mc_swz<CPR>(krb, q) + sub);
       }
     }
   }
@@ -221,7 +234,7 @@ struct DldsOperand {
         // precedes its first use (see substep()).
         asm volatile("ds_read_b64_tr_b16 %0, %1 offset:%2"
                      : "=v"(w)
-                     : "v"(rb[f]), "i"((16 * S + 4 * t) * R * 2 + J * BYTES));
+                     : "v"(rb[f]), "i"((16 * S + 4 * t) * KRB + J * BYTES));
 #endif
         out[2 * t] = w[0];
         out[2 * t + 1] = w[1];

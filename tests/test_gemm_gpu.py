@@ -140,10 +140,10 @@ def test_config1_fp32_linear_bias(mi, dev, oracle):
     got, ref = _run(mi, dev, oracle, 512, 768, 768, 0, 1, False, seed=1, bias=True)
     check(got, ref, TOL_F32, "config 1")
     assert oracle.l2_rel_err(got, ref) < 1e-4  # test_gpu_kernels.cpp:87-116 metric
-    # with the workspace the bridges pass, the same problem runs as split-K 3
+    # with the workspace the bridges pass, the same problem runs as split-K 7
     ws = torch.empty(mi.workspace_size(0, 1, 512, 768, 768, mi.MI_F32) // 4, dtype=torch.float32,
                      device=dev)
-    assert _split_of(mi, 0, 1, 512, 768, 768, False, ws) == 3
+    assert _split_of(mi, 0, 1, 512, 768, 768, False, ws) == 7
     got, ref = _run(mi, dev, oracle, 512, 768, 768, 0, 1, False, seed=1, bias=True, ws=ws)
     check(got, ref, TOL_F32, "config 1, split-K")
     assert oracle.l2_rel_err(got, ref) < 1e-4
@@ -254,9 +254,9 @@ def test_wave_split_k(mi, dev, oracle, tA, tB):
 
 @pytest.mark.parametrize("tA,tB", [(0, 0), (0, 1), (1, 0), (1, 1)], ids=["NN", "NT", "TN", "TT"])
 def test_tile_256x192(mi, dev, oracle, tA, tB):
-    """256x192 tiles (8 waves of 64x96; 24 chunks per LDS k-row of a row-contiguous
-    B, placed by the rotation swizzle): the direct epilogue, a K tail, and the bias
-    epilogue. Sampled rows against the oracle, every element through checksums."""
+    """256x192 tiles (8 waves of 64x96; a row-contiguous B stored in 128-byte granules
+    of 64 columns): the direct epilogue, a K tail, and the bias epilogue. Sampled rows
+    against the oracle, every element through checksums."""
     import torch
 
     M, N = 8192, 3072
@@ -331,7 +331,8 @@ def _block_set(mi, dev, oracle, M, H, Nqkv, I, bf16, seed, ws=None):
 @pytest.mark.parametrize("with_ws", [False, True], ids=["no_ws", "split_k"])
 def test_config2_gpt_small_fp32(mi, dev, oracle, with_ws):
     """Benchmark configuration 2: d=768, 12 heads MHA (QKV 768->2304), SwiGLU 2048, M=2048, fp32.
-    With the workspace the bridges pass, 11 of the 15 products run split-K (2, and 7 for o dW)."""
+    With the workspace the bridges pass, 11 of the 15 products run split-K (2, 4, 5, and 7
+    for o dW)."""
     import torch
 
     ws = torch.empty(8 << 20, dtype=torch.float32, device=dev) if with_ws else None
