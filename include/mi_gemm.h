@@ -213,9 +213,11 @@ int mi_flash_attn_bwd(void* stream, const void* Q, const void* K, const void* V,
                       int64_t head_dim, int32_t causal, int32_t o_layout, void* workspace,
                       size_t workspace_bytes);
 
-/* Workspace bytes for the dS^T form of mi_flash_attn_bwd (batch*n_heads*seq_len^2
- * bf16), or 0 when that form does not apply (seq_len not a multiple of 8, or
- * above 32767). */
+/* Workspace bytes for the dS^T form of mi_flash_attn_bwd: batch*n_heads*seq_len^2
+ * bf16 for dS^T, then batch*n_heads*seq_len*128 fp32 for the partial dK / dV sums
+ * of the balanced dK/dV schedule (a workspace holding dS^T only runs the dS^T form
+ * with one workgroup per key block); 0 when the form does not apply (seq_len not a
+ * multiple of 8, or above 32767). */
 size_t mi_flash_attn_bwd_workspace_size(int64_t batch, int64_t n_heads, int64_t seq_len);
 
 /*

@@ -24,6 +24,9 @@
 // v_mfma_f32_32x32x16_bf16 needs, so P never goes through LDS.
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
+#include <vector>
+
 #include "mi_attn.hpp"
 #include "mi_gemm_dlds.hpp"
 
@@ -609,11 +612,25 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1)))
   const int wave_u = uniform(wave);
   const int h32 = lane >> 5, l32 = lane & 31;
 
-  // Key blocks with the most query tiles (the first ones, causal) go first.
+  // Work unit: with a schedule, unit u (largest first) of every (batch, KV head) in
+  // turn, so each XCD (workgroups b mod 8) gets an even share of every size;
+  // without, one key block per workgroup, the ones with the most query tiles
+  // (causal: the first) first, each XCD a contiguous range.
   const int BKV = p.B * p.nKV;
-  const int lid = uniform(fa_xcd_major(blockIdx.x, gridDim.x));
-  const int kbi = uniform(lid / BKV);
-  const int bkv = uniform(lid - kbi * BKV);
+  int kbi, bkv, slot = -1, ib = 0, ie = -1;
+  if (p.n_units) {
+    const int u = uniform((int)blockIdx.x / BKV);
+    bkv = uniform((int)blockIdx.x - u * BKV);
+    const uint32_t uk = uniform(p.unit_kbi[u]), ur = uniform(p.unit_range[u]);
+    kbi = (int)(uk & 0xffffu);
+    slot = (int)(uk >> 16) - 1;
+    ib = (int)(ur & 0xffffu);
+    ie = (int)(ur >> 16);
+  } else {
+    const int lid = uniform(fa_xcd_major(blockIdx.x, gridDim.x));
+    kbi = uniform(lid / BKV);
+    bkv = uniform(lid - kbi * BKV);
+  }
   const int b = uniform(bkv / p.nKV), kvh = uniform(bkv - (bkv / p.nKV) * p.nKV);
   const int T = p.T;
   const int k0 = kbi * 128;
@@ -640,6 +657,7 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1)))
   const int qt0 = uniform(p.causal ? k0 / QT : 0);
   const int per_h = uniform(nqt - qt0);
   const int total = uniform(per_h > 0 ? per_h * p.group : 0);
+  if (ie < 0) ie = total;  // this workgroup runs iterations [ib, ie) of the key block
   const int go_stride = (p.o_bthd ? p.nH * D : D) * 2;  // bytes between dO rows
 
   uint32_t q_off[Tl::NU], g_off[Tl::NU];
@@ -805,17 +823,18 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1)))
   // visible whole.  Separate loops keep the accumulators in place across iterations.
   const int n_diag = uniform(p.causal ? (per_h < 2 ? per_h : 2) : 0);
   auto ring_step = [&](int it) __attribute__((always_inline)) {
-    if (DS && it > 0) wait_vmcnt<4>();  // the last tile's dS^T stores stay in flight
+    if (DS && it > ib) wait_vmcnt<4>();  // the last tile's dS^T stores stay in flight
     else wait_vmcnt<0>();
     lds_ring_barrier();
-    if (it + 1 < total) issue(it + 1);
+    if (it + 1 < ie) issue(it + 1);
     return lds0 + (uint32_t)((it & 1) * STAGE);
   };
-  if (total > 0) issue(0);
+  if (ib < ie) issue(ib);
   int it = 0;
   for (int hh = 0; hh < p.group; ++hh) {
     const int bh = uniform(b * p.nH + kvh * p.group + hh);
     for (int t = 0; t < n_diag; ++t, ++it) {
+      if (it < ib || it >= ie) continue;  // another unit's iteration
       const uint32_t st = ring_step(it);
       const int q0 = uniform((qt0 + t) * QT);
       if (q0 + QT - 1 < kw) {  // every query of the tile precedes every key
@@ -829,24 +848,42 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1)))
       block(q0, bh, st, std::true_type{});
     }
     for (int t = n_diag; t < per_h; ++t, ++it) {
+      if (it < ib || it >= ie) continue;
       const uint32_t st = ring_step(it);
       block(uniform((qt0 + t) * QT), bh, st, std::false_type{});
     }
   }
 
-  if (live) {
-    uint16_t* ok = (uint16_t*)p.dK + ((int64_t)bkv * T + key) * D;
-    uint16_t* ov = (uint16_t*)p.dV + ((int64_t)bkv * T + key) * D;
+  // Row bases in scalar registers, the lane's key row as a 32-bit element offset.
+  const int lrow = (32 * wave_u + l32) * D;
+  if (slot >= 0) {  // partial sums of a key block cut into several units
+    float* pk = uniform(p.part + ((int64_t)bkv * p.n_slots + slot) * 2 * 128 * D);
+    if (live) {
 #pragma unroll
-    for (int c = 0; c < NC; ++c)
+      for (int c = 0; c < NC; ++c)
 #pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        const int d = 32 * c + 8 * q + 4 * h32;
-        *(u32x2_t*)(ok + d) = u32x2_t{pack_bf16x2(dk[c][4 * q] * p.scale, dk[c][4 * q + 1] * p.scale),
-                                      pack_bf16x2(dk[c][4 * q + 2] * p.scale, dk[c][4 * q + 3] * p.scale)};
-        *(u32x2_t*)(ov + d) = u32x2_t{pack_bf16x2(dv[c][4 * q], dv[c][4 * q + 1]),
-                                      pack_bf16x2(dv[c][4 * q + 2], dv[c][4 * q + 3])};
-      }
+        for (int q = 0; q < 4; ++q) {
+          const int d = lrow + 32 * c + 8 * q + 4 * h32;
+          *(f32x4_t*)(pk + d) = f32x4_t{dk[c][4 * q], dk[c][4 * q + 1], dk[c][4 * q + 2], dk[c][4 * q + 3]};
+          *(f32x4_t*)(pk + 128 * D + d) =
+              f32x4_t{dv[c][4 * q], dv[c][4 * q + 1], dv[c][4 * q + 2], dv[c][4 * q + 3]};
+        }
+    }
+  } else {
+    uint16_t* ok = uniform((uint16_t*)p.dK + ((int64_t)bkv * T + k0) * D);
+    uint16_t* ov = uniform((uint16_t*)p.dV + ((int64_t)bkv * T + k0) * D);
+    if (live) {
+#pragma unroll
+      for (int c = 0; c < NC; ++c)
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const int d = lrow + 32 * c + 8 * q + 4 * h32;
+          *(u32x2_t*)(ok + d) = u32x2_t{pack_bf16x2(dk[c][4 * q] * p.scale, dk[c][4 * q + 1] * p.scale),
+                                        pack_bf16x2(dk[c][4 * q + 2] * p.scale, dk[c][4 * q + 3] * p.scale)};
+          *(u32x2_t*)(ov + d) = u32x2_t{pack_bf16x2(dv[c][4 * q], dv[c][4 * q + 1]),
+                                        pack_bf16x2(dv[c][4 * q + 2], dv[c][4 * q + 3])};
+        }
+    }
   }
 }
 
@@ -881,12 +918,107 @@ __global__ void __launch_bounds__(256) flash_bwd_delta_kernel(FbParams p) {
   if (live && h32 == 0) p.delta[r] = dsum;
 }
 
+// dK and dV of the key blocks the schedule cut into several units: the units'
+// fp32 partials summed in unit order, dK scaled, both stored as bf16.  One thread
+// per 4 consecutive d of one key.
+template <int D>
+__global__ void __launch_bounds__(256) flash_bwd_dkdv_reduce_kernel(FbParams p) {
+  constexpr int QPK = D / 4;          // quads per key
+  constexpr int PER = 128 * QPK;      // quads per key block
+  const int BKV = p.B * p.nKV;
+  const int64_t gid = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  const int i = (int)(gid / ((int64_t)BKV * PER));
+  if (i >= p.n_split) return;
+  const int rem = (int)(gid - (int64_t)i * BKV * PER);
+  const int bkv = rem / PER, r = rem - (rem / PER) * PER;
+  const int kl = r / QPK, d = (r - kl * QPK) * 4;
+  const uint32_t sp = p.split[i];
+  const int kbi = (int)(sp & 0xfffu), s0 = (int)((sp >> 12) & 0xfffu), ns = (int)(sp >> 24);
+  const int key = kbi * 128 + kl;
+  if (key >= p.T) return;
+  f32x4_t ak = {0.f, 0.f, 0.f, 0.f}, av = {0.f, 0.f, 0.f, 0.f};
+  for (int j = 0; j < ns; ++j) {
+    const float* src = p.part + (((int64_t)bkv * p.n_slots + s0 + j) * 2 * 128 + kl) * D + d;
+    ak += *(const f32x4_t*)src;
+    av += *(const f32x4_t*)(src + 128 * D);
+  }
+  const int64_t o = ((int64_t)bkv * p.T + key) * D + d;
+  *(u32x2_t*)((uint16_t*)p.dK + o) = u32x2_t{pack_bf16x2(ak[0] * p.scale, ak[1] * p.scale),
+                                             pack_bf16x2(ak[2] * p.scale, ak[3] * p.scale)};
+  *(u32x2_t*)((uint16_t*)p.dV + o) = u32x2_t{pack_bf16x2(av[0], av[1]), pack_bf16x2(av[2], av[3])};
+}
+
+// Balanced dK/dV schedule.  A key block's work is its iterations (query tiles of the
+// group's heads); causal attention gives the first key blocks many more than the
+// last, and one workgroup per key block leaves the CUs of the short ones idle while
+// the long ones run (configuration 4: 64 iterations for key block 0, 8 for key block
+// 7, 56 % of the CU time used).  Each key block is cut into units of at most W
+// iterations, W = the total over all (batch, KV head) pairs / the CU count, and the
+// units launch largest first, so the hardware's in-order dispatch to the CU that
+// frees up first packs them (longest-processing-time-first).  When the partials of
+// the cut blocks do not fit the room given, W grows by half until they do; when the
+// tables do not fit the kernel arguments, n_units stays 0.
+void plan_dkdv_schedule(FbParams& p) {
+  p.n_units = p.n_slots = p.n_split = 0;
+  if (!p.dsT || !p.part || p.cus <= 0) return;
+  const int NKB = p.k_blocks, nqt = (p.T + FA_BK - 1) / FA_BK;
+  const int64_t BKV = (int64_t)p.B * p.nKV;
+  const size_t slot_bytes = (size_t)BKV * 2 * 128 * 128 * sizeof(float);
+  std::vector<int> w(NKB);
+  int64_t sum = 0;
+  for (int k = 0; k < NKB; ++k) {
+    const int qt0 = p.causal ? k * 128 / FA_BK : 0;
+    w[k] = nqt > qt0 ? (nqt - qt0) * p.group : 0;
+    if (w[k] >= 65536) return;
+    sum += w[k];
+  }
+  struct Unit { int kbi, ib, ie, slot; };
+  std::vector<Unit> units;
+  int slots = 0, nsplit = 0;
+  for (int64_t W = std::max<int64_t>(1, (sum * BKV + p.cus - 1) / p.cus);; W += (W + 1) / 2) {
+    units.clear();
+    slots = nsplit = 0;
+    bool fits = true;
+    for (int k = 0; k < NKB && fits; ++k) {
+      if (w[k] <= W) {
+        units.push_back({k, 0, w[k], -1});
+        continue;
+      }
+      const int c = (int)std::max<int64_t>(W, (w[k] + 7) / 8);  // at most 8 units
+      const int n = (w[k] + c - 1) / c;
+      if (nsplit >= FB_MAX_SPLIT || slots + n > 4095) return;
+      p.split[nsplit++] = (uint32_t)k | (uint32_t)slots << 12 | (uint32_t)n << 24;
+      for (int j = 0; j < n; ++j) units.push_back({k, j * c, std::min(w[k], (j + 1) * c), slots + j});
+      slots += n;
+      fits = (size_t)slots * slot_bytes <= p.part_bytes;
+    }
+    if (nsplit == 0) return;  // nothing to balance (or W outgrew every key block)
+    if (fits) break;
+  }
+  if ((int)units.size() > FB_MAX_UNITS) return;
+  std::stable_sort(units.begin(), units.end(),
+                   [](const Unit& a, const Unit& b) { return a.ie - a.ib > b.ie - b.ib; });
+  for (size_t u = 0; u < units.size(); ++u) {
+    p.unit_kbi[u] = (uint32_t)units[u].kbi | (uint32_t)(units[u].slot + 1) << 16;
+    p.unit_range[u] = (uint32_t)units[u].ib | (uint32_t)units[u].ie << 16;
+  }
+  p.n_units = (int)units.size();
+  p.n_slots = slots;
+  p.n_split = nsplit;
+}
+
 }  // namespace
 
 int flash_fwd_blocks(int T) { return (T + FA_BQ - 1) / FA_BQ; }
 
-hipError_t launch_flash_bwd(const FbParams& p, int head_dim, hipStream_t stream) {
+size_t flash_bwd_partial_bytes(int64_t B, int64_t nH, int64_t T) {
+  return (size_t)B * (size_t)nH * (size_t)T * 128 * sizeof(float);
+}
+
+hipError_t launch_flash_bwd(const FbParams& p_in, int head_dim, hipStream_t stream) {
   if (head_dim != 128) return hipErrorInvalidValue;
+  FbParams p = p_in;
+  plan_dkdv_schedule(p);
   // dQ (and D) first: the dK/dV kernel reads D.  With the dS^T workspace only D here;
   // the dK/dV kernel then writes dS^T and the caller runs dQ = scale * dS K.
   if (p.dsT) {
@@ -899,11 +1031,17 @@ hipError_t launch_flash_bwd(const FbParams& p, int head_dim, hipStream_t stream)
   }
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
-  const int64_t nk = (int64_t)p.B * p.nKV * p.k_blocks;
+  const int64_t nk = (int64_t)p.B * p.nKV * (p.n_units ? p.n_units : p.k_blocks);
   if (p.dsT)
     hipLaunchKernelGGL((flash_bwd_dkdv_kernel<128, true>), dim3((unsigned)nk), dim3(256), 0, stream, p);
   else
     hipLaunchKernelGGL((flash_bwd_dkdv_kernel<128, false>), dim3((unsigned)nk), dim3(256), 0, stream, p);
+  if (!p.n_split) return hipGetLastError();
+  e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  const int64_t quads = (int64_t)p.n_split * p.B * p.nKV * 128 * (128 / 4);
+  hipLaunchKernelGGL(flash_bwd_dkdv_reduce_kernel<128>, dim3((unsigned)((quads + 255) / 256)), dim3(256), 0,
+                     stream, p);
   return hipGetLastError();
 }
 

@@ -811,10 +811,16 @@ int mi_flash_attn_fwd(void* stream, const void* Q, const void* K, const void* V,
   return e == hipSuccess ? MI_OK : fail(MI_ERR_HIP, "flash attention launch: %s", hipGetErrorString(e));
 }
 
-size_t mi_flash_attn_bwd_workspace_size(int64_t batch, int64_t n_heads, int64_t seq_len) {
+// dS^T (bf16), then room for the fp32 dK / dV partials of the balanced dK/dV schedule.
+static size_t flash_dst_bytes(int64_t batch, int64_t n_heads, int64_t seq_len) {
   // The dK/dV kernel stores dS^T in runs of 8 queries through 32-bit buffer offsets.
   if (batch <= 0 || n_heads <= 0 || seq_len <= 0 || seq_len % 8 || seq_len > 32767) return 0;
   return (size_t)batch * (size_t)n_heads * (size_t)seq_len * (size_t)seq_len * 2;
+}
+
+size_t mi_flash_attn_bwd_workspace_size(int64_t batch, int64_t n_heads, int64_t seq_len) {
+  const size_t dst = flash_dst_bytes(batch, n_heads, seq_len);
+  return dst ? dst + flash_bwd_partial_bytes(batch, n_heads, seq_len) : 0;
 }
 
 int mi_flash_attn_bwd(void* stream, const void* Q, const void* K, const void* V, const void* O,
@@ -859,8 +865,13 @@ int mi_flash_attn_bwd(void* stream, const void* Q, const void* K, const void* V,
   p.scale_log2 = (float)(1.4426950408889634 / std::sqrt((double)head_dim));
   // With room for dS^T the dK/dV kernel writes it and dQ = scale * dS K is one batched
   // GEMM (5 MFMA products instead of 7); otherwise the dQ kernel recomputes S and dP.
-  const size_t need = mi_flash_attn_bwd_workspace_size(batch, n_heads, seq_len);
+  // Room beyond dS^T holds the partials of the balanced dK/dV schedule.
+  const size_t need = flash_dst_bytes(batch, n_heads, seq_len);
   p.dsT = (workspace && need && workspace_bytes >= need && aligned16(workspace)) ? workspace : nullptr;
+  p.part = p.dsT ? (float*)((char*)workspace + need) : nullptr;
+  p.part_bytes = p.dsT ? workspace_bytes - need : 0;
+  p.cus = current_cus();
+  p.n_units = p.n_slots = p.n_split = 0;
   if (p.dsT && causal) {
     // Causal skipping in the dQ GEMM works on whole K tiles up to the end of a
     // 128-row output tile; the dK/dV kernel writes dS^T (zeros included) for every

@@ -233,7 +233,11 @@ def test_flash_backward_noncausal(mi, dev, oracle, ws):
 
 def test_flash_backward_layouts_and_determinism(mi, dev, oracle):
     """O/dO in [B,nH,T,d] give the same gradients as [B,T,nH*d], bit for bit, and two
-    launches agree bit for bit (no atomics)."""
+    launches agree bit for bit (no atomics), in the three schedules: dS^T form with the
+    balanced dK/dV units (full workspace), dS^T form with one workgroup per key block
+    (workspace for dS^T only), and the dQ kernel (no workspace).  The last two share
+    the dK/dV kernel and its order of summation: identical dK and dV; the balanced
+    units sum partials, equal to them within the bf16 bar."""
     import torch
 
     Bn, nH, nKV, T, d = 1, 8, 2, 384, 128
@@ -241,24 +245,30 @@ def test_flash_backward_layouts_and_determinism(mi, dev, oracle):
     Q, K, V, dO = (to_dev(x, dev, True) for x in (q, k, v, do))
     lse = torch.empty((Bn, nH, T), dtype=torch.float32, device=dev)
     O = mi.flash_attn_fwd(Q, K, V, lse=lse)
-    for ws in ("auto", None):
+    dst_only = torch.empty((Bn * nH * T * T,), dtype=torch.bfloat16, device=dev)
+    got = {}
+    for name, ws in (("balanced", "auto"), ("per_block", dst_only), ("dq_kernel", None)):
         g1 = mi.flash_attn_bwd(Q, K, V, O, dO, lse, workspace=ws)
         g2 = mi.flash_attn_bwd(Q, K, V, O, dO, lse, workspace=ws)
         O4 = O.view(Bn, T, nH, d).transpose(1, 2).contiguous()
         dO4 = dO.view(Bn, T, nH, d).transpose(1, 2).contiguous()
         g3 = mi.flash_attn_bwd(Q, K, V, O4, dO4, lse, layout="bhtd", workspace=ws)
         for a, b_, c in zip(g1, g2, g3):
-            assert torch.equal(a, b_), "backward differs between launches"
-            assert torch.equal(a, c), "backward differs between output layouts"
-        if ws is None:  # the two forms share the dK / dV kernel: identical dK and dV
-            assert torch.equal(g1[1], g_auto[1]) and torch.equal(g1[2], g_auto[2])
-        else:
-            g_auto = g1
+            assert torch.equal(a, b_), f"{name}: backward differs between launches"
+            assert torch.equal(a, c), f"{name}: backward differs between output layouts"
+        got[name] = g1
+    assert torch.equal(got["per_block"][1], got["dq_kernel"][1])
+    assert torch.equal(got["per_block"][2], got["dq_kernel"][2])
+    assert torch.equal(got["per_block"][0], got["balanced"][0])  # same dS^T, same dQ GEMM
+    for i, nm in ((1, "dK"), (2, "dV")):
+        check(host(got["balanced"][i]), host(got["per_block"][i]).astype(np.float64), TOL_BF16,
+              f"balanced {nm}")
 
 
 def test_flash_backward_config4(mi, dev, oracle):
     """Benchmark configuration 4 backward (B=8, 16/4 heads, T=1024, d=128) vs the oracle on
-    batch elements 0 and 7."""
+    batch elements 0 and 7 (the workspace form: key blocks 0-3 of every KV head cut into
+    two balanced units each, their partials summed by the reduction kernel)."""
     import torch
 
     Bn, nH, nKV, T, d = 8, 16, 4, 1024, 128
