@@ -108,6 +108,11 @@ size_t mi_gemm_workspace_size(int transA, int transB, int64_t M, int64_t N, int6
 /*
  * General GEMM with fused epilogue.  A and B share one input dtype (MI_BF16 or
  * MI_F32); C is MI_BF16 or MI_F32.  workspace may be NULL (then no split-K).
+ * With epi->A2 (SiLU-gate prologue), bf16 inputs, transA = 0 and a 16-byte
+ * aligned workspace of at least M*K*2 bytes, SiLU(A) (.) A2 is written to the
+ * workspace in one pass (bf16, as the prologue rounds it) and the GEMM runs on
+ * it with the rest of the workspace; otherwise the prologue is applied as each
+ * A tile is loaded.
  * Replaces metal_bridge::gemm_bf16 (MetalBridge.hpp:39-42), gemm_proj (:121),
  * gemm_backward (:122-123), gemm_proj_trans_b (:124-125), gemm_ffn (:119-120,
  * via epi->B2) and fused_swiglu_gemm (:44-46, via epi->A2), and the residual

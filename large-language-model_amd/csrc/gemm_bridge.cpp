@@ -127,7 +127,17 @@ int gemm(int ta, int tb, size_t M, size_t N, size_t K, float alpha, const void* 
   const int64_t ldb = tb ? (int64_t)K : (int64_t)N;
   hipStream_t st = get_stream();
   size_t ws_bytes = 0;
-  void* ws = epi ? nullptr : workspace_for(ta, tb, M, N, K, dt_in, dt_c, &ws_bytes);
+  void* ws = nullptr;
+  if (!epi) {
+    ws = workspace_for(ta, tb, M, N, K, dt_in, dt_c, &ws_bytes);
+  } else if (epi->A2 && dt_in == MI_BF16) {
+    // room for SiLU(A) * A2 (bf16, 256-byte rounded), which mi_gemm then writes in
+    // one pass before a plain GEMM, and the split-K need of that GEMM after it
+    const size_t act = (M * K * 2 + 255) / 256 * 256;
+    ws = grow_workspace(act + mi_gemm_workspace_size(ta, tb, (int64_t)M, (int64_t)N, (int64_t)K, dt_in,
+                                                     dt_c, 1),
+                        &ws_bytes);
+  }
   return mi_gemm(st, ta, tb, (int64_t)M, (int64_t)N, (int64_t)K, alpha, A, lda, B, ldb, dt_in, beta,
                  C, (int64_t)N, dt_c, epi, ws, ws_bytes);
 }

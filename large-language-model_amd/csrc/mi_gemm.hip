@@ -159,6 +159,22 @@ __global__ void __launch_bounds__(256) splitk_reduce_kernel(Params p) {
   }
 }
 
+// act[m, k] = SiLU(G[m, k]) * U[m, k] for the SiLU-gate prologue run as its own
+// pass (bf16, 8 elements per thread, K a multiple of 8; G and U share the
+// leading dimension ld, act is packed with leading dimension K).  The same
+// arithmetic as the in-load prologue (swiglu_chunk): fp32, rounded to bf16.
+__global__ void __launch_bounds__(256) swiglu_act_kernel(const __bf16* G, const __bf16* U, int64_t ld,
+                                                         int64_t M, int64_t K, __bf16* act) {
+  const int64_t cpr = K / 8;  // 16-byte chunks per row
+  const int64_t n = M * cpr;
+  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (int64_t)gridDim.x * 256) {
+    const int64_t m = i / cpr, c = i - m * cpr;
+    const u32x4_t g = *(const u32x4_t*)(G + m * ld + c * 8);
+    const u32x4_t u = *(const u32x4_t*)(U + m * ld + c * 8);
+    *(u32x4_t*)(act + m * K + c * 8) = swiglu_chunk<__bf16>(g, u);
+  }
+}
+
 // ---- planning ------------------------------------------------------------------
 
 struct Plan {
@@ -423,6 +439,31 @@ int run(const Problem& P, hipStream_t stream) {
   };
   const bool fast = vecA && vecB && mult(a_contig) && mult(b_contig) && extA < lim && extB < lim &&
                     span_ok(!P.transA, a_rows, P.lda) && span_ok(P.transB != 0, b_rows, P.ldb);
+
+  // SiLU-gate prologue as its own pass when the workspace holds SiLU(A) * A2 (bf16,
+  // one matrix, 16-byte rows): the activation is written once and the GEMM runs
+  // the direct-to-LDS kernel on it, where the in-load prologue would recompute it
+  // for every column tile in the register-staged loader (configuration 3's down
+  // projection 8192x2048x5632: 426 us in-load vs about 210 us in two passes).
+  if (mode == MODE_PROLOGUE && P.dtype_in == MI_BF16 && !P.transA && P.K > 0 && b.batch == 1 &&
+      b.k_segments == 1 && vecA && P.K % 8 == 0 && aligned16(P.ws) &&
+      P.ws_bytes >= (size_t)(P.M * P.K * 2)) {
+    const size_t act_bytes = (size_t)((P.M * P.K * 2 + 255) / 256 * 256);
+    __bf16* act = (__bf16*)P.ws;
+    const int64_t chunks = P.M * (P.K / 8);
+    const int64_t grid = std::min<int64_t>(cdiv(chunks, 256), 8 * (int64_t)current_cus());
+    hipLaunchKernelGGL(swiglu_act_kernel, dim3((unsigned)grid), dim3(256), 0, stream, (const __bf16*)P.A,
+                       (const __bf16*)P.ep.A2, P.lda, P.M, P.K, act);
+    const hipError_t ea = hipGetLastError();
+    if (ea != hipSuccess) return fail(MI_ERR_HIP, "SiLU-gate pass launch: %s", hipGetErrorString(ea));
+    Problem Q = P;
+    Q.A = act;
+    Q.lda = P.K;
+    Q.ep.A2 = nullptr;
+    Q.ws = P.ws_bytes > act_bytes ? (char*)P.ws + act_bytes : nullptr;
+    Q.ws_bytes = P.ws_bytes > act_bytes ? P.ws_bytes - act_bytes : 0;
+    return run(Q, stream);
+  }
 
   const int64_t Ktot = P.K * b.k_segments;
   const int64_t ws_elems = P.ws ? (int64_t)(P.ws_bytes / sizeof(float)) : 0;

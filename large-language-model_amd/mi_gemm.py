@@ -326,10 +326,19 @@ def gemm_bf16(A, B, C, M, N, K, transA=False, transB=False, is_forward=False):
 
 
 def fused_swiglu_gemm(gate_proj, up_proj, B, C, M, N, K):
-    """MetalBridge.hpp:44-46: C = (SiLU(gate) * up) @ B (fused_swiglu_gemm.metal:48-77)."""
+    """MetalBridge.hpp:44-46: C = (SiLU(gate) * up) @ B (fused_swiglu_gemm.metal:48-77).
+    With the pooled workspace holding SiLU(gate) * up, mi_gemm writes it in one pass and
+    runs the plain GEMM on it (as the C++ bridge does)."""
     if M == 0 or N == 0 or K == 0:
         return
-    gemm(gate_proj, B, C, M, N, K, A2=up_proj)
+    ws = None
+    if gate_proj.dtype == _torch().bfloat16:
+        need = (M * K * 2 + 255) // 256 * 256 + workspace_size(0, 0, M, N, K, MI_BF16, _dt(C))
+        ws = _WS_POOL.get(C.device)
+        if ws is None or ws.numel() * 4 < need:
+            ws = _torch().empty((need + 3) // 4, dtype=_torch().float32, device=C.device)
+            _WS_POOL[C.device] = ws
+    gemm(gate_proj, B, C, M, N, K, A2=up_proj, workspace=ws)
 
 
 def gemm_ffn(a, b_gate, b_up, c, M, N, K):

@@ -178,6 +178,44 @@ def test_prologue_silu_gate(mi, dev, oracle, bf16):
         check(got, ref, _tol(bf16), f"prologue {M}x{N}x{K}")
 
 
+def test_prologue_two_pass(mi, dev, oracle):
+    """bf16 SiLU-gate prologue with a workspace for SiLU(G) * U: one activation pass,
+    then the plain GEMM on it (the rest of the workspace left for its split-K).
+    Shapes: a full-tile NN and NT case, edge tiles with padded leading dimensions,
+    and a K that is not a multiple of 8 (in-load prologue, the workspace unused)."""
+    import torch
+
+    ws = torch.empty(8 << 20, dtype=torch.float32, device=dev)
+    for (M, N, K), tB, pad in [((512, 512, 512), 0, (0, 0, 0)), ((512, 256, 1024), 1, (0, 0, 0)),
+                               ((300, 200, 160), 0, (8, 4, 2)), ((64, 96, 100), 0, (0, 0, 0))]:
+        got, ref = _run(mi, dev, oracle, M, N, K, 0, tB, True, seed=43, prologue=True, pad=pad,
+                        ws=ws)
+        check(got, ref, TOL_BF16, f"two-pass prologue {M}x{N}x{K} tB={tB}")
+
+
+def test_fused_swiglu_gemm_config3_down(mi, dev, oracle):
+    """The reference-named fused_swiglu_gemm at configuration 3's down projection
+    (8192 x 2048, K = 5632): sampled rows against the oracle's SiLU-gate product and
+    the column / row checksums of (SiLU(G) * U) W."""
+    import torch
+
+    M, N, K = 8192, 2048, 5632
+    g = inputs(oracle, (M, K), 61, 1.0)
+    u = inputs(oracle, (M, K), 62, 1.0)
+    w = inputs(oracle, (K, N), 63, 0.02)
+    G, U, W = to_dev(g, dev, True), to_dev(u, dev, True), to_dev(w, dev, True)
+    C = torch.empty((M, N), dtype=torch.bfloat16, device=dev)
+    mi.fused_swiglu_gemm(G, U, W, C, M, N, K)
+    torch.cuda.synchronize()
+    rows = sample_rows(M, 6, 61)
+    got = host(C)
+    check(got[rows], oracle.gemm(0, 0, M, N, K, g, w, mode=2, A2=u, rows=rows), TOL_BF16, "down fwd rows")
+    act = oracle.round_bf16((g / (1.0 + np.exp(-g.astype(np.float64)))) * u)
+    col, row = checksums(act, w)
+    check(got.sum(axis=0), col, TOL_BF16, "down fwd column checksum")
+    check(got.sum(axis=1), row, TOL_BF16, "down fwd row checksum")
+
+
 def _split_of(mi, tA, tB, M, N, K, bf16, ws):
     text = mi.describe(tA, tB, M, N, K, mi.MI_BF16 if bf16 else mi.MI_F32,
                        workspace_bytes=ws.numel() * 4)
