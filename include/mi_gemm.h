@@ -226,6 +226,25 @@ int mi_flash_attn_bwd(void* stream, const void* Q, const void* K, const void* V,
 size_t mi_flash_attn_bwd_workspace_size(int64_t batch, int64_t n_heads, int64_t seq_len);
 
 /*
+ * mi_flash_attn_fwd / mi_flash_attn_bwd with the softmax scale given (the two
+ * functions above use 1/sqrt(head_dim), Attention.cpp:208).  For a head dimension
+ * d below 128 (the reference kernel's 64, flash_attn_fwd.metal:31), copy Q, K, V
+ * (and dO) into 128-column rows whose columns d..127 are zero and pass
+ * scale = 1/sqrt(d): the zero columns add exact zeros to every score, and the
+ * output and gradient columns d..127 come out zero.  The C++ bridge does this for
+ * flash_attn_fwd / fused_attn_bwd with a head_dim below 128.  scale must be
+ * positive and finite.
+ */
+int mi_flash_attn_fwd_scaled(void* stream, const void* Q, const void* K, const void* V, void* O,
+                             float* lse, int64_t batch, int64_t n_heads, int64_t n_kv, int64_t seq_len,
+                             int64_t head_dim, int32_t causal, int32_t o_layout, float scale);
+int mi_flash_attn_bwd_scaled(void* stream, const void* Q, const void* K, const void* V, const void* O,
+                             const void* dO, const float* lse, void* dQ, void* dK, void* dV, float* delta,
+                             int64_t batch, int64_t n_heads, int64_t n_kv, int64_t seq_len,
+                             int64_t head_dim, int32_t causal, int32_t o_layout, void* workspace,
+                             size_t workspace_bytes, float scale);
+
+/*
  * Softmax cross-entropy over rows of logits, the loss after the LM head.  For
  * row r (a token) with target y = targets[r]:
  *   p[v] = exp(x[v] - max x) / sum_v exp(x[v] - max x)

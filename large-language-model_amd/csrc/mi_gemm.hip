@@ -819,6 +819,13 @@ int mi_softmax_bwd(void* stream, const void* P, void* dP, int64_t rows, int64_t 
 int mi_flash_attn_fwd(void* stream, const void* Q, const void* K, const void* V, void* O,
                       float* lse, int64_t batch, int64_t n_heads, int64_t n_kv, int64_t seq_len,
                       int64_t head_dim, int32_t causal, int32_t o_layout) {
+  return mi_flash_attn_fwd_scaled(stream, Q, K, V, O, lse, batch, n_heads, n_kv, seq_len, head_dim,
+                                  causal, o_layout, (float)(1.0 / std::sqrt((double)(head_dim > 0 ? head_dim : 1))));
+}
+
+int mi_flash_attn_fwd_scaled(void* stream, const void* Q, const void* K, const void* V, void* O,
+                             float* lse, int64_t batch, int64_t n_heads, int64_t n_kv, int64_t seq_len,
+                             int64_t head_dim, int32_t causal, int32_t o_layout, float scale) {
   if (batch < 0 || n_heads < 0 || n_kv < 0 || seq_len < 0)
     return fail(MI_ERR_SHAPE, "negative size");
   if (batch == 0 || n_heads == 0 || seq_len == 0) return MI_OK;
@@ -846,7 +853,8 @@ int mi_flash_attn_fwd(void* stream, const void* Q, const void* K, const void* V,
   p.causal = causal != 0;
   p.o_bthd = o_layout == MI_ATTN_O_BTHD;
   p.q_blocks = flash_fwd_blocks(p.T);
-  p.scale_log2 = (float)(1.4426950408889634 / std::sqrt((double)head_dim));
+  if (!(scale > 0.0f) || !std::isfinite(scale)) return fail(MI_ERR_SHAPE, "softmax scale must be positive");
+  p.scale_log2 = (float)(1.4426950408889634 * (double)scale);
   if ((int64_t)p.B * p.nH * p.q_blocks > INT32_MAX) return fail(MI_ERR_SHAPE, "too many blocks");
   hipError_t e = launch_flash_fwd(p, (int)head_dim, (hipStream_t)stream);
   return e == hipSuccess ? MI_OK : fail(MI_ERR_HIP, "flash attention launch: %s", hipGetErrorString(e));
@@ -869,6 +877,16 @@ int mi_flash_attn_bwd(void* stream, const void* Q, const void* K, const void* V,
                       int64_t batch, int64_t n_heads, int64_t n_kv, int64_t seq_len,
                       int64_t head_dim, int32_t causal, int32_t o_layout, void* workspace,
                       size_t workspace_bytes) {
+  return mi_flash_attn_bwd_scaled(stream, Q, K, V, O, dO, lse, dQ, dK, dV, delta, batch, n_heads, n_kv,
+                                  seq_len, head_dim, causal, o_layout, workspace, workspace_bytes,
+                                  (float)(1.0 / std::sqrt((double)(head_dim > 0 ? head_dim : 1))));
+}
+
+int mi_flash_attn_bwd_scaled(void* stream, const void* Q, const void* K, const void* V, const void* O,
+                             const void* dO, const float* lse, void* dQ, void* dK, void* dV, float* delta,
+                             int64_t batch, int64_t n_heads, int64_t n_kv, int64_t seq_len,
+                             int64_t head_dim, int32_t causal, int32_t o_layout, void* workspace,
+                             size_t workspace_bytes, float scale) {
   if (batch < 0 || n_heads < 0 || n_kv < 0 || seq_len < 0)
     return fail(MI_ERR_SHAPE, "negative size");
   if (batch == 0 || n_heads == 0 || seq_len == 0) return MI_OK;
@@ -902,8 +920,9 @@ int mi_flash_attn_bwd(void* stream, const void* Q, const void* K, const void* V,
   p.o_bthd = o_layout == MI_ATTN_O_BTHD;
   p.q_blocks = flash_fwd_blocks(p.T);
   p.k_blocks = flash_bwd_key_blocks(p.T);
-  p.scale = (float)(1.0 / std::sqrt((double)head_dim));
-  p.scale_log2 = (float)(1.4426950408889634 / std::sqrt((double)head_dim));
+  if (!(scale > 0.0f) || !std::isfinite(scale)) return fail(MI_ERR_SHAPE, "softmax scale must be positive");
+  p.scale = scale;
+  p.scale_log2 = (float)(1.4426950408889634 * (double)scale);
   // With room for dS^T the dK/dV kernel writes it and dQ = scale * dS K is one batched
   // GEMM (5 MFMA products instead of 7); otherwise the dQ kernel recomputes S and dP.
   // Room beyond dS^T holds the partials of the balanced dK/dV schedule.

@@ -37,7 +37,7 @@ C_SYMBOLS = (
     "mi_cross_entropy", "mi_rmsnorm_fwd", "mi_rmsnorm_bwd", "mi_rmsnorm_bwd_workspace_size",
     "mi_convert_matrix", "mi_flash_attn_bwd_workspace_size", "mi_profiler_enable",
     "mi_profiler_begin_step", "mi_profiler_count", "mi_profiler_record", "mi_profiler_totals",
-    "mi_profiler_reset", "mi_gemm_noalloc",
+    "mi_profiler_reset", "mi_gemm_noalloc", "mi_flash_attn_fwd_scaled", "mi_flash_attn_bwd_scaled",
 )
 MI_ATTN_O_BHTD, MI_ATTN_O_BTHD = 0, 1
 
@@ -128,9 +128,13 @@ def load_library():
     L.mi_stream_sync.argtypes = [vp]
     L.mi_flash_attn_fwd.restype = ctypes.c_int
     L.mi_flash_attn_fwd.argtypes = [vp, vp, vp, vp, vp, vp, i64, i64, i64, i64, i64, i32, i32]
+    L.mi_flash_attn_fwd_scaled.restype = ctypes.c_int
+    L.mi_flash_attn_fwd_scaled.argtypes = L.mi_flash_attn_fwd.argtypes + [ctypes.c_float]
+    L.mi_flash_attn_bwd_scaled.restype = ctypes.c_int
     L.mi_flash_attn_bwd.restype = ctypes.c_int
     L.mi_flash_attn_bwd.argtypes = [vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, i64, i64, i64, i64,
                                     i64, i32, i32, vp, ctypes.c_size_t]
+    L.mi_flash_attn_bwd_scaled.argtypes = L.mi_flash_attn_bwd.argtypes + [ctypes.c_float]
     L.mi_flash_attn_bwd_workspace_size.restype = ctypes.c_size_t
     L.mi_flash_attn_bwd_workspace_size.argtypes = [i64, i64, i64]
     L.mi_cross_entropy.restype = ctypes.c_int
@@ -562,6 +566,24 @@ def flash_attn_fwd(Q4, K4, V4, O=None, lse=None, causal=True, layout="bthd", syn
     for t in (Q4, K4, V4):
         if t.dtype != torch.bfloat16 or not t.is_contiguous():
             raise ValueError("Q, K, V must be contiguous bf16 tensors")
+    if d < 128 and d % 8 == 0:
+        # the d = 128 kernels on rows padded with zero columns, at the scale of d
+        pad = lambda t: torch.nn.functional.pad(t, (0, 128 - d)).contiguous()
+        Qp, Kp, Vp = pad(Q4), pad(K4), pad(V4)  # held until the kernel has been queued
+        Op = torch.empty((Bn, nH, T, 128), dtype=torch.bfloat16, device=Q4.device)
+        st = load_library().mi_flash_attn_fwd_scaled(
+            _stream(), _ptr(Qp), _ptr(Kp), _ptr(Vp), _ptr(Op), _ptr(lse), Bn, nH, nKV, T,
+            128, int(bool(causal)), MI_ATTN_O_BHTD, 1.0 / math.sqrt(d))
+        _check("mi_flash_attn_fwd_scaled", st)
+        res = Op[..., :d]
+        res = res.permute(0, 2, 1, 3).reshape(Bn, T, nH * d) if layout == "bthd" else res
+        if O is None:
+            O = res.contiguous()
+        else:
+            O.copy_(res.reshape(O.shape))
+        if sync is None and _scope_depth == 0:
+            torch.cuda.synchronize(Q4.device)
+        return O
     if O is None:
         shape = (Bn, T, nH * d) if layout == "bthd" else (Bn, nH, T, d)
         O = torch.empty(shape, dtype=torch.bfloat16, device=Q4.device)
@@ -587,6 +609,32 @@ def flash_attn_bwd(Q4, K4, V4, O, dO, lse, causal=True, layout="bthd", sync=None
     for t in (Q4, K4, V4, O, dO):
         if t.dtype != torch.bfloat16 or not t.is_contiguous():
             raise ValueError("Q, K, V, O, dO must be contiguous bf16 tensors")
+    if d < 128 and d % 8 == 0:
+        # the d = 128 kernels on rows padded with zero columns, at the scale of d
+        pad = lambda t: torch.nn.functional.pad(t, (0, 128 - d)).contiguous()
+        if layout == "bthd":
+            padl = lambda t: pad(t.reshape(Bn, T, nH, d)).reshape(Bn, T, nH * 128)
+        else:
+            padl = pad
+        dQp = torch.empty((Bn, nH, T, 128), dtype=torch.bfloat16, device=Q4.device)
+        dKp = torch.empty((Bn, nKV, T, 128), dtype=torch.bfloat16, device=Q4.device)
+        dVp = torch.empty_like(dKp)
+        delta = torch.empty((Bn, nH, T), dtype=torch.float32, device=Q4.device)
+        code = MI_ATTN_O_BTHD if layout == "bthd" else MI_ATTN_O_BHTD
+        if isinstance(workspace, str) and workspace == "auto":
+            nbytes = load_library().mi_flash_attn_bwd_workspace_size(Bn, nH, T)
+            workspace = torch.empty((nbytes // 2,), dtype=torch.bfloat16, device=Q4.device) if nbytes else None
+        ws_bytes = 0 if workspace is None else workspace.numel() * workspace.element_size()
+        Qp, Kp, Vp, Op, dOp = pad(Q4), pad(K4), pad(V4), padl(O), padl(dO)  # held until queued
+        st = load_library().mi_flash_attn_bwd_scaled(
+            _stream(), _ptr(Qp), _ptr(Kp), _ptr(Vp), _ptr(Op), _ptr(dOp), _ptr(lse),
+            _ptr(dQp), _ptr(dKp), _ptr(dVp), _ptr(delta), Bn, nH, nKV, T, 128, int(bool(causal)), code,
+            _ptr(workspace), ws_bytes, 1.0 / math.sqrt(d))
+        _check("mi_flash_attn_bwd_scaled", st)
+        out = (dQp[..., :d].contiguous(), dKp[..., :d].contiguous(), dVp[..., :d].contiguous())
+        if sync is None and _scope_depth == 0:
+            torch.cuda.synchronize(Q4.device)
+        return out
     dQ = torch.empty_like(Q4)
     dK = torch.empty_like(K4)
     dV = torch.empty_like(V4)

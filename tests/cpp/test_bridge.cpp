@@ -248,7 +248,7 @@ int main() {
   // P = 1/(q+1), so O[q] = mean(V[0..q]), dV[k] = sum_{q>=k} dO[q] / (q+1), dK = 0
   // (dK = scale dS^T Q), dQ[q] = scale sum_{k<=q} dS[q,k] K[k] with dS = P (dP - rowsum(P dP)).
   // head_dim 128 runs the fused kernels (GB-11, GB-12); 64, the reference kernel's, the
-  // materialised path (GB-16, GB-17).
+  // fused kernels on zero-padded rows (GB-16, GB-17).
   for (size_t d : {128, 64}) {
     const size_t B = 1, nH = 2, nKV = 1, T = 96, g = nH / nKV;
     const bool fused = d == 128;
@@ -278,7 +278,7 @@ int main() {
         }
     row(fused ? "GB-11" : "GB-16",
         fused ? "flash_attn_fwd, Q = 0: O[q] = mean(V[0..q]), max rel <= 1e-2"
-              : "flash_attn_fwd d=64 (materialised), Q = 0: O[q] = mean(V[0..q]), <= 1e-2",
+              : "flash_attn_fwd d=64 (fused on zero-padded rows), Q = 0: O[q] = mean(V[0..q]), <= 1e-2",
         ok && err <= 1e-2 * mx, std::to_string(err / mx));
     mi_bridge::fused_attn_bwd(dq_in, dk_in, dv_in, dgo, dQg, dKg, dVg, B, nH, nKV, T, d);
     ok = mi_bridge::last_status() == MI_OK;
@@ -315,7 +315,7 @@ int main() {
     const double edv = rel(rdv, hdv), edq = rel(rdq, hdq);
     row(fused ? "GB-12" : "GB-17",
         fused ? "fused_attn_bwd, Q = 0: dV, dQ closed forms (1e-2), dK = 0"
-              : "fused_attn_bwd d=64 (materialised), Q = 0: dV, dQ closed forms, dK = 0",
+              : "fused_attn_bwd d=64 (fused on zero-padded rows), Q = 0: dV, dQ closed forms, dK = 0",
         ok && edv <= 1e-2 && edq <= 1e-2 && dk_zero,
         std::to_string(edv) + " " + std::to_string(edq));
     dfree(dq_in); dfree(dk_in); dfree(dv_in); dfree(dgo); dfree(dO_out);
