@@ -592,24 +592,39 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2)))
 
 // dK and dV for 128 keys of one (batch, KV head): the query tiles (64 rows) of
 // every query head of the KV group stream through a two-stage LDS ring (Q, dO,
-// the forward's log-sum-exp and D); a wave keeps its 32 keys' K and V fragments
-// and dK / dV accumulators in registers, computes S^T = K Q^T and dP^T = V dO^T
-// with one lane per key, P^T and dS^T = P^T (dP^T - D) in registers, and
-// accumulates dV += P^T dO and dK += scale * dS^T Q.  The KV-group reduction
-// (Attention.cpp:332,344-345) is the loop over the group's heads.  DS: also store
-// dS^T (bf16, [B, nH, key, query]) for dQ = scale * dS K as a batched GEMM.
+// the forward's log-sum-exp and D); S^T = K Q^T and dP^T = V dO^T with one lane
+// per key, P^T and dS^T = P^T (dP^T - D) in registers, then dV += P^T dO and
+// dK += scale * dS^T Q.  The KV-group reduction (Attention.cpp:332,344-345) is the
+// loop over the group's heads.  DS: also store dS^T (bf16, [B, nH, key, query]) for
+// dQ = scale * dS K as a batched GEMM.
+//
+// Eight waves, two per SIMD: waves w and w + 4 hold the same 32 keys and take the
+// first and second 32-query half of every tile, so one wave's softmax (VALU) runs
+// under the other's MFMAs.  The 128 keys' K and V tiles stay in LDS for the whole
+// unit and are read as MFMA fragments each tile, which leaves a wave its 32 x d dK
+// and dV accumulators within the 256 registers of two waves per SIMD; at the end
+// the halves are added in LDS (first half + second half).  Configuration 4's
+// dK/dV: 117 us against 128 us for four waves (one per SIMD, K and V fragments in
+// registers, the two halves interleaved in one wave).
 template <int D, bool DS>
-__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1)))
+__global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2)))
     flash_bwd_dkdv_kernel(FbParams p) {
   using Tl = FaTile<D>;
   using Rd = FaReads<D>;
   constexpr int NS = D / 16, NC = D / 32;
-  constexpr int QT = FA_BK;                      // query rows per tile
+  constexpr int QT = FA_BK;                          // query rows per tile
+  constexpr int KVB = 128 * Tl::ROW;                 // one 128-key K or V tile
+  constexpr int NU = Tl::NBLK / 8;                   // 1 KB DMA blocks per wave per 64-row tile
+  constexpr int NUK = KVB / 1024 / 8;                // ... per 128-key tile
   constexpr int STAGE = 2 * Tl::BYTES + 2 * QT * 4;  // Q, dO, lse, D
-  __shared__ __attribute__((aligned(16))) char smem[2 * STAGE];
+  constexpr int RING = 2 * KVB;                      // the ring follows K and V
+  static_assert(NS == 8 && NC == 4, "d = 128");
+  __shared__ __attribute__((aligned(16))) char smem[RING + 2 * STAGE];
   const uint32_t lds0 = lds_addr(smem);
+  const uint32_t lk = lds0, lv = lds0 + KVB, lr = lds0 + RING;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int wave_u = uniform(wave);
+  const int wq = uniform(wave_u & 3), qh = uniform(wave_u >> 2);
   const int h32 = lane >> 5, l32 = lane & 31;
 
   // Work unit: with a schedule, unit u (largest first) of every (batch, KV head) in
@@ -634,49 +649,60 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1)))
   const int b = uniform(bkv / p.nKV), kvh = uniform(bkv - (bkv / p.nKV) * p.nKV);
   const int T = p.T;
   const int k0 = kbi * 128;
-  const int kw = k0 + 32 * wave_u;
+  const int kw = k0 + 32 * wq;
   const int key = kw + l32;
   const bool live = key < T;
 
   const __bf16* Kb = (const __bf16*)p.K + ((int64_t)bkv * T) * D;
   const __bf16* Vb = (const __bf16*)p.V + ((int64_t)bkv * T) * D;
-  u32x4_t kf[NS], vf[NS];
+  // K and V tiles of the 128 keys into LDS (keys past T read as zero)
+  {
+    const uint32_t ext = (uint32_t)((T - k0) * Tl::ROW);
+    const __amdgpu_buffer_rsrc_t rk = scalar_rsrc(uniform(Kb + (int64_t)k0 * D), ext);
+    const __amdgpu_buffer_rsrc_t rv = scalar_rsrc(uniform(Vb + (int64_t)k0 * D), ext);
 #pragma unroll
-  for (int s = 0; s < NS; ++s) {
-    const int dd = 16 * s + 8 * h32;
-    if (live) {
-      kf[s] = *(const u32x4_t*)(Kb + (int64_t)key * D + dd);
-      vf[s] = *(const u32x4_t*)(Vb + (int64_t)key * D + dd);
-    } else {
-      kf[s] = u32x4_t{0u, 0u, 0u, 0u};
-      vf[s] = u32x4_t{0u, 0u, 0u, 0u};
+    for (int u = 0; u < NUK; ++u) {
+      const int blk = wave * NUK + u;
+      const uint32_t off = fa_dma_off<D>(blk, lane, Tl::ROW);
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(
+          rk, (__attribute__((address_space(3))) void*)(uintptr_t)(lk + (uint32_t)(blk * 1024)), 16, (int)off,
+          0, 0, 0);
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(
+          rv, (__attribute__((address_space(3))) void*)(uintptr_t)(lv + (uint32_t)(blk * 1024)), 16, (int)off,
+          0, 0, 0);
     }
   }
+  // Fragment s (d chunk 2s + h32) of this lane's key row in the K or V tile.
+  const int krow = 32 * wq + l32;
+  auto kv_frag = [&](uint32_t t, int s) __attribute__((always_inline)) {
+    const uint32_t a = t + (uint32_t)(krow * Tl::ROW + 16 * Tl::x_pos(krow, 2 * s + h32));
+    return *(const lds_u32x4_t*)(uintptr_t)a;
+  };
 
   const int nqt = (T + QT - 1) / QT;
   const int qt0 = uniform(p.causal ? k0 / QT : 0);
   const int per_h = uniform(nqt - qt0);
   const int total = uniform(per_h > 0 ? per_h * p.group : 0);
-  if (ie < 0) ie = total;  // this workgroup runs iterations [ib, ie) of the key block
-  const int go_stride = (p.o_bthd ? p.nH * D : D) * 2;  // bytes between dO rows
+  if (ie < 0) ie = total;
+  const int go_stride = (p.o_bthd ? p.nH * D : D) * 2;
 
-  uint32_t q_off[Tl::NU], g_off[Tl::NU];
+  uint32_t q_off[NU], g_off[NU];
 #pragma unroll
-  for (int u = 0; u < Tl::NU; ++u) {
-    q_off[u] = fa_dma_off<D>(wave * Tl::NU + u, lane, Tl::ROW);
-    g_off[u] = fa_dma_off<D>(wave * Tl::NU + u, lane, go_stride);
+  for (int u = 0; u < NU; ++u) {
+    q_off[u] = fa_dma_off<D>(wave * NU + u, lane, Tl::ROW);
+    g_off[u] = fa_dma_off<D>(wave * NU + u, lane, go_stride);
   }
-  const uint32_t dma_q = lds0 + (uint32_t)(wave_u * Tl::NU * 1024);
+  const uint32_t dma_q = lr + (uint32_t)(wave_u * NU * 1024);
   const uint32_t dma_g = dma_q + Tl::BYTES;
-  const uint32_t dma_l = lds0 + 2 * Tl::BYTES + (uint32_t)(wave_u * QT * 4);  // waves 0, 1
-  auto tile_of = [&](int it, int& h, int& q0) __attribute__((always_inline)) {
+  const uint32_t dma_l = lr + 2 * Tl::BYTES + (uint32_t)(wave_u * QT * 4);  // waves 0, 1
+  auto tile_at = [&](int it, int& h, int& q0) __attribute__((always_inline)) {
     const int hh = it / per_h;
     h = kvh * p.group + hh;
     q0 = (qt0 + (it - hh * per_h)) * QT;
   };
   auto issue = [&](int it) __attribute__((always_inline)) {
     int h, q0;
-    tile_of(it, h, q0);
+    tile_at(it, h, q0);
     const int bh = b * p.nH + h;
     const int rows = T - q0;
     const __amdgpu_buffer_rsrc_t rq =
@@ -686,7 +712,7 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1)))
                                                   (uint32_t)((rows - 1) * go_stride + Tl::ROW));
     const uint32_t st = (uint32_t)((it & 1) * STAGE);
 #pragma unroll
-    for (int u = 0; u < Tl::NU; ++u) {
+    for (int u = 0; u < NU; ++u) {
       __builtin_amdgcn_raw_ptr_buffer_load_lds(
           rq, (__attribute__((address_space(3))) void*)(uintptr_t)(dma_q + st + (uint32_t)(u * 1024)), 16,
           (int)q_off[u], 0, 0, 0);
@@ -711,140 +737,117 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1)))
     for (int e = 0; e < 16; ++e) dk[c][e] = dv[c][e] = 0.0f;
   const float sl2 = p.scale_log2;
 
-  // dS^T rows of this lane's key: registers base..base+7 of a run hold 8 consecutive
-  // queries, stored as one 16-byte buffer store, 4 per tile.  Lanes l and l + 32 hold
-  // the same key, so each key's 64 queries of a tile fill one 128-byte line.  Lanes
-  // past the last key, and runs past the last query (T % 8 == 0, so a run is all in or
-  // all out), get an offset beyond the tile descriptor's range, which the hardware
-  // drops: every wave issues exactly 4 stores per tile, and ring_step's wait counts
-  // them (vmcnt retires in issue order on gfx9-family parts).
+  // dS^T rows of this lane's key: registers 8kk .. 8kk+7 of the wave's half hold 8
+  // consecutive queries, stored as one 16-byte buffer store, 2 per wave and tile.
+  // Lanes l and l + 32 hold the same key, so the two halves' waves fill each key's
+  // 128-byte line of a tile.  Lanes past the last key, and runs past the last query
+  // (T % 8 == 0, so a run is all in or all out), get an offset beyond the tile
+  // descriptor's range, which the hardware drops: every wave issues exactly 2 stores
+  // per tile, and ring_step's wait counts them (vmcnt retires in issue order on
+  // gfx9-family parts).
   const uint32_t ds_lane = live ? (uint32_t)(key * T + 8 * h32) * 2u : 0x80000000u;
-  // The runs of half qh (k-steps 2qh and 2qh + 1); both halves: the 4 stores.
-  auto store_ds = [&](int bh, int q0, int qh, auto&& run) __attribute__((always_inline)) {
+  auto store_ds = [&](int bh, int q0, auto&& run) __attribute__((always_inline)) {
     const __amdgpu_buffer_rsrc_t rs =
         scalar_rsrc(uniform((const uint16_t*)p.dsT + (int64_t)bh * T * T + q0),
                     (uint32_t)(((int64_t)T * T - q0) * 2));
-    const int lim = T - q0 - 8 * h32;  // runs starting below lim exist
+    const int lim = T - q0 - 8 * h32;
 #pragma unroll
-    for (int ks = 2 * qh; ks < 2 * qh + 2; ++ks) {
-      const int c = 32 * (ks >> 1) + 16 * (ks & 1);
+    for (int kk = 0; kk < 2; ++kk) {
+      const int c = 32 * qh + 16 * kk;
       const uint32_t off = c < lim ? ds_lane : 0x80000000u;
-      __builtin_amdgcn_raw_buffer_store_b128(run(ks), rs, off + 2 * c, 0, 0);
+      __builtin_amdgcn_raw_buffer_store_b128(run(kk), rs, off + 2 * c, 0, 0);
     }
   };
-  // One query tile in two 32-query halves, so that each half's softmax (VALU) runs
-  // between MFMAs of the other half: S and dP of half 0; S and dP of half 1 with the
-  // softmax of half 0; dV and dK of half 0 with the softmax of half 1; dV and dK of
-  // half 1.  A wave is alone on its SIMD (488 VGPRs), so nothing else hides the VALU.
+  // One query tile, this wave's 32-query half qh: register i of sacc / pacc is query
+  // q0 + 32qh + 8*h32 + 16((i>>2)>>1) + 4((i>>2)&1) + (i&3) of this lane's key.
   auto block = [&](const int q0, const int bh, const uint32_t st, auto MASK_c) __attribute__((always_inline)) {
     constexpr bool MASK = decltype(MASK_c)::value;
     const uint32_t tq = st, tg = st + Tl::BYTES, tl = st + 2 * Tl::BYTES, td = tl + QT * 4;
-    f32x16_t sacc[2], pacc[2];
+    f32x16_t sacc, pacc;
 #pragma unroll
-    for (int qh = 0; qh < 2; ++qh)
-#pragma unroll
-      for (int e = 0; e < 16; ++e) sacc[qh][e] = pacc[qh][e] = 0.0f;
-    // register i of half qh: query q0 + 32qh + 8*h32 + 16((i>>2)>>1) + 4((i>>2)&1) + (i&3)
-    u32x4_t pf[4], df[4];
-    f32x4_t lv[2], dv4[2];  // log-sum-exp and D of the 8 queries of the current run
-    // Softmax of k-step ks (half ks >> 1), registers base + 2*w2 .. +1 of that half
-    // (base = 8 (ks & 1)): P and dS = P (dP - D) as bf16 pairs.
-    auto soft = [&](const int ks, const int w2) __attribute__((always_inline)) {
-      const int qh = ks >> 1, base = 8 * (ks & 1);
-      const int tix = 32 * qh + 8 * h32 + 16 * (ks & 1);  // tile index of register `base`
-      if (w2 == 0) {  // registers base..base+3 and base+4..base+7: 4 consecutive queries each
-        lv[0] = *(const __attribute__((address_space(3))) f32x4_t*)(uintptr_t)(tl + 4 * tix);
-        lv[1] = *(const __attribute__((address_space(3))) f32x4_t*)(uintptr_t)(tl + 4 * (tix + 4));
-        dv4[0] = *(const __attribute__((address_space(3))) f32x4_t*)(uintptr_t)(td + 4 * tix);
-        dv4[1] = *(const __attribute__((address_space(3))) f32x4_t*)(uintptr_t)(td + 4 * (tix + 4));
-      }
-      const int need = key - (q0 + tix);  // register base + r is visible iff its offset >= need
-      float pv[2], dsv[2];
-#pragma unroll
-      for (int u = 0; u < 2; ++u) {
-        const int r = 2 * w2 + u;  // 0..7 within the run: offsets 0..3, then 4..7
-        const float lse2 = lv[r >> 2][r & 3] * 1.4426950408889634f;
-        float x = __builtin_fmaf(sacc[qh][base + r], sl2, -lse2);
-        if constexpr (MASK) x = r >= need ? x : -INFINITY;
-        pv[u] = __builtin_amdgcn_exp2f(x);
-        dsv[u] = pv[u] * (pacc[qh][base + r] - dv4[r >> 2][r & 3]);
-      }
-      pf[ks][w2] = pack_bf16x2(pv[0], pv[1]);
-      df[ks][w2] = pack_bf16x2(dsv[0], dsv[1]);
-    };
-    // S^T = K Q^T and dP^T = V dO^T of half qh at k-step s
-    auto sdp = [&](const int qh, const int s) __attribute__((always_inline)) {
-      const u32x4_t qr = rd.row(tq, qh, s, h32);
-      const u32x4_t gr = rd.row(tg, qh, s, h32);
-      sacc[qh] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, qr),
-                                                        __builtin_bit_cast(bf16x8_t, kf[s]), sacc[qh], 0, 0, 0);
-      pacc[qh] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, gr),
-                                                        __builtin_bit_cast(bf16x8_t, vf[s]), pacc[qh], 0, 0, 0);
-    };
-    // dV += P^T dO (first operand dO^T), dK += dS^T Q (first operand Q^T) at k-step KS,
-    // with softmax steps of k-step KS + 2 between the MFMAs when KS < 2
-    auto dvdk = [&](auto ks_c) __attribute__((always_inline)) {
-      constexpr int KS = decltype(ks_c)::value;
-      u32x4_t gt[NC], qt[NC];
-#pragma unroll
-      for (int c = 0; c < NC; ++c) {
-        gt[c] = fa_tr_frag<D, KS>(tg, rd.tr[c]);
-        qt[c] = fa_tr_frag<D, KS>(tq, rd.tr[c]);
-      }
-      fa_lds_fence();
-#pragma unroll
-      for (int c = 0; c < NC; ++c) {
-        dv[c] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, gt[c]),
-                                                        __builtin_bit_cast(bf16x8_t, pf[KS]), dv[c], 0, 0, 0);
-        dk[c] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, qt[c]),
-                                                        __builtin_bit_cast(bf16x8_t, df[KS]), dk[c], 0, 0, 0);
-        if constexpr (KS < 2) soft(KS + 2, c);
-      }
-    };
-    static_assert(NS == 8 && NC == 4, "the interleave below assumes d = 128");
-    auto dsrun = [&](int ks) __attribute__((always_inline)) { return df[ks]; };
-#pragma unroll
-    for (int s = 0; s < NS; ++s) sdp(0, s);
+    for (int e = 0; e < 16; ++e) sacc[e] = pacc[e] = 0.0f;
 #pragma unroll
     for (int s = 0; s < NS; ++s) {
-      sdp(1, s);
-      soft(s >> 2, s & 3);  // k-steps 0 and 1: half 0
+      const u32x4_t qr = rd.row(tq, qh, s, h32);
+      const u32x4_t gr = rd.row(tg, qh, s, h32);
+      const u32x4_t kr = kv_frag(lk, s);
+      const u32x4_t vr = kv_frag(lv, s);
+      sacc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, qr),
+                                                     __builtin_bit_cast(bf16x8_t, kr), sacc, 0, 0, 0);
+      pacc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, gr),
+                                                     __builtin_bit_cast(bf16x8_t, vr), pacc, 0, 0, 0);
     }
-    if constexpr (DS) store_ds(bh, q0, 0, dsrun);
-    dvdk(ic<0>{});
-    dvdk(ic<1>{});
-    if constexpr (DS) store_ds(bh, q0, 1, dsrun);
-    dvdk(ic<2>{});
-    dvdk(ic<3>{});
+    // P and dS = P (dP - D) of the half's two k-steps, as bf16 pairs
+    u32x4_t pf[2], df[2];
+#pragma unroll
+    for (int kk = 0; kk < 2; ++kk) {
+      const int base = 8 * kk;
+      const int tix = 32 * qh + 8 * h32 + 16 * kk;  // tile index of register `base`
+      const f32x4_t l0 = *(const __attribute__((address_space(3))) f32x4_t*)(uintptr_t)(tl + 4 * tix);
+      const f32x4_t l1 = *(const __attribute__((address_space(3))) f32x4_t*)(uintptr_t)(tl + 4 * (tix + 4));
+      const f32x4_t d0 = *(const __attribute__((address_space(3))) f32x4_t*)(uintptr_t)(td + 4 * tix);
+      const f32x4_t d1 = *(const __attribute__((address_space(3))) f32x4_t*)(uintptr_t)(td + 4 * (tix + 4));
+      const int need = key - (q0 + tix);
+#pragma unroll
+      for (int w2 = 0; w2 < 4; ++w2) {
+        float pv[2], dsv[2];
+#pragma unroll
+        for (int u = 0; u < 2; ++u) {
+          const int r = 2 * w2 + u;
+          const float lsev = r < 4 ? l0[r & 3] : l1[r & 3];
+          const float dlt = r < 4 ? d0[r & 3] : d1[r & 3];
+          float x = __builtin_fmaf(sacc[base + r], sl2, -lsev * 1.4426950408889634f);
+          if constexpr (MASK) x = r >= need ? x : -INFINITY;
+          pv[u] = __builtin_amdgcn_exp2f(x);
+          dsv[u] = pv[u] * (pacc[base + r] - dlt);
+        }
+        pf[kk][w2] = pack_bf16x2(pv[0], pv[1]);
+        df[kk][w2] = pack_bf16x2(dsv[0], dsv[1]);
+      }
+    }
+    if constexpr (DS) store_ds(bh, q0, [&](int kk) { return df[kk]; });
+    // dV += P^T dO, dK += dS^T Q over the half's k-steps (query rows 32qh + 16kk ..)
+    const uint32_t hq = (uint32_t)(32 * qh * Tl::ROW);
+    // one 32-column block of d at a time (8 fragment registers in flight)
+    static_for<2>([&](auto kk_c) __attribute__((always_inline)) {
+      constexpr int KK = decltype(kk_c)::value;
+#pragma unroll
+      for (int c = 0; c < NC; ++c) {
+        const u32x4_t gt = fa_tr_frag<D, KK>(tg + hq, rd.tr[c]);
+        const u32x4_t qt = fa_tr_frag<D, KK>(tq + hq, rd.tr[c]);
+        fa_lds_fence();
+        dv[c] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, gt),
+                                                        __builtin_bit_cast(bf16x8_t, pf[KK]), dv[c], 0, 0, 0);
+        dk[c] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, qt),
+                                                        __builtin_bit_cast(bf16x8_t, df[KK]), dk[c], 0, 0, 0);
+      }
+    });
   };
 
   // Per head: the first n_diag tiles may hold queries before some of this wave's keys
-  // (causal mask, or skipped when every query precedes every key); the rest are
-  // visible whole.  Separate loops keep the accumulators in place across iterations.
+  // (causal mask); the rest are visible whole.  Separate loops keep the accumulators
+  // in place across iterations.
   const int n_diag = uniform(p.causal ? (per_h < 2 ? per_h : 2) : 0);
   auto ring_step = [&](int it) __attribute__((always_inline)) {
-    if (DS && it > ib) wait_vmcnt<4>();  // the last tile's dS^T stores stay in flight
+    if (DS && it > ib) wait_vmcnt<2>();  // the last tile's two dS^T stores stay in flight
     else wait_vmcnt<0>();
     lds_ring_barrier();
     if (it + 1 < ie) issue(it + 1);
-    return lds0 + (uint32_t)((it & 1) * STAGE);
+    return lr + (uint32_t)((it & 1) * STAGE);
   };
   if (ib < ie) issue(ib);
   int it = 0;
   for (int hh = 0; hh < p.group; ++hh) {
     const int bh = uniform(b * p.nH + kvh * p.group + hh);
     for (int t = 0; t < n_diag; ++t, ++it) {
-      if (it < ib || it >= ie) continue;  // another unit's iteration
+      if (it < ib || it >= ie) continue;
       const uint32_t st = ring_step(it);
       const int q0 = uniform((qt0 + t) * QT);
-      if (q0 + QT - 1 < kw) {  // every query of the tile precedes every key
-        if constexpr (DS) {  // zeros: the dQ GEMM reads whole K tiles around the diagonal
-          auto zero = [](int) __attribute__((always_inline)) { return u32x4_t{0u, 0u, 0u, 0u}; };
-          store_ds(bh, q0, 0, zero);
-          store_ds(bh, q0, 1, zero);
-        }
-        continue;
-      }
+      // A tile wholly above this wave's keys: skipped without dS^T; with it, the
+      // masked block writes its zeros (the dQ GEMM reads whole K tiles around the
+      // diagonal).  Zeros from the block itself keep the loop to one path, which
+      // the register allocator needs here.
+      if (!DS && q0 + QT - 1 < kw) continue;
       block(q0, bh, st, std::true_type{});
     }
     for (int t = n_diag; t < per_h; ++t, ++it) {
@@ -854,37 +857,73 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1)))
     }
   }
 
-  // Row bases in scalar registers, the lane's key row as a 32-bit element offset.
-  const int lrow = (32 * wave_u + l32) * D;
-  if (slot >= 0) {  // partial sums of a key block cut into several units
-    float* pk = uniform(p.part + ((int64_t)bkv * p.n_slots + slot) * 2 * 128 * D);
-    if (live) {
+  // Halves added in LDS: wave (wq, 0) finishes dK, wave (wq, 1) finishes dV, each as
+  // first half + second half.
+  wait_vmcnt<0>();
+  __syncthreads();
+  f32x4_t* xb = reinterpret_cast<f32x4_t*>(smem);
+  auto slot_of = [&](int w, int c, int q) __attribute__((always_inline)) {
+    return ((w * NC + c) * 4 + q) * 64 + lane;
+  };
+  // wave (wq, 1) sends its dK half to slots of wq; wave (wq, 0) sends its dV half to
+  // slots of 4 + wq
+  auto send = [&](f32x16_t (&src)[NC], int w) __attribute__((always_inline)) {
 #pragma unroll
-      for (int c = 0; c < NC; ++c)
+    for (int c = 0; c < NC; ++c)
 #pragma unroll
-        for (int q = 0; q < 4; ++q) {
-          const int d = lrow + 32 * c + 8 * q + 4 * h32;
-          *(f32x4_t*)(pk + d) = f32x4_t{dk[c][4 * q], dk[c][4 * q + 1], dk[c][4 * q + 2], dk[c][4 * q + 3]};
-          *(f32x4_t*)(pk + 128 * D + d) =
-              f32x4_t{dv[c][4 * q], dv[c][4 * q + 1], dv[c][4 * q + 2], dv[c][4 * q + 3]};
-        }
-    }
+      for (int q = 0; q < 4; ++q)
+        xb[slot_of(w, c, q)] = f32x4_t{src[c][4 * q], src[c][4 * q + 1], src[c][4 * q + 2], src[c][4 * q + 3]};
+  };
+  if (qh) send(dk, wq);
+  else send(dv, 4 + wq);
+  __syncthreads();
+  if (qh == 0) {
+#pragma unroll
+    for (int c = 0; c < NC; ++c)
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const f32x4_t o = xb[slot_of(wq, c, q)];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) dk[c][4 * q + e] = dk[c][4 * q + e] + o[e];  // half 0 + half 1
+      }
   } else {
-    uint16_t* ok = uniform((uint16_t*)p.dK + ((int64_t)bkv * T + k0) * D);
-    uint16_t* ov = uniform((uint16_t*)p.dV + ((int64_t)bkv * T + k0) * D);
-    if (live) {
+#pragma unroll
+    for (int c = 0; c < NC; ++c)
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const f32x4_t o = xb[slot_of(4 + wq, c, q)];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) dv[c][4 * q + e] = o[e] + dv[c][4 * q + e];
+      }
+  }
+
+  // wave (wq, 0) writes dK, wave (wq, 1) writes dV
+  const int lrow = krow * D;
+  auto write = [&](const f32x16_t (&res)[NC], int half, float* part_half, uint16_t* o, float sc)
+      __attribute__((always_inline)) {
+    if (!live) return;
+    if (slot >= 0) {
 #pragma unroll
       for (int c = 0; c < NC; ++c)
 #pragma unroll
-        for (int q = 0; q < 4; ++q) {
-          const int d = lrow + 32 * c + 8 * q + 4 * h32;
-          *(u32x2_t*)(ok + d) = u32x2_t{pack_bf16x2(dk[c][4 * q] * p.scale, dk[c][4 * q + 1] * p.scale),
-                                        pack_bf16x2(dk[c][4 * q + 2] * p.scale, dk[c][4 * q + 3] * p.scale)};
-          *(u32x2_t*)(ov + d) = u32x2_t{pack_bf16x2(dv[c][4 * q], dv[c][4 * q + 1]),
-                                        pack_bf16x2(dv[c][4 * q + 2], dv[c][4 * q + 3])};
-        }
+        for (int q = 0; q < 4; ++q)
+          *(f32x4_t*)(part_half + lrow + 32 * c + 8 * q + 4 * h32) =
+              f32x4_t{res[c][4 * q], res[c][4 * q + 1], res[c][4 * q + 2], res[c][4 * q + 3]};
+    } else {
+#pragma unroll
+      for (int c = 0; c < NC; ++c)
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+          *(u32x2_t*)(o + lrow + 32 * c + 8 * q + 4 * h32) =
+              u32x2_t{pack_bf16x2(res[c][4 * q] * sc, res[c][4 * q + 1] * sc),
+                      pack_bf16x2(res[c][4 * q + 2] * sc, res[c][4 * q + 3] * sc)};
     }
-  }
+    (void)half;
+  };
+  float* pk = slot >= 0 ? uniform(p.part + ((int64_t)bkv * p.n_slots + slot) * 2 * 128 * D) : nullptr;
+  const int64_t obase = ((int64_t)bkv * T + k0) * D;
+  if (qh == 0) write(dk, 0, pk, (uint16_t*)p.dK + obase, p.scale);
+  else write(dv, 1, pk ? pk + 128 * D : nullptr, (uint16_t*)p.dV + obase, 1.0f);
 }
 
 // D = rowsum(dO * O) for the dS^T path (the dQ kernel computes it otherwise), with the
@@ -1033,9 +1072,9 @@ hipError_t launch_flash_bwd(const FbParams& p_in, int head_dim, hipStream_t stre
   if (e != hipSuccess) return e;
   const int64_t nk = (int64_t)p.B * p.nKV * (p.n_units ? p.n_units : p.k_blocks);
   if (p.dsT)
-    hipLaunchKernelGGL((flash_bwd_dkdv_kernel<128, true>), dim3((unsigned)nk), dim3(256), 0, stream, p);
+    hipLaunchKernelGGL((flash_bwd_dkdv_kernel<128, true>), dim3((unsigned)nk), dim3(512), 0, stream, p);
   else
-    hipLaunchKernelGGL((flash_bwd_dkdv_kernel<128, false>), dim3((unsigned)nk), dim3(256), 0, stream, p);
+    hipLaunchKernelGGL((flash_bwd_dkdv_kernel<128, false>), dim3((unsigned)nk), dim3(512), 0, stream, p);
   if (!p.n_split) return hipGetLastError();
   e = hipGetLastError();
   if (e != hipSuccess) return e;
