@@ -11,11 +11,14 @@ value = algorithmic FLOPs x steps / timed seconds.
 
 Timing: after the warm-up, an attribution pass (untimed for `value`) brackets every launch
 with HIP events to get per-GEMM times and the kernel with the largest share of GPU time.
-In the timed region the launches run back to back; events bracket only the launches of
-that kernel (each run of consecutive ones), not all 15.
+In the timed region the launches run back to back; in its last two steps events bracket
+the launches of that kernel (each run of consecutive ones), not all 15.  An event record
+between two kernels leaves the GPU idle for about 6 us (a marker packet between the
+dispatches), so events in every step would add about 60 us to each 2 ms step.
 
-roofline: achieved = the dominant kernel's algorithmic FLOPs / its launch time summed over
-the timed region (HIP events on the launch stream), against the dense bf16 MFMA peak.
+roofline: achieved = the dominant kernel's algorithmic FLOPs / its launch time over the
+bracketed steps of the timed region (HIP events on the launch stream), against the dense
+bf16 MFMA peak.
 cpu_baseline: the oracle's fp32 OpenMP SGEMM (oracle/mi_oracle.c, cblas_sgemm
 semantics) on the same set (all M=8192 token rows by default; --cpu-rows bounds it), rank 0
 only.
@@ -32,6 +35,7 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, os.path.join(ROOT, "large-language-model_amd"))
 
 PEAK_BF16_TFLOPS = 2516.6   # MI355X dense bf16 MFMA
+EVENT_STEPS = 2             # timed steps, counted from the last, whose launches carry events
 PEAK_HBM_GBS = 8000.0
 
 # (name, d_in, d_out) of the config-3 decoder block, engine layout W[d_in, d_out]
@@ -76,6 +80,11 @@ def cpu_model() -> str:
     except OSError:
         pass
     return "unknown"
+
+
+def timed_event_steps(steps: int) -> list:
+    """Indices of the timed steps whose launches carry HIP events: the last EVENT_STEPS."""
+    return list(range(max(0, steps - EVENT_STEPS), steps))
 
 
 def block_flops(M: int, block=BLOCK) -> int:
@@ -197,17 +206,19 @@ def attention_main(args):
     for _ in range(args.warmup):
         step()
     torch.cuda.synchronize()
-    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
-           for _ in range(args.steps)]
+    # events (about 6 us of idle GPU per record) only in the last EVENT_STEPS timed steps
+    ev_steps = timed_event_steps(args.steps)
+    evs = {s_: (torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+           for s_ in ev_steps}
     t0 = time.perf_counter()
     for s_ in range(args.steps):
-        step(evs[s_])
+        step(evs.get(s_))
     torch.cuda.synchronize()
     elapsed = time.perf_counter() - t0
     flops = 6 * ATT_PRODUCT_FLOPS
     value = flops * args.steps / elapsed / 1e12
-    # the backward pass (its three launches, bracketed together) takes most of the step
-    ms_bwd = sum(a.elapsed_time(b) for a, b in evs) / args.steps
+    # the backward pass (its launches, bracketed together) takes most of the step
+    ms_bwd = sum(a.elapsed_time(b) for a, b in evs.values()) / len(evs)
     achieved = 4 * ATT_PRODUCT_FLOPS / (ms_bwd / 1e3) / 1e12
     out = {
         "metric": "GQA attention TFLOP/s (fused fwd+bwd, configuration 4)",
@@ -318,23 +329,26 @@ def lm_head_main(args):
               for i in range(len(ops))]
     dom = max((i for i in range(len(ops)) if ops[i][1]), key=lambda i: per_ms[i])
     xi = 1
-    # timed region: back to back, events around the dominant GEMM and the cross-entropy only
-    tev = [[(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
-            for _ in range(2)] for _ in range(args.steps)]
+    # timed region: back to back; in the last EVENT_STEPS steps events around the dominant
+    # GEMM and the cross-entropy (about 6 us of idle GPU per event record)
+    ev_steps = timed_event_steps(args.steps)
+    tev = {s_: [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+                for _ in range(2)] for s_ in ev_steps}
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     for s_ in range(args.steps):
+        marks = tev.get(s_)
         for i, op in enumerate(ops):
-            k = 0 if i == dom else (1 if i == xi else None)
+            k = None if marks is None else (0 if i == dom else (1 if i == xi else None))
             if k is not None:
-                tev[s_][k][0].record()
+                marks[k][0].record()
             op[3]()
             if k is not None:
-                tev[s_][k][1].record()
+                marks[k][1].record()
     torch.cuda.synchronize()
     elapsed = time.perf_counter() - t0
-    ms_dom = sum(a.elapsed_time(b) for (a, b), _ in tev) / args.steps
-    ms_x = sum(a.elapsed_time(b) for _, (a, b) in tev) / args.steps
+    ms_dom = sum(a.elapsed_time(b) for (a, b), _ in tev.values()) / len(tev)
+    ms_x = sum(a.elapsed_time(b) for _, (a, b) in tev.values()) / len(tev)
     flops = 3 * LMH_GEMM_FLOPS
     value = flops * args.steps / elapsed / 1e12
     achieved = LMH_GEMM_FLOPS / (ms_dom / 1e3) / 1e12
@@ -604,6 +618,9 @@ def main():
         print(json.dumps({"error": "this build runs on one GPU only; --gpus must be 1 "
                                    "(the multi-GPU sharding is a design, not run)"}))
         sys.exit(2)
+    if args.steps < 1 or args.warmup < 0:
+        print(json.dumps({"error": "--steps must be at least 1 and --warmup at least 0"}))
+        sys.exit(2)
     if args.workload == "attention":
         attention_main(args)
         return
@@ -703,29 +720,32 @@ def gemm_set_main(args, fp32: bool):
             i += 1
     dom_idx = [k for a, b in runs for k in range(a, b + 1)]
 
-    # Timed region: K steps back to back; events only around the dominant kernel's runs.
-    rev = [[(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
-            for _ in runs] for _ in range(args.steps)]
+    # Timed region: K steps back to back; in the last EVENT_STEPS of them events around
+    # the dominant kernel's runs.
+    ev_steps = timed_event_steps(args.steps)
+    rev = {s_: [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+                for _ in runs] for s_ in ev_steps}
     starts = {a: r for r, (a, b) in enumerate(runs)}
     ends = {b: r for r, (a, b) in enumerate(runs)}
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     for s_ in range(args.steps):
+        marks = rev.get(s_)
         for i, op in enumerate(ops):
-            if i in starts:
-                rev[s_][starts[i]][0].record(stream)
+            if marks is not None and i in starts:
+                marks[starts[i]][0].record(stream)
             op[-1]()
-            if i in ends:
-                rev[s_][ends[i]][1].record(stream)
+            if marks is not None and i in ends:
+                marks[ends[i]][1].record(stream)
     torch.cuda.synchronize()
     t1 = time.perf_counter()
     elapsed = t1 - t0
     flops = block_flops(M, block)
     value = flops * args.steps / elapsed / 1e12
     ms_dom = sum(rev[s_][r][0].elapsed_time(rev[s_][r][1])
-                 for s_ in range(args.steps) for r in range(len(runs)))
-    n_dom = len(dom_idx) * args.steps
-    fl_dom = sum(ops[k][2] for k in dom_idx) * args.steps
+                 for s_ in ev_steps for r in range(len(runs)))
+    n_dom = len(dom_idx) * len(ev_steps)
+    fl_dom = sum(ops[k][2] for k in dom_idx) * len(ev_steps)
     achieved = fl_dom / (ms_dom / 1e3) / 1e12
     traffic = hbm_bytes_per_launch(dom, TRAFFIC_FILE_FP32 if fp32 else TRAFFIC_FILE)
     dom_ops = sorted(f"{ops[k][0]} {ops[k][1]}" for k in dom_idx)

@@ -38,10 +38,18 @@ constexpr int FA_BQ = 128;   // query rows per workgroup (32 per wave)
 constexpr int FA_BK = 64;    // keys per K/V block
 constexpr float FA_TAU = 8.0f;  // growth of a row max (log2 units of p) that forces a rescale
 
-// Workgroup b runs on XCD b mod 8; renumber so each XCD holds a contiguous range.
-__device__ __forceinline__ int fa_xcd_major(int bid, int n) {
-  const int q = n / 8, rem = n % 8, x = bid % 8, j = bid / 8;
-  return x * q + (x < rem ? x : rem) + j;
+// Workgroup b runs on XCD b mod 8, as the (b / 8)-th there.  The n work items come
+// heaviest first in runs of g that should share one L2 (the query heads of a KV
+// group); run r goes to XCD r mod 8, so every XCD gets the same mix of weights,
+// heaviest first, and keeps whole runs.  (A contiguous range per XCD would give
+// XCD 0 all of the heaviest items: with B * nH = 128 and 8 causal query blocks,
+// XCD 0 would run every 16-block query block and XCD 7 every 2-block one.)  Items
+// past the last whole round of 8g runs keep their index.
+__device__ __forceinline__ int fa_xcd_spread(int bid, int n, int g) {
+  const int round = 8 * g, nfull = n - n % round;
+  if (bid >= nfull) return bid;
+  const int x = bid % 8, j = bid / 8;
+  return ((j / g) * 8 + x) * g + j % g;
 }
 
 // Key row read by lane row p (0..31) of a 32-key half: bits 2 and 3 swapped.
@@ -87,10 +95,10 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2)))
   const int h32 = lane >> 5, l32 = lane & 31;
 
   // Heaviest query blocks first (causal work grows with the block index); the
-  // (batch, head) pairs of one query block are spread XCD-major so the heads of a
-  // KV group share K/V in one L2.
+  // heads of a KV group stay on one XCD, so they share K/V in its L2 (with B * nKV
+  // a multiple of 8, every query block of the group runs there).
   const int BH = p.B * p.nH;
-  const int lid = uniform(fa_xcd_major(blockIdx.x, gridDim.x));
+  const int lid = uniform(fa_xcd_spread(blockIdx.x, gridDim.x, p.group));
   const int qb = uniform(p.q_blocks - 1 - lid / BH);
   const int bh = uniform(lid - (lid / BH) * BH);
   const int b = uniform(bh / p.nH), h = uniform(bh - (bh / p.nH) * p.nH);
@@ -425,7 +433,7 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2)))
   const int h32 = lane >> 5, l32 = lane & 31;
 
   const int BH = p.B * p.nH;
-  const int lid = uniform(fa_xcd_major(blockIdx.x, gridDim.x));
+  const int lid = uniform(fa_xcd_spread(blockIdx.x, gridDim.x, p.group));  // as the forward
   const int qb = uniform(p.q_blocks - 1 - lid / BH);
   const int bh = uniform(lid - (lid / BH) * BH);
   const int b = uniform(bh / p.nH), h = uniform(bh - (bh / p.nH) * p.nH);
@@ -630,7 +638,7 @@ __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2)))
   // Work unit: with a schedule, unit u (largest first) of every (batch, KV head) in
   // turn, so each XCD (workgroups b mod 8) gets an even share of every size;
   // without, one key block per workgroup, the ones with the most query tiles
-  // (causal: the first) first, each XCD a contiguous range.
+  // (causal: the first) first, spread over the XCDs the same way.
   const int BKV = p.B * p.nKV;
   int kbi, bkv, slot = -1, ib = 0, ie = -1;
   if (p.n_units) {
@@ -642,7 +650,7 @@ __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2)))
     ib = (int)(ur & 0xffffu);
     ie = (int)(ur >> 16);
   } else {
-    const int lid = uniform(fa_xcd_major(blockIdx.x, gridDim.x));
+    const int lid = uniform(fa_xcd_spread(blockIdx.x, gridDim.x, 1));
     kbi = uniform(lid / BKV);
     bkv = uniform(lid - kbi * BKV);
   }
