@@ -816,19 +816,28 @@ __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2)))
     if constexpr (DS) store_ds(bh, q0, [&](int kk) { return df[kk]; });
     // dV += P^T dO, dK += dS^T Q over the half's k-steps (query rows 32qh + 16kk ..)
     const uint32_t hq = (uint32_t)(32 * qh * Tl::ROW);
-    // one 32-column block of d at a time (8 fragment registers in flight)
-    static_for<2>([&](auto kk_c) __attribute__((always_inline)) {
-      constexpr int KK = decltype(kk_c)::value;
-#pragma unroll
-      for (int c = 0; c < NC; ++c) {
-        const u32x4_t gt = fa_tr_frag<D, KK>(tg + hq, rd.tr[c]);
-        const u32x4_t qt = fa_tr_frag<D, KK>(tq + hq, rd.tr[c]);
-        fa_lds_fence();
-        dv[c] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, gt),
-                                                        __builtin_bit_cast(bf16x8_t, pf[KK]), dv[c], 0, 0, 0);
-        dk[c] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, qt),
-                                                        __builtin_bit_cast(bf16x8_t, df[KK]), dk[c], 0, 0, 0);
+    // The 8 (k-step, 32-column block) pairs in turn, the next pair's 4 transposing
+    // reads issued before this pair's MFMAs: LDS returns in order, so lgkmcnt(4)
+    // leaves exactly the next pair's reads in flight.
+    u32x4_t gt[2], qt[2];
+    gt[0] = fa_tr_frag<D, 0>(tg + hq, rd.tr[0]);
+    qt[0] = fa_tr_frag<D, 0>(tq + hq, rd.tr[0]);
+    static_for<2 * NC>([&](auto i_c) __attribute__((always_inline)) {
+      constexpr int I = decltype(i_c)::value, KK = I / NC, C = I % NC, B = I & 1;
+      if constexpr (I + 1 < 2 * NC) {
+        constexpr int KN = (I + 1) / NC, CN = (I + 1) % NC;
+        gt[B ^ 1] = fa_tr_frag<D, KN>(tg + hq, rd.tr[CN]);
+        qt[B ^ 1] = fa_tr_frag<D, KN>(tq + hq, rd.tr[CN]);
+        __builtin_amdgcn_s_waitcnt(0xC07F | (4 << 8));  // lgkmcnt(4)
+      } else {
+        __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
       }
+      __builtin_amdgcn_sched_barrier(0);
+      dv[C] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, gt[B]),
+                                                      __builtin_bit_cast(bf16x8_t, pf[KK]), dv[C], 0, 0, 0);
+      dk[C] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, qt[B]),
+                                                      __builtin_bit_cast(bf16x8_t, df[KK]), dk[C], 0, 0, 0);
+      __builtin_amdgcn_sched_barrier(0);
     });
   };
 
