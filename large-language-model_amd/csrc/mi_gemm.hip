@@ -238,19 +238,23 @@ Plan make_plan(int dtype_in, int64_t M, int64_t N, int64_t Ktot, int64_t batch, 
       if (frac > 0.0 && frac <= 0.5 && tilesS >= cus) return plan_for(CFG_S, 1);
       return plan_for(CFG_L, 1);
     }
-    // Below one wave of L tiles (long K): one partial round of L tiles, 128x128
-    // tiles two 4-wave workgroups per CU (S), or one 8-wave workgroup per CU that
-    // splits every K tile between two wave groups (W, wave-level split-K).  Cost
-    // in units of one W tile, measured on the dW shapes at K = 8192: an L tile
-    // (4x the work) takes 2.6, S tiles take 1.8 per round of two per CU and 1.1
-    // alone (2048x5632: L 170 us, W 184, S 189; 2048x3072: S 119, W 123, L 165;
-    // 2048x2048: W 66, S 73, L 153).
+    // Below one wave of L tiles (long K): one partial round of L tiles or of 256x192
+    // tiles (M), 128x128 tiles two 4-wave workgroups per CU (S), or one 8-wave
+    // workgroup per CU that splits every K tile between two wave groups (W,
+    // wave-level split-K).  Cost in units of one W tile, measured on the dW shapes
+    // at K = 8192: an L tile (4x the work) takes 2.6, an M tile 3/4 of that, S tiles
+    // 1.8 per round of two per CU and 1.1 alone (2048x5632: M 167 us (240 tiles), L
+    // 177 (176), W 184, S 189; 5632x2048: M 164, L 172; 2048x3072: S 123, M 130, L
+    // 165; 2048x2048: W 69, S 73, M 135, L 153).  M needs N in 64-column blocks.
     if (tilesS * 2 >= cus || !allow_split) {
       if (fast && !sparse_L && Ktot >= 1024) {
         const double cW = (double)cdiv(tilesS, cus);
         const int64_t full2 = tilesS / (2 * cus), rem = tilesS - full2 * 2 * cus;
         const double cS = 1.8 * (double)full2 + (rem > cus ? 1.8 : rem > 0 ? 1.1 : 0.0);
         const double cL = 2.6 * (double)cdiv(tilesL, cus);
+        const int64_t tilesM = cdiv(M, 256) * cdiv(N, 192) * batch;
+        const double cM = N % 64 == 0 ? 1.95 * (double)cdiv(tilesM, cus) : 1e30;
+        if (cM < cL && cM <= cW && cM <= cS) return plan_for(CFG_M, 1);
         if (cL <= cW && cL <= cS) return plan_for(CFG_L, 1);
         if (cW < cS) return plan_for(CFG_W, 1);
       }

@@ -321,6 +321,33 @@ def test_tile_256x192(mi, dev, oracle, tA, tB):
         check(got.sum(axis=1), row, TOL_BF16, f"256x192 K={K} row checksum")
 
 
+def test_tile_256x192_partial_round(mi, dev, oracle):
+    """256x192 tiles for a grid below one round of 256x256 tiles (the dW shapes of
+    gate / up and down: 240 or 242 tiles instead of 176), TN with fp32 beta = 1
+    accumulation, and N not a multiple of 192 (a last column tile of 64 or 128
+    columns). Sampled rows against the oracle, every element through checksums."""
+    import torch
+
+    K = 1024
+    for M, N in [(2048, 5632), (5632, 2048)]:
+        plan = mi.describe(1, 0, M, N, K)
+        assert "256x192 TN" in plan, plan
+        a = inputs(oracle, (M, K), 131 + M, 1.0)
+        b = inputs(oracle, (K, N), 132 + M, 1e-2)
+        c0 = inputs(oracle, (M, N), 133 + M, 0.5, False)
+        C = torch.from_numpy(c0).to(dev)
+        mi.gemm(to_dev(layout(a, 1), dev, True), to_dev(b, dev, True), C, M, N, K, transA=True,
+                beta=1.0)
+        torch.cuda.synchronize()
+        got = C.cpu().numpy().astype(np.float64) - c0.astype(np.float64)
+        rows = sample_rows(M, 6, M)
+        check(got[rows], oracle.gemm(0, 0, M, N, K, a, b, rows=rows), TOL_F32,
+              f"256x192 TN {M}x{N} rows")
+        col, row = checksums(a, b)
+        check(got.sum(axis=0), col, TOL_F32, f"256x192 TN {M}x{N} column checksum")
+        check(got.sum(axis=1), row, TOL_F32, f"256x192 TN {M}x{N} row checksum")
+
+
 def test_zero_k(mi, dev, oracle):
     got, ref = _run(mi, dev, oracle, 70, 90, 0, 0, 0, False, seed=61, beta=0.5, bias=True)
     check(got, ref, TOL_F32, "K=0")
