@@ -489,8 +489,9 @@ int run(const Problem& P, hipStream_t stream) {
     return fail(MI_ERR_WORKSPACE, "split-K by %d needs %lld floats of workspace, %lld given",
                 plan.splits, (long long)plan.splits * P.M * P.N * b.batch, (long long)ws_elems);
   const CfgShape ts = shape_of(P.dtype_in, plan.cfg);
+  // the direct epilogue works in whole 32x32 blocks (an edge tile skips those past M, N)
   const bool fast_epi = plan.splits == 1 && !P.ep.bias && !P.ep.residual && cvec &&
-                        b.causal != MI_CAUSAL_OUT_LOWER && P.M % ts.bm == 0 && P.N % ts.bn == 0;
+                        b.causal != MI_CAUSAL_OUT_LOWER && P.M % 32 == 0 && P.N % 32 == 0;
   const int64_t kstep = plan.cfg == CFG_W ? MI_W_BK : 64;
   KernelFn fn = pick_kernel(P.dtype_in, P.transA, P.transB, plan.cfg, fast, P.K % kstep != 0, fast_epi);
   if (!fn) return fail(MI_ERR_UNSUPPORTED, "no kernel for this layout / mode");

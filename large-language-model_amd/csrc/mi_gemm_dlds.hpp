@@ -640,11 +640,13 @@ __global__ void __launch_bounds__(64 * WGM * WGN * KG)
       return p.alpha * acc[i][j][4 * q + e];
   };
   if constexpr (FAST_EPI) {
-    // Full tiles, epilogue alpha (SiLU gate), beta*C and the output conversion.
-    // Each 32x32 MFMA block goes through a wave-private LDS patch (rows padded
-    // by 4 floats) and back out row-major, so a store instruction writes 8 rows
-    // of 32 contiguous columns (64 or 128 bytes per row) instead of 32 rows of
-    // 16 bytes.  One barrier first: the patches reuse the ring's LDS.
+    // M and N multiples of 32, epilogue alpha (SiLU gate), beta*C and the output
+    // conversion.  Each 32x32 MFMA block goes through a wave-private LDS patch (rows
+    // padded by 4 floats) and back out row-major, so a store instruction writes 8
+    // rows of 32 contiguous columns (64 or 128 bytes per row) instead of 32 rows of
+    // 16 bytes.  A block is wholly inside the matrix or wholly past its edge (an
+    // edge tile's extra blocks are skipped).  One barrier first: the patches reuse
+    // the ring's LDS.
     __syncthreads();
     constexpr int PP = 36;  // patch pitch (floats)
     static_assert(NWAVE * 32 * PP * 4 <= LDS_BYTES, "epilogue patches fit the ring");
@@ -660,6 +662,7 @@ __global__ void __launch_bounds__(64 * WGM * WGN * KG)
         if (KG == 2 && i != kg) continue;
 #pragma unroll
         for (int j = 0; j < TN; ++j) {
+          if (uniform(m0 + wm * WTM + i * 32) >= p.M || uniform(n0 + wn * WTN + j * 32) >= p.N) continue;
 #pragma unroll
           for (int q = 0; q < 4; ++q) {
             f32x4_t v;

@@ -348,6 +348,17 @@ def test_tile_256x192_partial_round(mi, dev, oracle):
         check(got.sum(axis=1), row, TOL_F32, f"256x192 TN {M}x{N} row checksum")
 
 
+@pytest.mark.parametrize("out_bf16", [True, False], ids=["bf16_out", "f32_out"])
+def test_direct_epilogue_edge_tiles(mi, dev, oracle, out_bf16):
+    """M and N multiples of 32 but not of the tile: the direct epilogue stores the edge
+    tiles' 32x32 blocks inside the matrix and skips the rest (with beta * C read back)."""
+    for i, (M, N, K, tA, tB) in enumerate([(288, 416, 512, 0, 0), (1056, 800, 1024, 0, 1),
+                                           (512, 1120, 1024, 1, 0), (2080, 2272, 256, 0, 0)]):
+        got, ref = _run(mi, dev, oracle, M, N, K, tA, tB, True, seed=141 + i, out_bf16=out_bf16,
+                        beta=0.5)
+        check(got, ref, TOL_BF16, f"edge tiles {M}x{N}x{K} tA={tA} tB={tB}")
+
+
 def test_zero_k(mi, dev, oracle):
     got, ref = _run(mi, dev, oracle, 70, 90, 0, 0, 0, False, seed=61, beta=0.5, bias=True)
     check(got, ref, TOL_F32, "K=0")
