@@ -417,8 +417,8 @@ __device__ __forceinline__ uint32_t fa_dma_off(int u, int lane, int stride) {
 
 // dQ for 128 query rows of one (batch, head): recompute S = Q K^T and P from the
 // forward's log-sum-exp, dP = dO V^T, dS = P (dP - D), dQ = scale * dS K, with the
-// K/V blocks streamed like the forward's.  D = rowsum(dO O) is computed here from
-// the rows this workgroup owns and written for the dK/dV kernel.
+// K/V blocks streamed like the forward's.  D = rowsum(dO O) comes from the D kernel,
+// launched before this one.
 template <int D>
 __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2)))
     flash_bwd_dq_kernel(FbParams p) {
@@ -449,27 +449,21 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2)))
   const __bf16* Vb = (const __bf16*)p.V + ((int64_t)(b * p.nKV + kvh) * T) * D;
   const int64_t orow = p.o_bthd ? ((int64_t)(b * T + row) * p.nH + h) * D : ((int64_t)bh * T + row) * D;
 
-  // Q and dO fragments (second MFMA operands), the row's D and log-sum-exp.
+  // Q and dO fragments (second MFMA operands), the row's D (from the D kernel, which
+  // runs first) and log-sum-exp.
   u32x4_t qf[NS], gf[NS];
-  float dsum = 0.0f;
 #pragma unroll
   for (int s = 0; s < NS; ++s) {
     const int dd = 16 * s + 8 * h32;
     if (live) {
       qf[s] = *(const u32x4_t*)(Qb + (int64_t)row * D + dd);
       gf[s] = *(const u32x4_t*)((const __bf16*)p.dO + orow + dd);
-      const u32x4_t of = *(const u32x4_t*)((const __bf16*)p.O + orow + dd);
-#pragma unroll
-      for (int w2 = 0; w2 < 4; ++w2)
-        dsum += bf16_bits_to_f32(gf[s][w2] & 0xffffu) * bf16_bits_to_f32(of[w2] & 0xffffu) +
-                bf16_bits_to_f32(gf[s][w2] >> 16) * bf16_bits_to_f32(of[w2] >> 16);
     } else {
       qf[s] = u32x4_t{0u, 0u, 0u, 0u};
       gf[s] = u32x4_t{0u, 0u, 0u, 0u};
     }
   }
-  dsum += __shfl_xor(dsum, 32, 64);
-  if (live && h32 == 0) p.delta[(int64_t)bh * T + row] = dsum;
+  const float dsum = live ? p.delta[(int64_t)bh * T + row] : 0.0f;
   const float lse2 = live ? p.lse[(int64_t)bh * T + row] * 1.4426950408889634f : 0.0f;
   const float sl2 = p.scale_log2;
 
@@ -943,35 +937,48 @@ __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2)))
   else write(dv, 1, pk ? pk + 128 * D : nullptr, (uint16_t*)p.dV + obase, 1.0f);
 }
 
-// D = rowsum(dO * O) for the dS^T path (the dQ kernel computes it otherwise), with the
-// dQ kernel's lane layout and summation order: lane l32 of a wave is a row, lanes l
-// and l + 32 sum alternate 8-column chunks, then add their halves.
+// D = rowsum(dO * O), read by both backward forms.  Coalesced: the 16 lanes of a lane
+// group read one 256-byte row (16 bytes each), a wave 4 rows per load and 32 rows in
+// all, 8 loads of dO and 8 of O in flight per lane.  Each lane sums its 8 products
+// in order, then the group adds its 16 partial sums by a butterfly (lane distance 8,
+// 4, 2, 1), which leaves every lane of the group the same total; lane i of the group
+// keeps row i's.
 template <int D>
 __global__ void __launch_bounds__(256) flash_bwd_delta_kernel(FbParams p) {
-  constexpr int NS = D / 16;
+  static_assert(D == 128, "16 lanes of 16 bytes per row");
+  constexpr int RPW = 32;              // rows per wave
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int h32 = lane >> 5, l32 = lane & 31;
-  const int64_t r = (int64_t)blockIdx.x * 128 + wave * 32 + l32;  // row of [B, nH, T]
+  const int sub = lane & 15, grp = lane >> 4;
   const int64_t rows = (int64_t)p.B * p.nH * p.T;
-  const bool live = r < rows;
-  const int64_t bh = live ? r / p.T : 0, t = live ? r - bh * p.T : 0;
-  const int64_t b = bh / p.nH, h = bh - b * p.nH;
-  const int64_t orow = p.o_bthd ? ((b * p.T + t) * p.nH + h) * D : (bh * p.T + t) * D;
-  float dsum = 0.0f;
-  if (live) {
+  const int64_t r0 = (int64_t)blockIdx.x * 128 + wave * RPW;  // first row of the wave
+  u32x4_t gf[8], of[8];
 #pragma unroll
-    for (int s = 0; s < NS; ++s) {
-      const int dd = 16 * s + 8 * h32;
-      const u32x4_t gf = *(const u32x4_t*)((const __bf16*)p.dO + orow + dd);
-      const u32x4_t of = *(const u32x4_t*)((const __bf16*)p.O + orow + dd);
-#pragma unroll
-      for (int w2 = 0; w2 < 4; ++w2)
-        dsum += bf16_bits_to_f32(gf[w2] & 0xffffu) * bf16_bits_to_f32(of[w2] & 0xffffu) +
-                bf16_bits_to_f32(gf[w2] >> 16) * bf16_bits_to_f32(of[w2] >> 16);
+  for (int i = 0; i < 8; ++i) {
+    const int64_t r = r0 + 4 * i + grp;  // row of [B, nH, T]
+    if (r < rows) {
+      const int64_t bh = r / p.T, t = r - bh * p.T;
+      const int64_t b = bh / p.nH, h = bh - b * p.nH;
+      const int64_t orow = p.o_bthd ? ((b * p.T + t) * p.nH + h) * D : (bh * p.T + t) * D;
+      gf[i] = *(const u32x4_t*)((const __bf16*)p.dO + orow + 8 * sub);
+      of[i] = *(const u32x4_t*)((const __bf16*)p.O + orow + 8 * sub);
+    } else {
+      gf[i] = of[i] = u32x4_t{0u, 0u, 0u, 0u};
     }
   }
-  dsum += __shfl_xor(dsum, 32, 64);
-  if (live && h32 == 0) p.delta[r] = dsum;
+  float mine = 0.0f;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    float part = 0.0f;
+#pragma unroll
+    for (int w2 = 0; w2 < 4; ++w2)
+      part += bf16_bits_to_f32(gf[i][w2] & 0xffffu) * bf16_bits_to_f32(of[i][w2] & 0xffffu) +
+              bf16_bits_to_f32(gf[i][w2] >> 16) * bf16_bits_to_f32(of[i][w2] >> 16);
+#pragma unroll
+    for (int m = 8; m >= 1; m >>= 1) part += __shfl_xor(part, m, 64);
+    if (sub == i) mine = part;
+  }
+  const int64_t r = r0 + 4 * sub + grp;
+  if (sub < 8 && r < rows) p.delta[r] = mine;
 }
 
 // dK and dV of the key blocks the schedule cut into several units: the units'
@@ -1075,18 +1082,19 @@ hipError_t launch_flash_bwd(const FbParams& p_in, int head_dim, hipStream_t stre
   if (head_dim != 128) return hipErrorInvalidValue;
   FbParams p = p_in;
   plan_dkdv_schedule(p);
-  // dQ (and D) first: the dK/dV kernel reads D.  With the dS^T workspace only D here;
-  // the dK/dV kernel then writes dS^T and the caller runs dQ = scale * dS K.
-  if (p.dsT) {
-    const int64_t rows = (int64_t)p.B * p.nH * p.T;
-    hipLaunchKernelGGL(flash_bwd_delta_kernel<128>, dim3((unsigned)((rows + 127) / 128)), dim3(256), 0,
-                       stream, p);
-  } else {
-    const int64_t nq = (int64_t)p.B * p.nH * p.q_blocks;
-    hipLaunchKernelGGL(flash_bwd_dq_kernel<128>, dim3((unsigned)nq), dim3(256), 0, stream, p);
-  }
+  // D first (both kernels after it read it); then, without the dS^T workspace, the dQ
+  // kernel.  With it the dK/dV kernel writes dS^T and the caller runs dQ = scale * dS K.
+  const int64_t rows = (int64_t)p.B * p.nH * p.T;
+  hipLaunchKernelGGL(flash_bwd_delta_kernel<128>, dim3((unsigned)((rows + 127) / 128)), dim3(256), 0,
+                     stream, p);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
+  if (!p.dsT) {
+    const int64_t nq = (int64_t)p.B * p.nH * p.q_blocks;
+    hipLaunchKernelGGL(flash_bwd_dq_kernel<128>, dim3((unsigned)nq), dim3(256), 0, stream, p);
+    e = hipGetLastError();
+    if (e != hipSuccess) return e;
+  }
   const int64_t nk = (int64_t)p.B * p.nKV * (p.n_units ? p.n_units : p.k_blocks);
   if (p.dsT)
     hipLaunchKernelGGL((flash_bwd_dkdv_kernel<128, true>), dim3((unsigned)nk), dim3(512), 0, stream, p);
