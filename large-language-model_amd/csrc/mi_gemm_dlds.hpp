@@ -657,12 +657,34 @@ __global__ void __launch_bounds__(64 * WGM * WGN * KG)
     // BF: bf16 C; BETA: beta*C is added.  Both uniform, hoisted out of the tile.
     auto store_tile = [&](auto BF_c, auto BETA_c) __attribute__((always_inline)) {
       constexpr bool BF = decltype(BF_c)::value, BETA = decltype(BETA_c)::value;
+      using OldT = std::conditional_t<BF, u32x2_t, f32x4_t>;
 #pragma unroll
       for (int i = 0; i < TM; ++i) {
         if (KG == 2 && i != kg) continue;
+        if (uniform(m0 + wm * WTM + i * 32) >= p.M) continue;  // row block past M
+        const int64_t row0 = (int64_t)(m0 + wm * WTM + i * 32 + r_out);
+        auto col_of = [&](int j) __attribute__((always_inline)) { return n0 + wn * WTN + j * 32 + c_out; };
+        auto inside = [&](int j) __attribute__((always_inline)) {
+          return uniform(n0 + wn * WTN + j * 32) < p.N;
+        };
+        // beta: the row block's old C is loaded first, so its memory latency is paid
+        // once per row block rather than once per 32x32 block
+        OldT old[TN][4];
+        if constexpr (BETA) {
+#pragma unroll
+          for (int j = 0; j < TN; ++j) {
+            if (!inside(j)) continue;
+#pragma unroll
+            for (int st = 0; st < 4; ++st) {
+              const int64_t ci = (row0 + 8 * st) * p.ldc + col_of(j);
+              if constexpr (BF) old[j][st] = *(const u32x2_t*)((const uint16_t*)Cz + ci);
+              else old[j][st] = *(const f32x4_t*)((const float*)Cz + ci);
+            }
+          }
+        }
 #pragma unroll
         for (int j = 0; j < TN; ++j) {
-          if (uniform(m0 + wm * WTM + i * 32) >= p.M || uniform(n0 + wn * WTN + j * 32) >= p.N) continue;
+          if (!inside(j)) continue;
 #pragma unroll
           for (int q = 0; q < 4; ++q) {
             f32x4_t v;
@@ -670,30 +692,27 @@ __global__ void __launch_bounds__(64 * WGM * WGN * KG)
             for (int e = 0; e < 4; ++e) v[e] = value(i, j, q, e);
             *reinterpret_cast<f32x4_t*>(patch + r_in * PP + 8 * q + 4 * h_in) = v;
           }
-          const int64_t row0 = (int64_t)(m0 + wm * WTM + i * 32 + r_out);
-          const int col = n0 + wn * WTN + j * 32 + c_out;
+          const int col = col_of(j);
 #pragma unroll
           for (int st = 0; st < 4; ++st) {
             f32x4_t v = *reinterpret_cast<const f32x4_t*>(patch + (r_out + 8 * st) * PP + c_out);
             const int64_t ci = (row0 + 8 * st) * p.ldc + col;
             if constexpr (BF) {
-              u32x2_t* c = (u32x2_t*)((uint16_t*)Cz + ci);
               if constexpr (BETA) {
-                const u32x2_t o = *c;
+                const u32x2_t o = old[j][st];
                 v[0] += beta * bf16_bits_to_f32(o[0] & 0xffffu);
                 v[1] += beta * bf16_bits_to_f32(o[0] >> 16);
                 v[2] += beta * bf16_bits_to_f32(o[1] & 0xffffu);
                 v[3] += beta * bf16_bits_to_f32(o[1] >> 16);
               }
-              *c = u32x2_t{pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3])};
+              *(u32x2_t*)((uint16_t*)Cz + ci) = u32x2_t{pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3])};
             } else {
-              f32x4_t* c = (f32x4_t*)((float*)Cz + ci);
               if constexpr (BETA) {
-                const f32x4_t old = *c;
-                v[0] += beta * old[0]; v[1] += beta * old[1];
-                v[2] += beta * old[2]; v[3] += beta * old[3];
+                const f32x4_t o = old[j][st];
+                v[0] += beta * o[0]; v[1] += beta * o[1];
+                v[2] += beta * o[2]; v[3] += beta * o[3];
               }
-              *c = v;
+              *(f32x4_t*)((float*)Cz + ci) = v;
             }
           }
           __builtin_amdgcn_sched_barrier(0);
