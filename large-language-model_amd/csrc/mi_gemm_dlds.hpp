@@ -646,8 +646,7 @@ __global__ void __launch_bounds__(64 * WGM * WGN * KG)
     // rows of 32 contiguous columns (64 or 128 bytes per row) instead of 32 rows of
     // 16 bytes.  A block is wholly inside the matrix or wholly past its edge (an
     // edge tile's extra blocks are skipped).  One barrier first: the patches reuse
-    // the ring's LDS.
-    __syncthreads();
+    // the ring's LDS (the barrier is in store_tile, after the first beta loads).
     constexpr int PP = 36;  // patch pitch (floats)
     static_assert(NWAVE * 32 * PP * 4 <= LDS_BYTES, "epilogue patches fit the ring");
     float* patch = reinterpret_cast<float*>(smem) + wave * (32 * PP);
@@ -658,30 +657,42 @@ __global__ void __launch_bounds__(64 * WGM * WGN * KG)
     auto store_tile = [&](auto BF_c, auto BETA_c) __attribute__((always_inline)) {
       constexpr bool BF = decltype(BF_c)::value, BETA = decltype(BETA_c)::value;
       using OldT = std::conditional_t<BF, u32x2_t, f32x4_t>;
+      auto col_of = [&](int j) __attribute__((always_inline)) { return n0 + wn * WTN + j * 32 + c_out; };
+      auto row_of = [&](int i) __attribute__((always_inline)) {
+        return (int64_t)(m0 + wm * WTM + i * 32 + r_out);
+      };
+      auto inside = [&](int j) __attribute__((always_inline)) {
+        return uniform(n0 + wn * WTN + j * 32) < p.N;
+      };
+      auto valid = [&](int i) __attribute__((always_inline)) {  // row block i stored by this wave
+        return (KG == 1 || i == kg) && uniform(m0 + wm * WTM + i * 32) < p.M;
+      };
+      // beta: the old C of row block i + 1 is loaded while row block i is stored (row
+      // block 0's before the barrier), so the load latency overlaps other work
+      OldT old[2][TN][4];
+      auto load_old = [&](int i, OldT (&dst)[TN][4]) __attribute__((always_inline)) {
 #pragma unroll
-      for (int i = 0; i < TM; ++i) {
-        if (KG == 2 && i != kg) continue;
-        if (uniform(m0 + wm * WTM + i * 32) >= p.M) continue;  // row block past M
-        const int64_t row0 = (int64_t)(m0 + wm * WTM + i * 32 + r_out);
-        auto col_of = [&](int j) __attribute__((always_inline)) { return n0 + wn * WTN + j * 32 + c_out; };
-        auto inside = [&](int j) __attribute__((always_inline)) {
-          return uniform(n0 + wn * WTN + j * 32) < p.N;
-        };
-        // beta: the row block's old C is loaded first, so its memory latency is paid
-        // once per row block rather than once per 32x32 block
-        OldT old[TN][4];
-        if constexpr (BETA) {
+        for (int j = 0; j < TN; ++j) {
+          if (!inside(j)) continue;
 #pragma unroll
-          for (int j = 0; j < TN; ++j) {
-            if (!inside(j)) continue;
-#pragma unroll
-            for (int st = 0; st < 4; ++st) {
-              const int64_t ci = (row0 + 8 * st) * p.ldc + col_of(j);
-              if constexpr (BF) old[j][st] = *(const u32x2_t*)((const uint16_t*)Cz + ci);
-              else old[j][st] = *(const f32x4_t*)((const float*)Cz + ci);
-            }
+          for (int st = 0; st < 4; ++st) {
+            const int64_t ci = (row_of(i) + 8 * st) * p.ldc + col_of(j);
+            if constexpr (BF) dst[j][st] = *(const u32x2_t*)((const uint16_t*)Cz + ci);
+            else dst[j][st] = *(const f32x4_t*)((const float*)Cz + ci);
           }
         }
+      };
+      if constexpr (BETA) {
+        if (valid(0)) load_old(0, old[0]);
+      }
+      __syncthreads();  // the patches reuse the ring's LDS
+#pragma unroll
+      for (int i = 0; i < TM; ++i) {
+        if constexpr (BETA) {
+          if (i + 1 < TM && valid(i + 1)) load_old(i + 1, old[(i + 1) & 1]);
+        }
+        if (!valid(i)) continue;
+        const int64_t row0 = row_of(i);
 #pragma unroll
         for (int j = 0; j < TN; ++j) {
           if (!inside(j)) continue;
@@ -699,7 +710,7 @@ __global__ void __launch_bounds__(64 * WGM * WGN * KG)
             const int64_t ci = (row0 + 8 * st) * p.ldc + col;
             if constexpr (BF) {
               if constexpr (BETA) {
-                const u32x2_t o = old[j][st];
+                const u32x2_t o = old[i & 1][j][st];
                 v[0] += beta * bf16_bits_to_f32(o[0] & 0xffffu);
                 v[1] += beta * bf16_bits_to_f32(o[0] >> 16);
                 v[2] += beta * bf16_bits_to_f32(o[1] & 0xffffu);
@@ -708,7 +719,7 @@ __global__ void __launch_bounds__(64 * WGM * WGN * KG)
               *(u32x2_t*)((uint16_t*)Cz + ci) = u32x2_t{pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3])};
             } else {
               if constexpr (BETA) {
-                const f32x4_t o = old[j][st];
+                const f32x4_t o = old[i & 1][j][st];
                 v[0] += beta * o[0]; v[1] += beta * o[1];
                 v[2] += beta * o[2]; v[3] += beta * o[3];
               }
