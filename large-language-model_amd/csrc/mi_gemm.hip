@@ -254,6 +254,10 @@ Plan make_plan(int dtype_in, int64_t M, int64_t N, int64_t Ktot, int64_t batch, 
         const double cL = 2.6 * (double)cdiv(tilesL, cus);
         const int64_t tilesM = cdiv(M, 256) * cdiv(N, 192) * batch;
         const double cM = N % 64 == 0 ? 1.95 * (double)cdiv(tilesM, cus) : 1e30;
+        // 128x192 split-K tiles (V): 1.5 W tiles of work, one workgroup per CU
+        const int64_t tilesV = cdiv(M, 128) * cdiv(N, 192) * batch;
+        const double cV = N % 64 == 0 ? 1.5 * (double)cdiv(tilesV, cus) : 1e30;
+        if (cV < cM && cV < cL && cV < cW && cV < cS) return plan_for(CFG_V, 1);
         if (cM < cL && cM <= cW && cM <= cS) return plan_for(CFG_M, 1);
         if (cL <= cW && cL <= cS) return plan_for(CFG_L, 1);
         if (cW < cS) return plan_for(CFG_W, 1);
@@ -292,7 +296,7 @@ void describe_plan(char* buf, size_t len, int dtype_in, bool fast, const Plan& p
                    int transB, int64_t batch) {
   const CfgShape sh = shape_of(dtype_in, pl.cfg);
   const char* kind = (dtype_in == MI_BF16 && fast && pl.cfg != CFG_PRO)
-                         ? (pl.cfg == CFG_W ? "dlds-kg2" : "dlds")
+                         ? (pl.cfg == CFG_W || pl.cfg == CFG_V ? "dlds-kg2" : "dlds")
                          : "regstage";
   std::snprintf(buf, len, "%s %s %dx%d %s%s split%d tiles%lld", kind,
                 dtype_in == MI_BF16 ? "bf16" : "f32", sh.bm, sh.bn, transA ? "T" : "N",
@@ -492,7 +496,7 @@ int run(const Problem& P, hipStream_t stream) {
   // the direct epilogue works in whole 32x32 blocks (an edge tile skips those past M, N)
   const bool fast_epi = plan.splits == 1 && !P.ep.bias && !P.ep.residual && cvec &&
                         b.causal != MI_CAUSAL_OUT_LOWER && P.M % 32 == 0 && P.N % 32 == 0;
-  const int64_t kstep = plan.cfg == CFG_W ? MI_W_BK : 64;
+  const int64_t kstep = plan.cfg == CFG_W || plan.cfg == CFG_V ? MI_W_BK : 64;
   KernelFn fn = pick_kernel(P.dtype_in, P.transA, P.transB, plan.cfg, fast, P.K % kstep != 0, fast_epi);
   if (!fn) return fail(MI_ERR_UNSUPPORTED, "no kernel for this layout / mode");
 

@@ -41,6 +41,10 @@ typedef float elem_t;
 #ifndef MI_W_STAGES
 #define MI_W_STAGES 4
 #endif
+// 128x192 with wave-level split-K: ring depth (40 KB per stage at K tile 64).
+#ifndef MI_V_STAGES
+#define MI_V_STAGES 3
+#endif
 
 #define MI_CAT5(a, b, c, d, e) a##b##c##d##e
 #define MI_PICK_NAME(dt, ta, tb) MI_CAT5(pick_, dt, _, ta, tb)
@@ -63,6 +67,8 @@ KernelFn dlds_kernel(int cfg) {
       return gemm_dlds_kernel<128, 128, MI_W_BK, MI_W_STAGES, AK, BK, MODE_PLAIN, V, 2, 2, 2>;
     case CFG_M:
       return gemm_dlds_kernel<256, 192, MI_DLDS_BK, MI_DLDS_STAGES, AK, BK, MODE_PLAIN, V, 4, 2, 1>;
+    case CFG_V:
+      return gemm_dlds_kernel<128, 192, MI_W_BK, MI_V_STAGES, AK, BK, MODE_PLAIN, V, 2, 2, 2>;
     default: return nullptr;
   }
 }

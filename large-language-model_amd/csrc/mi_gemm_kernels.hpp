@@ -13,9 +13,10 @@ typedef void (*KernelFn)(Params);
 //         DUAL 256x128 (+ second B), PRO 256x256 with the SiLU-gate A prologue,
 //         W 128x128 with wave-level split-K (8 waves: two groups of 4 waves of
 //         64x64, each over half of every K tile, summed through LDS),
-//         M 256x192 (8 waves of 64x96).
+//         M 256x192 (8 waves of 64x96), V 128x192 with wave-level split-K (two
+//         groups of 4 waves of 64x96).
 //   fp32: L = S = W 128x128, DUAL 128x64, PRO 128x128.
-enum Cfg { CFG_L = 0, CFG_S = 1, CFG_DUAL = 2, CFG_PRO = 3, CFG_W = 4, CFG_M = 5, NCFG = 6 };
+enum Cfg { CFG_L = 0, CFG_S = 1, CFG_DUAL = 2, CFG_PRO = 3, CFG_W = 4, CFG_M = 5, CFG_V = 6, NCFG = 7 };
 
 struct CfgShape {
   int bm, bn;
@@ -34,6 +35,7 @@ inline CfgShape cfg_shape(bool bf16, int cfg) {
          : cfg == CFG_S ? CfgShape{128, 128}
          : cfg == CFG_W ? CfgShape{128, 128, 512}
          : cfg == CFG_M ? CfgShape{256, 192, 512}
+         : cfg == CFG_V ? CfgShape{128, 192, 512}
          : cfg == CFG_DUAL ? CfgShape{256, 128}
                            : CfgShape{256, 256};
   return cfg == CFG_DUAL ? CfgShape{128, 64} : CfgShape{128, 128};

@@ -321,6 +321,39 @@ def test_tile_256x192(mi, dev, oracle, tA, tB):
         check(got.sum(axis=1), row, TOL_BF16, f"256x192 K={K} row checksum")
 
 
+@pytest.mark.parametrize("tA,tB", [(0, 0), (0, 1), (1, 0), (1, 1)], ids=["NN", "NT", "TN", "TT"])
+def test_tile_128x192_split_k_groups(mi, dev, oracle, tA, tB):
+    """128x192 tiles with wave-level split-K (two groups of 4 waves over halves of every
+    K tile, summed through LDS; the qkv dW grid 2048x3072 in one round of 256 tiles):
+    bf16 output, and fp32 beta = 1 accumulation. Sampled rows against the oracle, every
+    element through checksums."""
+    import torch
+
+    M, N, K = 2048, 3072, 1024
+    plan = mi.describe(tA, tB, M, N, K)
+    assert "dlds-kg2 bf16 128x192" in plan, plan
+    a = inputs(oracle, (M, K), 151 + 2 * tA + tB, 1.0)
+    b = inputs(oracle, (K, N), 152 + 2 * tA + tB, 1e-2)
+    rows = sample_rows(M, 6, 7)
+    col, row = checksums(a, b)
+    A, B = to_dev(layout(a, tA), dev, True), to_dev(layout(b, tB), dev, True)
+    C = torch.empty((M, N), dtype=torch.bfloat16, device=dev)
+    mi.gemm(A, B, C, M, N, K, transA=tA, transB=tB)
+    torch.cuda.synchronize()
+    got = host(C)
+    ref_rows = oracle.gemm(0, 0, M, N, K, a, b, rows=rows)
+    check(got[rows], ref_rows, TOL_BF16, f"128x192 kg2 tA={tA} tB={tB} rows")
+    check(got.sum(axis=0), col, TOL_BF16, f"128x192 kg2 tA={tA} tB={tB} column checksum")
+    check(got.sum(axis=1), row, TOL_BF16, f"128x192 kg2 tA={tA} tB={tB} row checksum")
+    c0 = inputs(oracle, (M, N), 153, 0.5, False)
+    C32 = torch.from_numpy(c0).to(dev)
+    mi.gemm(A, B, C32, M, N, K, transA=tA, transB=tB, beta=1.0)
+    torch.cuda.synchronize()
+    got = C32.cpu().numpy().astype(np.float64) - c0.astype(np.float64)
+    check(got[rows], ref_rows, TOL_F32, f"128x192 kg2 tA={tA} tB={tB} beta=1 rows")
+    check(got.sum(axis=0), col, TOL_F32, f"128x192 kg2 tA={tA} tB={tB} beta=1 column checksum")
+
+
 def test_tile_256x192_partial_round(mi, dev, oracle):
     """256x192 tiles for a grid below one round of 256x256 tiles (the dW shapes of
     gate / up and down: 240 or 242 tiles instead of 176), TN with fp32 beta = 1
