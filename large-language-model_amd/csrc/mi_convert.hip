@@ -15,7 +15,10 @@
 //
 // HBM-bound.  The transpose goes through a 64 x 64 LDS tile (rows padded by one
 // element); global reads run along the source rows and global writes along the
-// destination rows, 4 elements (8 or 16 bytes) per access where aligned.
+// destination rows, 4 elements (8 or 16 bytes) per access where aligned, with all four
+// of a thread's reads in flight before the tile is written to LDS.  The row-preserving
+// copy moves 8 elements (16 bytes of bf16) per thread where aligned.  bf16 -> bf16
+// moves the bits as they are (NaN payloads included).
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
@@ -35,6 +38,13 @@ __device__ __forceinline__ float load_any(const void* p, int64_t i, int dt) {
 __device__ __forceinline__ void store_any(void* p, int64_t i, int dt, float v) {
   if (dt == 1) ((uint16_t*)p)[i] = (uint16_t)f32_to_bf16_rne(v);
   else ((float*)p)[i] = v;
+}
+
+// bf16 of a float that holds a bf16 value exactly: its upper half (== round to nearest
+// even for such a value, and a NaN keeps its payload).
+__device__ __forceinline__ uint32_t bf16_upper(float v) { return __float_as_uint(v) >> 16; }
+__device__ __forceinline__ uint32_t pack_upper2(float lo, float hi) {
+  return (__float_as_uint(lo) >> 16) | (__float_as_uint(hi) & 0xffff0000u);
 }
 
 constexpr int CT = 64;  // tile edge
@@ -64,84 +74,144 @@ __device__ __forceinline__ void ld4(const void* p, int64_t i, float* v) {
   }
 }
 
+// Eight consecutive elements at element index i (i % 8 == 0, base aligned).
 template <int DT>
+__device__ __forceinline__ void ld8(const void* p, int64_t i, float* v) {
+  if constexpr (DT == 0) {
+    ld4<0>(p, i, v);
+    ld4<0>(p, i + 4, v + 4);
+  } else {
+    const uint4 q = *(const uint4*)((const uint16_t*)p + i);
+    const uint32_t w[4] = {q.x, q.y, q.z, q.w};
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      if constexpr (DT == 1) {
+        v[2 * j] = __uint_as_float(w[j] << 16);
+        v[2 * j + 1] = __uint_as_float(w[j] & 0xffff0000u);
+      } else {
+        const _Float16* h = (const _Float16*)&w[j];
+        v[2 * j] = (float)h[0];
+        v[2 * j + 1] = (float)h[1];
+      }
+    }
+  }
+}
+
+// Stores: RAW (source bf16, destination bf16) takes the upper halves, anything else
+// rounds to nearest even.
+template <int DT, bool RAW>
 __device__ __forceinline__ void st1(void* p, int64_t i, float v) {
-  if constexpr (DT == 1) ((uint16_t*)p)[i] = (uint16_t)f32_to_bf16_rne(v);
+  if constexpr (DT == 1) ((uint16_t*)p)[i] = (uint16_t)(RAW ? bf16_upper(v) : f32_to_bf16_rne(v));
   else ((float*)p)[i] = v;
 }
 
-template <int DT>
+template <bool RAW>
+__device__ __forceinline__ uint32_t pack2(float lo, float hi) {
+  return RAW ? pack_upper2(lo, hi) : pack_bf16x2(lo, hi);
+}
+
+template <int DT, bool RAW>
 __device__ __forceinline__ void st4(void* p, int64_t i, const float* v) {
-  if constexpr (DT == 1) *(uint2*)((uint16_t*)p + i) = make_uint2(pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3]));
+  if constexpr (DT == 1) *(uint2*)((uint16_t*)p + i) = make_uint2(pack2<RAW>(v[0], v[1]), pack2<RAW>(v[2], v[3]));
   else *(float4*)((float*)p + i) = make_float4(v[0], v[1], v[2], v[3]);
+}
+
+template <int DT, bool RAW>
+__device__ __forceinline__ void st8(void* p, int64_t i, const float* v) {
+  if constexpr (DT == 1) {
+    *(uint4*)((uint16_t*)p + i) = make_uint4(pack2<RAW>(v[0], v[1]), pack2<RAW>(v[2], v[3]),
+                                             pack2<RAW>(v[4], v[5]), pack2<RAW>(v[6], v[7]));
+  } else {
+    st4<0, RAW>(p, i, v);
+    st4<0, RAW>(p, i + 4, v + 4);
+  }
 }
 
 // One 64 x 64 tile per workgroup of 256 threads.  Reads: each thread takes 4 runs of
 // 4 consecutive source elements (16 threads per 64-element source row); writes: 4
 // runs of 4 consecutive destination elements.  vec (uniform) says every run is
-// aligned for one 8- or 16-byte access; edge tiles fall back to single elements.
+// aligned for one 8- or 16-byte access.  An interior tile issues its four reads
+// before any LDS write and its four LDS reads before any global write; edge tiles
+// take single elements under bounds checks.  LDS: row lr, column j at bank
+// (lr + j) % 64, so a write (16 threads along a row, 4 rows) and a read (16 runs of
+// 4 rows down a column, 4 columns) touch 64 distinct banks per element step.
 template <int SRC, int DST>
 __global__ void __launch_bounds__(256) convert_transpose_kernel(ConvParams p, int vec) {
+  constexpr bool RAW = SRC == 1 && DST == 1;
   __shared__ float tile[CT][CT + 1];
   const int64_t r0 = (int64_t)blockIdx.y * CT, c0 = (int64_t)blockIdx.x * CT;
   const int t = threadIdx.x, j4 = (t & 15) * 4, sub = t >> 4;
-  const bool full_c = c0 + CT <= p.cols, full_r = r0 + CT <= p.rows;
+  const bool fast = vec && c0 + CT <= p.cols && r0 + CT <= p.rows;
+  float v[4][4];
+  if (fast) {
 #pragma unroll
-  for (int k = 0; k < 4; ++k) {
-    const int lr = sub + 16 * k;
-    const int64_t r = r0 + lr;
-    if (r >= p.rows) continue;
-    const int64_t base = (p.row0 + r) * p.src_ld + c0 + j4;
-    float v[4];
-    if (vec && full_c) {
-      ld4<SRC>(p.src, base, v);
-    } else {
+    for (int k = 0; k < 4; ++k) ld4<SRC>(p.src, (p.row0 + r0 + sub + 16 * k) * p.src_ld + c0 + j4, v[k]);
+  } else {
 #pragma unroll
-      for (int e = 0; e < 4; ++e) v[e] = c0 + j4 + e < p.cols ? ld1<SRC>(p.src, base + e) : 0.0f;
-    }
-#pragma unroll
-    for (int e = 0; e < 4; ++e) tile[lr][j4 + e] = v[e];
-  }
-  __syncthreads();
-#pragma unroll
-  for (int k = 0; k < 4; ++k) {
-    const int lc = sub + 16 * k;
-    const int64_t c = c0 + lc;  // destination row
-    if (c >= p.cols) continue;
-    float v[4];
-#pragma unroll
-    for (int e = 0; e < 4; ++e) v[e] = tile[j4 + e][lc];
-    const int64_t base = c * p.dst_ld + r0 + j4;
-    if (vec && full_r) {
-      st4<DST>(p.dst, base, v);
-    } else {
+    for (int k = 0; k < 4; ++k) {
+      const int64_t r = r0 + sub + 16 * k, base = (p.row0 + r) * p.src_ld + c0 + j4;
 #pragma unroll
       for (int e = 0; e < 4; ++e)
-        if (r0 + j4 + e < p.rows) st1<DST>(p.dst, base + e, v[e]);
+        v[k][e] = r < p.rows && c0 + j4 + e < p.cols ? ld1<SRC>(p.src, base + e) : 0.0f;
+    }
+  }
+#pragma unroll
+  for (int k = 0; k < 4; ++k)
+#pragma unroll
+    for (int e = 0; e < 4; ++e) tile[sub + 16 * k][j4 + e] = v[k][e];
+  __syncthreads();
+#pragma unroll
+  for (int k = 0; k < 4; ++k)
+#pragma unroll
+    for (int e = 0; e < 4; ++e) v[k][e] = tile[j4 + e][sub + 16 * k];
+  if (fast) {
+#pragma unroll
+    for (int k = 0; k < 4; ++k) st4<DST, RAW>(p.dst, (c0 + sub + 16 * k) * p.dst_ld + r0 + j4, v[k]);
+  } else {
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const int64_t c = c0 + sub + 16 * k;  // destination row
+      if (c >= p.cols) continue;
+      const int64_t base = c * p.dst_ld + r0 + j4;
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        if (r0 + j4 + e < p.rows) st1<DST, RAW>(p.dst, base + e, v[k][e]);
     }
   }
 }
 
-// Row-preserving copy, 4 elements (one 8- or 16-byte access each way) per thread: x
-// covers the columns, y the rows (strided past 65535).  Needs the alignment of the
-// transpose's vector path.
-template <int SRC, int DST>
+// Row-preserving copy, VE (4 or 8) elements per thread and access each way: x covers
+// the columns, y the rows (strided past 65535).  Needs cols, both leading dimensions
+// and the source row offset to be multiples of VE and both bases aligned to VE
+// elements.
+template <int SRC, int DST, int VE>
 __global__ void __launch_bounds__(256) convert_copy_vec_kernel(ConvParams p) {
-  const int64_t c = ((int64_t)blockIdx.x * 256 + threadIdx.x) * 4;
+  constexpr bool RAW = SRC == 1 && DST == 1;
+  const int64_t c = ((int64_t)blockIdx.x * 256 + threadIdx.x) * VE;
   if (c >= p.cols) return;
   for (int64_t r = blockIdx.y; r < p.rows; r += gridDim.y) {
-    float v[4];
-    ld4<SRC>(p.src, (p.row0 + r) * p.src_ld + c, v);
-    st4<DST>(p.dst, r * p.dst_ld + c, v);
+    float v[VE];
+    if constexpr (VE == 8) {
+      ld8<SRC>(p.src, (p.row0 + r) * p.src_ld + c, v);
+      st8<DST, RAW>(p.dst, r * p.dst_ld + c, v);
+    } else {
+      ld4<SRC>(p.src, (p.row0 + r) * p.src_ld + c, v);
+      st4<DST, RAW>(p.dst, r * p.dst_ld + c, v);
+    }
   }
 }
 
 __global__ void __launch_bounds__(256) convert_copy_kernel(ConvParams p) {
   const int64_t n = p.rows * p.cols;
+  const bool raw = p.src_dtype == 1 && p.dst_dtype == 1;
   for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (int64_t)gridDim.x * 256) {
     const int64_t r = i / p.cols, c = i - r * p.cols;
-    store_any(p.dst, r * p.dst_ld + c, p.dst_dtype,
-              load_any(p.src, (p.row0 + r) * p.src_ld + c, p.src_dtype));
+    if (raw) {
+      ((uint16_t*)p.dst)[r * p.dst_ld + c] = ((const uint16_t*)p.src)[(p.row0 + r) * p.src_ld + c];
+    } else {
+      store_any(p.dst, r * p.dst_ld + c, p.dst_dtype,
+                load_any(p.src, (p.row0 + r) * p.src_ld + c, p.src_dtype));
+    }
   }
 }
 
@@ -149,19 +219,26 @@ __global__ void __launch_bounds__(256) convert_copy_kernel(ConvParams p) {
 
 hipError_t launch_convert(const ConvParams& p, bool transpose, int cus, hipStream_t stream) {
   const int ses = p.src_dtype == 0 ? 4 : 2, des = p.dst_dtype == 0 ? 4 : 2;
-  const int vec = p.src_ld % 4 == 0 && p.dst_ld % 4 == 0 && (p.row0 * p.src_ld) % 4 == 0 &&
-                  (uintptr_t)p.src % (4 * ses) == 0 && (uintptr_t)p.dst % (4 * des) == 0;
+  auto aligned = [&](int n) {
+    return p.src_ld % n == 0 && p.dst_ld % n == 0 && (p.row0 * p.src_ld) % n == 0 &&
+           (uintptr_t)p.src % (n * ses) == 0 && (uintptr_t)p.dst % (n * des) == 0;
+  };
+  const int vec = aligned(4);
   if (!transpose && vec && p.cols % 4 == 0) {
-    const dim3 grid((unsigned)((p.cols + 1023) / 1024), (unsigned)std::min<int64_t>(p.rows, 65535));
-    auto go = [&](auto kern) { hipLaunchKernelGGL(kern, grid, dim3(256), 0, stream, p); };
+    const int ve = aligned(8) && p.cols % 8 == 0 ? 8 : 4;
+    const dim3 grid((unsigned)((p.cols + 256 * ve - 1) / (256 * ve)), (unsigned)std::min<int64_t>(p.rows, 65535));
+    auto go = [&](auto k8, auto k4) {
+      if (ve == 8) hipLaunchKernelGGL(k8, grid, dim3(256), 0, stream, p);
+      else hipLaunchKernelGGL(k4, grid, dim3(256), 0, stream, p);
+    };
     if (p.dst_dtype == 1) {
-      if (p.src_dtype == 1) go(convert_copy_vec_kernel<1, 1>);
-      else if (p.src_dtype == 2) go(convert_copy_vec_kernel<2, 1>);
-      else go(convert_copy_vec_kernel<0, 1>);
+      if (p.src_dtype == 1) go(convert_copy_vec_kernel<1, 1, 8>, convert_copy_vec_kernel<1, 1, 4>);
+      else if (p.src_dtype == 2) go(convert_copy_vec_kernel<2, 1, 8>, convert_copy_vec_kernel<2, 1, 4>);
+      else go(convert_copy_vec_kernel<0, 1, 8>, convert_copy_vec_kernel<0, 1, 4>);
     } else {
-      if (p.src_dtype == 1) go(convert_copy_vec_kernel<1, 0>);
-      else if (p.src_dtype == 2) go(convert_copy_vec_kernel<2, 0>);
-      else go(convert_copy_vec_kernel<0, 0>);
+      if (p.src_dtype == 1) go(convert_copy_vec_kernel<1, 0, 8>, convert_copy_vec_kernel<1, 0, 4>);
+      else if (p.src_dtype == 2) go(convert_copy_vec_kernel<2, 0, 8>, convert_copy_vec_kernel<2, 0, 4>);
+      else go(convert_copy_vec_kernel<0, 0, 8>, convert_copy_vec_kernel<0, 0, 4>);
     }
     return hipGetLastError();
   }

@@ -34,7 +34,9 @@ def test_load_weights(mi, dev, oracle, tmp_path, fmt, dst):
 @pytest.mark.parametrize("src_dt", ["f32", "bf16", "f16"])
 @pytest.mark.parametrize("transpose", [False, True])
 @pytest.mark.parametrize("R,C,row0,rows", [(130, 77, 5, 100),     # element-wise paths
-                                          (130, 96, 4, 100),     # 4-element accesses
+                                          (130, 96, 4, 100),     # 8-element copy, 4-element transpose
+                                          (130, 100, 4, 100),    # 4-element copy
+                                          (200, 192, 8, 192),    # interior transpose tiles
                                           (70000, 8, 0, 70000)])  # more rows than a grid column
 def test_convert_matrix_slices(mi, dev, src_dt, transpose, R, C, row0, rows):
     import torch
@@ -69,6 +71,26 @@ def test_convert_matrix_padded_destination(mi, dev, transpose):
     want = src.t() if transpose else src
     assert torch.equal(dst[:, :dcols], want)
     assert torch.all(dst[:, dcols:] == 7.0)
+
+
+@pytest.mark.parametrize("transpose", [False, True])
+@pytest.mark.parametrize("R,C,row0,rows", [(200, 192, 8, 192), (130, 77, 5, 100), (130, 100, 4, 100)])
+def test_convert_matrix_bf16_bits_exact(mi, dev, transpose, R, C, row0, rows):
+    """bf16 -> bf16 moves every bit pattern unchanged, NaN payloads and signalling NaNs
+    included, on the interior-tile, edge and copy paths."""
+    import torch
+
+    print(f"convert bf16 bits {R}x{C} rows {row0}+{rows} transpose={transpose}", flush=True)
+    g = torch.Generator().manual_seed(R * C + rows)
+    bits = torch.randint(-32768, 32768, (R, C), generator=g, dtype=torch.int32).to(torch.int16)
+    bits[0, :8] = torch.tensor([0x7f81, 0x7fc1, -0x7f, -0x3f, 0x7f80, -0x80, 0x0001, -0x8000],
+                               dtype=torch.int16)  # sNaN, qNaN, -sNaN, -qNaN, +-inf, subnormal, -0
+    src = bits.to(dev).view(torch.bfloat16)
+    dst = torch.zeros((C, rows) if transpose else (rows, C), dtype=torch.bfloat16, device=dev)
+    mi.convert_matrix(src, mi.MI_BF16, C, row0, rows, C, transpose, dst)
+    want = bits[row0:row0 + rows]
+    want = want.t() if transpose else want
+    assert torch.equal(dst.view(torch.int16).cpu(), want.contiguous())
 
 
 def test_missing_and_mismatched(mi, dev, tmp_path):
