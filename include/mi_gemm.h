@@ -318,6 +318,29 @@ int mi_convert_matrix(void* stream, const void* src, int32_t src_dtype, int64_t 
                       int64_t rows, int64_t cols, int32_t transpose, void* dst, int32_t dst_dtype,
                       int64_t dst_ld);
 
+/* One conversion of mi_convert_matrices: the arguments of mi_convert_matrix. */
+typedef struct mi_convert_job {
+  const void* src;
+  int32_t src_dtype, transpose;
+  int64_t src_ld, row0, rows, cols;
+  void* dst;
+  int32_t dst_dtype, reserved; /* reserved: 0 */
+  int64_t dst_ld;
+} mi_convert_job;
+
+/*
+ * n conversions as mi_convert_matrix would do them one by one, in as few launches
+ * as the dtype pairs allow (one launch per (src_dtype, dst_dtype) pair and 16
+ * jobs).  Replaces the loader's per-tensor loop (Checkpoint.cpp:532-570 around
+ * load_python_tensor / load_python_fused_tensor, :407-530): the three row ranges
+ * of a fused wqkv, the two of a w12 and every other matrix of a checkpoint go
+ * out together.  Every job is checked first (nothing runs if one fails, and the
+ * message names the job); sources may share bytes (row ranges of one fused
+ * matrix), but no destination may overlap another job's source or destination,
+ * since the tiles of a launch run in any order.
+ */
+int mi_convert_matrices(void* stream, const mi_convert_job* jobs, int64_t n);
+
 /*
  * Describe the kernel mi_gemm_batched would launch for this problem (tile,
  * loader, split-K factor) as text into buf (always NUL-terminated).  For

@@ -350,10 +350,22 @@ struct Loader {
   hipStream_t st;
   std::string err;
 
+  struct Range {
+    size_t row0, rows;
+    void* dst;
+  };
+
   // Copies rows [row0, row0 + rows) of the file matrix `name` (expected shape
   // file_rows x cols, or a vector when file_rows == 0) into dst, transposed or not.
   bool put(const std::string& name, size_t file_rows, size_t cols, size_t row0, size_t rows,
            bool transpose, void* dst, bool required = true) {
+    return put_ranges(name, file_rows, cols, {{row0, rows, dst}}, transpose, required);
+  }
+
+  // Several row ranges of one file matrix (the de-fused rows of wqkv or w12): the
+  // tensor is staged once and the ranges go out in one mi_convert_matrices call.
+  bool put_ranges(const std::string& name, size_t file_rows, size_t cols, const std::vector<Range>& ranges,
+                  bool transpose, bool required = true) {
     const TensorInfo* t = f.find(name);
     if (!t) {
       if (!required) return true;
@@ -367,7 +379,8 @@ struct Loader {
       return err = "tensor '" + name + "' has shape [ " + got + "]", false;
     }
     if (!dtype_bytes(t->dtype)) return err = "tensor '" + name + "' has dtype " + t->dtype, false;
-    if (!dst) return err = "no destination for '" + name + "'", false;
+    for (const Range& r : ranges)
+      if (!r.dst) return err = "no destination for '" + name + "'", false;
     const size_t bytes = t->end - t->begin;
     // The staging buffer is reused (and freed when it grows): the previous
     // conversion, which reads it on `st`, must be done first.
@@ -375,9 +388,23 @@ struct Loader {
     if (!stage(bytes)) return err = "cannot allocate the staging buffer", false;
     if (hipMemcpy(t_stage, f.data(*t), bytes, hipMemcpyHostToDevice) != hipSuccess)
       return err = "copy of '" + name + "' to the device failed", false;
-    const int64_t R = vec ? 1 : (int64_t)rows, C = (int64_t)cols;
-    const int s = mi_convert_matrix(st, t_stage, dtype_code(t->dtype), C, vec ? 0 : (int64_t)row0, R, C,
-                                    transpose ? 1 : 0, dst, dst_dtype, transpose ? R : C);
+    std::vector<mi_convert_job> jobs;
+    for (const Range& r : ranges) {
+      const int64_t R = vec ? 1 : (int64_t)r.rows, C = (int64_t)cols;
+      mi_convert_job j{};
+      j.src = t_stage;
+      j.src_dtype = dtype_code(t->dtype);
+      j.transpose = transpose ? 1 : 0;
+      j.src_ld = C;
+      j.row0 = vec ? 0 : (int64_t)r.row0;
+      j.rows = R;
+      j.cols = C;
+      j.dst = r.dst;
+      j.dst_dtype = dst_dtype;
+      j.dst_ld = transpose ? R : C;
+      jobs.push_back(j);
+    }
+    const int s = mi_convert_matrices(st, jobs.data(), (int64_t)jobs.size());
     if (s != MI_OK) return err = "converting '" + name + "': " + mi_last_error(), false;
     return true;
   }
@@ -412,12 +439,10 @@ bool load_weights(const std::string& path, const ModelConfig& c, const ModelWeig
       ok = ok && L.put(p + "attention.wo.weight", H, q, 0, H, true, lw.Wo);
       ok = ok && L.put(p + "feed_forward.w3.weight", H, I, 0, H, true, lw.w_down);
       // de-fused wqkv rows: Wq [0, q), Wk [q, q + kv), Wv [q + kv, q + 2 kv)
-      ok = ok && L.put(p + "attention.wqkv.weight", q + 2 * kv, H, 0, q, true, lw.Wq);
-      ok = ok && L.put(p + "attention.wqkv.weight", q + 2 * kv, H, q, kv, true, lw.Wk);
-      ok = ok && L.put(p + "attention.wqkv.weight", q + 2 * kv, H, q + kv, kv, true, lw.Wv);
+      ok = ok && L.put_ranges(p + "attention.wqkv.weight", q + 2 * kv, H,
+                              {{0, q, lw.Wq}, {q, kv, lw.Wk}, {q + kv, kv, lw.Wv}}, true);
       // de-fused w12 rows: w_gate [0, I), w_up [I, 2 I)
-      ok = ok && L.put(p + "feed_forward.w12.weight", 2 * I, H, 0, I, true, lw.w_gate);
-      ok = ok && L.put(p + "feed_forward.w12.weight", 2 * I, H, I, I, true, lw.w_up);
+      ok = ok && L.put_ranges(p + "feed_forward.w12.weight", 2 * I, H, {{0, I, lw.w_gate}, {I, I, lw.w_up}}, true);
     }
   } else {  // engine names and layout (Checkpoint.cpp:147-174, 331-388)
     ok = ok && L.put("token_embeddings", V, H, 0, V, false, w.token_embeddings);

@@ -13,15 +13,17 @@
 // destination dtype (fp32, or bf16 rounded to nearest even).  bf16 -> fp32 and
 // f16 -> fp32 are exact, as in the reference.
 //
-// HBM-bound.  The transpose goes through a 64 x 64 LDS tile (rows padded by one
-// element); global reads run along the source rows and global writes along the
-// destination rows, 4 elements (8 or 16 bytes) per access where aligned, with all four
-// of a thread's reads in flight before the tile is written to LDS.  The row-preserving
-// copy moves 8 elements (16 bytes of bf16) per thread where aligned.  bf16 -> bf16
-// moves the bits as they are (NaN payloads included).
+// HBM-bound.  The transpose goes through an LDS tile of 64 source rows x 256 source
+// columns (rows padded by one element); global reads run along the source rows and
+// global writes along the destination rows, 8 elements (16 bytes of bf16) per thread
+// and run where aligned, with all of a thread's reads in flight before the tile is
+// written to LDS.  The row-preserving copy moves 8 elements per thread where aligned.
+// mi_convert_matrices puts many conversions into one launch of such tiles.  bf16 ->
+// bf16 moves the bits as they are (NaN payloads included).
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <vector>
 
 #include "mi_convert.hpp"
 #include "mi_gemm_device.hpp"
@@ -47,7 +49,7 @@ __device__ __forceinline__ uint32_t pack_upper2(float lo, float hi) {
   return (__float_as_uint(lo) >> 16) | (__float_as_uint(hi) & 0xffff0000u);
 }
 
-constexpr int CT = 64;  // tile edge
+constexpr int TR = 64, TC = 256;  // transpose / batch tile: source rows x source columns
 
 template <int DT>
 __device__ __forceinline__ float ld1(const void* p, int64_t i) {
@@ -127,57 +129,144 @@ __device__ __forceinline__ void st8(void* p, int64_t i, const float* v) {
   }
 }
 
-// One 64 x 64 tile per workgroup of 256 threads.  Reads: each thread takes 4 runs of
-// 4 consecutive source elements (16 threads per 64-element source row); writes: 4
-// runs of 4 consecutive destination elements.  vec (uniform) says every run is
-// aligned for one 8- or 16-byte access.  An interior tile issues its four reads
-// before any LDS write and its four LDS reads before any global write; edge tiles
-// take single elements under bounds checks.  LDS: row lr, column j at bank
-// (lr + j) % 64, so a write (16 threads along a row, 4 rows) and a read (16 runs of
-// 4 rows down a column, 4 columns) touch 64 distinct banks per element step.
+// 8 consecutive elements at element index i: vec 2 one access per 8 (16 bytes of
+// bf16 / f16), vec 1 two 4-element accesses.
+template <int DT>
+__device__ __forceinline__ void ld_run(const void* p, int64_t i, float* v, int vec) {
+  if (vec == 2) {
+    ld8<DT>(p, i, v);
+  } else {
+    ld4<DT>(p, i, v);
+    ld4<DT>(p, i + 4, v + 4);
+  }
+}
+
+template <int DT, bool RAW>
+__device__ __forceinline__ void st_run(void* p, int64_t i, const float* v, int vec) {
+  if (vec == 2) {
+    st8<DT, RAW>(p, i, v);
+  } else {
+    st4<DT, RAW>(p, i, v);
+    st4<DT, RAW>(p, i + 4, v + 4);
+  }
+}
+
+// One tile of TR source rows x TC source columns per workgroup of 256 threads.
+// Reads: 32 threads per 256-element source row, 8 consecutive elements each, 8 rows
+// per pass, 8 passes (512-byte row segments of bf16: longer source segments beat
+// longer destination segments when the data does not fit the last-level cache);
+// writes: 8 threads per 64-element destination row, 8 elements each, 32 rows per
+// pass.  vec (uniform): 2 or 1 when every run is aligned for 8- or 4-element
+// accesses, 0 for single elements.  An interior tile issues all eight reads before
+// any LDS write and all eight LDS reads before any global write; edge tiles take
+// single elements under bounds checks.  LDS row lr, column j sits at bank
+// (lr + j) % 64, so the reads down a column (8 runs of 8 rows, 8 columns per wave)
+// touch 64 distinct banks per element step.
 template <int SRC, int DST>
-__global__ void __launch_bounds__(256) convert_transpose_kernel(ConvParams p, int vec) {
+__device__ __forceinline__ void transpose_tile(const ConvParams& p, int vec, int64_t r0, int64_t c0,
+                                               float (*tile)[TC + 1]) {
   constexpr bool RAW = SRC == 1 && DST == 1;
-  __shared__ float tile[CT][CT + 1];
-  const int64_t r0 = (int64_t)blockIdx.y * CT, c0 = (int64_t)blockIdx.x * CT;
-  const int t = threadIdx.x, j4 = (t & 15) * 4, sub = t >> 4;
-  const bool fast = vec && c0 + CT <= p.cols && r0 + CT <= p.rows;
-  float v[4][4];
+  const int t = threadIdx.x, rj = (t & 31) * 8, rs = t >> 5, wj = (t & 7) * 8, ws = t >> 3;
+  const bool fast = vec && c0 + TC <= p.cols && r0 + TR <= p.rows;
+  float v[8][8];
   if (fast) {
 #pragma unroll
-    for (int k = 0; k < 4; ++k) ld4<SRC>(p.src, (p.row0 + r0 + sub + 16 * k) * p.src_ld + c0 + j4, v[k]);
+    for (int k = 0; k < 8; ++k) ld_run<SRC>(p.src, (p.row0 + r0 + rs + 8 * k) * p.src_ld + c0 + rj, v[k], vec);
   } else {
 #pragma unroll
-    for (int k = 0; k < 4; ++k) {
-      const int64_t r = r0 + sub + 16 * k, base = (p.row0 + r) * p.src_ld + c0 + j4;
+    for (int k = 0; k < 8; ++k) {
+      const int64_t r = r0 + rs + 8 * k, base = (p.row0 + r) * p.src_ld + c0 + rj;
 #pragma unroll
-      for (int e = 0; e < 4; ++e)
-        v[k][e] = r < p.rows && c0 + j4 + e < p.cols ? ld1<SRC>(p.src, base + e) : 0.0f;
+      for (int e = 0; e < 8; ++e)
+        v[k][e] = r < p.rows && c0 + rj + e < p.cols ? ld1<SRC>(p.src, base + e) : 0.0f;
     }
   }
 #pragma unroll
-  for (int k = 0; k < 4; ++k)
+  for (int k = 0; k < 8; ++k)
 #pragma unroll
-    for (int e = 0; e < 4; ++e) tile[sub + 16 * k][j4 + e] = v[k][e];
+    for (int e = 0; e < 8; ++e) tile[rs + 8 * k][rj + e] = v[k][e];
   __syncthreads();
 #pragma unroll
-  for (int k = 0; k < 4; ++k)
+  for (int k = 0; k < 8; ++k)
 #pragma unroll
-    for (int e = 0; e < 4; ++e) v[k][e] = tile[j4 + e][sub + 16 * k];
+    for (int e = 0; e < 8; ++e) v[k][e] = tile[wj + e][ws + 32 * k];
   if (fast) {
 #pragma unroll
-    for (int k = 0; k < 4; ++k) st4<DST, RAW>(p.dst, (c0 + sub + 16 * k) * p.dst_ld + r0 + j4, v[k]);
+    for (int k = 0; k < 8; ++k) st_run<DST, RAW>(p.dst, (c0 + ws + 32 * k) * p.dst_ld + r0 + wj, v[k], vec);
   } else {
 #pragma unroll
-    for (int k = 0; k < 4; ++k) {
-      const int64_t c = c0 + sub + 16 * k;  // destination row
+    for (int k = 0; k < 8; ++k) {
+      const int64_t c = c0 + ws + 32 * k;  // destination row
       if (c >= p.cols) continue;
-      const int64_t base = c * p.dst_ld + r0 + j4;
+      const int64_t base = c * p.dst_ld + r0 + wj;
 #pragma unroll
-      for (int e = 0; e < 4; ++e)
-        if (r0 + j4 + e < p.rows) st1<DST, RAW>(p.dst, base + e, v[k][e]);
+      for (int e = 0; e < 8; ++e)
+        if (r0 + wj + e < p.rows) st1<DST, RAW>(p.dst, base + e, v[k][e]);
     }
   }
+}
+
+// The same tile copied without the transpose (global to global, the read runs).
+template <int SRC, int DST>
+__device__ __forceinline__ void copy_tile(const ConvParams& p, int vec, int64_t r0, int64_t c0) {
+  constexpr bool RAW = SRC == 1 && DST == 1;
+  const int t = threadIdx.x, rj = (t & 31) * 8, rs = t >> 5;
+  if (vec && c0 + TC <= p.cols && r0 + TR <= p.rows) {
+    float v[8][8];
+#pragma unroll
+    for (int k = 0; k < 8; ++k) ld_run<SRC>(p.src, (p.row0 + r0 + rs + 8 * k) * p.src_ld + c0 + rj, v[k], vec);
+#pragma unroll
+    for (int k = 0; k < 8; ++k) st_run<DST, RAW>(p.dst, (r0 + rs + 8 * k) * p.dst_ld + c0 + rj, v[k], vec);
+    return;
+  }
+#pragma unroll
+  for (int k = 0; k < 8; ++k) {
+    const int64_t r = r0 + rs + 8 * k;
+    if (r >= p.rows) continue;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const int64_t c = c0 + rj + e;
+      if (c < p.cols) st1<DST, RAW>(p.dst, r * p.dst_ld + c, ld1<SRC>(p.src, (p.row0 + r) * p.src_ld + c));
+    }
+  }
+}
+
+template <int SRC, int DST>
+__global__ void __launch_bounds__(256) convert_transpose_kernel(ConvParams p, int vec) {
+  __shared__ float tile[TR][TC + 1];
+  transpose_tile<SRC, DST>(p, vec, (int64_t)blockIdx.y * TR, (int64_t)blockIdx.x * TC, tile);
+}
+
+// A launch of several conversions: job j owns the tiles [tile0, tile0 + its tile
+// count) of a 1-D grid, row-major over its tiles_x columns of tiles.  The job table
+// travels in the kernel arguments; the workgroup picks its job with uniform selects
+// over the fixed-size table (no indexed access to the argument block).
+struct ConvBatchJob {
+  ConvParams p;
+  int64_t tile0, tiles_x;
+  int32_t transpose, vec;
+};
+
+struct ConvBatch {
+  ConvBatchJob job[CONV_BATCH];
+  int32_t n;
+};
+
+template <int SRC, int DST>
+__global__ void __launch_bounds__(256) convert_batch_kernel(ConvBatch b) {
+  __shared__ float tile[TR][TC + 1];
+  const int64_t bid = blockIdx.x;
+  int j = 0;
+#pragma unroll
+  for (int i = 1; i < CONV_BATCH; ++i)
+    if (i < b.n && bid >= b.job[i].tile0) j = i;
+  ConvBatchJob J = b.job[0];
+#pragma unroll
+  for (int i = 1; i < CONV_BATCH; ++i)
+    if (i == j) J = b.job[i];
+  const int64_t t = bid - J.tile0, r0 = t / J.tiles_x * TR, c0 = t % J.tiles_x * TC;
+  if (J.transpose) transpose_tile<SRC, DST>(J.p, J.vec, r0, c0, tile);
+  else copy_tile<SRC, DST>(J.p, J.vec, r0, c0);
 }
 
 // Row-preserving copy, VE (4 or 8) elements per thread and access each way: x covers
@@ -243,8 +332,9 @@ hipError_t launch_convert(const ConvParams& p, bool transpose, int cus, hipStrea
     return hipGetLastError();
   }
   if (transpose) {
-    const dim3 grid((unsigned)((p.cols + CT - 1) / CT), (unsigned)((p.rows + CT - 1) / CT));
-    auto go = [&](auto kern) { hipLaunchKernelGGL(kern, grid, dim3(256), 0, stream, p, vec); };
+    const dim3 grid((unsigned)((p.cols + TC - 1) / TC), (unsigned)((p.rows + TR - 1) / TR));
+    const int v = aligned(8) ? 2 : vec;
+    auto go = [&](auto kern) { hipLaunchKernelGGL(kern, grid, dim3(256), 0, stream, p, v); };
     if (p.dst_dtype == 1) {
       if (p.src_dtype == 1) go(convert_transpose_kernel<1, 1>);
       else if (p.src_dtype == 2) go(convert_transpose_kernel<2, 1>);
@@ -260,6 +350,79 @@ hipError_t launch_convert(const ConvParams& p, bool transpose, int cus, hipStrea
     hipLaunchKernelGGL(convert_copy_kernel, dim3((unsigned)blocks), dim3(256), 0, stream, p);
   }
   return hipGetLastError();
+}
+
+namespace {
+
+// 2 when every 8-element run of p is aligned for one access per 8 elements, 1 for 4,
+// 0 otherwise.
+int vec_ok(const ConvParams& p) {
+  const int ses = p.src_dtype == 0 ? 4 : 2, des = p.dst_dtype == 0 ? 4 : 2;
+  auto aligned = [&](int n) {
+    return p.src_ld % n == 0 && p.dst_ld % n == 0 && (p.row0 * p.src_ld) % n == 0 &&
+           (uintptr_t)p.src % (n * ses) == 0 && (uintptr_t)p.dst % (n * des) == 0;
+  };
+  return aligned(8) ? 2 : aligned(4) ? 1 : 0;
+}
+
+template <int SRC, int DST>
+hipError_t launch_batch_group(const ConvParams* jobs, const int* transpose, const int64_t* idx,
+                              int64_t n, hipStream_t stream) {
+  ConvBatch b;
+  int64_t i = 0;
+  while (i < n) {
+    b.n = 0;
+    int64_t tiles = 0;
+    // at most CONV_BATCH jobs and 2^31 - 1 tiles per launch (each job has fewer than 2^30)
+    while (i < n && b.n < CONV_BATCH) {
+      const ConvParams& p = jobs[idx[i]];
+      const int64_t tx = (p.cols + TC - 1) / TC, ty = (p.rows + TR - 1) / TR;
+      if (b.n > 0 && tiles + tx * ty > INT32_MAX) break;
+      ConvBatchJob& J = b.job[b.n++];
+      J.p = p;
+      J.tile0 = tiles;
+      J.tiles_x = tx;
+      J.transpose = transpose[idx[i]] ? 1 : 0;
+      J.vec = vec_ok(p);
+      tiles += tx * ty;
+      ++i;
+    }
+    for (int k = b.n; k < CONV_BATCH; ++k) b.job[k] = b.job[0];
+    hipLaunchKernelGGL((convert_batch_kernel<SRC, DST>), dim3((unsigned)tiles), dim3(256), 0, stream, b);
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+  }
+  return hipSuccess;
+}
+
+}  // namespace
+
+hipError_t launch_convert_batch(const ConvParams* jobs, const int* transpose, int64_t n,
+                                hipStream_t stream) {
+  std::vector<int64_t> idx;
+  idx.reserve((size_t)n);
+  for (int sd = 0; sd < 3; ++sd) {
+    for (int dd = 0; dd < 2; ++dd) {
+      idx.clear();
+      for (int64_t i = 0; i < n; ++i)
+        if (jobs[i].src_dtype == sd && jobs[i].dst_dtype == dd && jobs[i].rows > 0 && jobs[i].cols > 0)
+          idx.push_back(i);
+      if (idx.empty()) continue;
+      const int64_t m = (int64_t)idx.size();
+      hipError_t e;
+      if (dd == 1) {
+        e = sd == 1 ? launch_batch_group<1, 1>(jobs, transpose, idx.data(), m, stream)
+            : sd == 2 ? launch_batch_group<2, 1>(jobs, transpose, idx.data(), m, stream)
+                      : launch_batch_group<0, 1>(jobs, transpose, idx.data(), m, stream);
+      } else {
+        e = sd == 1 ? launch_batch_group<1, 0>(jobs, transpose, idx.data(), m, stream)
+            : sd == 2 ? launch_batch_group<2, 0>(jobs, transpose, idx.data(), m, stream)
+                      : launch_batch_group<0, 0>(jobs, transpose, idx.data(), m, stream);
+      }
+      if (e != hipSuccess) return e;
+    }
+  }
+  return hipSuccess;
 }
 
 }  // namespace mig

@@ -15,6 +15,15 @@ struct ConvParams {
   int src_dtype, dst_dtype;  // 0 fp32, 1 bf16, 2 f16 (source only)
 };
 
+constexpr int CONV_BATCH = 16;  // jobs per launch of launch_convert_batch
+
 hipError_t launch_convert(const ConvParams& p, bool transpose, int cus, hipStream_t stream);
+
+// Several conversions in as few launches as possible: jobs of one (source, destination)
+// dtype pair go into one launch of 64 x 256 tiles (CONV_BATCH jobs per launch at most).
+// The caller has validated every job and checked that no destination overlaps another
+// job's source or destination (the tiles of a launch run in any order).
+hipError_t launch_convert_batch(const ConvParams* jobs, const int* transpose, int64_t n,
+                                hipStream_t stream);
 
 }  // namespace mig

@@ -1045,34 +1045,107 @@ int mi_rmsnorm_bwd(void* stream, const void* dy, const void* x, const void* weig
   return e == hipSuccess ? MI_OK : fail(MI_ERR_HIP, "rmsnorm_bwd launch: %s", hipGetErrorString(e));
 }
 
-int mi_convert_matrix(void* stream, const void* src, int32_t src_dtype, int64_t src_ld, int64_t row0,
-                      int64_t rows, int64_t cols, int32_t transpose, void* dst, int32_t dst_dtype,
-                      int64_t dst_ld) {
-  if (rows < 0 || cols < 0 || row0 < 0) return fail(MI_ERR_SHAPE, "negative size or row offset");
+}  // extern "C"
+
+namespace {
+
+// Argument checks of one conversion (mi_convert_matrix, and each job of
+// mi_convert_matrices; `what` names the job in messages).  On success fills p and the
+// byte extents [s0, s1) of the source rows read and [d0, d1) of the destination
+// rows written; an empty conversion returns MI_OK with p.rows or p.cols 0.
+int check_convert(const void* src, int32_t src_dtype, int64_t src_ld, int64_t row0, int64_t rows,
+                  int64_t cols, int32_t transpose, void* dst, int32_t dst_dtype, int64_t dst_ld,
+                  const char* what, ConvParams& p, uintptr_t& s0, uintptr_t& s1, uintptr_t& d0,
+                  uintptr_t& d1) {
+  p = ConvParams{};
+  s0 = s1 = d0 = d1 = 0;
+  if (rows < 0 || cols < 0 || row0 < 0) return fail(MI_ERR_SHAPE, "%snegative size or row offset", what);
   if (rows == 0 || cols == 0) return MI_OK;
   if (src_dtype != MI_F32 && src_dtype != MI_BF16 && src_dtype != MI_F16)
-    return fail(MI_ERR_DTYPE, "source dtype %d", src_dtype);
-  if (dst_dtype != MI_F32 && dst_dtype != MI_BF16) return fail(MI_ERR_DTYPE, "destination dtype %d", dst_dtype);
-  if (!src || !dst) return fail(MI_ERR_NULL, "src or dst is NULL");
-  if (src_ld < cols) return fail(MI_ERR_LD, "src_ld=%lld < cols=%lld", (long long)src_ld, (long long)cols);
+    return fail(MI_ERR_DTYPE, "%ssource dtype %d", what, src_dtype);
+  if (dst_dtype != MI_F32 && dst_dtype != MI_BF16)
+    return fail(MI_ERR_DTYPE, "%sdestination dtype %d", what, dst_dtype);
+  if (!src || !dst) return fail(MI_ERR_NULL, "%ssrc or dst is NULL", what);
+  if (src_ld < cols)
+    return fail(MI_ERR_LD, "%ssrc_ld=%lld < cols=%lld", what, (long long)src_ld, (long long)cols);
   if (dst_ld < (transpose ? rows : cols))
-    return fail(MI_ERR_LD, "dst_ld=%lld < %lld", (long long)dst_ld, (long long)(transpose ? rows : cols));
-  if (transpose && (rows + 63) / 64 > 65535) return fail(MI_ERR_SHAPE, "too many rows to transpose");
+    return fail(MI_ERR_LD, "%sdst_ld=%lld < %lld", what, (long long)dst_ld,
+                (long long)(transpose ? rows : cols));
+  if (transpose && (rows + 63) / 64 > 65535) return fail(MI_ERR_SHAPE, "%stoo many rows to transpose", what);
   const int64_t ses = src_dtype == MI_F32 ? 4 : 2, des = dst_dtype == MI_F32 ? 4 : 2;
   if ((uintptr_t)src % ses || (uintptr_t)dst % des)
-    return fail(MI_ERR_UNSUPPORTED, "src and dst must be aligned to their element size");
-  const uintptr_t s0 = (uintptr_t)src + (uintptr_t)(row0 * src_ld * ses);
-  const uintptr_t s1 = (uintptr_t)src + (uintptr_t)(((row0 + rows - 1) * src_ld + cols) * ses);
+    return fail(MI_ERR_UNSUPPORTED, "%ssrc and dst must be aligned to their element size", what);
+  s0 = (uintptr_t)src + (uintptr_t)(row0 * src_ld * ses);
+  s1 = (uintptr_t)src + (uintptr_t)(((row0 + rows - 1) * src_ld + cols) * ses);
   const int64_t drows = transpose ? cols : rows, dcols = transpose ? rows : cols;
-  const uintptr_t d0 = (uintptr_t)dst, d1 = d0 + (uintptr_t)(((drows - 1) * dst_ld + dcols) * des);
-  if (d0 < s1 && s0 < d1) return fail(MI_ERR_UNSUPPORTED, "dst overlaps the source rows");
-  int st = init_devices();
-  if (st != MI_OK) return st;
-  ConvParams p;
+  d0 = (uintptr_t)dst;
+  d1 = d0 + (uintptr_t)(((drows - 1) * dst_ld + dcols) * des);
+  if (d0 < s1 && s0 < d1) return fail(MI_ERR_UNSUPPORTED, "%sdst overlaps the source rows", what);
   p.src = src; p.dst = dst; p.src_ld = src_ld; p.dst_ld = dst_ld;
   p.row0 = row0; p.rows = rows; p.cols = cols;
   p.src_dtype = src_dtype; p.dst_dtype = dst_dtype;
+  return MI_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int mi_convert_matrix(void* stream, const void* src, int32_t src_dtype, int64_t src_ld, int64_t row0,
+                      int64_t rows, int64_t cols, int32_t transpose, void* dst, int32_t dst_dtype,
+                      int64_t dst_ld) {
+  ConvParams p;
+  uintptr_t s0, s1, d0, d1;
+  int st = check_convert(src, src_dtype, src_ld, row0, rows, cols, transpose, dst, dst_dtype, dst_ld,
+                         "", p, s0, s1, d0, d1);
+  if (st != MI_OK || p.rows == 0 || p.cols == 0) return st;
+  st = init_devices();
+  if (st != MI_OK) return st;
   hipError_t e = launch_convert(p, transpose != 0, current_cus(), (hipStream_t)stream);
+  return e == hipSuccess ? MI_OK : fail(MI_ERR_HIP, "convert launch: %s", hipGetErrorString(e));
+}
+
+int mi_convert_matrices(void* stream, const mi_convert_job* jobs, int64_t n) {
+  if (n < 0) return fail(MI_ERR_SHAPE, "negative job count");
+  if (n == 0) return MI_OK;
+  if (!jobs) return fail(MI_ERR_NULL, "jobs is NULL");
+  std::vector<ConvParams> ps((size_t)n);
+  std::vector<int> tr((size_t)n);
+  // byte extents: (begin, end, is_destination), swept in order of begin
+  struct Extent { uintptr_t b, e; int dst; int64_t job; };
+  std::vector<Extent> ext;
+  ext.reserve(2 * (size_t)n);
+  for (int64_t i = 0; i < n; ++i) {
+    const mi_convert_job& j = jobs[i];
+    char what[48];
+    std::snprintf(what, sizeof what, "job %lld: ", (long long)i);
+    uintptr_t s0, s1, d0, d1;
+    const int st = check_convert(j.src, j.src_dtype, j.src_ld, j.row0, j.rows, j.cols, j.transpose, j.dst,
+                                 j.dst_dtype, j.dst_ld, what, ps[(size_t)i], s0, s1, d0, d1);
+    if (st != MI_OK) return st;
+    tr[(size_t)i] = j.transpose != 0;
+    if (ps[(size_t)i].rows == 0 || ps[(size_t)i].cols == 0) continue;
+    ext.push_back({s0, s1, 0, i});
+    ext.push_back({d0, d1, 1, i});
+  }
+  if (ext.empty()) return MI_OK;
+  // A destination may not overlap any other extent; sources may share bytes.
+  std::sort(ext.begin(), ext.end(), [](const Extent& x, const Extent& y) { return x.b < y.b; });
+  uintptr_t end_any = 0, end_dst = 0;
+  int64_t job_any = -1, job_dst = -1;
+  for (const Extent& x : ext) {
+    if (x.dst && x.b < end_any)
+      return fail(MI_ERR_UNSUPPORTED, "job %lld: dst overlaps the source or destination of job %lld",
+                  (long long)x.job, (long long)job_any);
+    if (!x.dst && x.b < end_dst)
+      return fail(MI_ERR_UNSUPPORTED, "job %lld: source rows overlap the destination of job %lld",
+                  (long long)x.job, (long long)job_dst);
+    if (x.e > end_any) end_any = x.e, job_any = x.job;
+    if (x.dst && x.e > end_dst) end_dst = x.e, job_dst = x.job;
+  }
+  const int st = init_devices();
+  if (st != MI_OK) return st;
+  hipError_t e = launch_convert_batch(ps.data(), tr.data(), n, (hipStream_t)stream);
   return e == hipSuccess ? MI_OK : fail(MI_ERR_HIP, "convert launch: %s", hipGetErrorString(e));
 }
 

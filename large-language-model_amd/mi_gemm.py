@@ -38,6 +38,7 @@ C_SYMBOLS = (
     "mi_convert_matrix", "mi_flash_attn_bwd_workspace_size", "mi_profiler_enable",
     "mi_profiler_begin_step", "mi_profiler_count", "mi_profiler_record", "mi_profiler_totals",
     "mi_profiler_reset", "mi_gemm_noalloc", "mi_flash_attn_fwd_scaled", "mi_flash_attn_bwd_scaled",
+    "mi_convert_matrices",
 )
 MI_ATTN_O_BHTD, MI_ATTN_O_BTHD = 0, 1
 
@@ -68,6 +69,16 @@ class MiBatch(ctypes.Structure):
         ("r_outer", ctypes.c_int64), ("r_inner", ctypes.c_int64),
         ("k_segments", ctypes.c_int64), ("seg_a", ctypes.c_int64), ("seg_b", ctypes.c_int64),
         ("causal", ctypes.c_int32), ("mask_value", ctypes.c_float),
+    ]
+
+
+class MiConvertJob(ctypes.Structure):
+    """mi_convert_job: the arguments of one mi_convert_matrix call."""
+    _fields_ = [
+        ("src", ctypes.c_void_p), ("src_dtype", ctypes.c_int32), ("transpose", ctypes.c_int32),
+        ("src_ld", ctypes.c_int64), ("row0", ctypes.c_int64), ("rows", ctypes.c_int64),
+        ("cols", ctypes.c_int64), ("dst", ctypes.c_void_p), ("dst_dtype", ctypes.c_int32),
+        ("reserved", ctypes.c_int32), ("dst_ld", ctypes.c_int64),
     ]
 
 
@@ -149,6 +160,8 @@ def load_library():
                                  i32, ctypes.c_float, vp, ctypes.c_size_t]
     L.mi_convert_matrix.restype = ctypes.c_int
     L.mi_convert_matrix.argtypes = [vp, vp, i32, i64, i64, i64, i64, i32, vp, i32, i64]
+    L.mi_convert_matrices.restype = ctypes.c_int
+    L.mi_convert_matrices.argtypes = [vp, ctypes.POINTER(MiConvertJob), i64]
     L.mi_profiler_enable.restype = ctypes.c_int
     L.mi_profiler_enable.argtypes = [ctypes.c_int]
     L.mi_profiler_begin_step.restype = ctypes.c_int
@@ -901,6 +914,32 @@ def convert_matrix(src, src_dtype, src_ld, row0, rows, cols, transpose, dst, syn
     return dst
 
 
+def convert_jobs(jobs):
+    """A ctypes array of mi_convert_job from (src, src_dtype, src_ld, row0, rows, cols,
+    transpose, dst) tuples (src and dst device tensors; the destination dtype and leading
+    dimension come from dst); built once, it can be handed to convert_matrices any number
+    of times."""
+    arr = (MiConvertJob * len(jobs))()
+    for a, (src, sdt, sld, row0, rows, cols, tr, dst) in zip(arr, jobs):
+        a.src, a.src_dtype, a.transpose = src.data_ptr(), sdt, int(bool(tr))
+        a.src_ld, a.row0, a.rows, a.cols = sld, row0, rows, cols
+        a.dst, a.dst_dtype, a.reserved = dst.data_ptr(), _dt(dst), 0
+        a.dst_ld = dst.stride(0) if dst.dim() == 2 else (rows if tr else cols)
+    return arr
+
+
+def convert_matrices(jobs, sync=None):
+    """mi_convert_matrices: several mi_convert_matrix conversions in as few launches as
+    their dtype pairs allow (Checkpoint.cpp:532-570).  jobs: a list of tuples as for
+    convert_jobs, or an array it returned."""
+    arr = jobs if isinstance(jobs, ctypes.Array) else convert_jobs(jobs)
+    st = load_library().mi_convert_matrices(_stream(), arr, len(arr))
+    if sync is None:
+        _finish("mi_convert_matrices", st)
+    else:
+        _check("mi_convert_matrices", st)
+
+
 def engine_weight_shapes(cfg):
     """Engine names and [in, out] shapes of a model's weights (Checkpoint.cpp:147-174).
     cfg: dict with n_layers, hidden_dim, n_heads, n_kv_heads, head_dim, intermediate_dim,
@@ -949,7 +988,8 @@ def load_weights(path, cfg, dtype=None, device="cuda"):
     """Mirror of the model part of Checkpoint::load (Checkpoint.cpp:331-388, 532-570): reads a
     Python/MLX or an engine safetensors file into new device tensors in the engine layout
     (dict keyed by the engine names), dtype bf16 (default) or fp32. Each file tensor's bytes
-    go to the device once; slicing, transposing and widening run in mi_convert_matrix."""
+    go to the device once; slicing, transposing and widening run in mi_convert_matrices, one
+    call per file tensor (the row ranges of a fused wqkv or w12 together)."""
     import numpy as np
     torch = _torch()
 
@@ -958,6 +998,7 @@ def load_weights(path, cfg, dtype=None, device="cuda"):
     python_format = "tok_embeddings.weight" in head
     mm = np.memmap(path, dtype=np.uint8, mode="r")
     staged = {}
+    pending = []
     out = {}
     for name, shape in engine_weight_shapes(cfg).items():
         fname, fshape, row0, rows, transpose = weight_sources(cfg, python_format)[name]
@@ -973,10 +1014,16 @@ def load_weights(path, cfg, dtype=None, device="cuda"):
         if e - b != int(np.prod(fshape)) * es or payload + e > mm.size:
             raise ValueError(f"tensor '{fname}' has a byte range that does not match its shape")
         if fname not in staged:
+            if pending:
+                convert_matrices(pending, sync=False)
+                pending = []
             staged = {fname: torch.from_numpy(np.array(mm[payload + b: payload + e])).to(device)}
         cols = fshape[-1]
         dst = torch.empty(shape, dtype=dtype, device=device)
-        convert_matrix(staged[fname], code, cols, row0, rows, cols, transpose, dst, sync=False)
+        pending.append((staged[fname], code, cols, row0, rows, cols, transpose,
+                        dst if dst.dim() == 2 else dst.view(1, -1)))
         out[name] = dst
+    if pending:
+        convert_matrices(pending, sync=False)
     _finish("load_weights", 0)
     return out

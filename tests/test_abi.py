@@ -128,6 +128,44 @@ def test_aux_validation(mi):
     assert lib.mi_flash_attn_bwd_workspace_size(1, 1, 32760) == 32760 * (32760 * 2 + 512)
 
 
+def test_convert_matrices_validation(mi):
+    """mi_convert_matrices checks every job before anything runs (no device needed):
+    the job count, each job's arguments (the message names the job), and that no
+    destination overlaps another job's source or destination; sources may share bytes."""
+    lib = mi.load_library()
+
+    def job(src, dst, row0=0, rows=64, cols=64, tr=1, sdt=mi.MI_BF16, ddt=mi.MI_BF16, ld=64):
+        j = mi.MiConvertJob()
+        j.src, j.src_dtype, j.transpose, j.src_ld = src, sdt, tr, cols
+        j.row0, j.rows, j.cols = row0, rows, cols
+        j.dst, j.dst_dtype, j.reserved, j.dst_ld = dst, ddt, 0, ld
+        return j
+
+    def run(*jobs):
+        arr = (mi.MiConvertJob * len(jobs))(*jobs)
+        return lib.mi_convert_matrices(None, arr, len(jobs)), lib.mi_last_error().decode()
+
+    S, D = 1 << 20, 1 << 24            # fake device addresses: no call reaches the GPU
+    assert lib.mi_convert_matrices(None, None, 0) == 0
+    assert lib.mi_convert_matrices(None, None, -1) == 1
+    assert lib.mi_convert_matrices(None, None, 2) == 3
+    assert run(job(S, D, rows=0))[0] == 0                       # empty jobs only: nothing to do
+    st, msg = run(job(S, D), job(S, D + 8192, sdt=7))
+    assert st == 4 and "job 1" in msg                            # dtype of the second job
+    st, msg = run(job(S, D), job(S, D + 8192, ld=32))
+    assert st == 2 and "job 1" in msg                            # dst_ld < rows
+    st, msg = run(job(S, D), job(S, D + 4096))                   # destinations 8 KiB each
+    assert st == 5 and "job 1" in msg and "job 0" in msg
+    st, msg = run(job(S, D), job(D + 100, D + 65536))            # a source inside job 0's dst
+    assert st == 5 and "job 1" in msg
+    st, msg = run(job(S, D), job(S + 64, D - 8192 + 2))          # dst runs into job 0's dst
+    assert st == 5
+    # row ranges of one fused source (disjoint destinations) pass validation: without a
+    # GPU the call then stops at device initialisation
+    st, _ = run(job(S, D, row0=0, rows=64), job(S, D + 8192, row0=32, rows=64))
+    assert st in (0, 8)
+
+
 def test_matmul_shape_rules(mi):
     assert mi.matmul_shape((2, 3), (3, 2)) == (2, 2)
     assert mi.matmul_shape((8, 1024, 2048), (2048, 3072)) == (8, 1024, 3072)

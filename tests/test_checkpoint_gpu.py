@@ -34,9 +34,10 @@ def test_load_weights(mi, dev, oracle, tmp_path, fmt, dst):
 @pytest.mark.parametrize("src_dt", ["f32", "bf16", "f16"])
 @pytest.mark.parametrize("transpose", [False, True])
 @pytest.mark.parametrize("R,C,row0,rows", [(130, 77, 5, 100),     # element-wise paths
-                                          (130, 96, 4, 100),     # 8-element copy, 4-element transpose
+                                          (130, 96, 4, 100),     # 8-element copy, edge tiles
                                           (130, 100, 4, 100),    # 4-element copy
-                                          (200, 192, 8, 192),    # interior transpose tiles
+                                          (300, 520, 8, 260),    # interior 64 x 256 tiles, 8-element runs
+                                          (130, 516, 4, 100),    # interior tiles, 4-element runs
                                           (70000, 8, 0, 70000)])  # more rows than a grid column
 def test_convert_matrix_slices(mi, dev, src_dt, transpose, R, C, row0, rows):
     import torch
@@ -74,7 +75,8 @@ def test_convert_matrix_padded_destination(mi, dev, transpose):
 
 
 @pytest.mark.parametrize("transpose", [False, True])
-@pytest.mark.parametrize("R,C,row0,rows", [(200, 192, 8, 192), (130, 77, 5, 100), (130, 100, 4, 100)])
+@pytest.mark.parametrize("R,C,row0,rows", [(300, 520, 8, 260), (130, 516, 4, 100), (130, 77, 5, 100),
+                                          (130, 100, 4, 100)])
 def test_convert_matrix_bf16_bits_exact(mi, dev, transpose, R, C, row0, rows):
     """bf16 -> bf16 moves every bit pattern unchanged, NaN payloads and signalling NaNs
     included, on the interior-tile, edge and copy paths."""
@@ -91,6 +93,65 @@ def test_convert_matrix_bf16_bits_exact(mi, dev, transpose, R, C, row0, rows):
     want = bits[row0:row0 + rows]
     want = want.t() if transpose else want
     assert torch.equal(dst.view(torch.int16).cpu(), want.contiguous())
+
+
+def test_convert_matrices_mixed(mi, dev):
+    """One mi_convert_matrices call over jobs of every dtype pair, transposed and not,
+    interior and edge tiles, shared fused sources, a padded destination and more jobs
+    than one launch holds, against the same conversions done one by one."""
+    import torch
+
+    torch.manual_seed(5)
+    codes = {torch.float32: mi.MI_F32, torch.bfloat16: mi.MI_BF16, torch.float16: mi.MI_F16}
+    fused = torch.randn((200, 512), device=dev).to(torch.bfloat16)     # a wqkv-like source
+    srcs = [torch.randn((R, C), device=dev).to(dt) for R, C, dt in
+            [(130, 77, torch.float32), (96, 100, torch.float16), (64, 64, torch.bfloat16),
+             (257, 40, torch.float32), (70, 130, torch.float16), (140, 520, torch.float32),
+             (133, 516, torch.bfloat16)]]
+    jobs, want = [], []
+
+    def add(src, row0, rows, tr, out_dt, pad=0):
+        C = src.shape[1]
+        shape = (C, rows + pad) if tr else (rows, C + pad)
+        dst = torch.full(shape, 7.0, dtype=out_dt, device=dev)
+        view = dst[:, :rows] if tr else dst[:, :C]
+        jobs.append((src, codes[src.dtype], C, row0, rows, C, tr, view))
+        w = src[row0:row0 + rows].float()
+        want.append((dst, (w.t() if tr else w).to(out_dt), pad))
+
+    for row0, rows in ((0, 128), (128, 36), (164, 36)):                 # de-fused row ranges
+        add(fused, row0, rows, True, torch.bfloat16)
+    add(fused, 8, 192, False, torch.float32)
+    for row0 in range(0, 200, 10):                                      # 23 bf16 -> bf16 jobs: 2 launches
+        add(fused, row0, 10, True, torch.bfloat16)
+    for i, s in enumerate(srcs):
+        for tr in (False, True):
+            for out_dt in (torch.float32, torch.bfloat16):
+                add(s, i % 3, s.shape[0] - i % 3, tr, out_dt, pad=8 if (i + tr) % 2 else 0)
+    assert len(jobs) > 16
+    print(f"convert_matrices {len(jobs)} jobs", flush=True)
+    mi.convert_matrices(jobs)
+    for k, (dst, w, pad) in enumerate(want):
+        if pad:
+            tr_view = dst[:, :dst.shape[1] - pad]
+            assert torch.equal(tr_view, w), k
+            assert torch.all(dst[:, dst.shape[1] - pad:] == 7.0), k
+        else:
+            assert torch.equal(dst, w), k
+
+
+def test_convert_matrices_overlap_runs_nothing(mi, dev):
+    """Two destinations that overlap: the call fails and writes nothing."""
+    import torch
+
+    src = torch.randn((64, 64), device=dev).to(torch.bfloat16)
+    out = torch.full((96, 64), 7.0, dtype=torch.bfloat16, device=dev)
+    jobs = [(src, mi.MI_BF16, 64, 0, 64, 64, True, out[:64]), (src, mi.MI_BF16, 64, 0, 64, 64, False, out[32:])]
+    with pytest.raises(mi.MiError) as e:
+        mi.convert_matrices(jobs)
+    assert e.value.code == 5 and "job" in str(e.value)
+    torch.cuda.synchronize()
+    assert torch.all(out == 7.0)
 
 
 def test_missing_and_mismatched(mi, dev, tmp_path):
