@@ -469,8 +469,24 @@ struct TileCoord {
 #endif
 
 __device__ __forceinline__ TileCoord map_tile(int bid, int nblocks, int tiles_m, int tiles_n,
-                                              int splits) {
+                                              int splits, int causal) {
   constexpr int NXCD = 8, GROUP_M = MI_GROUP_M;
+  if (causal == CAUSAL_A_LOWER || causal == CAUSAL_A_UPPER) {
+    // Causal-skipping products: a tile's K range grows with its row block (A_LOWER)
+    // or shrinks with it (A_UPPER).  Workgroups are dispatched in block order, so
+    // handing out the longest row blocks of every problem first lets the short ones
+    // fill the tail (longest processing time first) instead of a long tile starting
+    // last.  Consecutive blocks cycle over the XCDs, each of which gets the same mix.
+    const int per = nblocks / tiles_m;  // problems x splits x column blocks per row block
+    const int r = bid / per, rest = bid - r * per;
+    TileCoord tc;
+    tc.tm = causal == CAUSAL_A_LOWER ? tiles_m - 1 - r : r;
+    tc.tn = rest % tiles_n;
+    const int zs = rest / tiles_n;
+    tc.z = zs / splits;
+    tc.split = zs - tc.z * splits;
+    return tc;
+  }
 #if MI_XCD_REMAP
   const int q = nblocks / NXCD, rem = nblocks % NXCD;
   const int x = bid % NXCD, j = bid / NXCD;
@@ -527,7 +543,7 @@ __global__ void __launch_bounds__(256)
   __shared__ u32x4_t smem[2][(BM + BROWS) * 8];
 
   const int nblocks = gridDim.x;
-  const TileCoord tc = map_tile(blockIdx.x, nblocks, p.tiles_m, p.tiles_n, p.splits);
+  const TileCoord tc = map_tile(blockIdx.x, nblocks, p.tiles_m, p.tiles_n, p.splits, p.causal);
   const int m0 = uniform(tc.tm * BM), n0 = uniform(tc.tn * BN);
   const int zo = uniform(tc.z / p.heads), zi = uniform(tc.z - (tc.z / p.heads) * p.heads);
   const int ziA = uniform(zi / p.gA), ziB = uniform(zi / p.gB), ziC = uniform(zi / p.gC);

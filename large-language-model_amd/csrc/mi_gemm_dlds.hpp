@@ -291,7 +291,7 @@ __global__ void __launch_bounds__(64 * WGM * WGN * KG)
   const uint32_t lds0 = lds_addr(smem);
 
   const int nblocks = gridDim.x;
-  const TileCoord tc = map_tile(blockIdx.x, nblocks, p.tiles_m, p.tiles_n, p.splits);
+  const TileCoord tc = map_tile(blockIdx.x, nblocks, p.tiles_m, p.tiles_n, p.splits, p.causal);
   const int m0 = uniform(tc.tm * BM), n0 = uniform(tc.tn * BN);
   const int zo = uniform(tc.z / p.heads), zi = uniform(tc.z - (tc.z / p.heads) * p.heads);
   const int ziA = uniform(zi / p.gA), ziB = uniform(zi / p.gB), ziC = uniform(zi / p.gC);
