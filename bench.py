@@ -315,10 +315,12 @@ def lm_head_main(args):
     for _ in range(args.warmup):
         step()
     torch.cuda.synchronize()
-    # attribution pass: events around every launch
+    # attribution pass: events around every launch, after one step without events (the
+    # GPU busy when the first bracket opens)
     n_attr = 3
     evs = [[(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
             for _ in ops] for _ in range(n_attr)]
+    step()
     for s_ in range(n_attr):
         for i, op in enumerate(ops):
             evs[s_][i][0].record()
@@ -697,10 +699,14 @@ def gemm_set_main(args, fp32: bool):
     torch.cuda.synchronize()
     stream = torch.cuda.current_stream()
 
-    # Attribution pass: every launch bracketed by events on the launch stream.
+    # Attribution pass: every launch bracketed by events on the launch stream. One step
+    # without events goes first, so the GPU is busy (clocks up, host ahead) when the
+    # first bracketed launch starts: otherwise the first GEMM's bracket holds the
+    # launch from an idle GPU.
     n_attr = 3
     evs = [[(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
             for _ in ops] for _ in range(n_attr)]
+    step()
     for s_ in range(n_attr):
         for i, op in enumerate(ops):
             evs[s_][i][0].record(stream)
