@@ -321,23 +321,43 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2)))
   }
 
   // ---- normalise and store ----
+  // O goes out through LDS so that 16 lanes store one 256-byte row: each wave writes
+  // its 32 x 128 tile to an 8 KB region (16-byte chunk c of row r at c ^ (r & 15):
+  // the 16 rows of a write land in 16 distinct chunks) and reads it back as whole
+  // rows (16 lanes per row, 4 rows per read, all 64 banks per row).  The barrier
+  // keeps the regions, which overlap stage 0 of the ring, from other waves' reads of
+  // their last block.  (8-byte stores straight from the accumulators: 1-1.5 us
+  // slower at configuration 4.)
   const float l_tot = l_run + __shfl_xor(l_run, 32, 64);
   const float inv = l_tot > 0.0f ? 1.0f / l_tot : 0.0f;
-  if (row < T) {
-    uint16_t* orow = (uint16_t*)p.O + (p.o_bthd ? ((int64_t)(b * T + row) * p.nH + h) * D
-                                                : ((int64_t)bh * T + row) * D);
+  __syncthreads();
+  const uint32_t ob = lds0 + (uint32_t)(wave_u * 32 * Tl::ROW);
 #pragma unroll
-    for (int c = 0; c < NC; ++c)
+  for (int c = 0; c < NC; ++c)
 #pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        const int d = 32 * c + 8 * q + 4 * h32;
-        *(u32x2_t*)(orow + d) = u32x2_t{pack_bf16x2(o[c][4 * q] * inv, o[c][4 * q + 1] * inv),
-                                        pack_bf16x2(o[c][4 * q + 2] * inv, o[c][4 * q + 3] * inv)};
-      }
-    if (p.lse && h32 == 0)
-      p.lse[(int64_t)bh * T + row] = l_tot > 0.0f ? (m_run * sl2 + __log2f(l_tot)) * 0.69314718055994531f
-                                                 : -INFINITY;
+    for (int q = 0; q < 4; ++q) {
+      const int ch = 4 * c + q;  // chunk of d = 32c + 8q + 4*h32 .. +3, half h32
+      const uint32_t a = ob + (uint32_t)(l32 * Tl::ROW + ((ch ^ (l32 & 15)) * 16) + h32 * 8);
+      *(__attribute__((address_space(3))) u32x2_t*)(uintptr_t)a =
+          u32x2_t{pack_bf16x2(o[c][4 * q] * inv, o[c][4 * q + 1] * inv),
+                  pack_bf16x2(o[c][4 * q + 2] * inv, o[c][4 * q + 3] * inv)};
+    }
+  const int oj = lane & 15;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const int rr = 4 * i + (lane >> 4);
+    const u32x4_t v = *(const __attribute__((address_space(3))) u32x4_t*)(uintptr_t)(
+        ob + (uint32_t)(rr * Tl::ROW + ((oj ^ (rr & 15)) * 16)));
+    const int orow_i = qw + rr;
+    if (orow_i < T) {
+      uint16_t* orow = (uint16_t*)p.O + (p.o_bthd ? ((int64_t)(b * T + orow_i) * p.nH + h) * D
+                                                  : ((int64_t)bh * T + orow_i) * D);
+      *(u32x4_t*)(orow + 8 * oj) = v;
+    }
   }
+  if (row < T && p.lse && h32 == 0)
+    p.lse[(int64_t)bh * T + row] = l_tot > 0.0f ? (m_run * sl2 + __log2f(l_tot)) * 0.69314718055994531f
+                                               : -INFINITY;
 }
 
 // Lane-row reads of a 32-row half of a [row][d] tile read with the bit-2/3 swapped
