@@ -112,15 +112,9 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2)))
   const __bf16* Kb = (const __bf16*)p.K + ((int64_t)(b * p.nKV + kvh) * T) * D;
   const __bf16* Vb = (const __bf16*)p.V + ((int64_t)(b * p.nKV + kvh) * T) * D;
 
-  // Q fragments (second MFMA operand of S): row qw + l32, d = 16s + 8*h32 .. +7.
+  // Q fragments (second MFMA operand of S): row qw + l32, d = 16s + 8*h32 .. +7;
+  // read from LDS before the first block.
   u32x4_t qf[NS];
-#pragma unroll
-  for (int s = 0; s < NS; ++s) {
-    if (row < T)
-      qf[s] = *(const u32x4_t*)(Qb + (int64_t)row * D + 16 * s + 8 * h32);
-    else
-      qf[s] = u32x4_t{0u, 0u, 0u, 0u};
-  }
 
   // Keys this workgroup needs: causal -> up to its last query row.
   const int kv_end = p.causal ? (q0 + FA_BQ < T ? q0 + FA_BQ : T) : T;
@@ -304,12 +298,40 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2)))
   const int jd = uniform(p.causal ? (qw + 1) / FA_BK : T / FA_BK);
   const int j_split = jd < nblk ? jd : nblk;
   auto ring_step = [&](int j) __attribute__((always_inline)) {
-    wait_vmcnt<0>();     // this wave's share of block j (and the Q loads) landed
+    wait_vmcnt<0>();     // this wave's share of block j landed
     lds_ring_barrier();  // every share landed; every wave is done with block j-1
     if (j + 1 < nblk) issue_block(j + 1);
     return lds0 + (uint32_t)((j & 1) * STAGE);
   };
+  // Q goes global -> LDS stage 1 as whole 256-byte rows (the K tile's layout and DMA
+  // offsets, 64 rows per half; rows past T read as zero), together with block 0.
+  // Each wave then reads its 32 rows' fragments; ring_step(0)'s barrier (after
+  // lgkmcnt(0)) frees stage 1 for block 1.  (Per-lane 16-byte global loads of the
+  // fragments: about 1 us slower at configuration 4.)
+  {
+    const uint32_t dst = lds0 + (uint32_t)STAGE + (uint32_t)(wave_u * Tl::NU * 1024);
+#pragma unroll
+    for (int half = 0; half < 2; ++half) {
+      const int r0 = q0 + 64 * half;
+      const uint32_t ext = r0 < T ? (uint32_t)((T - r0) * Tl::ROW) : 0u;
+      const __amdgpu_buffer_rsrc_t rq = scalar_rsrc(uniform(Qb + (int64_t)(r0 < T ? r0 : 0) * D), ext);
+#pragma unroll
+      for (int u = 0; u < Tl::NU; ++u)
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(
+            rq, (__attribute__((address_space(3))) void*)(uintptr_t)(dst + (uint32_t)(half * Tl::BYTES + u * 1024)),
+            16, (int)k_off[u], 0, 0, 0);
+    }
+  }
   if (nblk > 0) issue_block(0);
+  wait_vmcnt<0>();
+  lds_ring_barrier();
+  {
+    const int qr = 32 * (wave_u & 1) + l32;  // row within the wave's 64-row half
+    const uint32_t qbase = lds0 + (uint32_t)(STAGE + (wave_u >> 1) * Tl::BYTES + qr * Tl::ROW);
+#pragma unroll
+    for (int s = 0; s < NS; ++s)
+      qf[s] = *(const lds_u32x4_t*)(uintptr_t)(qbase + (uint32_t)(16 * Tl::k_pos(qr, 2 * s + h32)));
+  }
   for (int j = 0; j < j_split; ++j) {
     const uint32_t st = ring_step(j);
     block(j * FA_BK, st, std::false_type{});
