@@ -311,3 +311,45 @@ def test_flash_head_dim_below_128(mi, dev, oracle, d, layout):
     check(host(dV), dV_ref, TOL_BF16, f"dV d={d}")
     check(host(dK), dK_ref, TOL_BF16, f"dK d={d}")
     check(host(dQ), dQ_ref, TOL_BF16, f"dQ d={d}")
+
+
+def test_flash_backward_graph_replays(mi, dev):
+    """The dS^T-form backward (D, dK/dV with the balanced schedule, the partial sums and
+    the dQ GEMM) captured in a HIP graph: every replay, with eager launches and
+    synchronisations between replays, gives the eager result bit for bit."""
+    import torch
+
+    Bn, nH, nKV, T, d = 2, 16, 4, 1024, 128
+    g = torch.Generator(device=dev)
+    g.manual_seed(31)
+    Q = torch.randn((Bn, nH, T, d), generator=g, device=dev).to(torch.bfloat16)
+    K = torch.randn((Bn, nKV, T, d), generator=g, device=dev).to(torch.bfloat16)
+    V = torch.randn((Bn, nKV, T, d), generator=g, device=dev).to(torch.bfloat16)
+    dO = (torch.randn((Bn, T, nH * d), generator=g, device=dev) * 1e-2).to(torch.bfloat16)
+    lse = torch.empty((Bn, nH, T), dtype=torch.float32, device=dev)
+    O = mi.flash_attn_fwd(Q, K, V, lse=lse)
+    ws = torch.empty((mi.load_library().mi_flash_attn_bwd_workspace_size(Bn, nH, T) // 2,),
+                     dtype=torch.bfloat16, device=dev)
+    print("flash backward graph: eager reference", flush=True)
+    ref = [t.clone() for t in mi.flash_attn_bwd(Q, K, V, O, dO, lse, workspace=ws)]
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        mi.flash_attn_bwd(Q, K, V, O, dO, lse, sync=False, workspace=ws)
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    print("flash backward graph: capture", flush=True)
+    with torch.cuda.graph(graph):
+        out = mi.flash_attn_bwd(Q, K, V, O, dO, lse, sync=False, workspace=ws)
+    for i in range(3):
+        print(f"flash backward graph: replay {i}", flush=True)
+        for t in out:
+            t.fill_(7.0)
+        graph.replay()
+        torch.cuda.synchronize()
+        for got, want in zip(out, ref):
+            assert torch.equal(got, want), i
+        eager = mi.flash_attn_bwd(Q, K, V, O, dO, lse, workspace=ws)
+        for got, want in zip(eager, ref):
+            assert torch.equal(got, want), i
