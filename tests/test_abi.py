@@ -166,6 +166,21 @@ def test_convert_matrices_validation(mi):
     assert st in (0, 8)
 
 
+def test_convert_job_layout(mi):
+    """The ctypes mirror of mi_convert_job has the C struct's size and field offsets
+    (pointers and int64 fields 8-aligned, the int32 pairs packed)."""
+    J = mi.MiConvertJob
+    assert ctypes.sizeof(J) == 72
+    want = {"src": 0, "src_dtype": 8, "transpose": 12, "src_ld": 16, "row0": 24, "rows": 32,
+            "cols": 40, "dst": 48, "dst_dtype": 56, "reserved": 60, "dst_ld": 64}
+    assert {n: getattr(J, n).offset for n in want} == want
+    hdr = open(os.path.join(ROOT, "include", "mi_gemm.h")).read()
+    body = hdr[hdr.index("typedef struct mi_convert_job"):hdr.index("} mi_convert_job;")]
+    body = re.sub(r"/\*.*?\*/", "", body, flags=re.S)
+    order = re.findall(r"\b(src|src_dtype|transpose|src_ld|row0|rows|cols|dst|dst_dtype|reserved|dst_ld)\b", body)
+    assert order == list(want), order
+
+
 def test_matmul_shape_rules(mi):
     assert mi.matmul_shape((2, 3), (3, 2)) == (2, 2)
     assert mi.matmul_shape((8, 1024, 2048), (2048, 3072)) == (8, 1024, 3072)
