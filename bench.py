@@ -5,8 +5,11 @@ GQA 16 q / 4 kv heads x 128 -> fused QKV 2048->3072, attention-out 2048->2048,
 SwiGLU gate/up 2048->5632, down 5632->2048; tokens M = 8 x 1024 = 8192):
 forward Y = X W (NN, bf16 out), dX = dY W^T (NT, bf16 out), dW += X^T dY (TN, fp32
 accumulate), bf16 inputs, fp32 accumulation, all operands resident in HBM. A step issues
-them per projection, forward, dX, dW, as a training step does (dX and dW of a projection
-read the same dY, dW and forward the same X).
+them in the reference engine's order: the forward set (qkv, o, gate, up, down), then the
+backward with each projection's dW before its dX, down first and qkv last (REF_ORDER
+cites the lines).  Operands are shared as the engine shares them: dX and dW of a
+projection read the same dY, dW and forward the same X, and gate and up the same X
+(ffn_in).  --order projection issues fwd, dX, dW per projection instead (for comparison).
 value = algorithmic FLOPs x steps / timed seconds.
 
 Timing: after the warm-up, an attribution pass (untimed for `value`) brackets every launch
@@ -42,6 +45,18 @@ PEAK_HBM_GBS = 8000.0
 BLOCK = [("qkv", 2048, 3072), ("o", 2048, 2048), ("gate", 2048, 5632), ("up", 2048, 5632),
          ("down", 5632, 2048)]
 M_TOKENS = 8192
+# The reference engine's issue order of one block's GEMMs (under /root/reference/cpp/src):
+# forward Attention.cpp:196-201 (Wq, Wk, Wv: the fused qkv here), :282 (o),
+# Transformer.cpp:161-162 (gate, up), :164-167 (down); backward TransformerLayer::backward:
+# Transformer.cpp:382 (down dW) before :388 (down dX), :414 (gate dW, up dW; :276-289)
+# before :420-424 (gate dX, up dX), Attention.cpp:474 (o dW) before :489 (o dX),
+# :553-561 (q/k/v dW) before :571-585 (q/k/v dX).
+REF_ORDER = [("qkv", "fwd"), ("o", "fwd"), ("gate", "fwd"), ("up", "fwd"), ("down", "fwd"),
+             ("down", "dW"), ("down", "dX"), ("gate", "dW"), ("up", "dW"), ("gate", "dX"),
+             ("up", "dX"), ("o", "dW"), ("o", "dX"), ("qkv", "dW"), ("qkv", "dX")]
+# projections whose forward input is another projection's (gate and up both read ffn_in,
+# Transformer.cpp:161-162, and so do their dW, :276-289)
+SHARED_X = {"up": "gate"}
 # benchmark configuration 2 (GPT-small, fp32): MHA 12 x 64 -> QKV 768->2304, SwiGLU 2048, M=4*512
 BLOCK_FP32 = [("qkv", 768, 2304), ("o", 768, 768), ("gate", 768, 2048), ("up", 768, 2048),
               ("down", 2048, 768)]
@@ -101,6 +116,10 @@ def parse():
                     help="token rows of the CPU sample (default: the whole set, M=8192)")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="also launch a 1 GiB device copy (for PMC byte-counter scaling)")
+    ap.add_argument("--order", choices=("reference", "projection"), default="reference",
+                    help="GEMM issue order of a block step: reference = the engine's (forward "
+                         "set, then per projection dW before dX, down first); projection = "
+                         "fwd, dX, dW per projection")
     ap.add_argument("--workload",
                     choices=("block", "block_fp32", "attention", "lm_head", "norm", "convert"),
                     default="block",
@@ -665,27 +684,41 @@ def gemm_set_main(args, fp32: bool):
     g.manual_seed(1234)
     # split-K workspace, as the bridge's pool provides it (the planner decides per GEMM)
     ws = torch.empty(WS_BYTES // 4, dtype=torch.float32, device=dev)
-    ops = []
+    by_key, xs = {}, {}
     for name, din, dout in block:
-        X = torch.randn((M, din), generator=g, device=dev).to(dt_in)
+        X = (xs[SHARED_X[name]] if name in SHARED_X
+             else torch.randn((M, din), generator=g, device=dev).to(dt_in))
+        xs[name] = X
         W = (torch.randn((din, dout), generator=g, device=dev) * 0.02).to(dt_in)
         dY = (torch.randn((M, dout), generator=g, device=dev) * 1e-2).to(dt_in)
         Y = torch.empty((M, dout), dtype=dt_in, device=dev)
         dX = torch.empty((M, din), dtype=dt_in, device=dev)
         dW = torch.zeros((din, dout), dtype=torch.float32, device=dev)
-        ops.append((name, "fwd NN", 2 * M * din * dout,
-                    mi.describe(0, 0, M, dout, din, dtype_in=mi_dt, workspace_bytes=WS_BYTES),
-                    lambda X=X, W=W, Y=Y, din=din, dout=dout:
-                    mi.gemm(X, W, Y, M, dout, din, workspace=ws, sync=False)))
-        ops.append((name, "dX NT", 2 * M * din * dout,
-                    mi.describe(0, 1, M, din, dout, dtype_in=mi_dt, workspace_bytes=WS_BYTES),
-                    lambda dY=dY, W=W, dX=dX, din=din, dout=dout:
-                    mi.gemm(dY, W, dX, M, din, dout, transB=True, workspace=ws, sync=False)))
-        ops.append((name, "dW TN", 2 * M * din * dout,
-                    mi.describe(1, 0, din, dout, M, dtype_in=mi_dt, workspace_bytes=WS_BYTES),
-                    lambda X=X, dY=dY, dW=dW, din=din, dout=dout:
-                    mi.gemm(X, dY, dW, din, dout, M, transA=True, beta=1.0, workspace=ws,
-                            sync=False)))
+        by_key[(name, "fwd")] = (
+            name, "fwd NN", 2 * M * din * dout,
+            mi.describe(0, 0, M, dout, din, dtype_in=mi_dt, workspace_bytes=WS_BYTES),
+            lambda X=X, W=W, Y=Y, din=din, dout=dout:
+            mi.gemm(X, W, Y, M, dout, din, workspace=ws, sync=False))
+        by_key[(name, "dX")] = (
+            name, "dX NT", 2 * M * din * dout,
+            mi.describe(0, 1, M, din, dout, dtype_in=mi_dt, workspace_bytes=WS_BYTES),
+            lambda dY=dY, W=W, dX=dX, din=din, dout=dout:
+            mi.gemm(dY, W, dX, M, din, dout, transB=True, workspace=ws, sync=False))
+        by_key[(name, "dW")] = (
+            name, "dW TN", 2 * M * din * dout,
+            mi.describe(1, 0, din, dout, M, dtype_in=mi_dt, workspace_bytes=WS_BYTES),
+            lambda X=X, dY=dY, dW=dW, din=din, dout=dout:
+            mi.gemm(X, dY, dW, din, dout, M, transA=True, beta=1.0, workspace=ws,
+                    sync=False))
+    if args.order == "reference":
+        order_keys = REF_ORDER
+        order_desc = ("reference engine: fwd qkv, o, gate, up, down; then down dW, down dX, "
+                      "gate dW, up dW, gate dX, up dX, o dW, o dX, qkv dW, qkv dX "
+                      "(Transformer.cpp:161-167,382-424; Attention.cpp:196-201,282,474-585)")
+    else:
+        order_keys = [(name, k) for name, _, _ in block for k in ("fwd", "dX", "dW")]
+        order_desc = "per projection: fwd, dX, dW"
+    ops = [by_key[k] for k in order_keys]
 
     def step():
         for op in ops:
@@ -798,7 +831,7 @@ def gemm_set_main(args, fp32: bool):
         "config": {"workload": workload,
                    "M": M, "d_model": block[0][1], "gemms_per_step": len(ops),
                    "flops_per_step": flops, "pct_of_peak": round(100 * value / peak, 2),
-                   "order": "per projection: fwd, dX, dW",
+                   "order": order_desc,
                    "per_gemm_tflops": breakdown,
                    "per_gemm_plan": {f"{op[0]} {op[1]}": op[3] for op in ops},
                    "per_gemm_source": f"attribution pass, {n_attr} steps, events around every launch"},

@@ -132,8 +132,11 @@ int mi_gemm(void* stream, int transA, int transB, int64_t M, int64_t N, int64_t 
  * on each GPU it runs on until the process ends (its address is set up by mi_init
  * or the first call on a device).  A split-K plan writes at most two 128x128 fp32
  * tiles of partials per CU, 32 MiB on a 256-CU MI355X, so every problem fits; a
- * plan needing more (a larger device) fails with MI_ERR_WORKSPACE.  Calls no
- * allocating routine.  Every call on a
+ * plan needing more (a larger device) fails with MI_ERR_WORKSPACE.  With the
+ * SiLU-gate prologue (epi->A2) it runs the plan mi_gemm makes given no workspace
+ * (the activation applied while each A tile is loaded, no split): the two-pass
+ * form mi_gemm takes when its workspace holds the M x K activation does not fit
+ * the scratch.  Calls no allocating routine.  Every call on a
  * GPU shares that GPU's array: calls that overlap in time on one GPU (different
  * streams, or different host threads) race and must be serialised by the caller.
  * Not recorded by the profiler.
@@ -331,13 +334,15 @@ typedef struct mi_convert_job {
 /*
  * n conversions as mi_convert_matrix would do them one by one, in as few launches
  * as the dtype pairs allow (one launch per (src_dtype, dst_dtype) pair and 16
- * jobs).  Replaces the loader's per-tensor loop (Checkpoint.cpp:532-570 around
- * load_python_tensor / load_python_fused_tensor, :407-530): the three row ranges
- * of a fused wqkv, the two of a w12 and every other matrix of a checkpoint go
- * out together.  Every job is checked first (nothing runs if one fails, and the
- * message names the job); sources may share bytes (row ranges of one fused
- * matrix), but no destination may overlap another job's source or destination,
- * since the tiles of a launch run in any order.
+ * jobs).  Replaces the conversions of load_python_fused_tensor and
+ * load_python_tensor (Checkpoint.cpp:407-530): the loaders here make one call per
+ * file tensor, so the three row ranges of a fused wqkv (or the two of a w12) go
+ * out in one launch; a caller with several matrices already on the device can
+ * pass them all in one call.  Every job is checked first (nothing runs if one
+ * fails, and the message names the job; the reserved field must be 0); sources
+ * may share bytes (row ranges of one fused matrix), but no destination may
+ * overlap another job's source or destination, since the tiles of a launch run
+ * in any order.
  */
 int mi_convert_matrices(void* stream, const mi_convert_job* jobs, int64_t n);
 

@@ -407,6 +407,69 @@ int validate(const Problem& P) {
   return MI_OK;
 }
 
+// Tile rows per column sweep of the tile order (group_m of map_tile).  The tiles
+// an XCD holds at once share their A and B panels in that XCD's L2, which fetches
+// each panel's K rows once per K step; fewer distinct panels per XCD means fewer
+// L2 fills.  For one bf16 problem without split-K, the host walks map_tile's order
+// for each XCD's resident tiles (its first round: 32 CUs x workgroups per CU)
+// and takes the group height in {1, 2, 4, 8, 16} whose XCDs fill the fewest panel
+// bytes, sum over XCDs of (distinct row panels x BM + distinct column panels x BN)
+// per K row; ties keep 8.  Configuration 3's 2048 x 5632 weight gradients (240
+// tiles of 256 x 192, 30 per XCD) get 4 (4 row panels x 7.5 column panels:
+// 2464 panel columns per K row against 2768 for 8 x 3.75); block set with
+// per-XCD K rotation 1110-1114 -> 1126-1128 TFLOP/s on one box (gate dW
+// 917-926 -> 1022-1036).
+int group_rows(const Problem& P, const Plan& plan) {
+  const mi_batch& b = P.bt;
+  if (P.dtype_in != MI_BF16 || plan.splits != 1 || b.batch != 1 || b.causal != MI_CAUSAL_NONE)
+    return MI_GROUP_M;
+  const CfgShape ts = shape_of(P.dtype_in, plan.cfg);
+  const int64_t tm = plan.tiles_m, tn = plan.tiles_n, tiles = tm * tn;
+  const int per_cu = ts.threads >= 512 ? 1 : 2;
+  const int64_t resident = std::max<int64_t>(1, (int64_t)current_cus() / 8 * per_cu);
+  const int64_t q = tiles / 8, rem = tiles % 8;
+  int best = MI_GROUP_M;
+  int64_t best_cost = INT64_MAX;
+  std::vector<char> seen_m((size_t)tm), seen_n((size_t)tn);
+  for (int g : {8, 16, 4, 2, 1}) {
+    int64_t cost = 0;
+    for (int64_t x = 0; x < 8; ++x) {
+      const int64_t first = x * q + std::min<int64_t>(x, rem);
+      const int64_t count = std::min<int64_t>(q + (x < rem ? 1 : 0), resident);
+      std::fill(seen_m.begin(), seen_m.end(), 0);
+      std::fill(seen_n.begin(), seen_n.end(), 0);
+      int64_t dm = 0, dn = 0;
+      for (int64_t t = first; t < first + count; ++t) {
+        // map_tile's order (mi_gemm_device.hpp) for logical tile t
+        const int64_t group = (int64_t)g * tn, gi = t / group, first_m = gi * g;
+        const int64_t gm = std::min<int64_t>(tm - first_m, g), r = t - gi * group;
+        const int64_t m = first_m + r % gm, n = r / gm;
+        if (!seen_m[(size_t)m]) seen_m[(size_t)m] = 1, ++dm;
+        if (!seen_n[(size_t)n]) seen_n[(size_t)n] = 1, ++dn;
+      }
+      cost += dm * ts.bm + dn * ts.bn;
+    }
+    if (cost < best_cost) best_cost = cost, best = g;
+  }
+  return best;
+}
+
+// Operand layouts whose GEMMs rotate K per XCD.
+bool rotate_policy(int transA, int transB) {
+  (void)transA; (void)transB;
+  return true;
+}
+
+// Per-XCD K rotation of the direct-to-LDS kernels (see gemm_dlds_kernel): one
+// problem, one K segment, no split-K, no causal skipping.
+bool rotate_k(const Problem& P, const Plan& plan) {
+  const mi_batch& b = P.bt;
+  if (P.dtype_in != MI_BF16 || plan.splits != 1 || b.batch != 1 || b.k_segments != 1 ||
+      b.causal != MI_CAUSAL_NONE || plan.cfg == CFG_PRO)
+    return false;
+  return rotate_policy(P.transA, P.transB);
+}
+
 int run(const Problem& P, hipStream_t stream) {
   int st = validate(P);
   if (st != MI_OK) return st;
@@ -453,7 +516,11 @@ int run(const Problem& P, hipStream_t stream) {
   // the direct-to-LDS kernel on it, where the in-load prologue would recompute it
   // for every column tile in the register-staged loader (configuration 3's down
   // projection 8192x2048x5632: 426 us in-load vs about 210 us in two passes).
-  if (mode == MODE_PROLOGUE && P.dtype_in == MI_BF16 && !P.transA && P.K > 0 && b.batch == 1 &&
+  // mi_gemm_noalloc never takes it: its fixed scratch is sized for split-K partials,
+  // not for an M x K activation, so it runs the in-load prologue (the plan mi_gemm
+  // makes without a workspace).
+  if (mode == MODE_PROLOGUE && !P.noalloc && P.dtype_in == MI_BF16 && !P.transA && P.K > 0 &&
+      b.batch == 1 &&
       b.k_segments == 1 && vecA && P.K % 8 == 0 && aligned16(P.ws) &&
       P.ws_bytes >= (size_t)(P.M * P.K * 2)) {
     const size_t act_bytes = (size_t)((P.M * P.K * 2 + 255) / 256 * 256);
@@ -544,6 +611,8 @@ int run(const Problem& P, hipStream_t stream) {
   p.cvec = cvec;
   p.extA = (uint32_t)(fast ? extA : 0);
   p.extB = (uint32_t)(fast ? extB : 0);
+  p.krot = rotate_k(P, plan) ? 1 : 0;
+  p.group_m = group_rows(P, plan);
 
   const int64_t nblocks = (int64_t)plan.tiles_m * plan.tiles_n * plan.splits * b.batch;
   if (nblocks > INT32_MAX) return fail(MI_ERR_SHAPE, "too many tiles");
@@ -1119,6 +1188,8 @@ int mi_convert_matrices(void* stream, const mi_convert_job* jobs, int64_t n) {
     const mi_convert_job& j = jobs[i];
     char what[48];
     std::snprintf(what, sizeof what, "job %lld: ", (long long)i);
+    if (j.reserved != 0)
+      return fail(MI_ERR_SHAPE, "job %lld: reserved field is %d, must be 0", (long long)i, (int)j.reserved);
     uintptr_t s0, s1, d0, d1;
     const int st = check_convert(j.src, j.src_dtype, j.src_ld, j.row0, j.rows, j.cols, j.transpose, j.dst,
                                  j.dst_dtype, j.dst_ld, what, ps[(size_t)i], s0, s1, d0, d1);

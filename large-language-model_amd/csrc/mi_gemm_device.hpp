@@ -60,6 +60,8 @@ struct Params {
   int vecA, vecB;  // 16-byte global loads legal for A (and A2) / B (and B2)
   int cvec;        // 4-wide C / R / bias accesses legal
   uint32_t extA, extB;  // byte extent of one batch/segment matrix of A (A2) / B (B2)
+  int krot;             // direct-to-LDS kernels: start each XCD's tiles at its own K offset
+  int group_m;          // tile rows per column sweep of the tile order (map_tile)
 };
 
 // ---------------------------------------------------------------------------
@@ -456,7 +458,7 @@ struct TileCoord {
 };
 
 // Hardware hands workgroup b to XCD (b mod 8).  Renumber so each XCD receives a
-// contiguous range of logical tiles, then order tiles in groups of GROUP_M tile
+// contiguous range of logical tiles, then order tiles in groups of group_m tile
 // rows so that the workgroups resident on one XCD share A and B panels in its L2.
 #ifndef MI_GROUP_M
 #define MI_GROUP_M 8
@@ -469,8 +471,9 @@ struct TileCoord {
 #endif
 
 __device__ __forceinline__ TileCoord map_tile(int bid, int nblocks, int tiles_m, int tiles_n,
-                                              int splits, int causal) {
-  constexpr int NXCD = 8, GROUP_M = MI_GROUP_M;
+                                              int splits, int causal, int group_m) {
+  constexpr int NXCD = 8;
+  const int GROUP_M = group_m;
   if (causal == CAUSAL_A_LOWER || causal == CAUSAL_A_UPPER) {
     // Causal-skipping products: a tile's K range grows with its row block (A_LOWER)
     // or shrinks with it (A_UPPER).  Workgroups are dispatched in block order, so
@@ -543,7 +546,7 @@ __global__ void __launch_bounds__(256)
   __shared__ u32x4_t smem[2][(BM + BROWS) * 8];
 
   const int nblocks = gridDim.x;
-  const TileCoord tc = map_tile(blockIdx.x, nblocks, p.tiles_m, p.tiles_n, p.splits, p.causal);
+  const TileCoord tc = map_tile(blockIdx.x, nblocks, p.tiles_m, p.tiles_n, p.splits, p.causal, p.group_m);
   const int m0 = uniform(tc.tm * BM), n0 = uniform(tc.tn * BN);
   const int zo = uniform(tc.z / p.heads), zi = uniform(tc.z - (tc.z / p.heads) * p.heads);
   const int ziA = uniform(zi / p.gA), ziB = uniform(zi / p.gB), ziC = uniform(zi / p.gC);

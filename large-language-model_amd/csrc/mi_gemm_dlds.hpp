@@ -291,7 +291,7 @@ __global__ void __launch_bounds__(64 * WGM * WGN * KG)
   const uint32_t lds0 = lds_addr(smem);
 
   const int nblocks = gridDim.x;
-  const TileCoord tc = map_tile(blockIdx.x, nblocks, p.tiles_m, p.tiles_n, p.splits, p.causal);
+  const TileCoord tc = map_tile(blockIdx.x, nblocks, p.tiles_m, p.tiles_n, p.splits, p.causal, p.group_m);
   const int m0 = uniform(tc.tm * BM), n0 = uniform(tc.tn * BN);
   const int zo = uniform(tc.z / p.heads), zi = uniform(tc.z - (tc.z / p.heads) * p.heads);
   const int ziA = uniform(zi / p.gA), ziB = uniform(zi / p.gB), ziC = uniform(zi / p.gC);
@@ -361,9 +361,20 @@ __global__ void __launch_bounds__(64 * WGM * WGN * KG)
   // it1 gets an empty extent and loads zeros.
   const uint32_t a_step = (uint32_t)BK * (AK ? 2u : (uint32_t)p.lda * 2u);  // bytes per K tile
   const uint32_t b_step = (uint32_t)BK * (BKC ? 2u : (uint32_t)p.ldb * 2u);
+  // K rotation (krot; one problem, one K segment, no split, no causal skipping):
+  // the workgroups of XCD x (hardware dispatch: block id mod 8) walk the K tiles
+  // starting at tile x*per_seg/8 and wrap around (the segment-crossing step below
+  // re-seats the descriptors at the same matrix, segA and segB being 0).  All tiles
+  // of one XCD still share their A and B panels in its L2 at the same K, but the
+  // eight XCDs read different rows of the operands at any moment, so the first
+  // XCD to touch a row takes the HBM latency and the others find it in the
+  // memory-side last-level cache, instead of all eight missing on the same rows
+  // together.  The order of the fp32 sum over K tiles changes with the XCD index
+  // and is fixed for a given problem and plan.
+  const int rot = p.krot ? uniform((int)(((int64_t)(blockIdx.x & 7) * per_seg) >> 3)) : 0;
   int d_it = it0;
   int d_seg = uniform(per_seg > 0 ? it0 / per_seg : 0);
-  int d_kt = uniform(it0 - d_seg * per_seg);
+  int d_kt = uniform(it0 - d_seg * per_seg + rot);
   const char* a_ptr = (const char*)(Ab + (int64_t)d_seg * p.segA) + (uint32_t)(klo + d_kt) * a_step;
   const char* b_ptr = (const char*)(Bb + (int64_t)d_seg * p.segB) + (uint32_t)(klo + d_kt) * b_step;
   const char* b2_ptr = DUAL ? (const char*)(B2b + (int64_t)d_seg * p.segB) + (uint32_t)(klo + d_kt) * b_step

@@ -45,6 +45,21 @@ typedef float elem_t;
 #ifndef MI_V_STAGES
 #define MI_V_STAGES 3
 #endif
+// 256x192 (8 waves of 64x96): K tile and ring depth by operand layout (ak: A is
+// K-contiguous, bk: B is K-contiguous).
+#ifndef MI_M_BK
+#define MI_M_BK(ak, bk) MI_DLDS_BK
+#endif
+#ifndef MI_M_STAGES
+#define MI_M_STAGES(ak, bk) MI_DLDS_STAGES
+#endif
+// 256x256 (8 waves of 128x64): K tile and ring depth by operand layout.
+#ifndef MI_L_BK
+#define MI_L_BK(ak, bk) MI_DLDS_BK
+#endif
+#ifndef MI_L_STAGES
+#define MI_L_STAGES(ak, bk) MI_DLDS_STAGES
+#endif
 
 #define MI_CAT5(a, b, c, d, e) a##b##c##d##e
 #define MI_PICK_NAME(dt, ta, tb) MI_CAT5(pick_, dt, _, ta, tb)
@@ -60,13 +75,13 @@ template <bool AK, bool BK, int V>
 KernelFn dlds_kernel(int cfg) {
   switch (cfg) {
     case CFG_L:
-      return gemm_dlds_kernel<256, 256, MI_DLDS_BK, MI_DLDS_STAGES, AK, BK, MODE_PLAIN, V, 2, 4, 1>;
+      return gemm_dlds_kernel<256, 256, MI_L_BK(AK, BK), MI_L_STAGES(AK, BK), AK, BK, MODE_PLAIN, V, 2, 4, 1>;
     case CFG_S: return gemm_dlds_kernel<128, 128, MI_S_BK(AK), MI_S_STAGES(AK), AK, BK, MODE_PLAIN, V>;
     case CFG_DUAL: return gemm_dlds_kernel<256, 128, 32, 4, AK, BK, MODE_DUAL, V>;
     case CFG_W:
       return gemm_dlds_kernel<128, 128, MI_W_BK, MI_W_STAGES, AK, BK, MODE_PLAIN, V, 2, 2, 2>;
     case CFG_M:
-      return gemm_dlds_kernel<256, 192, MI_DLDS_BK, MI_DLDS_STAGES, AK, BK, MODE_PLAIN, V, 4, 2, 1>;
+      return gemm_dlds_kernel<256, 192, MI_M_BK(AK, BK), MI_M_STAGES(AK, BK), AK, BK, MODE_PLAIN, V, 4, 2, 1>;
     case CFG_V:
       return gemm_dlds_kernel<128, 192, MI_W_BK, MI_V_STAGES, AK, BK, MODE_PLAIN, V, 2, 2, 2>;
     default: return nullptr;

@@ -160,6 +160,10 @@ def test_convert_matrices_validation(mi):
     assert st == 5 and "job 1" in msg
     st, msg = run(job(S, D), job(S + 64, D - 8192 + 2))          # dst runs into job 0's dst
     assert st == 5
+    bad = job(S, D + 8192)
+    bad.reserved = 1
+    st, msg = run(job(S, D), bad)
+    assert st == 1 and "job 1" in msg and "reserved" in msg      # MI_ERR_SHAPE
     # row ranges of one fused source (disjoint destinations) pass validation: without a
     # GPU the call then stops at device initialisation
     st, _ = run(job(S, D, row0=0, rows=64), job(S, D + 8192, row0=32, rows=64))
