@@ -21,7 +21,9 @@ dispatches), so events in every step would add about 60 us to each 2 ms step.
 
 roofline: achieved = the dominant kernel's algorithmic FLOPs / its launch time over the
 bracketed steps of the timed region (HIP events on the launch stream), against the dense
-bf16 MFMA peak.
+bf16 MFMA peak.  traffic = HBM bytes per launch of that kernel from the workload's committed
+rocprofv3 --pmc summary (profiles/*_hbm_bytes.md, made by --traffic-table), used only while
+the summary's recorded kernel-source hash matches this tree (else null and traffic_note).
 cpu_baseline: the oracle's fp32 OpenMP SGEMM (oracle/mi_oracle.c, cblas_sgemm
 semantics) on the same set (all M=8192 token rows by default; --cpu-rows bounds it), rank 0
 only.
@@ -65,24 +67,74 @@ PEAK_FP32_TFLOPS = 157.3    # MI355X dense fp32 MFMA
 
 
 WS_BYTES = 512 << 20
-TRAFFIC_FILE = os.path.join(ROOT, "profiles", "gemm_block_set_bf16_m8192_hbm_bytes.md")
-TRAFFIC_FILE_FP32 = os.path.join(ROOT, "profiles", "gemm_block_set_f32_m2048_hbm_bytes.md")
+PROFILES = os.path.join(ROOT, "profiles")
+TRAFFIC_FILES = {   # per workload: the rocprofv3 --pmc summary that bench.py reads traffic from
+    "block": os.path.join(PROFILES, "gemm_block_set_bf16_m8192_hbm_bytes.md"),
+    "block_fp32": os.path.join(PROFILES, "gemm_block_set_f32_m2048_hbm_bytes.md"),
+    "attention": os.path.join(PROFILES, "flash_attention_gqa_b8_t1024_hbm_bytes.md"),
+    "lm_head": os.path.join(PROFILES, "lm_head_xent_m8192_v32000_hbm_bytes.md"),
+}
+CSRC = "large-language-model_amd/csrc/"
+_GEMM_SRC = [CSRC + f for f in ("mi_gemm_dlds.hpp", "mi_gemm_device.hpp", "mi_gemm_inst.hip",
+                                "mi_gemm_kernels.hpp", "mi_gemm.hip")]
+KERNEL_SOURCES = {  # the sources whose kernels (and launch plans) a workload's traffic describes
+    "block": _GEMM_SRC,
+    "block_fp32": _GEMM_SRC,
+    "attention": _GEMM_SRC + [CSRC + "mi_attn.hip", CSRC + "mi_attn.hpp"],
+    "lm_head": _GEMM_SRC + [CSRC + "mi_xent.hip", CSRC + "mi_xent.hpp"],
+}
 
 
-def hbm_bytes_per_launch(kernel: str, path: str = TRAFFIC_FILE):
-    """HBM bytes per launch of `kernel` from the committed rocprofv3 --pmc summary
-    (FETCH_SIZE and WRITE_SIZE per dispatch, scaled by the copy-kernel calibration),
-    or None when the summary has no row for it."""
+def sources_sha16(workload: str) -> str:
+    """sha256 (first 16 hex digits) over the kernel sources of a workload, names and bytes."""
+    import hashlib
+
+    h = hashlib.sha256()
+    for rel in KERNEL_SOURCES[workload]:
+        h.update(rel.encode())
+        with open(os.path.join(ROOT, rel), "rb") as f:
+            h.update(f.read())
+    return h.hexdigest()[:16]
+
+
+def hbm_bytes_per_launch(kernel: str, workload: str = "block"):
+    """(bytes, note): HBM bytes per launch of `kernel` from the workload's committed
+    rocprofv3 --pmc summary (FETCH_SIZE and WRITE_SIZE per dispatch, scaled by the
+    copy-kernel calibration), or (None, reason) when there is no summary, when the summary
+    was measured on other kernel sources than this tree's (its recorded source hash
+    differs), or when it has no row for the kernel."""
+    path = TRAFFIC_FILES[workload]
     if not os.path.exists(path):
-        return None
-    for line in open(path):
+        return None, f"no traffic summary {os.path.relpath(path, ROOT)}"
+    want = sources_sha16(workload)
+    text = open(path).read()
+    import re
+
+    m = re.search(r"kernel sources sha16: `([0-9a-f]{16})`", text)
+    if not m:
+        return None, "traffic summary records no kernel source hash"
+    if m.group(1) != want:
+        return None, (f"traffic summary measured on kernel sources {m.group(1)}, this tree has "
+                      f"{want}: stale, not used")
+    for line in text.splitlines():
         cells = [c.strip() for c in line.strip().strip("|").split("|")]
-        if len(cells) >= 5 and cells[0] == kernel:
+        if len(cells) >= 6 and cells[0] == kernel:
             try:
-                return int(float(cells[4]))
+                return int(float(cells[5])), None
             except ValueError:
-                return None
-    return None
+                break
+    return None, f"traffic summary has no row for {kernel}"
+
+
+def copy_calibration() -> None:
+    """One 1 GiB device-to-device copy (--copy-calibration): the known byte count that scales
+    the FETCH_SIZE and WRITE_SIZE counters of a --pmc run."""
+    import torch
+
+    a = torch.empty(1 << 28, dtype=torch.float32, device="cuda:0")
+    b = torch.empty_like(a)
+    b.copy_(a)
+    torch.cuda.synchronize()
 
 
 def cpu_model() -> str:
@@ -116,6 +168,11 @@ def parse():
                     help="token rows of the CPU sample (default: the whole set, M=8192)")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="also launch a 1 GiB device copy (for PMC byte-counter scaling)")
+    ap.add_argument("--traffic-table", nargs=2, metavar=("FETCH_DIR", "WRITE_DIR"),
+                    help="print the HBM-traffic summary of --workload (block, block_fp32, attention, "
+                         "lm_head) from two rocprofv3 --pmc output directories (FETCH_SIZE, "
+                         "WRITE_SIZE) of a run of this script with the same --steps, --warmup and "
+                         "--copy-calibration; runs no GPU work")
     ap.add_argument("--order", choices=("reference", "projection"), default="reference",
                     help="GEMM issue order of a block step: reference = the engine's (forward "
                          "set, then per projection dW before dX, down first); projection = "
@@ -164,6 +221,7 @@ def cpu_baseline(m_rows: int, block=BLOCK, m_full: int = M_TOKENS, label: str = 
 
 ATT = dict(B=8, nH=16, nKV=4, T=1024, d=128)   # benchmark configuration 4
 ATT_PRODUCT_FLOPS = 17_196_646_400                # one causal product: 2*B*nH*d*T(T+1)/2
+ATT_BWD_KEY = "backward (every kernel of one flash_attn_bwd call)"
 
 
 def cpu_attention_baseline() -> dict:
@@ -239,6 +297,9 @@ def attention_main(args):
     # the backward pass (its launches, bracketed together) takes most of the step
     ms_bwd = sum(a.elapsed_time(b) for a, b in evs.values()) / len(evs)
     achieved = 4 * ATT_PRODUCT_FLOPS / (ms_bwd / 1e3) / 1e12
+    traffic, traffic_note = hbm_bytes_per_launch(ATT_BWD_KEY, "attention")
+    if args.copy_calibration:
+        copy_calibration()
     out = {
         "metric": "GQA attention TFLOP/s (fused fwd+bwd, configuration 4)",
         "value": round(value, 2), "unit": "TFLOP/s", "n_gpus": 1, "steps": args.steps,
@@ -251,8 +312,9 @@ def attention_main(args):
                    "also recomputes S"},
         "roofline": {"bound": "mfma", "achieved": round(achieved, 2), "peak": PEAK_BF16_TFLOPS,
                      "unit": "TFLOP/s", "frac": round(achieved / PEAK_BF16_TFLOPS, 4),
-                     "traffic": None, "kernel": "flash_bwd_delta_kernel + flash_bwd_dkdv_kernel "
+                     "traffic": traffic, "kernel": "flash_bwd_delta_kernel + flash_bwd_dkdv_kernel "
                      "+ dQ batched GEMM (gemm_dlds_kernel)",
+                     **({"traffic_note": traffic_note} if traffic_note else {}),
                      "avg_launch_ms": round(ms_bwd, 4)},
     }
     if not args.no_cpu:
@@ -375,6 +437,9 @@ def lm_head_main(args):
     achieved = LMH_GEMM_FLOPS / (ms_dom / 1e3) / 1e12
     x_bytes = M * V * 2 * 2 + M * 4 * 2           # logits read + gradient written, targets, row losses
     x_gbs = x_bytes / (ms_x / 1e3) / 1e9
+    traffic, traffic_note = hbm_bytes_per_launch(ops[dom][2].rsplit(" tiles", 1)[0], "lm_head")
+    if args.copy_calibration:
+        copy_calibration()
     out = {
         "metric": "LM head + cross-entropy TFLOP/s (configuration 5: logits NT, dX NN, dE TN)",
         "value": round(value, 2), "unit": "TFLOP/s", "n_gpus": 1, "steps": args.steps,
@@ -394,7 +459,8 @@ def lm_head_main(args):
                                      "frac": round(x_gbs / PEAK_HBM_GBS, 4)}},
         "roofline": {"bound": "mfma", "achieved": round(achieved, 2), "peak": PEAK_BF16_TFLOPS,
                      "unit": "TFLOP/s", "frac": round(achieved / PEAK_BF16_TFLOPS, 4),
-                     "traffic": None, "kernel": ops[dom][2], "gemms": [ops[dom][0]],
+                     "traffic": traffic, "kernel": ops[dom][2], "gemms": [ops[dom][0]],
+                     **({"traffic_note": traffic_note} if traffic_note else {}),
                      "avg_launch_ms": round(ms_dom, 4)},
     }
     if not args.no_cpu:
@@ -643,8 +709,208 @@ def convert_main(args):
     print(json.dumps(out))
 
 
+def pmc_dispatches(d: str, counter: str) -> list:
+    """(kernel name, value) per dispatch, in dispatch order, of one counter from a rocprofv3
+    --pmc --output-format csv directory."""
+    import csv
+    import glob
+
+    files = sorted(glob.glob(os.path.join(d, "**", "*counter_collection.csv"), recursive=True))
+    if not files:
+        raise SystemExit(f"no counter_collection.csv under {d}")
+    rows = []
+    for f in files:
+        for r in csv.DictReader(open(f)):
+            if r["Counter_Name"] == counter:
+                rows.append((int(r["Dispatch_Id"]), r["Kernel_Name"], float(r["Counter_Value"])))
+    rows.sort()
+    return [(n, v) for _, n, v in rows]
+
+
+def traffic_table_main(args):
+    """Markdown summary of HBM bytes per launch (FETCH_SIZE and WRITE_SIZE, each scaled by the
+    1 GiB copy of --copy-calibration) for the workload's dominant kernels, with the hash of the
+    kernel sources it was measured on (hbm_bytes_per_launch refuses a summary whose hash is not
+    this tree's)."""
+    fetch = pmc_dispatches(args.traffic_table[0], "FETCH_SIZE")
+    write = pmc_dispatches(args.traffic_table[1], "WRITE_SIZE")
+
+    def calib(rows):
+        c = [v for n, v in rows if "copyBuffer" in n and v > 1 << 18]
+        if not c:
+            raise SystemExit("no 1 GiB copy in the run: use --copy-calibration")
+        return (1 << 20) / c[-1]      # KiB moved / counter reading
+
+    fs, ws_ = calib(fetch), calib(write)
+    ours = lambda rows: [(n, v) for n, v in rows if "mig::" in n]
+    fetch, write = ours(fetch), ours(write)
+    if len(fetch) != len(write):
+        raise SystemExit(f"the two runs dispatched {len(fetch)} and {len(write)} kernels")
+    w = args.workload
+    R = "$R"
+    lines = []
+    title = {"block": "config-3 decoder-block GEMM set, bf16, M=8192",
+             "block_fp32": "config-2 decoder-block GEMM set, fp32, M=2048",
+             "attention": "fused GQA flash attention, configuration 4",
+             "lm_head": "LM head + cross-entropy, configuration 5"}[w]
+    lines.append(f"# HBM bytes per launch: {title}\n")
+    lines.append("Source: two `rocprofv3 --pmc` runs of `bench.py` on one MI355X ($R = repository "
+                 "root), then this summary from their output:\n")
+    lines.append("```")
+    flags = f"--workload {w} --steps {args.steps} --warmup {args.warmup} --no-cpu --copy-calibration"
+    if w.startswith("block") and args.order != "reference":
+        flags += f" --order {args.order}"
+    for c in ("FETCH_SIZE", "WRITE_SIZE"):
+        lines.append(f"cd /tmp && export TMPDIR=/tmp && timeout -s KILL 120 rocprofv3 --pmc {c} -d "
+                     f"{R}/gpurun_out/pmc_{c}_{w} -o run --output-format csv -- python3 -u "
+                     f"{R}/bench.py {flags}")
+    lines.append(f"python3 {R}/bench.py {flags} --traffic-table {R}/gpurun_out/pmc_FETCH_SIZE_{w} "
+                 f"{R}/gpurun_out/pmc_WRITE_SIZE_{w}")
+    lines.append("```\n")
+    lines.append(f"kernel sources sha16: `{sources_sha16(w)}` (`bench.py` reports `roofline.traffic` "
+                 "from this file only while its kernel sources, `KERNEL_SOURCES` in bench.py, hash "
+                 "to this value)\n")
+    lines.append(f"Calibration: a 1 GiB device copy in the same runs read FETCH_SIZE x{fs:.3f} and "
+                 f"WRITE_SIZE x{ws_:.3f} of the bytes it moved; the counters below are scaled by "
+                 "those factors. FETCH_SIZE counts L2 fills from the memory fabric, so reads the "
+                 "memory-side last-level cache serves count as well.\n")
+    hdr = ("| key | kernels | launches | FETCH KiB (scaled) | WRITE KiB (scaled) | bytes per launch "
+           "| algorithmic bytes per launch | ratio |")
+    sep = "|---|---|---|---|---|---|---|---|"
+    short = lambda n: n.replace("void mig::", "").replace("(anonymous namespace)::", "").split("(")[0]
+
+    def row(key, names, n, fk, wk, alg):
+        by = int(round((fk + wk) * 1024))
+        ratio = f"{by / alg:.2f}" if alg else "-"
+        return f"| {key} | {names} | {n} | {fk:.0f} | {wk:.0f} | {by} | {alg if alg else '-'} | {ratio} |"
+
+    if w in ("block", "block_fp32"):
+        seq, order_desc = block_sequence(w == "block_fp32", args.order)
+        n_steps = args.warmup + 1 + 3 + args.steps   # warm-up, pre-attribution, attribution, timed
+        esz = 4 if w == "block_fp32" else 2
+        launches = []
+        for _ in range(n_steps):
+            for name, kind, label, flops, desc, din, dout in seq:
+                launches.append((f"{name} {label}", desc, False))
+                if " split1 " not in desc + " ":
+                    launches.append((f"{name} {label}", desc, True))
+        if len(launches) != len(fetch):
+            raise SystemExit(f"expected {len(launches)} GEMM launches, the run has {len(fetch)}")
+        per_op, per_desc = {}, {}
+        for (op, desc, red), (n, fv), (_, wv) in zip(launches, fetch, write):
+            want = "splitk_reduce" if red else "gemm"
+            if want not in n:
+                raise SystemExit(f"dispatch {n} where {want} of {op} was expected")
+            e = per_op.setdefault(op, [desc, set(), 0, 0.0, 0.0])
+            e[1].add(short(n))
+            e[2] += 0 if red else 1
+            e[3] += fv * fs
+            e[4] += wv * ws_
+        M = M_TOKENS_FP32 if w == "block_fp32" else M_TOKENS
+        alg_of = {}
+        for name, kind, label, flops, desc, din, dout in seq:
+            m, n_, k = {"fwd": (M, dout, din), "dX": (M, din, dout), "dW": (din, dout, M)}[kind]
+            cb = 4 if kind == "dW" else esz
+            alg_of[f"{name} {label}"] = esz * (m * k + k * n_) + m * n_ * cb * (2 if kind == "dW" else 1)
+        for op, (desc, names, n, fk, wk) in per_op.items():
+            key = desc.rsplit(" tiles", 1)[0]
+            d = per_desc.setdefault(key, [set(), [], 0, 0.0, 0.0, 0])
+            d[0] |= names
+            d[1].append(op)
+            d[2] += n
+            d[3] += fk
+            d[4] += wk
+            d[5] += alg_of[op] * n
+        lines.append(f"Launch order: {order_desc}; {n_steps} steps per run (warm-up, one step before "
+                     "the attribution pass, 3 attribution steps, timed steps). A split-K GEMM's row "
+                     "adds its reduce kernel's bytes. `algorithmic` = A and B read once, C written "
+                     "once (dW: fp32 C read and written, beta = 1).\n")
+        lines.append("## Per kernel description (the key `bench.py` uses for `roofline.traffic`)\n")
+        lines.append(hdr)
+        lines.append(sep)
+        for key, (names, ops_, n, fk, wk, alg) in per_desc.items():
+            lines.append(row(key, ", ".join(sorted(names)) + " (" + ", ".join(ops_) + ")", n, fk / n,
+                             wk / n, alg // n))
+        lines.append("\n## Per GEMM\n")
+        lines.append(hdr)
+        lines.append(sep)
+        for op, (desc, names, n, fk, wk) in per_op.items():
+            lines.append(row(op, desc, n, fk / n, wk / n, alg_of[op]))
+    elif w == "attention":
+        B, nH, nKV, T, d = (ATT[k] for k in ("B", "nH", "nKV", "T", "d"))
+        steps = sum(1 for n, _ in fetch if "flash_fwd_kernel" in n)
+        names = {}
+        for (n, fv), (_, wv) in zip(fetch, write):
+            e = names.setdefault(short(n), [0, 0.0, 0.0])
+            e[0] += 1
+            e[1] += fv * fs
+            e[2] += wv * ws_
+        alg_bwd = 2 * (4 * B * nH * T * d + 4 * B * nKV * T * d) + 4 * B * nH * T
+        alg_fwd = 2 * (2 * B * nH * T * d + 2 * B * nKV * T * d) + 4 * B * nH * T
+        bwd = [(k, v) for k, v in names.items() if "flash_fwd_kernel" not in k]
+        lines.append(f"{steps} forward + backward steps per run. `algorithmic`: the backward reads Q, "
+                     "K, V, O, dO and the row log-sum-exp and writes dQ, dK, dV once; the forward "
+                     "reads Q, K, V and writes O and the log-sum-exp once (bf16).\n")
+        lines.append(hdr)
+        lines.append(sep)
+        fk = sum(v[1] for _, v in bwd) / steps
+        wk = sum(v[2] for _, v in bwd) / steps
+        lines.append(row(ATT_BWD_KEY, ", ".join(k for k, _ in bwd), steps, fk, wk, alg_bwd))
+        for k, (n, f_, w_) in names.items():
+            lines.append(row(k, k, n, f_ / n, w_ / n, alg_fwd if "flash_fwd" in k else 0))
+    elif w == "lm_head":
+        M, H, V = LMH["M"], LMH["H"], LMH["V"]
+        import mi_gemm as mi
+
+        gemms = [("logits NT", mi.describe(0, 1, M, V, H, workspace_bytes=WS_BYTES),
+                  2 * (M * H + V * H) + 2 * M * V),
+                 ("dX NN", mi.describe(0, 0, M, H, V, workspace_bytes=WS_BYTES),
+                  2 * (M * V + V * H) + 2 * M * H),
+                 ("dE TN", mi.describe(1, 0, V, H, M, workspace_bytes=WS_BYTES),
+                  2 * (M * V + M * H) + 8 * V * H)]
+        n_steps = args.warmup + 1 + 3 + args.steps
+        gl = [(f, w_) for f, w_ in zip(fetch, write) if "gemm" in f[0] or "splitk" in f[0]]
+        other = [(f, w_) for f, w_ in zip(fetch, write) if not ("gemm" in f[0] or "splitk" in f[0])]
+        per = {}
+        it = iter(gl)
+        for _ in range(n_steps):
+            for label, desc, alg in gemms:
+                parts = [next(it)] + ([next(it)] if " split1 " not in desc + " " else [])
+                e = per.setdefault(label, [desc, set(), 0, 0.0, 0.0, alg])
+                for (n, fv), (_, wv) in parts:
+                    e[1].add(short(n))
+                    e[3] += fv * fs
+                    e[4] += wv * ws_
+                e[2] += 1
+        if next(it, None) is not None:
+            raise SystemExit("more GEMM launches in the run than the workload issues")
+        lines.append(f"{n_steps} steps per run (warm-up, one step before the attribution pass, 3 "
+                     "attribution steps, timed steps). `algorithmic` = A and B read once, C written "
+                     "once (dE: fp32 C read and written); cross-entropy: the logits read and the "
+                     "gradient written once in place, bf16.\n")
+        lines.append(hdr)
+        lines.append(sep)
+        for label, (desc, names, n, fk, wk, alg) in per.items():
+            lines.append(row(desc.rsplit(" tiles", 1)[0], f"{label}: " + ", ".join(sorted(names)), n,
+                             fk / n, wk / n, alg))
+        names = {}
+        for (n, fv), (_, wv) in other:
+            e = names.setdefault(short(n), [0, 0.0, 0.0])
+            e[0] += 1
+            e[1] += fv * fs
+            e[2] += wv * ws_
+        for k, (n, f_, w_) in names.items():
+            lines.append(row(k, k, n, f_ / n, w_ / n, 2 * 2 * M * V if "xent_vec" in k else 0))
+    else:
+        raise SystemExit(f"no traffic summary for workload {w}")
+    print("\n".join(lines))
+
+
 def main():
     args = parse()
+    if args.traffic_table:
+        traffic_table_main(args)
+        return
     if args.gpus != 1:
         print(json.dumps({"error": "this build runs on one GPU only; --gpus must be 1 "
                                    "(the multi-GPU sharding is a design, not run)"}))
@@ -667,6 +933,33 @@ def main():
     gemm_set_main(args, fp32=args.workload == "block_fp32")
 
 
+def block_sequence(fp32: bool, order: str = "reference"):
+    """The GEMMs of one block step in issue order: (projection, kind, label, FLOPs, planner
+    description, d_in, d_out), and the order's description."""
+    import mi_gemm as mi
+
+    block, M = (BLOCK_FP32, M_TOKENS_FP32) if fp32 else (BLOCK, M_TOKENS)
+    mi_dt = mi.MI_F32 if fp32 else mi.MI_BF16
+    dims = {name: (din, dout) for name, din, dout in block}
+    if order == "reference":
+        keys = REF_ORDER
+        desc = ("reference engine: fwd qkv, o, gate, up, down; then down dW, down dX, "
+                "gate dW, up dW, gate dX, up dX, o dW, o dX, qkv dW, qkv dX "
+                "(Transformer.cpp:161-167,382-424; Attention.cpp:196-201,282,474-585)")
+    else:
+        keys = [(name, k) for name, _, _ in block for k in ("fwd", "dX", "dW")]
+        desc = "per projection: fwd, dX, dW"
+    seq = []
+    for name, kind in keys:
+        din, dout = dims[name]
+        tA, tB, m, n, k, label = {"fwd": (0, 0, M, dout, din, "fwd NN"),
+                                  "dX": (0, 1, M, din, dout, "dX NT"),
+                                  "dW": (1, 0, din, dout, M, "dW TN")}[kind]
+        plan = mi.describe(tA, tB, m, n, k, dtype_in=mi_dt, workspace_bytes=WS_BYTES)
+        seq.append((name, kind, label, 2 * M * din * dout, plan, din, dout))
+    return seq, desc
+
+
 def gemm_set_main(args, fp32: bool):
     """Configuration 3 (bf16 in, bf16 Y/dX, fp32 dW +=) or, with fp32, configuration 2
     (fp32 everywhere): the 15 GEMMs of one decoder block per step."""
@@ -684,7 +977,7 @@ def gemm_set_main(args, fp32: bool):
     g.manual_seed(1234)
     # split-K workspace, as the bridge's pool provides it (the planner decides per GEMM)
     ws = torch.empty(WS_BYTES // 4, dtype=torch.float32, device=dev)
-    by_key, xs = {}, {}
+    xs, tensors = {}, {}
     for name, din, dout in block:
         X = (xs[SHARED_X[name]] if name in SHARED_X
              else torch.randn((M, din), generator=g, device=dev).to(dt_in))
@@ -694,31 +987,21 @@ def gemm_set_main(args, fp32: bool):
         Y = torch.empty((M, dout), dtype=dt_in, device=dev)
         dX = torch.empty((M, din), dtype=dt_in, device=dev)
         dW = torch.zeros((din, dout), dtype=torch.float32, device=dev)
-        by_key[(name, "fwd")] = (
-            name, "fwd NN", 2 * M * din * dout,
-            mi.describe(0, 0, M, dout, din, dtype_in=mi_dt, workspace_bytes=WS_BYTES),
-            lambda X=X, W=W, Y=Y, din=din, dout=dout:
-            mi.gemm(X, W, Y, M, dout, din, workspace=ws, sync=False))
-        by_key[(name, "dX")] = (
-            name, "dX NT", 2 * M * din * dout,
-            mi.describe(0, 1, M, din, dout, dtype_in=mi_dt, workspace_bytes=WS_BYTES),
-            lambda dY=dY, W=W, dX=dX, din=din, dout=dout:
-            mi.gemm(dY, W, dX, M, din, dout, transB=True, workspace=ws, sync=False))
-        by_key[(name, "dW")] = (
-            name, "dW TN", 2 * M * din * dout,
-            mi.describe(1, 0, din, dout, M, dtype_in=mi_dt, workspace_bytes=WS_BYTES),
-            lambda X=X, dY=dY, dW=dW, din=din, dout=dout:
-            mi.gemm(X, dY, dW, din, dout, M, transA=True, beta=1.0, workspace=ws,
-                    sync=False))
-    if args.order == "reference":
-        order_keys = REF_ORDER
-        order_desc = ("reference engine: fwd qkv, o, gate, up, down; then down dW, down dX, "
-                      "gate dW, up dW, gate dX, up dX, o dW, o dX, qkv dW, qkv dX "
-                      "(Transformer.cpp:161-167,382-424; Attention.cpp:196-201,282,474-585)")
-    else:
-        order_keys = [(name, k) for name, _, _ in block for k in ("fwd", "dX", "dW")]
-        order_desc = "per projection: fwd, dX, dW"
-    ops = [by_key[k] for k in order_keys]
+        tensors[name] = dict(X=X, W=W, dY=dY, Y=Y, dX=dX, dW=dW)
+
+    def launcher(name, kind, din, dout):
+        t = tensors[name]
+        if kind == "fwd":      # Y = X W
+            return lambda: mi.gemm(t["X"], t["W"], t["Y"], M, dout, din, workspace=ws, sync=False)
+        if kind == "dX":       # dX = dY W^T
+            return lambda: mi.gemm(t["dY"], t["W"], t["dX"], M, din, dout, transB=True, workspace=ws,
+                                   sync=False)
+        return lambda: mi.gemm(t["X"], t["dY"], t["dW"], din, dout, M, transA=True, beta=1.0,  # dW += X^T dY
+                               workspace=ws, sync=False)
+
+    seq, order_desc = block_sequence(fp32, args.order)
+    ops = [(name, label, flops, desc, launcher(name, kind, din, dout))
+           for name, kind, label, flops, desc, din, dout in seq]
 
     def step():
         for op in ops:
@@ -796,14 +1079,11 @@ def gemm_set_main(args, fp32: bool):
     n_dom = len(dom_idx) * len(ev_steps)
     fl_dom = sum(ops[k][2] for k in dom_idx) * len(ev_steps)
     achieved = fl_dom / (ms_dom / 1e3) / 1e12
-    traffic = hbm_bytes_per_launch(dom, TRAFFIC_FILE_FP32 if fp32 else TRAFFIC_FILE)
+    traffic, traffic_note = hbm_bytes_per_launch(dom, "block_fp32" if fp32 else "block")
     dom_ops = sorted(f"{ops[k][0]} {ops[k][1]}" for k in dom_idx)
 
     if args.copy_calibration:
-        a = torch.empty(1 << 28, dtype=torch.float32, device=dev)
-        b = torch.empty_like(a)
-        b.copy_(a)
-        torch.cuda.synchronize()
+        copy_calibration()
 
     if fp32:
         metric = "GEMM TFLOP/s (fwd+bwd, GPT-small block fp32, M=2048) and % of MI355X fp32 MFMA peak"
@@ -838,6 +1118,7 @@ def gemm_set_main(args, fp32: bool):
         "roofline": {"bound": "mfma", "achieved": round(achieved, 2), "peak": peak,
                      "unit": "TFLOP/s", "frac": round(achieved / peak, 4),
                      "traffic": traffic, "kernel": dom, "gemms": dom_ops,
+                     **({"traffic_note": traffic_note} if traffic_note else {}),
                      "launches": n_dom, "avg_launch_ms": round(ms_dom / n_dom, 4),
                      "time_share": round(per_kernel[dom] / sum(per_kernel.values()), 3)},
     }
