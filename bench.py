@@ -173,6 +173,9 @@ def parse():
                          "lm_head) from two rocprofv3 --pmc output directories (FETCH_SIZE, "
                          "WRITE_SIZE) of a run of this script with the same --steps, --warmup and "
                          "--copy-calibration; runs no GPU work")
+    ap.add_argument("--head-dim", type=int, default=ATT["d"], choices=(64, 128),
+                    help="attention workload: head dimension (128 = configuration 4; 64 = the "
+                         "reference kernels' compiled size at configuration 4's batch and heads)")
     ap.add_argument("--order", choices=("reference", "projection"), default="reference",
                     help="GEMM issue order of a block step: reference = the engine's (forward "
                          "set, then per projection dW before dX, down first); projection = "
@@ -221,6 +224,12 @@ def cpu_baseline(m_rows: int, block=BLOCK, m_full: int = M_TOKENS, label: str = 
 
 ATT = dict(B=8, nH=16, nKV=4, T=1024, d=128)   # benchmark configuration 4
 ATT_PRODUCT_FLOPS = 17_196_646_400                # one causal product: 2*B*nH*d*T(T+1)/2
+
+
+def att_product_flops(d: int) -> int:
+    """One causal product of configuration 4's batch and heads at head dimension d."""
+    B, nH, T = ATT["B"], ATT["nH"], ATT["T"]
+    return 2 * B * nH * d * T * (T + 1) // 2
 ATT_BWD_KEY = "backward (every kernel of one flash_attn_bwd call)"
 
 
@@ -261,6 +270,8 @@ def attention_main(args):
     dev = torch.device("cuda:0")
     mi.init()
     B, nH, nKV, T, d = (ATT[k] for k in ("B", "nH", "nKV", "T", "d"))
+    d = args.head_dim
+    prod = att_product_flops(d)
     g = torch.Generator(device=dev)
     g.manual_seed(4)
     Q = torch.randn((B, nH, T, d), generator=g, device=dev).to(torch.bfloat16)
@@ -273,6 +284,8 @@ def attention_main(args):
                      dtype=torch.bfloat16, device=dev)
 
     def step(ev=None):
+        if ev is not None:
+            ev[2].record()
         mi.flash_attn_fwd(Q, K, V, O=O, lse=lse, sync=False)
         if ev is not None:
             ev[0].record()
@@ -285,19 +298,20 @@ def attention_main(args):
     torch.cuda.synchronize()
     # events (about 6 us of idle GPU per record) only in the last EVENT_STEPS timed steps
     ev_steps = timed_event_steps(args.steps)
-    evs = {s_: (torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
-           for s_ in ev_steps}
+    evs = {s_: tuple(torch.cuda.Event(enable_timing=True) for _ in range(3)) for s_ in ev_steps}
     t0 = time.perf_counter()
     for s_ in range(args.steps):
         step(evs.get(s_))
     torch.cuda.synchronize()
     elapsed = time.perf_counter() - t0
-    flops = 6 * ATT_PRODUCT_FLOPS
+    flops = 6 * prod
     value = flops * args.steps / elapsed / 1e12
     # the backward pass (its launches, bracketed together) takes most of the step
-    ms_bwd = sum(a.elapsed_time(b) for a, b in evs.values()) / len(evs)
-    achieved = 4 * ATT_PRODUCT_FLOPS / (ms_bwd / 1e3) / 1e12
-    traffic, traffic_note = hbm_bytes_per_launch(ATT_BWD_KEY, "attention")
+    ms_bwd = sum(a.elapsed_time(b) for a, b, _ in evs.values()) / len(evs)
+    ms_fwd = sum(c.elapsed_time(a) for a, _, c in evs.values()) / len(evs)
+    achieved = 4 * prod / (ms_bwd / 1e3) / 1e12
+    traffic, traffic_note = (hbm_bytes_per_launch(ATT_BWD_KEY, "attention") if d == ATT["d"]
+                             else (None, "traffic summary is for head_dim 128"))
     if args.copy_calibration:
         copy_calibration()
     out = {
@@ -306,10 +320,13 @@ def attention_main(args):
         "warmup": args.warmup, "ms_per_step": round(elapsed / args.steps * 1e3, 4),
         "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
         "data": "synthetic (torch.randn on device; Q,K,V~N(0,1), dO~N(0,1e-2))",
-        "config": {"workload": "GQA attention B=8, 16 q / 4 kv heads, T=1024, d=128, causal: "
-                               "fused forward + backward (dQ, dK, dV)",
+        "config": {"workload": f"GQA attention B=8, 16 q / 4 kv heads, T=1024, d={d}, causal: "
+                               "fused forward + backward (dQ, dK, dV)"
+                               + ("" if d == ATT["d"] else " (configuration 4 at another head_dim)"),
                    "flops_per_step": flops, "flops_note": "6 causal products; the backward "
-                   "also recomputes S"},
+                   "also recomputes S",
+                   "fwd_ms": round(ms_fwd, 4), "bwd_ms": round(ms_bwd, 4),
+                   "fwd_tflops": round(2 * prod / (ms_fwd / 1e3) / 1e12, 1)},
         "roofline": {"bound": "mfma", "achieved": round(achieved, 2), "peak": PEAK_BF16_TFLOPS,
                      "unit": "TFLOP/s", "frac": round(achieved / PEAK_BF16_TFLOPS, 4),
                      "traffic": traffic, "kernel": "flash_bwd_delta_kernel + flash_bwd_dkdv_kernel "

@@ -76,10 +76,10 @@ void gemm_proj_trans_b(const float* a, const float* b_transposed, float* c, size
 
 // MetalBridge.hpp:49-51: causal GQA attention forward, bf16.  Q [B,nH,S,d], K/V
 // [B,nKV,S,d], O [B,nH,S,d] (the output layout of flash_attn_fwd.metal); query
-// head h reads KV head h / (nH/nKV).  head_dim 128 runs the fused kernel; a head_dim
-// below 128 and a multiple of 8 (the reference kernel's is 64) runs it too, on
-// bridge-owned copies of Q, K, V in 128-column rows zero past head_dim, with the
-// scale 1/sqrt(head_dim) (mi_flash_attn_fwd_scaled); any other head_dim runs the
+// head h reads KV head h / (nH/nKV).  head_dim 64 (the reference kernel's) and 128
+// run the fused kernel; another head_dim below 128 and a multiple of 8 runs the next
+// larger one on bridge-owned copies of Q, K, V whose columns past head_dim are zero,
+// with the scale 1/sqrt(head_dim) (mi_flash_attn_fwd_scaled); any other head_dim runs the
 // materialised form: S and P in a bridge-owned [B,nH,S,S] bf16 buffer, batched
 // GEMMs and the softmax kernel.
 void flash_attn_fwd(const void* Q, const void* K, const void* V, void* O, size_t batch,
@@ -88,9 +88,10 @@ void flash_attn_fwd(const void* Q, const void* K, const void* V, void* O, size_t
 // MetalBridge.hpp:54-57: gradients of the causal GQA attention, bf16, dO and dQ
 // [B,nH,S,d], dK/dV [B,nKV,S,d] summed over each KV group's query heads.  Like
 // the reference kernel it takes no forward state: the forward's O and row
-// log-sum-exp are recomputed into bridge-owned device buffers first.  head_dim
-// below 128 (multiple of 8): the fused kernels on zero-padded copies, as in
-// flash_attn_fwd; any other head_dim: the materialised backward (P and dP in
+// log-sum-exp are recomputed into bridge-owned device buffers first.  head_dim 64
+// and 128: the fused kernels; another head_dim below 128 (multiple of 8): the next
+// larger fused kernels on zero-padded copies, as in flash_attn_fwd; any other
+// head_dim: the materialised backward (P and dP in
 // bridge-owned buffers).
 void fused_attn_bwd(const void* Q, const void* K, const void* V, const void* dO, void* dQ,
                     void* dK, void* dV, size_t batch, size_t n_heads, size_t n_kv,

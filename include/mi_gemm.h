@@ -191,8 +191,9 @@ typedef enum mi_attn_layout {
  * softmax).  Q [batch, n_heads, seq_len, d], K and V [batch, n_kv, seq_len, d], O
  * per o_layout, all bf16 and 16-byte aligned; lse (optional, fp32 [batch,
  * n_heads, seq_len]) receives each row's natural-log log-sum-exp of the scaled
- * scores, for a backward pass.  causal = 0 attends to every key.  head_dim must
- * be 128; n_heads a multiple of n_kv.  Replaces metal_bridge::flash_attn_fwd
+ * scores, for a backward pass.  causal = 0 attends to every key.  head_dim 64
+ * (the reference kernel's compiled size, flash_attn_fwd.metal:31) or 128; n_heads
+ * a multiple of n_kv.  Replaces metal_bridge::flash_attn_fwd
  * (MetalBridge.hpp:49-51) and the forward of Attention::forward
  * (Attention.cpp:236-280).
  */
@@ -206,7 +207,7 @@ int mi_flash_attn_fwd(void* stream, const void* Q, const void* K, const void* V,
  * computes dQ [batch, n_heads, seq_len, d] and dK, dV [batch, n_kv, seq_len, d]
  * (bf16), dK/dV summed over the n_heads/n_kv query heads of each KV head.  O
  * and dO use o_layout; delta is caller workspace of batch*n_heads*seq_len fp32
- * (receives rowsum(dO * O)).  Deterministic (no atomics).  head_dim must be 128.
+ * (receives rowsum(dO * O)).  Deterministic (no atomics).  head_dim 64 or 128.
  * With workspace of mi_flash_attn_bwd_workspace_size bytes (16-byte aligned;
  * seq_len a multiple of 8, at most 32767) the dK/dV kernel also writes dS^T there and dQ is
  * one batched GEMM (5 MFMA products); with NULL / too little workspace a dQ
@@ -222,7 +223,7 @@ int mi_flash_attn_bwd(void* stream, const void* Q, const void* K, const void* V,
                       size_t workspace_bytes);
 
 /* Workspace bytes for the dS^T form of mi_flash_attn_bwd: batch*n_heads*seq_len^2
- * bf16 for dS^T, then batch*n_heads*seq_len*128 fp32 for the partial dK / dV sums
+ * bf16 for dS^T, then batch*n_heads*seq_len*128 fp32 (enough for head_dim 128) for the partial dK / dV sums
  * of the balanced dK/dV schedule (a workspace holding dS^T only runs the dS^T form
  * with one workgroup per key block); 0 when the form does not apply (seq_len not a
  * multiple of 8, or above 32767). */
@@ -231,12 +232,12 @@ size_t mi_flash_attn_bwd_workspace_size(int64_t batch, int64_t n_heads, int64_t 
 /*
  * mi_flash_attn_fwd / mi_flash_attn_bwd with the softmax scale given (the two
  * functions above use 1/sqrt(head_dim), Attention.cpp:208).  For a head dimension
- * d below 128 (the reference kernel's 64, flash_attn_fwd.metal:31), copy Q, K, V
- * (and dO) into 128-column rows whose columns d..127 are zero and pass
- * scale = 1/sqrt(d): the zero columns add exact zeros to every score, and the
- * output and gradient columns d..127 come out zero.  The C++ bridge does this for
- * flash_attn_fwd / fused_attn_bwd with a head_dim below 128.  scale must be
- * positive and finite.
+ * d that is neither 64 nor 128 (a multiple of 8 below 128), copy Q, K, V (and dO)
+ * into rows of the next kernel size (64 or 128 columns) whose columns past d are
+ * zero and pass scale = 1/sqrt(d): the zero columns add exact zeros to every
+ * score, and the output and gradient columns past d come out zero.  The C++
+ * bridge does this for flash_attn_fwd / fused_attn_bwd.  scale must be positive
+ * and finite.
  */
 int mi_flash_attn_fwd_scaled(void* stream, const void* Q, const void* K, const void* V, void* O,
                              float* lse, int64_t batch, int64_t n_heads, int64_t n_kv, int64_t seq_len,

@@ -1,6 +1,7 @@
 // gemm_bridge.cpp -- C++ mirror of the reference GEMM operator layer over the
 // C ABI (declarations and the reference citations are in include/gemm_bridge.hpp).
 #include "../../include/gemm_bridge.hpp"
+#include "mi_convert.hpp"
 
 #include <hip/hip_runtime.h>
 
@@ -331,29 +332,32 @@ int materialised_bwd(const void* Q, const void* K, const void* V, const void* dO
   return s;
 }
 
-// Head dimensions below 128 (the reference kernel's 64) run the fused d = 128
-// kernels on copies of the operands in 128-column rows whose extra columns are
-// zero, with the softmax scale of the real head dimension (mi_flash_attn_*_scaled).
-// The pool holds Q, K, V, dO, O, dQ, dK, dV in that layout; input columns past the
-// head dimension are never written after the pool is zeroed (on allocation, or
-// when the head dimension changes).
-thread_local void* t_pad = nullptr;
-thread_local size_t t_pad_bytes = 0, t_pad_dim = 0;
+// The fused kernels are built for head_dim 64 (the reference kernels' compiled size)
+// and 128.  Other head dimensions that are multiples of 8 and below 128 run the next
+// larger kernel on copies of the operands whose extra columns are zero, with the
+// softmax scale of the real head dimension (mi_flash_attn_*_scaled): the zero columns
+// add exact zeros to every score, and the extra output and gradient columns are
+// discarded.  The pool holds Q, K, V, dO, O, dQ, dK, dV in rows of kd columns; every
+// call writes all kd columns of its inputs (zeros past head_dim), so nothing a previous
+// call left in the pool (other shapes, NaN from non-finite inputs) reaches the scores.
+size_t fused_dim(size_t head_dim) {
+  if (head_dim == 0 || head_dim % 8 || head_dim > 128) return 0;
+  return head_dim <= 64 ? 64 : 128;
+}
 
-bool pad_state(size_t bytes, size_t head_dim) {
+thread_local void* t_pad = nullptr;
+thread_local size_t t_pad_bytes = 0;
+
+bool pad_state(size_t bytes) {
   if (bytes > t_pad_bytes) {
     if (t_pad) {
       if (hipStreamSynchronize(get_stream()) != hipSuccess) return false;
       (void)hipFree(t_pad);
     }
     t_pad = nullptr;
-    t_pad_bytes = t_pad_dim = 0;
+    t_pad_bytes = 0;
     if (hipMalloc(&t_pad, bytes) != hipSuccess) return false;
     t_pad_bytes = bytes;
-  }
-  if (t_pad_dim != head_dim) {
-    if (hipMemsetAsync(t_pad, 0, t_pad_bytes, get_stream()) != hipSuccess) return false;
-    t_pad_dim = head_dim;
   }
   return true;
 }
@@ -362,10 +366,10 @@ struct Padded {
   char *q, *k, *v, *o, *dout, *dq, *dk, *dv;
 };
 
-// Carve the pool for rows_q query rows and rows_kv key rows of 128 bf16 each.
-bool padded_buffers(size_t rows_q, size_t rows_kv, size_t head_dim, bool backward, Padded* b) {
-  const size_t rq = (rows_q * 256 + 255) / 256 * 256, rk = (rows_kv * 256 + 255) / 256 * 256;
-  if (!pad_state(backward ? 4 * rq + 4 * rk : 2 * rq + 2 * rk, head_dim)) return false;
+// Carve the pool for rows_q query rows and rows_kv key rows of kd bf16 each.
+bool padded_buffers(size_t rows_q, size_t rows_kv, size_t kd, bool backward, Padded* b) {
+  const size_t rq = (rows_q * kd * 2 + 255) / 256 * 256, rk = (rows_kv * kd * 2 + 255) / 256 * 256;
+  if (!pad_state(backward ? 4 * rq + 4 * rk : 2 * rq + 2 * rk)) return false;
   char* w = (char*)t_pad;
   b->q = w; w += rq;
   b->o = w; w += rq;
@@ -380,44 +384,54 @@ bool padded_buffers(size_t rows_q, size_t rows_kv, size_t head_dim, bool backwar
   return true;
 }
 
-// rows x d bf16 <-> rows x 128 bf16 (the first d columns).
-int widen(const void* src, void* dst, size_t rows, size_t d) {
-  return mi_convert_matrix(get_stream(), src, MI_BF16, (int64_t)d, 0, (int64_t)rows, (int64_t)d, 0, dst,
-                           MI_BF16, 128);
+// rows x d bf16 -> rows x kd bf16 (zeros past d), and back (the first d columns).
+int widen(const void* src, void* dst, size_t rows, size_t d, size_t kd) {
+  int dev = 0;
+  int cus = 0;
+  if (hipGetDevice(&dev) == hipSuccess)
+    (void)hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
+  const hipError_t e = mig::launch_pad_rows(src, (int64_t)d, (int64_t)rows, (int64_t)d, dst, (int64_t)kd, cus,
+                                            get_stream());
+  if (e != hipSuccess) {
+    std::fprintf(stderr, "[mi_bridge] padded attention operand: %s\n", hipGetErrorString(e));
+    return MI_ERR_HIP;
+  }
+  return MI_OK;
 }
-int narrow(const void* src, void* dst, size_t rows, size_t d) {
-  return mi_convert_matrix(get_stream(), src, MI_BF16, 128, 0, (int64_t)rows, (int64_t)d, 0, dst, MI_BF16,
-                           (int64_t)d);
+int narrow(const void* src, void* dst, size_t rows, size_t d, size_t kd) {
+  return mi_convert_matrix(get_stream(), src, MI_BF16, (int64_t)kd, 0, (int64_t)rows, (int64_t)d, 0, dst,
+                           MI_BF16, (int64_t)d);
 }
 
 }  // namespace
 
 void flash_attn_fwd(const void* Q, const void* K, const void* V, void* O, size_t batch,
                     size_t n_heads, size_t n_kv, size_t seq_len, size_t head_dim) {
-  if (head_dim < 128 && head_dim % 8 == 0 && batch && n_heads && seq_len && head_dim) {
+  const size_t kd = fused_dim(head_dim);
+  if (kd && kd != head_dim && batch && n_heads && seq_len) {
     if (n_kv == 0 || n_heads % n_kv) {
       finish("flash_attn_fwd", MI_ERR_SHAPE);
       return;
     }
     const size_t rq = batch * n_heads * seq_len, rk = batch * n_kv * seq_len;
     Padded b;
-    if (!padded_buffers(rq, rk, head_dim, false, &b)) {
+    if (!padded_buffers(rq, rk, kd, false, &b)) {
       t_status = MI_ERR_HIP;
       std::fprintf(stderr, "[mi_bridge] flash_attn_fwd: could not allocate the padded operands\n");
       return;
     }
-    int st = widen(Q, b.q, rq, head_dim);
-    if (st == MI_OK) st = widen(K, b.k, rk, head_dim);
-    if (st == MI_OK) st = widen(V, b.v, rk, head_dim);
+    int st = widen(Q, b.q, rq, head_dim, kd);
+    if (st == MI_OK) st = widen(K, b.k, rk, head_dim, kd);
+    if (st == MI_OK) st = widen(V, b.v, rk, head_dim, kd);
     if (st == MI_OK)
       st = mi_flash_attn_fwd_scaled(get_stream(), b.q, b.k, b.v, b.o, nullptr, (int64_t)batch,
-                                    (int64_t)n_heads, (int64_t)n_kv, (int64_t)seq_len, 128, 1,
+                                    (int64_t)n_heads, (int64_t)n_kv, (int64_t)seq_len, (int64_t)kd, 1,
                                     MI_ATTN_O_BHTD, (float)(1.0 / std::sqrt((double)head_dim)));
-    if (st == MI_OK) st = narrow(b.o, O, rq, head_dim);
+    if (st == MI_OK) st = narrow(b.o, O, rq, head_dim, kd);
     finish("flash_attn_fwd", st);
     return;
   }
-  if (head_dim != 128 && batch && n_heads && seq_len && head_dim) {
+  if (!kd && batch && n_heads && seq_len && head_dim) {
     if (n_kv == 0 || n_heads % n_kv) {
       finish("flash_attn_fwd", MI_ERR_SHAPE);
       return;
@@ -517,14 +531,15 @@ void fused_attn_bwd(const void* Q, const void* K, const void* V, const void* dO,
     t_status = MI_OK;
     return;
   }
-  if (head_dim < 128 && head_dim % 8 == 0) {
+  const size_t kd = fused_dim(head_dim);
+  if (kd && kd != head_dim) {
     if (n_kv == 0 || n_heads % n_kv) {
       finish("fused_attn_bwd", MI_ERR_SHAPE);
       return;
     }
     const size_t rq = rows, rk = batch * n_kv * seq_len;
     Padded b;
-    if (!padded_buffers(rq, rk, head_dim, true, &b) || !attention_state(256, rows)) {
+    if (!padded_buffers(rq, rk, kd, true, &b) || !attention_state(256, rows)) {
       t_status = MI_ERR_HIP;
       std::fprintf(stderr, "[mi_bridge] fused_attn_bwd: could not allocate the padded operands\n");
       return;
@@ -532,27 +547,27 @@ void fused_attn_bwd(const void* Q, const void* K, const void* V, const void* dO,
     const float scale = (float)(1.0 / std::sqrt((double)head_dim));
     float* lse = t_att_f;
     float* delta = t_att_f + t_att_rows;
-    int st = widen(Q, b.q, rq, head_dim);
-    if (st == MI_OK) st = widen(K, b.k, rk, head_dim);
-    if (st == MI_OK) st = widen(V, b.v, rk, head_dim);
-    if (st == MI_OK) st = widen(dO, b.dout, rq, head_dim);
+    int st = widen(Q, b.q, rq, head_dim, kd);
+    if (st == MI_OK) st = widen(K, b.k, rk, head_dim, kd);
+    if (st == MI_OK) st = widen(V, b.v, rk, head_dim, kd);
+    if (st == MI_OK) st = widen(dO, b.dout, rq, head_dim, kd);
     if (st == MI_OK)
       st = mi_flash_attn_fwd_scaled(get_stream(), b.q, b.k, b.v, b.o, lse, (int64_t)batch, (int64_t)n_heads,
-                                    (int64_t)n_kv, (int64_t)seq_len, 128, 1, MI_ATTN_O_BHTD, scale);
+                                    (int64_t)n_kv, (int64_t)seq_len, (int64_t)kd, 1, MI_ATTN_O_BHTD, scale);
     const size_t ws = mi_flash_attn_bwd_workspace_size((int64_t)batch, (int64_t)n_heads, (int64_t)seq_len);
     const bool have_ws = ws && sp_state(ws);
     if (st == MI_OK)
       st = mi_flash_attn_bwd_scaled(get_stream(), b.q, b.k, b.v, b.o, b.dout, lse, b.dq, b.dk, b.dv, delta,
-                                    (int64_t)batch, (int64_t)n_heads, (int64_t)n_kv, (int64_t)seq_len, 128,
-                                    1, MI_ATTN_O_BHTD, have_ws ? t_sp : nullptr, have_ws ? t_sp_bytes : 0,
-                                    scale);
-    if (st == MI_OK) st = narrow(b.dq, dQ, rq, head_dim);
-    if (st == MI_OK) st = narrow(b.dk, dK, rk, head_dim);
-    if (st == MI_OK) st = narrow(b.dv, dV, rk, head_dim);
+                                    (int64_t)batch, (int64_t)n_heads, (int64_t)n_kv, (int64_t)seq_len,
+                                    (int64_t)kd, 1, MI_ATTN_O_BHTD, have_ws ? t_sp : nullptr,
+                                    have_ws ? t_sp_bytes : 0, scale);
+    if (st == MI_OK) st = narrow(b.dq, dQ, rq, head_dim, kd);
+    if (st == MI_OK) st = narrow(b.dk, dK, rk, head_dim, kd);
+    if (st == MI_OK) st = narrow(b.dv, dV, rk, head_dim, kd);
     finish("fused_attn_bwd", st);
     return;
   }
-  if (head_dim != 128) {
+  if (!kd) {
     if (n_kv == 0 || n_heads % n_kv) {
       finish("fused_attn_bwd", MI_ERR_SHAPE);
       return;

@@ -57,27 +57,56 @@ __device__ __forceinline__ int fa_key_perm(int p) {
   return (p & ~0xC) | ((p & 4) << 1) | ((p & 8) >> 1);
 }
 
+// LDS layout of a [row][d] bf16 tile of 64 rows (a K, V, Q or dO block): rows of
+// ROW bytes in 16-byte chunks, the chunk position XOR-swizzled by the row.  Head
+// dimension 128 (256-byte rows, 16 chunks, four rows per 1 KB DMA block) and 64
+// (128-byte rows, 8 chunks, eight rows per block; the reference kernels' compiled
+// size, flash_attn_fwd.metal:31).  Every swizzle is an involution in the chunk
+// index, so a DMA lane fetches the logical chunk stored at its LDS position with the
+// same function.
 template <int D>
 struct FaTile {
-  static constexpr int ROW = D * 2;            // bytes per key row
+  static_assert(D == 64 || D == 128, "head_dim 64 or 128");
+  static constexpr int ROW = D * 2;            // bytes per row
   static constexpr int NCH = D / 8;            // 16-byte chunks per row
+  static constexpr int RPB = 1024 / ROW;       // rows per 1 KB DMA block
   static constexpr int BYTES = FA_BK * ROW;    // one K or V block
   static constexpr int NBLK = BYTES / 1024;    // 1 KB DMA blocks per block
   static constexpr int NU = NBLK / 4;          // DMA instructions per wave per operand
-  static_assert(NCH == 16, "the LDS swizzles below assume 256-byte key rows (d = 128)");
-  // K tile [key][d]: chunk c of key row r sits at position c ^ (r & 15); the 16
-  // lanes of one ds_read_b128 phase read 16 rows with distinct r & 15.
-  __device__ static __forceinline__ int k_pos(int r, int c) { return c ^ (r & 15); }
-  // V tile [key][d]: chunk q of key row r at position q ^ ((r & 3) << 2); a
-  // transposing read touches 4 consecutive key rows -> 4 distinct 64-byte groups.
-  __device__ static __forceinline__ int v_pos(int r, int q) { return q ^ ((r & 3) << 2); }
-  // Tiles read both ways (backward): chunk c of row r at c ^ f(r), f(r) = (r & 3) << 2
-  // | (r >> 2) & 3.  f is a bijection on r & 15, so the row reads stay conflict
-  // free, and the 4 rows of a transposing read share bits 0-1 of f, so their
-  // 32-byte chunk pairs still land in 4 distinct 64-byte groups.
+  // Tiles read both ways (backward, and every d = 64 tile): chunk c of row r at
+  // c ^ f(r).
+  //   d = 128: f(r) = (r & 3) << 2 | (r >> 2) & 3.  f is a bijection on r & 15, so
+  //     the 16 rows of a row read (16 lanes x 16 bytes) hit 16 distinct chunk
+  //     positions; the 4 rows of a transposing read share bits 0-1 of f, so their
+  //     32-byte chunk pairs still land in 4 distinct 64-byte groups.
+  //   d = 64: a row is half of the 256-byte bank window, so rows r and r + 1 sit in
+  //     opposite halves.  f(r) = ((r >> 1) & 1) << 2 | (r >> 2) & 3: over 16
+  //     consecutive rows of one parity f takes all 8 values (row reads conflict
+  //     free); of the 4 rows of a transposing read (4-aligned), the two of each
+  //     parity differ in bit 2 of f, so their 64-byte segments (one half of the
+  //     row's chunks, 32c .. 32c + 31 of d) land in opposite quarters of the window.
   __device__ static __forceinline__ int x_pos(int r, int c) {
-    return c ^ (((r & 3) << 2) | ((r >> 2) & 3));
+    if constexpr (D == 128) return c ^ (((r & 3) << 2) | ((r >> 2) & 3));
+    else return c ^ ((((r >> 1) & 1) << 2) | ((r >> 2) & 3));
   }
+  // K tile [key][d], read as rows only: d = 128: chunk c of row r at c ^ (r & 15),
+  // the 16 lanes of one ds_read_b128 phase reading 16 rows with distinct r & 15.
+  __device__ static __forceinline__ int k_pos(int r, int c) {
+    if constexpr (D == 128) return c ^ (r & 15);
+    else return x_pos(r, c);
+  }
+  // V tile [key][d], read transposed only, its reads at rows krb + 4t + 16ks addressed
+  // by one base per d block (the swizzle must not change with row bits 2 and up):
+  // d = 128: chunk q of row r at q ^ ((r & 3) << 2), a transposing read touching 4
+  // consecutive rows in 4 distinct 64-byte groups; d = 64: q ^ (((r >> 1) & 1) << 2),
+  // rows r and r + 2 (same half of the bank window) in opposite quarters.
+  __device__ static __forceinline__ int v_pos(int r, int q) {
+    if constexpr (D == 128) return q ^ ((r & 3) << 2);
+    else return q ^ (((r >> 1) & 1) << 2);
+  }
+  // DMA lane `lane` of 1 KB block u: tile row and LDS chunk position.
+  __device__ static __forceinline__ int dma_row(int u, int lane) { return RPB * u + lane / NCH; }
+  __device__ static __forceinline__ int dma_pos(int lane) { return lane % NCH; }
 };
 
 template <int D>
@@ -121,12 +150,12 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2)))
   const int nblk = uniform((kv_end + FA_BK - 1) / FA_BK);
 
   // DMA: wave w moves 1 KB blocks w*NU .. w*NU+NU-1 of the K and of the V block;
-  // lane l of block u covers key row 4u + l/16, LDS chunk position l % 16.
+  // lane l of block u covers key row RPB*u + l/NCH, LDS chunk position l % NCH.
   uint32_t k_off[Tl::NU], v_off[Tl::NU];
 #pragma unroll
   for (int u = 0; u < Tl::NU; ++u) {
     const int blk = wave * Tl::NU + u;
-    const int r = 4 * blk + (lane >> 4), pos = lane & 15;
+    const int r = Tl::dma_row(blk, lane), pos = Tl::dma_pos(lane);
     k_off[u] = (uint32_t)(r * Tl::ROW + 16 * Tl::k_pos(r, pos));  // k_pos is an involution
     v_off[u] = (uint32_t)(r * Tl::ROW + 16 * Tl::v_pos(r, pos));  // so is v_pos
   }
@@ -152,7 +181,8 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2)))
   // Fragment read addresses (stage 0).
   // K: first operand of S, row = key 32kb + perm(l32), d chunk 2s + h32.
   const uint32_t k_rd = (uint32_t)(fa_key_perm(l32) * Tl::ROW);
-  const int k_row_lo = fa_key_perm(l32) & 15;  // r & 15 of both halves' rows
+  // the swizzle of both halves' rows (32kb + perm(l32)) depends on row bits 0-3 only
+  const int k_row = fa_key_perm(l32);
   // V: first operand of P V (rows = d, k = keys) through ds_read_b64_tr_b16: the
   // 16-lane group g reads key rows 8(g>>1) + (j>>2) (+4 for the second read) and
   // d columns 32c + 16(g&1) + 4(j&3) .. +3 and hands lane j the column 32c +
@@ -194,7 +224,7 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2)))
 #pragma unroll
       for (int kb = 0; kb < 2; ++kb) {
         const int c = 2 * s + h32;
-        const uint32_t a = st + k_rd + (uint32_t)(32 * kb * Tl::ROW) + (uint32_t)(16 * (c ^ k_row_lo));
+        const uint32_t a = st + k_rd + (uint32_t)(32 * kb * Tl::ROW) + (uint32_t)(16 * Tl::k_pos(k_row, c));
         kf[s][kb] = *(const lds_u32x4_t*)(uintptr_t)a;
       }
 #pragma unroll
@@ -343,10 +373,9 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2)))
   }
 
   // ---- normalise and store ----
-  // O goes out through LDS so that 16 lanes store one 256-byte row: each wave writes
-  // its 32 x 128 tile to an 8 KB region (16-byte chunk c of row r at c ^ (r & 15):
-  // the 16 rows of a write land in 16 distinct chunks) and reads it back as whole
-  // rows (16 lanes per row, 4 rows per read, all 64 banks per row).  The barrier
+  // O goes out through LDS so that NCH lanes store one whole row: each wave writes
+  // its 32 x d tile to a region in the K tile's layout (k_pos) and reads it back as
+  // whole rows (16 lanes per 256-byte row, or 8 per 128-byte row).  The barrier
   // keeps the regions, which overlap stage 0 of the ring, from other waves' reads of
   // their last block.  (8-byte stores straight from the accumulators: 1-1.5 us
   // slower at configuration 4.)
@@ -359,17 +388,18 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2)))
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
       const int ch = 4 * c + q;  // chunk of d = 32c + 8q + 4*h32 .. +3, half h32
-      const uint32_t a = ob + (uint32_t)(l32 * Tl::ROW + ((ch ^ (l32 & 15)) * 16) + h32 * 8);
+      const uint32_t a = ob + (uint32_t)(l32 * Tl::ROW + Tl::k_pos(l32, ch) * 16 + h32 * 8);
       *(__attribute__((address_space(3))) u32x2_t*)(uintptr_t)a =
           u32x2_t{pack_bf16x2(o[c][4 * q] * inv, o[c][4 * q + 1] * inv),
                   pack_bf16x2(o[c][4 * q + 2] * inv, o[c][4 * q + 3] * inv)};
     }
-  const int oj = lane & 15;
+  // read back as whole rows: NCH lanes per row, 64 / NCH rows per read
+  const int oj = lane % Tl::NCH;
 #pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    const int rr = 4 * i + (lane >> 4);
+  for (int i = 0; i < 32 * Tl::NCH / 64; ++i) {
+    const int rr = (64 / Tl::NCH) * i + lane / Tl::NCH;
     const u32x4_t v = *(const __attribute__((address_space(3))) u32x4_t*)(uintptr_t)(
-        ob + (uint32_t)(rr * Tl::ROW + ((oj ^ (rr & 15)) * 16)));
+        ob + (uint32_t)(rr * Tl::ROW + Tl::k_pos(rr, oj) * 16));
     const int orow_i = qw + rr;
     if (orow_i < T) {
       uint16_t* orow = (uint16_t*)p.O + (p.o_bthd ? ((int64_t)(b * T + orow_i) * p.nH + h) * D
@@ -388,7 +418,7 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2)))
 template <int D>
 struct FaReads {
   uint32_t row_base;  // perm(l32) * ROW
-  int row_lo;         // perm(l32) & 15
+  int row_lo;         // perm(l32): x_pos of rows 32*half + perm(l32) depends on bits 0-3
   // transposing-read bases for the rows krb (first read) and krb + 4 (second): the
   // swizzle depends on row bits 2-3, so the two reads need their own base
   uint32_t tr[D / 32][2];
@@ -396,7 +426,7 @@ struct FaReads {
     using Tl = FaTile<D>;
     const int l32 = lane & 31;
     row_base = (uint32_t)(fa_key_perm(l32) * Tl::ROW);
-    row_lo = fa_key_perm(l32) & 15;
+    row_lo = fa_key_perm(l32);
     const int g = lane >> 4, jj = lane & 15;
     const int krb = 8 * (g >> 1) + (jj >> 2);
 #pragma unroll
@@ -413,9 +443,8 @@ struct FaReads {
   __device__ __forceinline__ u32x4_t row(uint32_t t, int half, int s, int h32) const {
     using Tl = FaTile<D>;
     const int c = 2 * s + h32;
-    // rows 32*half + perm(l32): (r & 15) is row_lo for both halves
-    const uint32_t a = t + row_base + (uint32_t)(32 * half * Tl::ROW) +
-                       (uint32_t)(16 * (c ^ (((row_lo & 3) << 2) | ((row_lo >> 2) & 3))));
+    // rows 32*half + perm(l32): the swizzle is row_lo's for both halves
+    const uint32_t a = t + row_base + (uint32_t)(32 * half * Tl::ROW) + (uint32_t)(16 * Tl::x_pos(row_lo, c));
     return *(const lds_u32x4_t*)(uintptr_t)a;
   }
 };
@@ -447,13 +476,13 @@ __device__ __forceinline__ void fa_lds_fence() {
   __builtin_amdgcn_sched_barrier(0);
 }
 
-// One 16-byte DMA of a [row][d] tile: lane l of 1 KB block u covers row 4u + l/16,
-// LDS position l % 16 (dual swizzle), reading row `r` of a matrix whose rows are
-// `stride` bytes apart.
+// One 16-byte DMA of a [row][d] tile: lane l of 1 KB block u covers row RPB*u +
+// l/NCH, LDS position l % NCH (dual swizzle), reading row `r` of a matrix whose rows
+// are `stride` bytes apart.
 template <int D>
 __device__ __forceinline__ uint32_t fa_dma_off(int u, int lane, int stride) {
   using Tl = FaTile<D>;
-  const int r = 4 * u + (lane >> 4), pos = lane & 15;
+  const int r = Tl::dma_row(u, lane), pos = Tl::dma_pos(lane);
   return (uint32_t)(r * stride + 16 * Tl::x_pos(r, pos));  // x_pos is an involution in c
 }
 
@@ -662,7 +691,7 @@ __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2)))
   constexpr int NUK = KVB / 1024 / 8;                // ... per 128-key tile
   constexpr int STAGE = 2 * Tl::BYTES + 2 * QT * 4;  // Q, dO, lse, D
   constexpr int RING = 2 * KVB;                      // the ring follows K and V
-  static_assert(NS == 8 && NC == 4, "d = 128");
+  static_assert(NU >= 1 && NUK >= 1, "whole DMA blocks per wave");
   __shared__ __attribute__((aligned(16))) char smem[RING + 2 * STAGE];
   const uint32_t lds0 = lds_addr(smem);
   const uint32_t lk = lds0, lv = lds0 + KVB, lr = lds0 + RING;
@@ -979,24 +1008,28 @@ __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2)))
   else write(dv, 1, pk ? pk + 128 * D : nullptr, (uint16_t*)p.dV + obase, 1.0f);
 }
 
-// D = rowsum(dO * O), read by both backward forms.  Coalesced: the 16 lanes of a lane
-// group read one 256-byte row (16 bytes each), a wave 4 rows per load and 32 rows in
-// all, 8 loads of dO and 8 of O in flight per lane.  Each lane sums its 8 products
-// in order, then the group adds its 16 partial sums by a butterfly (lane distance 8,
-// 4, 2, 1), which leaves every lane of the group the same total; lane i of the group
-// keeps row i's.
+// D = rowsum(dO * O), read by both backward forms.  Coalesced: the LPR = d/8 lanes of
+// a lane group read one row (16 bytes each: 16 lanes per 256-byte row at d = 128, 8
+// per 128-byte row at d = 64), a wave 64/LPR rows per load and 32 rows in all, NL =
+// 32 LPR / 64 loads of dO and of O in flight per lane.  Each lane sums its products
+// in order, then the group adds its LPR partial sums by a butterfly (lane distance
+// LPR/2 .. 1), which leaves every lane of the group the same total; lane i of the
+// group keeps the total of its load i.
 template <int D>
 __global__ void __launch_bounds__(256) flash_bwd_delta_kernel(FbParams p) {
-  static_assert(D == 128, "16 lanes of 16 bytes per row");
+  constexpr int LPR = D / 8;           // lanes per row
+  constexpr int RPL = 64 / LPR;        // rows per load
   constexpr int RPW = 32;              // rows per wave
+  constexpr int NL = RPW / RPL;        // loads per lane
+  static_assert(NL <= LPR, "a lane keeps at most one total");
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int sub = lane & 15, grp = lane >> 4;
+  const int sub = lane % LPR, grp = lane / LPR;
   const int64_t rows = (int64_t)p.B * p.nH * p.T;
   const int64_t r0 = (int64_t)blockIdx.x * 128 + wave * RPW;  // first row of the wave
-  u32x4_t gf[8], of[8];
+  u32x4_t gf[NL], of[NL];
 #pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    const int64_t r = r0 + 4 * i + grp;  // row of [B, nH, T]
+  for (int i = 0; i < NL; ++i) {
+    const int64_t r = r0 + RPL * i + grp;  // row of [B, nH, T]
     if (r < rows) {
       const int64_t bh = r / p.T, t = r - bh * p.T;
       const int64_t b = bh / p.nH, h = bh - b * p.nH;
@@ -1009,18 +1042,18 @@ __global__ void __launch_bounds__(256) flash_bwd_delta_kernel(FbParams p) {
   }
   float mine = 0.0f;
 #pragma unroll
-  for (int i = 0; i < 8; ++i) {
+  for (int i = 0; i < NL; ++i) {
     float part = 0.0f;
 #pragma unroll
     for (int w2 = 0; w2 < 4; ++w2)
       part += bf16_bits_to_f32(gf[i][w2] & 0xffffu) * bf16_bits_to_f32(of[i][w2] & 0xffffu) +
               bf16_bits_to_f32(gf[i][w2] >> 16) * bf16_bits_to_f32(of[i][w2] >> 16);
 #pragma unroll
-    for (int m = 8; m >= 1; m >>= 1) part += __shfl_xor(part, m, 64);
+    for (int m = LPR / 2; m >= 1; m >>= 1) part += __shfl_xor(part, m, 64);
     if (sub == i) mine = part;
   }
-  const int64_t r = r0 + 4 * sub + grp;
-  if (sub < 8 && r < rows) p.delta[r] = mine;
+  const int64_t r = r0 + RPL * sub + grp;
+  if (sub < NL && r < rows) p.delta[r] = mine;
 }
 
 // dK and dV of the key blocks the schedule cut into several units: the units'
@@ -1063,12 +1096,12 @@ __global__ void __launch_bounds__(256) flash_bwd_dkdv_reduce_kernel(FbParams p) 
 // frees up first packs them (longest-processing-time-first).  When the partials of
 // the cut blocks do not fit the room given, W grows by half until they do; when the
 // tables do not fit the kernel arguments, n_units stays 0.
-void plan_dkdv_schedule(FbParams& p) {
+void plan_dkdv_schedule(FbParams& p, int head_dim) {
   p.n_units = p.n_slots = p.n_split = 0;
   if (!p.dsT || !p.part || p.cus <= 0) return;
   const int NKB = p.k_blocks, nqt = (p.T + FA_BK - 1) / FA_BK;
   const int64_t BKV = (int64_t)p.B * p.nKV;
-  const size_t slot_bytes = (size_t)BKV * 2 * 128 * 128 * sizeof(float);
+  const size_t slot_bytes = (size_t)BKV * 2 * 128 * (size_t)head_dim * sizeof(float);
   std::vector<int> w(NKB);
   int64_t sum = 0;
   for (int k = 0; k < NKB; ++k) {
@@ -1120,35 +1153,41 @@ size_t flash_bwd_partial_bytes(int64_t B, int64_t nH, int64_t T) {
   return (size_t)B * (size_t)nH * (size_t)T * 128 * sizeof(float);
 }
 
-hipError_t launch_flash_bwd(const FbParams& p_in, int head_dim, hipStream_t stream) {
-  if (head_dim != 128) return hipErrorInvalidValue;
-  FbParams p = p_in;
-  plan_dkdv_schedule(p);
+template <int D>
+hipError_t launch_flash_bwd_d(FbParams& p, hipStream_t stream) {
+  plan_dkdv_schedule(p, D);
   // D first (both kernels after it read it); then, without the dS^T workspace, the dQ
   // kernel.  With it the dK/dV kernel writes dS^T and the caller runs dQ = scale * dS K.
   const int64_t rows = (int64_t)p.B * p.nH * p.T;
-  hipLaunchKernelGGL(flash_bwd_delta_kernel<128>, dim3((unsigned)((rows + 127) / 128)), dim3(256), 0,
+  hipLaunchKernelGGL(flash_bwd_delta_kernel<D>, dim3((unsigned)((rows + 127) / 128)), dim3(256), 0,
                      stream, p);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
   if (!p.dsT) {
     const int64_t nq = (int64_t)p.B * p.nH * p.q_blocks;
-    hipLaunchKernelGGL(flash_bwd_dq_kernel<128>, dim3((unsigned)nq), dim3(256), 0, stream, p);
+    hipLaunchKernelGGL(flash_bwd_dq_kernel<D>, dim3((unsigned)nq), dim3(256), 0, stream, p);
     e = hipGetLastError();
     if (e != hipSuccess) return e;
   }
   const int64_t nk = (int64_t)p.B * p.nKV * (p.n_units ? p.n_units : p.k_blocks);
   if (p.dsT)
-    hipLaunchKernelGGL((flash_bwd_dkdv_kernel<128, true>), dim3((unsigned)nk), dim3(512), 0, stream, p);
+    hipLaunchKernelGGL((flash_bwd_dkdv_kernel<D, true>), dim3((unsigned)nk), dim3(512), 0, stream, p);
   else
-    hipLaunchKernelGGL((flash_bwd_dkdv_kernel<128, false>), dim3((unsigned)nk), dim3(512), 0, stream, p);
+    hipLaunchKernelGGL((flash_bwd_dkdv_kernel<D, false>), dim3((unsigned)nk), dim3(512), 0, stream, p);
   if (!p.n_split) return hipGetLastError();
   e = hipGetLastError();
   if (e != hipSuccess) return e;
-  const int64_t quads = (int64_t)p.n_split * p.B * p.nKV * 128 * (128 / 4);
-  hipLaunchKernelGGL(flash_bwd_dkdv_reduce_kernel<128>, dim3((unsigned)((quads + 255) / 256)), dim3(256), 0,
+  const int64_t quads = (int64_t)p.n_split * p.B * p.nKV * 128 * (D / 4);
+  hipLaunchKernelGGL(flash_bwd_dkdv_reduce_kernel<D>, dim3((unsigned)((quads + 255) / 256)), dim3(256), 0,
                      stream, p);
   return hipGetLastError();
+}
+
+hipError_t launch_flash_bwd(const FbParams& p_in, int head_dim, hipStream_t stream) {
+  FbParams p = p_in;
+  if (head_dim == 128) return launch_flash_bwd_d<128>(p, stream);
+  if (head_dim == 64) return launch_flash_bwd_d<64>(p, stream);
+  return hipErrorInvalidValue;
 }
 
 int flash_bwd_key_blocks(int T) { return (T + 127) / 128; }
@@ -1157,6 +1196,8 @@ hipError_t launch_flash_fwd(const FaParams& p, int head_dim, hipStream_t stream)
   const int64_t n = (int64_t)p.B * p.nH * p.q_blocks;
   if (head_dim == 128)
     hipLaunchKernelGGL(flash_fwd_kernel<128>, dim3((unsigned)n), dim3(256), 0, stream, p);
+  else if (head_dim == 64)
+    hipLaunchKernelGGL(flash_fwd_kernel<64>, dim3((unsigned)n), dim3(256), 0, stream, p);
   else
     return hipErrorInvalidValue;
   return hipGetLastError();

@@ -65,11 +65,11 @@ int flash_bwd_key_blocks(int T);
 // Bytes of fp32 dK / dV partials the balanced dK/dV schedule may need (dS^T form).
 size_t flash_bwd_partial_bytes(int64_t B, int64_t nH, int64_t T);
 
-// Launch the backward kernels (head_dim 128) on `stream`: dQ and D, then dK / dV
+// Launch the backward kernels (head_dim 64 or 128) on `stream`: dQ and D, then dK / dV
 // (and, with a balanced schedule, the reduction of the partials).
 hipError_t launch_flash_bwd(const FbParams& p, int head_dim, hipStream_t stream);
 
-// Launch the forward kernel (head_dim 128) on `stream`.
+// Launch the forward kernel (head_dim 64 or 128) on `stream`.
 hipError_t launch_flash_fwd(const FaParams& p, int head_dim, hipStream_t stream);
 
 }  // namespace mig

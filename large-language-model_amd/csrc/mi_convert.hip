@@ -304,7 +304,48 @@ __global__ void __launch_bounds__(256) convert_copy_kernel(ConvParams p) {
   }
 }
 
+// rows x cols bf16 -> rows x dst_cols bf16 (dst_cols >= cols, both multiples of 8), the
+// columns past cols written as zeros: one thread per 8-element chunk of a destination
+// row; VEC: 16-byte source loads (source base and row pitch 16-byte aligned).
+template <bool VEC>
+__global__ void __launch_bounds__(256) pad_rows_kernel(const uint16_t* src, int64_t src_ld, int64_t rows,
+                                                       int64_t cols, uint16_t* dst, int64_t dst_cols) {
+  const int64_t cpr = dst_cols / 8;
+  const int64_t n = rows * cpr;
+  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (int64_t)gridDim.x * 256) {
+    const int64_t r = i / cpr, c = (i - r * cpr) * 8;
+    u32x4_t v = {0u, 0u, 0u, 0u};
+    if (c < cols) {
+      const uint16_t* s = src + r * src_ld + c;
+      if constexpr (VEC) {
+        v = *(const u32x4_t*)s;
+      } else {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) v[e] = (uint32_t)s[2 * e] | ((uint32_t)s[2 * e + 1] << 16);
+      }
+    }
+    *(u32x4_t*)(dst + r * dst_cols + c) = v;
+  }
+}
+
 }  // namespace
+
+hipError_t launch_pad_rows(const void* src, int64_t src_ld, int64_t rows, int64_t cols, void* dst,
+                           int64_t dst_cols, int cus, hipStream_t stream) {
+  if (rows <= 0) return hipSuccess;
+  if (cols % 8 || dst_cols % 8 || cols > dst_cols || src_ld < cols || ((uintptr_t)dst & 15u))
+    return hipErrorInvalidValue;
+  const int64_t n = rows * (dst_cols / 8);
+  const int64_t grid = std::min<int64_t>((n + 255) / 256, 8 * (int64_t)(cus > 0 ? cus : 256));
+  const bool vec = ((uintptr_t)src & 15u) == 0 && src_ld % 8 == 0;
+  if (vec)
+    hipLaunchKernelGGL(pad_rows_kernel<true>, dim3((unsigned)grid), dim3(256), 0, stream, (const uint16_t*)src,
+                       src_ld, rows, cols, (uint16_t*)dst, dst_cols);
+  else
+    hipLaunchKernelGGL(pad_rows_kernel<false>, dim3((unsigned)grid), dim3(256), 0, stream,
+                       (const uint16_t*)src, src_ld, rows, cols, (uint16_t*)dst, dst_cols);
+  return hipGetLastError();
+}
 
 hipError_t launch_convert(const ConvParams& p, bool transpose, int cus, hipStream_t stream) {
   const int ses = p.src_dtype == 0 ? 4 : 2, des = p.dst_dtype == 0 ? 4 : 2;

@@ -26,4 +26,10 @@ hipError_t launch_convert(const ConvParams& p, bool transpose, int cus, hipStrea
 hipError_t launch_convert_batch(const ConvParams* jobs, const int* transpose, int64_t n,
                                 hipStream_t stream);
 
+// Internal (the C++ bridge's padded attention operands): rows x cols bf16 from `src`
+// (row pitch src_ld elements) into rows of dst_cols elements at `dst` (16-byte
+// aligned), columns cols .. dst_cols-1 set to zero.  cols and dst_cols multiples of 8.
+hipError_t launch_pad_rows(const void* src, int64_t src_ld, int64_t rows, int64_t cols, void* dst,
+                           int64_t dst_cols, int cus, hipStream_t stream);
+
 }  // namespace mig

@@ -911,8 +911,8 @@ int mi_flash_attn_fwd_scaled(void* stream, const void* Q, const void* K, const v
   if (n_kv <= 0 || n_heads % n_kv != 0)
     return fail(MI_ERR_SHAPE, "n_heads=%lld is not a multiple of n_kv=%lld", (long long)n_heads,
                 (long long)n_kv);
-  if (head_dim != 128)
-    return fail(MI_ERR_UNSUPPORTED, "flash attention supports head_dim 128 (got %lld)",
+  if (head_dim != 128 && head_dim != 64)
+    return fail(MI_ERR_UNSUPPORTED, "flash attention supports head_dim 64 and 128 (got %lld)",
                 (long long)head_dim);
   if (o_layout != MI_ATTN_O_BHTD && o_layout != MI_ATTN_O_BTHD)
     return fail(MI_ERR_SHAPE, "unknown output layout %d", o_layout);
@@ -973,8 +973,8 @@ int mi_flash_attn_bwd_scaled(void* stream, const void* Q, const void* K, const v
   if (n_kv <= 0 || n_heads % n_kv != 0)
     return fail(MI_ERR_SHAPE, "n_heads=%lld is not a multiple of n_kv=%lld", (long long)n_heads,
                 (long long)n_kv);
-  if (head_dim != 128)
-    return fail(MI_ERR_UNSUPPORTED, "flash attention supports head_dim 128 (got %lld)",
+  if (head_dim != 128 && head_dim != 64)
+    return fail(MI_ERR_UNSUPPORTED, "flash attention supports head_dim 64 and 128 (got %lld)",
                 (long long)head_dim);
   if (o_layout != MI_ATTN_O_BHTD && o_layout != MI_ATTN_O_BTHD)
     return fail(MI_ERR_SHAPE, "unknown output layout %d", o_layout);

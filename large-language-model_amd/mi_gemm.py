@@ -568,6 +568,15 @@ def attention_forward(Q4, K4, V4, out_dtype=None):
     return O, S
 
 
+def flash_kernel_dim(d):
+    """Head dimension of the fused kernels that run head_dim d: 64 (the reference kernels'
+    compiled size, flash_attn_fwd.metal:31) and 128 natively; another multiple of 8 below
+    128 on operands padded with zero columns to the next of them; 0 otherwise."""
+    if d <= 0 or d % 8 or d > 128:
+        return 0
+    return 64 if d <= 64 else 128
+
+
 def flash_attn_fwd(Q4, K4, V4, O=None, lse=None, causal=True, layout="bthd", sync=None):
     """Fused forward (metal_bridge::flash_attn_fwd, MetalBridge.hpp:49-51; Attention.cpp:236-280):
     Q4 [B,nH,T,d], K4/V4 [B,nKV,T,d] bf16 -> O [B,T,nH*d] (layout "bthd", the CPU path's)
@@ -579,14 +588,15 @@ def flash_attn_fwd(Q4, K4, V4, O=None, lse=None, causal=True, layout="bthd", syn
     for t in (Q4, K4, V4):
         if t.dtype != torch.bfloat16 or not t.is_contiguous():
             raise ValueError("Q, K, V must be contiguous bf16 tensors")
-    if d < 128 and d % 8 == 0:
-        # the d = 128 kernels on rows padded with zero columns, at the scale of d
-        pad = lambda t: torch.nn.functional.pad(t, (0, 128 - d)).contiguous()
+    kd = flash_kernel_dim(d)
+    if kd and kd != d:
+        # the next larger kernel on rows padded with zero columns, at the scale of d
+        pad = lambda t: torch.nn.functional.pad(t, (0, kd - d)).contiguous()
         Qp, Kp, Vp = pad(Q4), pad(K4), pad(V4)  # held until the kernel has been queued
-        Op = torch.empty((Bn, nH, T, 128), dtype=torch.bfloat16, device=Q4.device)
+        Op = torch.empty((Bn, nH, T, kd), dtype=torch.bfloat16, device=Q4.device)
         st = load_library().mi_flash_attn_fwd_scaled(
             _stream(), _ptr(Qp), _ptr(Kp), _ptr(Vp), _ptr(Op), _ptr(lse), Bn, nH, nKV, T,
-            128, int(bool(causal)), MI_ATTN_O_BHTD, 1.0 / math.sqrt(d))
+            kd, int(bool(causal)), MI_ATTN_O_BHTD, 1.0 / math.sqrt(d))
         _check("mi_flash_attn_fwd_scaled", st)
         res = Op[..., :d]
         res = res.permute(0, 2, 1, 3).reshape(Bn, T, nH * d) if layout == "bthd" else res
@@ -622,15 +632,16 @@ def flash_attn_bwd(Q4, K4, V4, O, dO, lse, causal=True, layout="bthd", sync=None
     for t in (Q4, K4, V4, O, dO):
         if t.dtype != torch.bfloat16 or not t.is_contiguous():
             raise ValueError("Q, K, V, O, dO must be contiguous bf16 tensors")
-    if d < 128 and d % 8 == 0:
-        # the d = 128 kernels on rows padded with zero columns, at the scale of d
-        pad = lambda t: torch.nn.functional.pad(t, (0, 128 - d)).contiguous()
+    kd = flash_kernel_dim(d)
+    if kd and kd != d:
+        # the next larger kernels on rows padded with zero columns, at the scale of d
+        pad = lambda t: torch.nn.functional.pad(t, (0, kd - d)).contiguous()
         if layout == "bthd":
-            padl = lambda t: pad(t.reshape(Bn, T, nH, d)).reshape(Bn, T, nH * 128)
+            padl = lambda t: pad(t.reshape(Bn, T, nH, d)).reshape(Bn, T, nH * kd)
         else:
             padl = pad
-        dQp = torch.empty((Bn, nH, T, 128), dtype=torch.bfloat16, device=Q4.device)
-        dKp = torch.empty((Bn, nKV, T, 128), dtype=torch.bfloat16, device=Q4.device)
+        dQp = torch.empty((Bn, nH, T, kd), dtype=torch.bfloat16, device=Q4.device)
+        dKp = torch.empty((Bn, nKV, T, kd), dtype=torch.bfloat16, device=Q4.device)
         dVp = torch.empty_like(dKp)
         delta = torch.empty((Bn, nH, T), dtype=torch.float32, device=Q4.device)
         code = MI_ATTN_O_BTHD if layout == "bthd" else MI_ATTN_O_BHTD
@@ -641,7 +652,7 @@ def flash_attn_bwd(Q4, K4, V4, O, dO, lse, causal=True, layout="bthd", sync=None
         Qp, Kp, Vp, Op, dOp = pad(Q4), pad(K4), pad(V4), padl(O), padl(dO)  # held until queued
         st = load_library().mi_flash_attn_bwd_scaled(
             _stream(), _ptr(Qp), _ptr(Kp), _ptr(Vp), _ptr(Op), _ptr(dOp), _ptr(lse),
-            _ptr(dQp), _ptr(dKp), _ptr(dVp), _ptr(delta), Bn, nH, nKV, T, 128, int(bool(causal)), code,
+            _ptr(dQp), _ptr(dKp), _ptr(dVp), _ptr(delta), Bn, nH, nKV, T, kd, int(bool(causal)), code,
             _ptr(workspace), ws_bytes, 1.0 / math.sqrt(d))
         _check("mi_flash_attn_bwd_scaled", st)
         out = (dQp[..., :d].contiguous(), dKp[..., :d].contiguous(), dVp[..., :d].contiguous())

@@ -17,6 +17,16 @@
 
 #include "gemm_bridge.hpp"
 
+// The CPU oracle (oracle/mi_oracle.c, test infrastructure): the reference's attention
+// forward and backward in float64 (Attention.cpp:236-348).  O and dO are [B,T,nH*d].
+extern "C" {
+void mo_attention_fwd(int64_t Bn, int64_t nH, int64_t nKV, int64_t T, int64_t d, const float* Q4,
+                      const float* K4, const float* V4, double* O, double* P);
+void mo_attention_bwd(int64_t Bn, int64_t nH, int64_t nKV, int64_t T, int64_t d, const float* Q4,
+                      const float* K4, const float* V4, const float* dO, double* dQ, double* dK,
+                      double* dV);
+}
+
 static int g_total = 0, g_passed = 0;
 
 static void row(const char* id, const char* what, bool pass, const std::string& detail = "") {
@@ -247,8 +257,8 @@ int main() {
   // flash_attn_fwd / fused_attn_bwd with Q = 0 (closed forms): every visible key gets
   // P = 1/(q+1), so O[q] = mean(V[0..q]), dV[k] = sum_{q>=k} dO[q] / (q+1), dK = 0
   // (dK = scale dS^T Q), dQ[q] = scale sum_{k<=q} dS[q,k] K[k] with dS = P (dP - rowsum(P dP)).
-  // head_dim 128 runs the fused kernels (GB-11, GB-12); 64, the reference kernel's, the
-  // fused kernels on zero-padded rows (GB-16, GB-17).
+  // head_dim 128 (GB-11, GB-12) and 64, the reference kernel's (GB-16, GB-17), both run
+  // the fused kernels.
   for (size_t d : {128, 64}) {
     const size_t B = 1, nH = 2, nKV = 1, T = 96, g = nH / nKV;
     const bool fused = d == 128;
@@ -278,7 +288,7 @@ int main() {
         }
     row(fused ? "GB-11" : "GB-16",
         fused ? "flash_attn_fwd, Q = 0: O[q] = mean(V[0..q]), max rel <= 1e-2"
-              : "flash_attn_fwd d=64 (fused on zero-padded rows), Q = 0: O[q] = mean(V[0..q]), <= 1e-2",
+              : "flash_attn_fwd d=64 (fused), Q = 0: O[q] = mean(V[0..q]), <= 1e-2",
         ok && err <= 1e-2 * mx, std::to_string(err / mx));
     mi_bridge::fused_attn_bwd(dq_in, dk_in, dv_in, dgo, dQg, dKg, dVg, B, nH, nKV, T, d);
     ok = mi_bridge::last_status() == MI_OK;
@@ -315,7 +325,7 @@ int main() {
     const double edv = rel(rdv, hdv), edq = rel(rdq, hdq);
     row(fused ? "GB-12" : "GB-17",
         fused ? "fused_attn_bwd, Q = 0: dV, dQ closed forms (1e-2), dK = 0"
-              : "fused_attn_bwd d=64 (fused on zero-padded rows), Q = 0: dV, dQ closed forms, dK = 0",
+              : "fused_attn_bwd d=64 (fused), Q = 0: dV, dQ closed forms, dK = 0",
         ok && edv <= 1e-2 && edq <= 1e-2 && dk_zero,
         std::to_string(edv) + " " + std::to_string(edq));
     dfree(dq_in); dfree(dk_in); dfree(dv_in); dfree(dgo); dfree(dO_out);
@@ -528,6 +538,82 @@ int main() {
     dfree(B);
     dfree(C);
     dfree(D);
+  }
+  {  // GB-19: flash_attn_fwd / fused_attn_bwd with random bf16 Q, K, V, dO against the
+     // oracle: head_dim 64 (the reference kernel's size, fused natively), 32 and 96 (fused
+     // kernels of 64 and 128 on the bridge's zero-padded copies).  Each head_dim runs two
+     // shapes in a row, so the second call re-carves the bridge's pools the first left.
+    struct Shape { size_t B, nH, nKV, T; };
+    const Shape shapes[2] = {{1, 4, 2, 160}, {2, 2, 1, 96}};
+    uint32_t seed = 12345u;
+    auto rnd = [&](size_t n, float sc) {  // bf16-exact values, uniform in [-sc, sc)
+      std::vector<float> v(n);
+      for (auto& x : v) {
+        seed = seed * 1664525u + 1013904223u;
+        x = fb(bf(sc * ((float)(seed >> 8) / 8388608.0f - 1.0f)));
+      }
+      return v;
+    };
+    auto to_bf = [](const std::vector<float>& v) {
+      std::vector<uint16_t> h(v.size());
+      for (size_t i = 0; i < v.size(); ++i) h[i] = bf(v[i]);
+      return h;
+    };
+    for (size_t d : {64, 32, 96}) {
+      bool ok = true;
+      double worst = 0;
+      for (const Shape& sh : shapes) {
+        const size_t nq = sh.B * sh.nH * sh.T * d, nk = sh.B * sh.nKV * sh.T * d;
+        const auto q = rnd(nq, 2.0f), k = rnd(nk, 2.0f), v = rnd(nk, 1.0f), g4 = rnd(nq, 0.5f);
+        // dO for the oracle: [B,T,nH*d] from the bridge's [B,nH,T,d]
+        std::vector<float> gt(nq);
+        for (size_t b = 0; b < sh.B; ++b)
+          for (size_t h = 0; h < sh.nH; ++h)
+            for (size_t t = 0; t < sh.T; ++t)
+              for (size_t c = 0; c < d; ++c)
+                gt[((b * sh.T + t) * sh.nH + h) * d + c] = g4[((b * sh.nH + h) * sh.T + t) * d + c];
+        std::vector<double> O(nq), dQ(nq), dK(nk), dV(nk);
+        mo_attention_fwd(sh.B, sh.nH, sh.nKV, sh.T, d, q.data(), k.data(), v.data(), O.data(), nullptr);
+        mo_attention_bwd(sh.B, sh.nH, sh.nKV, sh.T, d, q.data(), k.data(), v.data(), gt.data(), dQ.data(),
+                         dK.data(), dV.data());
+        uint16_t *Qd = dev(to_bf(q)), *Kd = dev(to_bf(k)), *Vd = dev(to_bf(v)), *Gd = dev(to_bf(g4));
+        uint16_t* Od = dev(std::vector<uint16_t>(nq, 0));
+        uint16_t *dQd = dev(std::vector<uint16_t>(nq, 0)), *dKd = dev(std::vector<uint16_t>(nk, 0)),
+                 *dVd = dev(std::vector<uint16_t>(nk, 0));
+        mi_bridge::flash_attn_fwd(Qd, Kd, Vd, Od, sh.B, sh.nH, sh.nKV, sh.T, d);
+        ok = ok && mi_bridge::last_status() == MI_OK;
+        mi_bridge::fused_attn_bwd(Qd, Kd, Vd, Gd, dQd, dKd, dVd, sh.B, sh.nH, sh.nKV, sh.T, d);
+        ok = ok && mi_bridge::last_status() == MI_OK;
+        const auto ho = host(Od, nq), hq = host(dQd, nq), hk = host(dKd, nk), hv = host(dVd, nk);
+        // bridge O is [B,nH,T,d]; the oracle's [B,T,nH*d]
+        double m = 0, e = 0;
+        for (size_t b = 0; b < sh.B; ++b)
+          for (size_t h = 0; h < sh.nH; ++h)
+            for (size_t t = 0; t < sh.T; ++t)
+              for (size_t c = 0; c < d; ++c) {
+                const double ref = O[((b * sh.T + t) * sh.nH + h) * d + c];
+                m = std::fmax(m, std::fabs(ref));
+                e = std::fmax(e, std::fabs(ref - fb(ho[((b * sh.nH + h) * sh.T + t) * d + c])));
+              }
+        auto rel = [](const std::vector<double>& ref, const std::vector<uint16_t>& got) {
+          double mm = 0, ee = 0;
+          for (size_t i = 0; i < ref.size(); ++i) {
+            mm = std::fmax(mm, std::fabs(ref[i]));
+            ee = std::fmax(ee, std::fabs(ref[i] - fb(got[i])));
+          }
+          return mm > 0 ? ee / mm : ee;
+        };
+        const double errs[4] = {m > 0 ? e / m : e, rel(dQ, hq), rel(dK, hk), rel(dV, hv)};
+        for (double x : errs) {
+          worst = std::fmax(worst, x);
+          ok = ok && std::isfinite(x) && x <= 1e-2;
+        }
+        dfree(Qd); dfree(Kd); dfree(Vd); dfree(Gd); dfree(Od); dfree(dQd); dfree(dKd); dfree(dVd);
+      }
+      const std::string what = "flash_attn_fwd + fused_attn_bwd d=" + std::to_string(d) +
+                               (d == 64 ? " (native)" : " (padded)") + ", random, 2 shapes, <= 1e-2";
+      row("GB-19", what.c_str(), ok, std::to_string(worst));
+    }
   }
   std::printf("%d/%d checks passed\n", g_passed, g_total);
   return g_passed == g_total ? 0 : 1;

@@ -120,7 +120,7 @@ def test_aux_validation(mi):
     fb = lib.mi_flash_attn_bwd
     assert fb(None, *([None] * 10), 0, 4, 2, 64, 128, 1, 1, None, 0) == 0        # empty batch
     assert fb(None, *([p16] * 9), None, 1, 4, 2, 64, 128, 1, 1, None, 0) == 3    # delta NULL
-    assert fb(None, *([p16] * 10), 1, 4, 2, 64, 64, 1, 1, None, 0) == 5          # head_dim 64
+    assert fb(None, *([p16] * 10), 1, 4, 2, 64, 96, 1, 1, None, 0) == 5          # head_dim 96
     # dS^T (bf16), then the fp32 partials of the balanced dK/dV units (128 floats per row)
     assert lib.mi_flash_attn_bwd_workspace_size(8, 16, 1024) == 8 * 16 * 1024 * (1024 * 2 + 512)
     assert lib.mi_flash_attn_bwd_workspace_size(1, 4, 300) == 0                   # T % 8 != 0

@@ -118,14 +118,15 @@ def _dense_attention(q, k, v, causal):
     return o, lse
 
 
+@pytest.mark.parametrize("d", [128, 64])
 @pytest.mark.parametrize("Bn,nH,nKV,T", [(2, 16, 4, 256), (1, 4, 2, 300), (1, 2, 1, 64),
                                          (1, 4, 4, 520)])
-def test_flash_forward(mi, dev, oracle, Bn, nH, nKV, T):
+def test_flash_forward(mi, dev, oracle, Bn, nH, nKV, T, d):
     """Fused forward vs the oracle (causal, Attention.cpp:236-280) in both output layouts,
-    and the row log-sum-exp vs its closed form."""
+    and the row log-sum-exp vs its closed form; head_dim 128 and 64 (the reference kernel's
+    compiled size, flash_attn_fwd.metal:31), both native kernels."""
     import torch
 
-    d = 128
     q, k, v, _ = _qkv(oracle, Bn, nH, nKV, T, d, 1300 + T)
     Q, K, V = (to_dev(x, dev, True) for x in (q, k, v))
     lse = torch.empty((Bn, nH, T), dtype=torch.float32, device=dev)
@@ -139,9 +140,10 @@ def test_flash_forward(mi, dev, oracle, Bn, nH, nKV, T):
     assert err < 1e-3, f"lse max abs err {err:.3e}"
 
 
-def test_flash_forward_noncausal(mi, dev, oracle):
+@pytest.mark.parametrize("d", [128, 64])
+def test_flash_forward_noncausal(mi, dev, oracle, d):
     """causal = 0 attends to every key, including the zero-padded tail block (T % 64 != 0)."""
-    d, Bn, nH, nKV, T = 128, 1, 4, 2, 200
+    Bn, nH, nKV, T = 1, 4, 2, 200
     q, k, v, _ = _qkv(oracle, Bn, nH, nKV, T, d, 1700)
     Q, K, V = (to_dev(x, dev, True) for x in (q, k, v))
     O = mi.flash_attn_fwd(Q, K, V, causal=False, layout="bhtd")
@@ -163,22 +165,23 @@ def test_flash_forward_config4(mi, dev, oracle):
         check(O[sl], oracle.attention_fwd(q[sl], k[sl], v[sl]), TOL_BF16, f"O[{b}]")
 
 
+@pytest.mark.parametrize("d", [128, 64])
 @pytest.mark.parametrize("ws", ["auto", None])
 @pytest.mark.parametrize("Bn,nH,nKV,T", [(2, 16, 4, 256), (1, 4, 2, 300), (1, 2, 1, 64),
                                          (1, 4, 4, 520), (1, 2, 1, 130), (2, 4, 1, 200)])
-def test_flash_backward(mi, dev, oracle, Bn, nH, nKV, T, ws):
+def test_flash_backward(mi, dev, oracle, Bn, nH, nKV, T, ws, d):
     """Fused backward vs the oracle (Attention.cpp:292-348: dV = P^T dO, dS = P (dP - rowsum),
     dQ = scale dS K, dK = scale dS^T Q summed over the query heads of a KV head), in both
     forms: dS^T workspace + batched dQ GEMM ("auto"; T = 300 and 130 are not multiples of 8
-    and fall back; 520 and 200 end in a partial query tile) and the dQ kernel (None)."""
+    and fall back; 520 and 200 end in a partial query tile) and the dQ kernel (None), at
+    head_dim 128 and 64."""
     import torch
 
-    d = 128
     q, k, v, do = _qkv(oracle, Bn, nH, nKV, T, d, 1900 + T)
     Q, K, V, dO = (to_dev(x, dev, True) for x in (q, k, v, do))
     lse = torch.empty((Bn, nH, T), dtype=torch.float32, device=dev)
     O = mi.flash_attn_fwd(Q, K, V, lse=lse)
-    print(f"flash backward B={Bn} nH={nH} nKV={nKV} T={T} workspace={ws}", flush=True)
+    print(f"flash backward B={Bn} nH={nH} nKV={nKV} T={T} d={d} workspace={ws}", flush=True)
     dQ, dK, dV = mi.flash_attn_bwd(Q, K, V, O, dO, lse, workspace=ws)
     dQ_ref, dK_ref, dV_ref = oracle.attention_bwd(q, k, v, do)
     check(host(dV), dV_ref, TOL_BF16, "dV")
@@ -210,13 +213,14 @@ def _dense_attention_bwd(q, k, v, do, causal):
     return dq, dk, dv
 
 
+@pytest.mark.parametrize("d", [128, 64])
 @pytest.mark.parametrize("ws", ["auto", None])
-def test_flash_backward_noncausal(mi, dev, oracle, ws):
+def test_flash_backward_noncausal(mi, dev, oracle, ws, d):
     """causal = 0: gradients over every key (T % 64 != 0: a partial last query tile and key
     block) vs the closed form, which is itself pinned to the oracle on the causal case."""
     import torch
 
-    d, Bn, nH, nKV, T = 128, 1, 4, 2, 200
+    Bn, nH, nKV, T = 1, 4, 2, 200
     q, k, v, do = _qkv(oracle, Bn, nH, nKV, T, d, 2300)
     for ref, got in zip(_dense_attention_bwd(q, k, v, do, True), oracle.attention_bwd(q, k, v, do)):
         assert np.abs(ref - got).max() <= 1e-9 * max(1.0, np.abs(got).max())
@@ -231,7 +235,8 @@ def test_flash_backward_noncausal(mi, dev, oracle, ws):
     check(host(dQ), dq_ref, TOL_BF16, "dQ")
 
 
-def test_flash_backward_layouts_and_determinism(mi, dev, oracle):
+@pytest.mark.parametrize("d", [128, 64])
+def test_flash_backward_layouts_and_determinism(mi, dev, oracle, d):
     """O/dO in [B,nH,T,d] give the same gradients as [B,T,nH*d], bit for bit, and two
     launches agree bit for bit (no atomics), in the three schedules: dS^T form with the
     balanced dK/dV units (full workspace), dS^T form with one workgroup per key block
@@ -240,7 +245,7 @@ def test_flash_backward_layouts_and_determinism(mi, dev, oracle):
     units sum partials, equal to them within the bf16 bar."""
     import torch
 
-    Bn, nH, nKV, T, d = 1, 8, 2, 384, 128
+    Bn, nH, nKV, T = 1, 8, 2, 384
     q, k, v, do = _qkv(oracle, Bn, nH, nKV, T, d, 2100)
     Q, K, V, dO = (to_dev(x, dev, True) for x in (q, k, v, do))
     lse = torch.empty((Bn, nH, T), dtype=torch.float32, device=dev)
@@ -285,12 +290,13 @@ def test_flash_backward_config4(mi, dev, oracle):
         check(dV[sl], dV_ref, TOL_BF16, f"dV[{b}]")
 
 
-@pytest.mark.parametrize("d", [64, 96])
+@pytest.mark.parametrize("d", [32, 96])
 @pytest.mark.parametrize("layout", ["bthd", "bhtd"])
-def test_flash_head_dim_below_128(mi, dev, oracle, d, layout):
-    """Head dimensions below 128 (the reference kernel's 64, flash_attn_fwd.metal:31) run
-    the d = 128 kernels on zero-padded rows at the scale 1/sqrt(d) (mi_flash_attn_*_scaled):
-    forward, row log-sum-exp and backward vs the oracle, both output layouts."""
+def test_flash_head_dim_padded(mi, dev, oracle, d, layout):
+    """Head dimensions other than 64 and 128 (multiples of 8 below 128) run the next larger
+    fused kernels (64 for 32, 128 for 96) on zero-padded rows at the scale 1/sqrt(d)
+    (mi_flash_attn_*_scaled): forward, row log-sum-exp and backward vs the oracle, both
+    output layouts."""
     import torch
 
     Bn, nH, nKV, T = 2, 8, 2, 320
@@ -311,6 +317,32 @@ def test_flash_head_dim_below_128(mi, dev, oracle, d, layout):
     check(host(dV), dV_ref, TOL_BF16, f"dV d={d}")
     check(host(dK), dK_ref, TOL_BF16, f"dK d={d}")
     check(host(dQ), dQ_ref, TOL_BF16, f"dQ d={d}")
+
+
+def test_flash_config4_head_dim_64(mi, dev, oracle):
+    """Configuration 4's batch and heads (B=8, 16 q / 4 kv heads, T=1024) at head_dim 64, the
+    reference kernels' compiled size (flash_attn_fwd.metal:31, fused_attn_bwd.metal): the
+    native d = 64 forward and backward (dS^T form, balanced schedule) vs the oracle on batch
+    elements 0 and 7, and the forward vs the materialised S/P path on the whole batch."""
+    import torch
+
+    Bn, nH, nKV, T, d = 8, 16, 4, 1024, 64
+    q, k, v, do = _qkv(oracle, Bn, nH, nKV, T, d, 4064)
+    Q, K, V, dO = (to_dev(x, dev, True) for x in (q, k, v, do))
+    lse = torch.empty((Bn, nH, T), dtype=torch.float32, device=dev)
+    print("flash configuration 4 at head_dim 64", flush=True)
+    O = mi.flash_attn_fwd(Q, K, V, lse=lse)
+    O_mat, _ = mi.attention_forward(Q, K, V)
+    Oh = host(O)
+    check(Oh, host(O_mat), TOL_BF16, "fused vs materialised (d=64)")
+    dQ, dK, dV = (host(t) for t in mi.flash_attn_bwd(Q, K, V, O, dO, lse))
+    for b in (0, 7):
+        sl = slice(b, b + 1)
+        check(Oh[sl], oracle.attention_fwd(q[sl], k[sl], v[sl]), TOL_BF16, f"O[{b}] d=64")
+        dQ_ref, dK_ref, dV_ref = oracle.attention_bwd(q[sl], k[sl], v[sl], do[sl])
+        check(dQ[sl], dQ_ref, TOL_BF16, f"dQ[{b}] d=64")
+        check(dK[sl], dK_ref, TOL_BF16, f"dK[{b}] d=64")
+        check(dV[sl], dV_ref, TOL_BF16, f"dV[{b}] d=64")
 
 
 def test_flash_backward_graph_replays(mi, dev):
