@@ -142,11 +142,28 @@ __global__ void __launch_bounds__(256) splitk_reduce_kernel(Params p) {
     const int m = (int)(r / ((p.N + 3) / 4));
     const int n = (int)(r - (int64_t)m * ((p.N + 3) / 4)) * 4;
     float v[4] = {0.f, 0.f, 0.f, 0.f};
-    for (int s = 0; s < p.splits; ++s) {
-      const float* W = p.ws + ((int64_t)z * p.splits + s) * (int64_t)p.M * p.N + (int64_t)m * p.N;
+    const bool vec = (p.N & 3) == 0;  // whole, 16-byte aligned quads of the partial slabs
+    const float* W0 = p.ws + (int64_t)z * p.splits * (int64_t)p.M * p.N + (int64_t)m * p.N + n;
+    const int64_t slab = (int64_t)p.M * p.N;
+    if (vec) {
+      // all splits' loads issued before the sum, which keeps the fixed split order
+      for (int s = 0; s < p.splits; s += 8) {
+        f32x4_t w[8];
 #pragma unroll
-      for (int e = 0; e < 4; ++e)
-        if (n + e < p.N) v[e] += W[n + e];
+        for (int u = 0; u < 8; ++u)
+          w[u] = s + u < p.splits ? *(const f32x4_t*)(W0 + (s + u) * slab) : f32x4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int u = 0; u < 8; ++u)
+          if (s + u < p.splits)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) v[e] += w[u][e];
+      }
+    } else {
+      for (int s = 0; s < p.splits; ++s) {
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          if (n + e < p.N) v[e] += W0[s * slab + e];
+      }
     }
 #pragma unroll
     for (int e = 0; e < 4; ++e) v[e] *= p.alpha;

@@ -764,9 +764,14 @@ __global__ void __launch_bounds__(256)
       const int m = mrow0 + r, n = ncol0 + c4 * 4;
       if (W) {
         if (m < p.M) {
+          // partial slabs are 16-byte aligned (the workspace is; M*N*4 per slab)
+          if ((p.N & 3) == 0 && n + 3 < p.N) {
+            *reinterpret_cast<f32x4_t*>(W + (int64_t)m * p.N + n) = sv;
+          } else {
 #pragma unroll
-          for (int e = 0; e < 4; ++e)
-            if (n + e < p.N) W[(int64_t)m * p.N + n + e] = sv[e];
+            for (int e = 0; e < 4; ++e)
+              if (n + e < p.N) W[(int64_t)m * p.N + n + e] = sv[e];
+          }
         }
       } else {
         float v[4];

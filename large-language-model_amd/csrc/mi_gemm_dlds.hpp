@@ -786,9 +786,13 @@ __global__ void __launch_bounds__(64 * WGM * WGN * KG)
       if (W) {
         // split-K partials: alpha is applied by the reduction
         if (m < p.M) {
+          if ((p.N & 3) == 0 && n + 3 < p.N) {
+            *reinterpret_cast<f32x4_t*>(W + (int64_t)m * p.N + n) = sv;
+          } else {
 #pragma unroll
-          for (int e = 0; e < 4; ++e)
-            if (n + e < p.N) W[(int64_t)m * p.N + n + e] = sv[e];
+            for (int e = 0; e < 4; ++e)
+              if (n + e < p.N) W[(int64_t)m * p.N + n + e] = sv[e];
+          }
         }
       } else {
         float v[4];
