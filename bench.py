@@ -181,7 +181,8 @@ def parse():
                          "set, then per projection dW before dX, down first); projection = "
                          "fwd, dX, dW per projection")
     ap.add_argument("--workload",
-                    choices=("block", "block_fp32", "attention", "lm_head", "norm", "convert"),
+                    choices=("block", "block_fp32", "attention", "lm_head", "norm", "norm_gemm",
+                             "convert"),
                     default="block",
                     help="block: the configuration-3 GEMM set (the headline metric); block_fp32: "
                          "configuration 2's fp32 GEMM set (GPT-small, M=2048); attention: "
@@ -574,6 +575,91 @@ def norm_main(args):
     print(json.dumps(out))
 
 
+def norm_gemm_main(args):
+    """Configuration 3's norms folded into the GEMMs that consume them (Transformer.cpp:147-162,
+    Attention.cpp:196-201): h += a; qkv = rmsnorm(h) Wqkv, then h2 += a2; gate/up =
+    rmsnorm(h2) Wg / Wu. Folded step: the norm's row statistic only (1/rms, residual add), the
+    norm weight multiplied into the rows of each weight (per step: weights change every
+    training step), and the GEMMs on h with 1/rms as their epilogue row scale. Unfused step:
+    the add + RMSNorm kernel writing the normalised activations, then the GEMMs on them.
+    value = the GEMMs' FLOPs / folded step time; both steps' times are reported."""
+    import torch
+
+    import mi_gemm as mi
+
+    dev = torch.device("cuda:0")
+    mi.init()
+    M, H, I, Q = M_TOKENS, 2048, 5632, 3072
+    g = torch.Generator(device=dev)
+    g.manual_seed(6)
+    mk = lambda r, c, s=1.0: (torch.randn((r, c), generator=g, device=dev) * s).to(torch.bfloat16)
+    h, a, h2, a2 = mk(M, H), mk(M, H), mk(M, H), mk(M, H)
+    wn1 = (1.0 + 0.1 * torch.randn((H,), generator=g, device=dev)).float()
+    wn2 = (1.0 + 0.1 * torch.randn((H,), generator=g, device=dev)).float()
+    Wq, Wg, Wu = mk(H, Q, 0.02), mk(H, I, 0.02), mk(H, I, 0.02)
+    Fq, Fg, Fu = torch.empty_like(Wq), torch.empty_like(Wg), torch.empty_like(Wu)
+    qkv, gate, up = mk(M, Q), mk(M, I), mk(M, I)
+    y, y2 = torch.empty_like(h), torch.empty_like(h2)
+    r1 = torch.empty((M,), dtype=torch.float32, device=dev)
+    r2 = torch.empty_like(r1)
+    ws = torch.empty(WS_BYTES // 4, dtype=torch.float32, device=dev)
+
+    def folded():
+        mi.rms_norm_forward(h, wn1, residual=a, out=False, rstd=r1, sync=False)
+        mi.rms_norm_fold_weight(wn1, Wq, out=Fq, sync=False)
+        mi.gemm(h, Fq, qkv, M, Q, H, row_scale=r1, workspace=ws, sync=False)
+        mi.rms_norm_forward(h2, wn2, residual=a2, out=False, rstd=r2, sync=False)
+        mi.rms_norm_fold_weight(wn2, Wg, out=Fg, sync=False)
+        mi.rms_norm_fold_weight(wn2, Wu, out=Fu, sync=False)
+        mi.gemm(h2, Fg, gate, M, I, H, row_scale=r2, workspace=ws, sync=False)
+        mi.gemm(h2, Fu, up, M, I, H, row_scale=r2, workspace=ws, sync=False)
+
+    def folded_cached():  # weights folded once (serving, or a fold fused into the optimizer)
+        mi.rms_norm_forward(h, wn1, residual=a, out=False, rstd=r1, sync=False)
+        mi.gemm(h, Fq, qkv, M, Q, H, row_scale=r1, workspace=ws, sync=False)
+        mi.rms_norm_forward(h2, wn2, residual=a2, out=False, rstd=r2, sync=False)
+        mi.gemm(h2, Fg, gate, M, I, H, row_scale=r2, workspace=ws, sync=False)
+        mi.gemm(h2, Fu, up, M, I, H, row_scale=r2, workspace=ws, sync=False)
+
+    def unfused():
+        mi.rms_norm_forward(h, wn1, residual=a, out=y, sync=False)
+        mi.gemm(y, Wq, qkv, M, Q, H, workspace=ws, sync=False)
+        mi.rms_norm_forward(h2, wn2, residual=a2, out=y2, sync=False)
+        mi.gemm(y2, Wg, gate, M, I, H, workspace=ws, sync=False)
+        mi.gemm(y2, Wu, up, M, I, H, workspace=ws, sync=False)
+
+    def timed(fn, n):
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(n):
+            fn()
+        torch.cuda.synchronize()
+        return (time.perf_counter() - t0) / n * 1e3
+
+    for _ in range(args.warmup):
+        folded()
+        unfused()
+    ms_unfused = timed(unfused, args.steps)
+    ms_folded = timed(folded, args.steps)
+    ms_unfused2 = timed(unfused, args.steps)
+    ms_cached = timed(folded_cached, args.steps)
+    flops = 2 * M * H * (Q + 2 * I)
+    out = {
+        "metric": "norm + GEMM TFLOP/s (configuration 3: RMSNorm folded into the QKV and gate/up GEMMs)",
+        "value": round(flops / (ms_folded / 1e3) / 1e12, 2), "unit": "TFLOP/s", "n_gpus": 1,
+        "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms_folded, 4),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
+        "data": "synthetic (torch.randn on device)",
+        "config": {"workload": "M=8192, H=2048: h += a; qkv = rmsnorm(h) Wqkv [2048->3072]; h2 += a2; "
+                               "gate/up = rmsnorm(h2) Wg/Wu [2048->5632]; norm weights folded per step",
+                   "flops_per_step": flops, "folded_ms": round(ms_folded, 4),
+                   "unfused_ms": round(min(ms_unfused, ms_unfused2), 4),
+                   "unfused_tflops": round(flops / (min(ms_unfused, ms_unfused2) / 1e3) / 1e12, 2),
+                   "folded_weights_cached_ms": round(ms_cached, 4)},
+    }
+    print(json.dumps(out))
+
+
 def cpu_norm_baseline(rows: int = 8192, min_seconds: float = 2.0) -> dict:
     """The oracle's RMSNorm forward (residual add, bf16-rounded sum) and backward (residual
     gradient, weight gradient) over the same 8192 x 2048 rows (RMSNorm.cpp:40-180, float64
@@ -943,6 +1029,9 @@ def main():
         return
     if args.workload == "norm":
         norm_main(args)
+        return
+    if args.workload == "norm_gemm":
+        norm_gemm_main(args)
         return
     if args.workload == "convert":
         convert_main(args)

@@ -124,6 +124,18 @@ void rms_norm_backward(const float* grad_output, const float* input, const float
 void fused_add_norm(float* x_residual, const float* residual, const float* weight, float* output,
                     size_t num_rows, size_t D, float eps);
 
+// The decoder layer's norm and the projection that consumes it as one call
+// (Transformer.cpp:147-162: fused_add_norm, then ffn_in.matmul(w_gate / w_up);
+// Attention.cpp:196-201: x_norm.matmul(Wq / Wk / Wv)): x += residual (when given,
+// in place, bf16), then out = rmsnorm(x) * W with the norm folded into the GEMM:
+// 1/rms per row (mi_rmsnorm_fwd without y), W' = diag(norm_weight) W
+// (mi_rmsnorm_fold_weight, bridge-owned), out = diag(1/rms) x W' (mi_gemm with
+// epi->row_scale).  The normalised activations are never written.  x, residual, W
+// [dims, N], out [rows, N] bf16; norm_weight fp32 [dims].  No counterpart in the
+// reference: it replaces the pair of calls.
+void fused_norm_matmul(void* x, const void* residual, const float* norm_weight, const void* W, void* out,
+                       size_t rows, size_t dims, size_t N, float eps);
+
 // MetalBridge.hpp:82-85: grad_input = rmsnorm_backward(grad_output, input) + residual,
 // bf16 activations, fp32 weight (fused_backward_add_norm.metal, Transformer.cpp:441-466).
 void fused_backward_add_norm(const void* grad_output, const void* input, const void* weight,

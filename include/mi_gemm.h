@@ -19,6 +19,7 @@
  *
  * Epilogue, applied in fp32 to the fp32 accumulator acc = sum_k op(A)*op(B):
  *   t = alpha*acc                         (dual-B: t = SiLU(alpha*acc_g) * (alpha*acc_u))
+ *   t *= row_scale[m]                     if epi->row_scale
  *   t += bias[n]                          if epi->bias
  *   t += beta * C[m,n]                    if beta != 0 (C read in its own dtype)
  *   t += R[m*ldr + n]                     if epi->residual
@@ -66,6 +67,8 @@ typedef struct mi_epilogue {
   int64_t ldr;
   const void* B2;        /* dual-B SiLU gate: C = SiLU(A*B) (.) (A*B2), B2 laid out as B     */
   const void* A2;        /* SiLU-gate prologue: op(A) := SiLU(A) (.) A2, A2 laid out as A    */
+  const float* row_scale; /* [M] fp32 factor per output row (a folded RMSNorm: 1/rms of
+                             row m, mi_rmsnorm_fwd with y = NULL); one problem, no B2       */
 } mi_epilogue;
 
 /*
@@ -276,7 +279,10 @@ int mi_cross_entropy(void* stream, const void* logits, int32_t logits_dtype, int
  *   y = x / sqrt(sum(x^2)/dims + eps) * weight
  * computed in fp32.  x, residual, y are [rows, ld] of `dtype` (MI_BF16 or
  * MI_F32), weight [dims] of w_dtype; rstd (optional, fp32 [rows]) receives
- * 1/rms per row.  y may be x itself; arrays must otherwise not overlap.
+ * 1/rms per row.  y may be x itself; arrays must otherwise not overlap.  y = NULL
+ * (rstd required) computes only x += residual and rstd: the norm is then folded
+ * into the next GEMM, rmsnorm(x) W = diag(rstd) x W' with W' = diag(weight) W
+ * (mi_rmsnorm_fold_weight), rstd passed as that GEMM's epi->row_scale.
  * Replaces metal_bridge::rms_norm_forward (MetalBridge.hpp:60-61,
  * rms_norm_forward.metal; RMSNorm::forward, RMSNorm.cpp:48-75) and
  * metal_bridge::fused_add_norm (MetalBridge.hpp:79-81, fused_add_norm.metal;
@@ -288,6 +294,22 @@ int mi_rmsnorm_fwd(void* stream, void* x, const void* residual, const void* weig
 
 /* Workspace bytes mi_rmsnorm_bwd needs when it computes dw. */
 size_t mi_rmsnorm_bwd_workspace_size(int64_t rows, int64_t dims);
+
+/*
+ * W_out[k, n] = weight[k] * W[k, n] for k < K, n < N (fp32 product stored in W's
+ * dtype, bf16 rounded to nearest even): the RMSNorm weight moved into the rows of
+ * the GEMM that consumes the norm (the QKV and gate/up projections,
+ * Transformer.cpp:147-162, Attention.cpp:196-201), so that
+ *   rmsnorm(x) W = diag(1/rms) x W_out.
+ * With mi_rmsnorm_fwd's statistic-only mode and the GEMM's epi->row_scale this
+ * replaces the pair fused_add_norm / rms_norm_forward -> matmul
+ * (MetalBridge.hpp:60-61,79-81 then Tensor::matmul) by a row statistic and one
+ * GEMM on x itself: the normalised activations are never written.  W_out may be W
+ * (ld_out == ldw) or disjoint from it.  dtype MI_BF16 or MI_F32; weight MI_BF16
+ * or MI_F32.
+ */
+int mi_rmsnorm_fold_weight(void* stream, const void* weight, int32_t w_dtype, const void* W, int64_t ldw,
+                           int64_t K, int64_t N, int32_t dtype, void* W_out, int64_t ld_out);
 
 /*
  * RMSNorm backward: with xhat = x / rms and rms = sqrt(sum(x^2)/dims + eps),

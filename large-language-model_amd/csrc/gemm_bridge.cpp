@@ -514,6 +514,56 @@ void fused_add_norm(float* x_residual, const float* residual, const float* weigh
                         (int64_t)num_rows, (int64_t)D, (int64_t)D, MI_F32, eps));
 }
 
+namespace {
+// W' (the norm weight folded into the projection) and 1/rms per row for fused_norm_matmul.
+thread_local void* t_fold = nullptr;
+thread_local size_t t_fold_bytes = 0;
+
+bool fold_state(size_t bytes) {
+  if (bytes <= t_fold_bytes) return true;
+  if (t_fold) {
+    if (hipStreamSynchronize(get_stream()) != hipSuccess) return false;
+    (void)hipFree(t_fold);
+  }
+  t_fold = nullptr;
+  t_fold_bytes = 0;
+  if (hipMalloc(&t_fold, bytes) != hipSuccess) return false;
+  t_fold_bytes = bytes;
+  return true;
+}
+}  // namespace
+
+void fused_norm_matmul(void* x, const void* residual, const float* norm_weight, const void* W, void* out,
+                       size_t rows, size_t dims, size_t N, float eps) {
+  if (rows == 0 || dims == 0 || N == 0) {
+    t_status = MI_OK;
+    return;
+  }
+  const size_t wb = (dims * N * 2 + 255) / 256 * 256;
+  if (!fold_state(wb + rows * sizeof(float))) {
+    t_status = MI_ERR_HIP;
+    std::fprintf(stderr, "[mi_bridge] fused_norm_matmul: could not allocate the folded weight\n");
+    return;
+  }
+  void* Wf = t_fold;
+  float* rstd = (float*)((char*)t_fold + wb);
+  hipStream_t st = get_stream();
+  int s = mi_rmsnorm_fwd(st, x, residual, norm_weight, MI_F32, nullptr, rstd, (int64_t)rows, (int64_t)dims,
+                         (int64_t)dims, MI_BF16, eps);
+  if (s == MI_OK)
+    s = mi_rmsnorm_fold_weight(st, norm_weight, MI_F32, W, (int64_t)N, (int64_t)dims, (int64_t)N, MI_BF16, Wf,
+                               (int64_t)N);
+  size_t wsb = 0;
+  void* ws = s == MI_OK ? workspace_for(0, 0, rows, N, dims, MI_BF16, MI_BF16, &wsb) : nullptr;
+  mi_epilogue e;
+  std::memset(&e, 0, sizeof(e));
+  e.row_scale = rstd;
+  if (s == MI_OK)
+    s = mi_gemm(st, 0, 0, (int64_t)rows, (int64_t)N, (int64_t)dims, 1.0f, x, (int64_t)dims, Wf, (int64_t)N,
+                MI_BF16, 0.0f, out, (int64_t)N, MI_BF16, &e, ws, wsb);
+  finish("fused_norm_matmul", s);
+}
+
 void fused_backward_add_norm(const void* grad_output, const void* input, const void* weight,
                              const void* residual, void* grad_input, size_t num_rows, size_t D,
                              float eps) {

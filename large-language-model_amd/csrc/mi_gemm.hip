@@ -421,6 +421,10 @@ int validate(const Problem& P) {
     return fail(MI_ERR_DTYPE, "residual dtype %d", e.residual_dtype);
   if (e.B2 && b.causal == MI_CAUSAL_OUT_LOWER)
     return fail(MI_ERR_UNSUPPORTED, "dual-B with causal output mask");
+  if (e.row_scale && (e.B2 || b.batch != 1))
+    return fail(MI_ERR_UNSUPPORTED, "row_scale needs one problem without dual-B");
+  if (e.row_scale && ((uintptr_t)e.row_scale & 3u))
+    return fail(MI_ERR_UNSUPPORTED, "row_scale must be 4-byte aligned");
   return MI_OK;
 }
 
@@ -593,6 +597,7 @@ int run(const Problem& P, hipStream_t stream) {
   p.C = P.C;
   p.bias = P.ep.bias;
   p.R = P.ep.residual;
+  p.row_scale = P.ep.row_scale;
   p.ws = (float*)P.ws;
   p.lda = P.lda;
   p.ldb = P.ldb;
@@ -1065,7 +1070,7 @@ int mi_rmsnorm_fwd(void* stream, void* x, const void* residual, const void* weig
   if (rows > INT32_MAX || dims > INT32_MAX) return fail(MI_ERR_SHAPE, "size exceeds 2^31-1");
   if ((dtype != MI_F32 && dtype != MI_BF16) || (w_dtype != MI_F32 && w_dtype != MI_BF16))
     return fail(MI_ERR_DTYPE, "dtype %d / weight dtype %d", dtype, w_dtype);
-  if (!x || !weight || !y) return fail(MI_ERR_NULL, "x, weight or y is NULL");
+  if (!x || !weight || (!y && !rstd)) return fail(MI_ERR_NULL, "x, weight, or both y and rstd are NULL");
   if (ld < dims) return fail(MI_ERR_LD, "ld=%lld < dims=%lld", (long long)ld, (long long)dims);
   const int64_t es = dtype == MI_BF16 ? 2 : 4, wes = w_dtype == MI_BF16 ? 2 : 4;
   const void* rows_arr[] = {x, y, residual};
@@ -1077,7 +1082,7 @@ int mi_rmsnorm_fwd(void* stream, void* x, const void* residual, const void* weig
   if (rows_overlap(y, x, extent) || rows_overlap(y, residual, extent) || rows_overlap(x, residual, extent))
     return fail(MI_ERR_UNSUPPORTED, "x, residual and y must each be the same array or disjoint");
   const int64_t ev = 16 / es;
-  const bool vector_path = dims % ev == 0 && (ld * es) % 16 == 0 && aligned16(x) && aligned16(y) &&
+  const bool vector_path = dims % ev == 0 && (ld * es) % 16 == 0 && aligned16(x) && (!y || aligned16(y)) &&
                            (!residual || aligned16(residual)) &&
                            (uintptr_t)weight % (w_dtype == MI_BF16 && ev == 4 ? 8 : 16) == 0 &&
                            dims / ev <= 64 * NORM_MAX_VEC_PER_LANE;
@@ -1088,6 +1093,32 @@ int mi_rmsnorm_fwd(void* stream, void* x, const void* residual, const void* weig
   p.ld = ld; p.rows = (int)rows; p.dims = (int)dims; p.eps = eps;
   hipError_t e = launch_norm_fwd(p, dtype == MI_BF16, w_dtype == MI_BF16, vector_path, (hipStream_t)stream);
   return e == hipSuccess ? MI_OK : fail(MI_ERR_HIP, "rmsnorm_fwd launch: %s", hipGetErrorString(e));
+}
+
+int mi_rmsnorm_fold_weight(void* stream, const void* weight, int32_t w_dtype, const void* W, int64_t ldw,
+                           int64_t K, int64_t N, int32_t dtype, void* W_out, int64_t ld_out) {
+  if (K < 0 || N < 0) return fail(MI_ERR_SHAPE, "negative size");
+  if (K == 0 || N == 0) return MI_OK;
+  if ((dtype != MI_F32 && dtype != MI_BF16) || (w_dtype != MI_F32 && w_dtype != MI_BF16))
+    return fail(MI_ERR_DTYPE, "dtype %d / weight dtype %d", dtype, w_dtype);
+  if (!weight || !W || !W_out) return fail(MI_ERR_NULL, "weight, W or W_out is NULL");
+  if (ldw < N || ld_out < N) return fail(MI_ERR_LD, "ldw=%lld / ld_out=%lld < N=%lld", (long long)ldw,
+                                         (long long)ld_out, (long long)N);
+  if (K > INT32_MAX || N > INT32_MAX) return fail(MI_ERR_SHAPE, "size exceeds 2^31-1");
+  const int64_t es = dtype == MI_BF16 ? 2 : 4, wes = w_dtype == MI_BF16 ? 2 : 4;
+  if ((uintptr_t)W % es || (uintptr_t)W_out % es || (uintptr_t)weight % wes)
+    return fail(MI_ERR_UNSUPPORTED, "arrays must be aligned to their element size");
+  const int64_t ext_in = ((K - 1) * ldw + N) * es, ext_out = ((K - 1) * ld_out + N) * es;
+  if (W != W_out && rows_overlap(W_out, W, std::max(ext_in, ext_out)))
+    return fail(MI_ERR_UNSUPPORTED, "W_out must be W itself or disjoint from it");
+  if (W == W_out && ldw != ld_out) return fail(MI_ERR_LD, "in place needs ld_out == ldw");
+  const int64_t ev = 16 / es;
+  const bool vec = N % ev == 0 && ldw % ev == 0 && ld_out % ev == 0 && aligned16(W) && aligned16(W_out);
+  int st = init_devices();
+  if (st != MI_OK) return st;
+  hipError_t e = launch_norm_fold_weight(weight, w_dtype == MI_BF16, W, ldw, K, N, dtype == MI_BF16, W_out,
+                                         ld_out, vec, current_cus(), (hipStream_t)stream);
+  return e == hipSuccess ? MI_OK : fail(MI_ERR_HIP, "rmsnorm weight fold launch: %s", hipGetErrorString(e));
 }
 
 int mi_rmsnorm_bwd(void* stream, const void* dy, const void* x, const void* weight, int32_t w_dtype,

@@ -60,6 +60,7 @@ struct Params {
   int vecA, vecB;  // 16-byte global loads legal for A (and A2) / B (and B2)
   int cvec;        // 4-wide C / R / bias accesses legal
   uint32_t extA, extB;  // byte extent of one batch/segment matrix of A (A2) / B (B2)
+  const float* row_scale;  // optional [M] fp32 factor on row m of alpha * acc (a folded RMSNorm)
   int krot;             // direct-to-LDS kernels: start each XCD's tiles at its own K offset
   int group_m;          // tile rows per column sweep of the tile order (map_tile)
 };
@@ -368,6 +369,11 @@ __device__ __forceinline__ float ld_any(const void* p, int64_t i, int is_bf16) {
 __device__ __forceinline__ void epilogue4(const Params& p, void* Cz, const void* Rz, int m, int n,
                                           float v[4]) {
   if (m >= p.M || n >= p.N) return;
+  if (p.row_scale) {
+    const float s = p.row_scale[m];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) v[e] *= s;
+  }
   const bool full = (n + 3 < p.N) && p.cvec;
   const int64_t ci = (int64_t)m * p.ldc + n;
   if (p.bias) {

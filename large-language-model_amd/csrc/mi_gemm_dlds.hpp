@@ -651,6 +651,14 @@ __global__ void __launch_bounds__(64 * WGM * WGN * KG)
       return p.alpha * acc[i][j][4 * q + e];
   };
   if constexpr (FAST_EPI) {
+    // row scale (a folded RMSNorm): row block i of this lane is row m0 + wm*WTM + 32i +
+    // (lane & 31); blocks past M (edge tiles) are not stored and read no scale
+    float rsv[TM];
+#pragma unroll
+    for (int i = 0; i < TM; ++i) {
+      const int r = m0 + wm * WTM + 32 * i + (lane & 31);
+      rsv[i] = p.row_scale ? (r < p.M ? p.row_scale[r] : 0.0f) : 1.0f;
+    }
     // M and N multiples of 32, epilogue alpha (SiLU gate), beta*C and the output
     // conversion.  Each 32x32 MFMA block goes through a wave-private LDS patch (rows
     // padded by 4 floats) and back out row-major, so a store instruction writes 8
@@ -711,7 +719,7 @@ __global__ void __launch_bounds__(64 * WGM * WGN * KG)
           for (int q = 0; q < 4; ++q) {
             f32x4_t v;
 #pragma unroll
-            for (int e = 0; e < 4; ++e) v[e] = value(i, j, q, e);
+            for (int e = 0; e < 4; ++e) v[e] = value(i, j, q, e) * rsv[i];
             *reinterpret_cast<f32x4_t*>(patch + r_in * PP + 8 * q + 4 * h_in) = v;
           }
           const int col = col_of(j);

@@ -28,6 +28,8 @@
 #include <hip/hip_runtime.h>
 #include <math.h>
 
+#include <algorithm>
+
 #include "mi_gemm_device.hpp"
 #include "mi_norm.hpp"
 
@@ -153,6 +155,7 @@ __global__ void __launch_bounds__(256) norm_fwd_vec(NormParams p) {
   ss = nwave_sum(ss);
   const float rs = 1.0f / sqrtf(ss / (float)p.dims + p.eps);
   if (p.rstd && lane == 0) p.rstd[row] = rs;
+  if (!p.y) return;  // statistic only (the norm folded into a GEMM)
   char* yr = (char*)p.y + (int64_t)row * p.ld * ES;
 #pragma unroll
   for (int i = 0; i < NV; ++i) {
@@ -184,6 +187,7 @@ __global__ void __launch_bounds__(256) norm_fwd_gen(NormParams p) {
   ss = block_sum256(ss, red);
   const float rs = 1.0f / sqrtf(ss / (float)p.dims + p.eps);
   if (p.rstd && threadIdx.x == 0) p.rstd[row] = rs;
+  if (!p.y) return;  // statistic only (the norm folded into a GEMM)
   for (int c = threadIdx.x; c < p.dims; c += 256)  // each thread re-reads what it wrote
     st_elem<BF16>(yr, c, ld_elem<BF16>(xr, c) * rs * ld_elem<W_BF16>(p.w, c));
 }
@@ -402,6 +406,34 @@ __global__ void __launch_bounds__(1024) norm_dw_reduce(const float* ws, int G, i
   }
 }
 
+// ---- weight folding ------------------------------------------------------------
+// W'[k, n] = weight[k] * W[k, n] (fp32 product, stored in W's dtype, bf16 rounded to
+// nearest even): the RMSNorm weight moved into the rows of the next GEMM's B operand,
+// so that rmsnorm(x) W = diag(1/rms) x W'.  VEC: 8 (bf16) or 4 (fp32) columns per
+// thread with 16-byte accesses.
+template <bool BF16, bool W_BF16, bool VEC>
+__global__ void __launch_bounds__(256) norm_fold_weight_kernel(const void* w, const void* W, int64_t ldw,
+                                                               int64_t K, int64_t N, void* out, int64_t ldo) {
+  constexpr int EV = BF16 ? 8 : 4, ES = BF16 ? 2 : 4;
+  const int64_t per_row = VEC ? N / EV : N;
+  const int64_t n_items = K * per_row;
+  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n_items; i += (int64_t)gridDim.x * 256) {
+    const int64_t k = i / per_row, c = i - k * per_row;
+    const float s = ld_elem<W_BF16>(w, (int)k);
+    const char* src = (const char*)W + k * ldw * ES;
+    char* dst = (char*)out + k * ldo * ES;
+    if constexpr (VEC) {
+      float v[EV];
+      load_act<BF16>(src, (int)(c * EV), v);
+#pragma unroll
+      for (int e = 0; e < EV; ++e) v[e] *= s;
+      store_act<BF16>(dst, (int)(c * EV), v);
+    } else {
+      st_elem<BF16>(dst, (int)c, ld_elem<BF16>(src, (int)c) * s);
+    }
+  }
+}
+
 int vec_per_lane(int dims, bool bf16) {
   const int per = (dims / (bf16 ? 8 : 4) + 63) / 64;
   return per <= 1 ? 1 : per <= 2 ? 2 : per <= 4 ? 4 : 8;
@@ -452,6 +484,24 @@ hipError_t launch_norm_fwd(const NormParams& p, bool bf16, bool w_bf16, bool vec
                           : fwd_one<true, false>(p, vector_path, stream);
   return w_bf16 ? fwd_one<false, true>(p, vector_path, stream)
                 : fwd_one<false, false>(p, vector_path, stream);
+}
+
+hipError_t launch_norm_fold_weight(const void* w, bool w_bf16, const void* W, int64_t ldw, int64_t K,
+                                   int64_t N, bool bf16, void* out, int64_t ldo, bool vec, int cus,
+                                   hipStream_t stream) {
+  const int64_t items = K * (vec ? N / (bf16 ? 8 : 4) : N);
+  const int64_t grid = std::min<int64_t>((items + 255) / 256, 8 * (int64_t)(cus > 0 ? cus : 256));
+  auto go = [&](auto kern) {
+    hipLaunchKernelGGL(kern, dim3((unsigned)grid), dim3(256), 0, stream, w, W, ldw, K, N, out, ldo);
+  };
+  if (bf16) {
+    if (w_bf16) vec ? go(norm_fold_weight_kernel<true, true, true>) : go(norm_fold_weight_kernel<true, true, false>);
+    else vec ? go(norm_fold_weight_kernel<true, false, true>) : go(norm_fold_weight_kernel<true, false, false>);
+  } else {
+    if (w_bf16) vec ? go(norm_fold_weight_kernel<false, true, true>) : go(norm_fold_weight_kernel<false, true, false>);
+    else vec ? go(norm_fold_weight_kernel<false, false, true>) : go(norm_fold_weight_kernel<false, false, false>);
+  }
+  return hipGetLastError();
 }
 
 hipError_t launch_norm_bwd(const NormParams& p, bool bf16, bool w_bf16, bool dw_bf16,

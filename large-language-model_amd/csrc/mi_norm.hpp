@@ -10,7 +10,7 @@ struct NormParams {
   void* x;            // [rows, ld] input; forward with r: updated in place to x + r
   const void* r;      // forward: residual added into x first; backward: gradient added to dx
   const void* w;      // [dims] weight
-  void* y;            // forward output [rows, ld]
+  void* y;            // forward output [rows, ld], or null: rstd only
   const void* dy;     // backward: gradient of y [rows, ld]
   void* dx;           // backward output [rows, ld]
   float* rstd;        // forward: optional [rows] 1 / rms
@@ -35,5 +35,9 @@ hipError_t launch_norm_fwd(const NormParams& p, bool bf16, bool w_bf16, bool vec
                            hipStream_t stream);
 hipError_t launch_norm_bwd(const NormParams& p, bool bf16, bool w_bf16, bool dw_bf16,
                            bool vector_path, hipStream_t stream);
+// out[k, n] = w[k] * W[k, n] for k < K, n < N (W's dtype; vec: 16-byte column groups).
+hipError_t launch_norm_fold_weight(const void* w, bool w_bf16, const void* W, int64_t ldw, int64_t K,
+                                   int64_t N, bool bf16, void* out, int64_t ldo, bool vec, int cus,
+                                   hipStream_t stream);
 
 }  // namespace mig

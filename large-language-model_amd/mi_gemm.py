@@ -38,7 +38,7 @@ C_SYMBOLS = (
     "mi_convert_matrix", "mi_flash_attn_bwd_workspace_size", "mi_profiler_enable",
     "mi_profiler_begin_step", "mi_profiler_count", "mi_profiler_record", "mi_profiler_totals",
     "mi_profiler_reset", "mi_gemm_noalloc", "mi_flash_attn_fwd_scaled", "mi_flash_attn_bwd_scaled",
-    "mi_convert_matrices",
+    "mi_convert_matrices", "mi_rmsnorm_fold_weight",
 )
 MI_ATTN_O_BHTD, MI_ATTN_O_BTHD = 0, 1
 
@@ -56,7 +56,7 @@ class MiEpilogue(ctypes.Structure):
         ("bias", ctypes.c_void_p), ("bias_dtype", ctypes.c_int32),
         ("residual", ctypes.c_void_p), ("residual_dtype", ctypes.c_int32),
         ("ldr", ctypes.c_int64),
-        ("B2", ctypes.c_void_p), ("A2", ctypes.c_void_p),
+        ("B2", ctypes.c_void_p), ("A2", ctypes.c_void_p), ("row_scale", ctypes.c_void_p),
     ]
 
 
@@ -158,6 +158,8 @@ def load_library():
     L.mi_rmsnorm_bwd.restype = ctypes.c_int
     L.mi_rmsnorm_bwd.argtypes = [vp, vp, vp, vp, i32, vp, vp, vp, i32, ctypes.c_float, i64, i64, i64,
                                  i32, ctypes.c_float, vp, ctypes.c_size_t]
+    L.mi_rmsnorm_fold_weight.restype = ctypes.c_int
+    L.mi_rmsnorm_fold_weight.argtypes = [vp, vp, i32, vp, i64, i64, i64, i32, vp, i64]
     L.mi_convert_matrix.restype = ctypes.c_int
     L.mi_convert_matrix.argtypes = [vp, vp, i32, i64, i64, i64, i64, i32, vp, i32, i64]
     L.mi_convert_matrices.restype = ctypes.c_int
@@ -236,10 +238,12 @@ def _finish(fn, st):
 
 # ---- general entry points -----------------------------------------------------
 
-def _epilogue(bias=None, residual=None, ldr=None, B2=None, A2=None):
-    if bias is None and residual is None and B2 is None and A2 is None:
+def _epilogue(bias=None, residual=None, ldr=None, B2=None, A2=None, row_scale=None):
+    if bias is None and residual is None and B2 is None and A2 is None and row_scale is None:
         return None
     e = MiEpilogue()
+    if row_scale is not None:
+        e.row_scale = row_scale.data_ptr()
     if bias is not None:
         e.bias, e.bias_dtype = bias.data_ptr(), _dt(bias)
     if residual is not None:
@@ -254,8 +258,9 @@ def _epilogue(bias=None, residual=None, ldr=None, B2=None, A2=None):
 
 def gemm(A, B, C, M, N, K, *, transA=False, transB=False, alpha=1.0, beta=0.0, lda=None,
          ldb=None, ldc=None, bias=None, residual=None, ldr=None, B2=None, A2=None,
-         workspace=None, sync=None):
-    """mi_gemm on torch device tensors; C = epilogue(alpha*op(A)op(B))."""
+         row_scale=None, workspace=None, sync=None):
+    """mi_gemm on torch device tensors; C = epilogue(alpha*op(A)op(B)); row_scale: optional
+    fp32 [M] tensor multiplying row m of alpha*op(A)op(B) before bias / beta / residual."""
     L = load_library()
     lda = lda if lda is not None else (M if transA else K)
     ldb = ldb if ldb is not None else (K if transB else N)
@@ -264,7 +269,7 @@ def gemm(A, B, C, M, N, K, *, transA=False, transB=False, alpha=1.0, beta=0.0, l
     wsb = 0 if workspace is None else workspace.numel() * workspace.element_size()
     st = L.mi_gemm(_stream(), int(transA), int(transB), M, N, K, alpha, _ptr(A), lda, _ptr(B),
                    ldb, _dt(A), beta, _ptr(C), ldc, _dt(C),
-                   _epilogue(bias, residual, ldr, B2, A2), ws, wsb)
+                   _epilogue(bias, residual, ldr, B2, A2, row_scale), ws, wsb)
     if sync is None:
         _finish("mi_gemm", st)
     else:
@@ -815,9 +820,19 @@ def rms_norm_forward(x, weight, eps=1e-5, residual=None, out=None, rstd=None, sy
     y = x / sqrt(mean(x^2) + eps) * weight over the last dimension. With residual, first
     x += residual in place (metal_bridge::fused_add_norm, Transformer.cpp:150-158). x, residual,
     out: bf16 or fp32 with one row stride; weight [dims] bf16 or fp32; rstd: optional fp32 [rows]
-    tensor receiving 1/rms. out may be x. Returns y."""
+    tensor receiving 1/rms. out may be x; out=False computes only the residual add and rstd
+    (the norm folded into the next GEMM: rms_norm_matmul). Returns y (or rstd)."""
     torch = _torch()
     rows, dims, ld = _rows_of(x, "x")
+    if out is False:
+        if rstd is None:
+            raise ValueError("the statistic-only form needs rstd")
+        if residual is not None and (residual.dtype != x.dtype or _rows_of(residual, "residual") != (rows, dims, ld)):
+            raise ValueError("residual must match x's dtype, shape and row stride")
+        st = load_library().mi_rmsnorm_fwd(_stream(), _ptr(x), _ptr(residual), _ptr(weight), _dt(weight),
+                                           None, _ptr(rstd), rows, dims, ld, _dt(x), float(eps))
+        (_finish if sync is None else _check)("mi_rmsnorm_fwd", st)
+        return rstd
     if out is None:
         out = torch.empty_strided(x.shape, x.stride(), dtype=x.dtype, device=x.device)
     for t, n in ((out, "out"), (residual, "residual")):
@@ -830,6 +845,43 @@ def rms_norm_forward(x, weight, eps=1e-5, residual=None, out=None, rstd=None, sy
     else:
         _check("mi_rmsnorm_fwd", st)
     return out
+
+
+def rms_norm_fold_weight(weight, W, out=None, sync=None):
+    """W'[k, n] = weight[k] * W[k, n] (mi_rmsnorm_fold_weight): the RMSNorm weight moved into
+    the rows of the GEMM's B operand (engine layout W[in, out]). out may be W. Returns W'."""
+    torch = _torch()
+    if W.dim() != 2 or W.stride(1) != 1 or weight.numel() != W.shape[0]:
+        raise ValueError("W must be a row-major [K, N] matrix and weight [K]")
+    if out is None:
+        out = torch.empty_like(W)
+    st = load_library().mi_rmsnorm_fold_weight(_stream(), _ptr(weight), _dt(weight), _ptr(W), W.stride(0),
+                                               W.shape[0], W.shape[1], _dt(W), _ptr(out), out.stride(0))
+    (_finish if sync is None else _check)("mi_rmsnorm_fold_weight", st)
+    return out
+
+
+def rms_norm_matmul(x, norm_weight, W, C=None, eps=1e-5, residual=None, folded=None, rstd=None,
+                    workspace=None, sync=None):
+    """rmsnorm(x [+= residual]) @ W with the norm folded into the GEMM (Transformer.cpp:147-162,
+    Attention.cpp:196-201: fused_add_norm / rms_norm_forward, then the QKV or gate/up matmul):
+    one row statistic (rstd = 1/rms, x += residual in place first) and one GEMM on x itself,
+    C = diag(rstd) x W' with W' = diag(norm_weight) W and rstd as the GEMM's row scale; the
+    normalised activations are never written. folded: W' from rms_norm_fold_weight (computed
+    here when not given). x [M, K] bf16 or fp32, W [K, N]. Returns C [M, N] in x's dtype."""
+    torch = _torch()
+    M, K = x.shape
+    N = W.shape[1]
+    if rstd is None:
+        rstd = torch.empty((M,), dtype=torch.float32, device=x.device)
+    rms_norm_forward(x, norm_weight, eps=eps, residual=residual, out=False, rstd=rstd, sync=False)
+    if folded is None:
+        folded = rms_norm_fold_weight(norm_weight, W, sync=False)
+    if C is None:
+        C = torch.empty((M, N), dtype=x.dtype, device=x.device)
+    gemm(x, folded, C, M, N, K, lda=x.stride(0), ldb=folded.stride(0), row_scale=rstd,
+         workspace=workspace, sync=sync)
+    return C
 
 
 def rms_norm_backward(dy, x, weight, eps=1e-5, residual_grad=None, dx=None, dw=None, dw_beta=0.0,

@@ -25,6 +25,9 @@ void mo_attention_fwd(int64_t Bn, int64_t nH, int64_t nKV, int64_t T, int64_t d,
 void mo_attention_bwd(int64_t Bn, int64_t nH, int64_t nKV, int64_t T, int64_t d, const float* Q4,
                       const float* K4, const float* V4, const float* dO, double* dQ, double* dK,
                       double* dV);
+// RMSNorm.cpp:40-75 with the residual add of Transformer.cpp:150-158 (x updated in place)
+void mo_rmsnorm_fwd(float* x, const float* r, const float* w, int64_t rows, int64_t dims, double eps,
+                    int round_bf16, double* y, double* rstd);
 }
 
 static int g_total = 0, g_passed = 0;
@@ -614,6 +617,46 @@ int main() {
                                (d == 64 ? " (native)" : " (padded)") + ", random, 2 shapes, <= 1e-2";
       row("GB-19", what.c_str(), ok, std::to_string(worst));
     }
+  }
+  {  // GB-20: fused_norm_matmul (the norm folded into the projection) against the oracle's
+     // add + RMSNorm and a float64 GEMM: out = rmsnorm(x + r) W, x updated to x + r.
+    const size_t rows = 96, dims = 256, N = 192;
+    uint32_t seed = 777u;
+    auto rnd = [&](size_t n, float sc) {
+      std::vector<float> v(n);
+      for (auto& x : v) {
+        seed = seed * 1664525u + 1013904223u;
+        x = fb(bf(sc * ((float)(seed >> 8) / 8388608.0f - 1.0f)));
+      }
+      return v;
+    };
+    auto x = rnd(rows * dims, 2.0f), r = rnd(rows * dims, 1.0f), W = rnd(dims * N, 0.1f);
+    std::vector<float> w(dims);
+    for (size_t i = 0; i < dims; ++i) w[i] = 1.0f + 0.001f * (float)((int)(i % 37) - 18);
+    std::vector<uint16_t> hx(rows * dims), hr(rows * dims), hW(dims * N);
+    for (size_t i = 0; i < rows * dims; ++i) { hx[i] = bf(x[i]); hr[i] = bf(r[i]); }
+    for (size_t i = 0; i < dims * N; ++i) hW[i] = bf(W[i]);
+    uint16_t *dx = dev(hx), *dr = dev(hr), *dW = dev(hW), *dout = dev(std::vector<uint16_t>(rows * N, 0));
+    float* dw = dev(w);
+    mi_bridge::fused_norm_matmul(dx, dr, dw, dW, dout, rows, dims, N, 1e-5f);
+    bool ok = mi_bridge::last_status() == MI_OK;
+    std::vector<float> xs = x;
+    std::vector<double> y(rows * dims), rs(rows);
+    mo_rmsnorm_fwd(xs.data(), r.data(), w.data(), rows, dims, 1e-5, 1, y.data(), rs.data());
+    const auto ho = host(dout, rows * N), hx2 = host(dx, rows * dims);
+    double m = 0, e = 0;
+    for (size_t i = 0; i < rows; ++i)
+      for (size_t n = 0; n < N; ++n) {
+        double ref = 0;
+        for (size_t k = 0; k < dims; ++k) ref += y[i * dims + k] * (double)W[k * N + n];
+        m = std::fmax(m, std::fabs(ref));
+        e = std::fmax(e, std::fabs(ref - fb(ho[i * N + n])));
+      }
+    bool sum_ok = true;  // x + r as the bf16 kernel stores it
+    for (size_t i = 0; i < rows * dims; ++i) sum_ok = sum_ok && fb(hx2[i]) == xs[i];
+    row("GB-20", "fused_norm_matmul: rmsnorm(x + r) W folded, <= 1e-2; x + r stored", ok && sum_ok &&
+        e <= 1e-2 * m, std::to_string(e / m));
+    dfree(dx); dfree(dr); dfree(dW); dfree(dout); dfree(dw);
   }
   std::printf("%d/%d checks passed\n", g_passed, g_total);
   return g_passed == g_total ? 0 : 1;
