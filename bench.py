@@ -176,18 +176,22 @@ def parse():
     ap.add_argument("--head-dim", type=int, default=ATT["d"], choices=(64, 128),
                     help="attention workload: head dimension (128 = configuration 4; 64 = the "
                          "reference kernels' compiled size at configuration 4's batch and heads)")
+    ap.add_argument("--lm-chunk", type=int, default=8192,
+                    help="lm_head_chunked: vocabulary columns per chunk (0 = one chunk)")
     ap.add_argument("--order", choices=("reference", "projection"), default="reference",
                     help="GEMM issue order of a block step: reference = the engine's (forward "
                          "set, then per projection dW before dX, down first); projection = "
                          "fwd, dX, dW per projection")
     ap.add_argument("--workload",
-                    choices=("block", "block_fp32", "attention", "lm_head", "norm", "norm_gemm",
-                             "convert"),
+                    choices=("block", "block_fp32", "attention", "lm_head", "lm_head_chunked",
+                             "norm", "norm_gemm", "convert"),
                     default="block",
                     help="block: the configuration-3 GEMM set (the headline metric); block_fp32: "
                          "configuration 2's fp32 GEMM set (GPT-small, M=2048); attention: "
                          "configuration 4, fused GQA attention forward + backward; lm_head: "
                          "configuration 5, LM-head GEMMs with the fused cross-entropy between; "
+                         "lm_head_chunked: configuration 5 in vocabulary chunks without the logits "
+                         "buffer (mi_lm_head_xent, --lm-chunk); "
                          "norm: configuration 3's residual add + RMSNorm forward and backward; "
                          "convert: checkpoint weight conversion of one configuration-3 layer and "
                          "the LM head (Python/MLX layout -> engine layout)")
@@ -480,6 +484,119 @@ def lm_head_main(args):
                      "traffic": traffic, "kernel": ops[dom][2], "gemms": [ops[dom][0]],
                      **({"traffic_note": traffic_note} if traffic_note else {}),
                      "avg_launch_ms": round(ms_dom, 4)},
+    }
+    if not args.no_cpu:
+        out["cpu_baseline"] = cpu_lm_head_baseline()
+    print(json.dumps(out))
+
+
+def lm_head_chunked_main(args):
+    """Configuration 5 through mi_lm_head_xent: the same step as the lm_head workload (loss,
+    dX bf16, dE += fp32 with beta 1) without the 524 MB logits, in vocabulary chunks of
+    --lm-chunk columns (pass 1: logits GEMM + running max / sum per chunk; pass 2: the
+    chunks again, last first, logits recomputed except the last chunk's, gradient in place,
+    dX and dE GEMMs). value counts the reference's three GEMMs' FLOPs over the step time
+    (recomputed logits are overhead, not work). The same run also times the reference
+    weight layout (W [H, V]) and the unfused lm_head step, for a same-box comparison."""
+    import torch
+
+    import mi_gemm as mi
+
+    dev = torch.device("cuda:0")
+    mi.init()
+    M, H, V = LMH["M"], LMH["H"], LMH["V"]
+    chunk = args.lm_chunk
+    g = torch.Generator(device=dev)
+    g.manual_seed(5)
+    X = torch.randn((M, H), generator=g, device=dev).to(torch.bfloat16)
+    E = (torch.randn((V, H), generator=g, device=dev) * 0.02).to(torch.bfloat16)
+    W0 = E.t().contiguous()                       # the reference's output_projection_ [H, V]
+    T = torch.randint(0, V, (M,), generator=g, device=dev).to(torch.int32)
+    dX = torch.empty((M, H), dtype=torch.bfloat16, device=dev)
+    dE = torch.zeros((V, H), dtype=torch.float32, device=dev)
+    dW0 = torch.zeros((H, V), dtype=torch.float32, device=dev)
+    row_loss = torch.empty((M,), dtype=torch.float32, device=dev)
+    loss = torch.empty((1,), dtype=torch.float32, device=dev)
+    ws_bytes = mi.lm_head_xent_workspace_size(M, H, V, chunk)
+    ws = torch.empty((ws_bytes,), dtype=torch.uint8, device=dev)
+
+    def call(layout):
+        W, dW = (E, dE) if layout == 1 else (W0, dW0)
+        mi.lm_head_xent(X, W, T, w_layout=layout, chunk=chunk, dX=dX, dW=dW, dw_beta=1.0,
+                        row_loss=row_loss, loss=loss, workspace=ws, sync=False)
+
+    # the unfused step of the lm_head workload, for comparison in the same run
+    logits = torch.empty((M, V), dtype=torch.bfloat16, device=dev)
+    gws = torch.empty(WS_BYTES // 4, dtype=torch.float32, device=dev)
+
+    def unfused():
+        mi.gemm(X, E, logits, M, V, H, transB=True, workspace=gws, sync=False)
+        mi.cross_entropy(logits, T, grad="inplace", sync=False, row_loss=row_loss, loss=loss)
+        mi.gemm(logits, E, dX, M, H, V, workspace=gws, sync=False)
+        mi.gemm(logits, X, dE, V, H, M, transA=True, beta=1.0, workspace=gws, sync=False)
+
+    def timed(fn, steps):
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(steps):
+            fn()
+        torch.cuda.synchronize()
+        return (time.perf_counter() - t0) / steps
+
+    for _ in range(args.warmup):
+        call(1)
+    torch.cuda.synchronize()
+    # attribution: one call with the library's GEMM profiler on (HIP events around every GEMM
+    # launch, on the stream the GEMMs run on)
+    prof = mi.GemmProfiler.instance()
+    prof.enable(True)
+    prof.begin_step()
+    t_attr = timed(lambda: call(1), 1)
+    recs = prof.summary()
+    prof.enable(False)
+    gemm_ms = sum(a["ms"] for a in recs)
+    dom = recs[0]
+    # timed region: --steps calls back to back, no events
+    t1 = timed(lambda: call(1), args.steps)
+    flops = 3 * LMH_GEMM_FLOPS
+    value = flops / t1 / 1e12
+    # same-box comparisons (not the headline figure)
+    call(0)
+    t0_layout = timed(lambda: call(0), max(1, args.steps // 2))
+    unfused()
+    t_unf = timed(unfused, max(1, args.steps // 2))
+    achieved = 2.0 * dom["M"] * dom["N"] * dom["K"] / (dom["ms"] / dom["calls"] / 1e3) / 1e12
+    nch = (V + chunk - 1) // chunk if 0 < chunk < V else 1
+    out = {
+        "metric": "LM head + cross-entropy TFLOP/s (configuration 5, vocabulary chunks, no logits "
+                  "buffer)",
+        "value": round(value, 2), "unit": "TFLOP/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": round(t1 * 1e3, 4),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
+        "data": "synthetic (torch.randn on device; X~N(0,1), E~N(0,0.02), uniform targets)",
+        "config": {"workload": f"LM head M={M} tokens, H={H}, V={V} through mi_lm_head_xent, "
+                               f"chunks of {chunk} vocabulary columns ({nch} chunks): loss, dX "
+                               "(bf16), dE += (fp32); W = E [V, H] (tied-table layout)",
+                   "flops_per_step": flops,
+                   # every chunk but the last is recomputed in pass 2
+                   "gemm_flops_executed": int(flops + LMH_GEMM_FLOPS * (nch - 1) * chunk // V),
+                   "workspace_bytes": ws_bytes,
+                   "unfused_logits_bytes": M * V * 2,
+                   "reference_layout_ms": round(t0_layout * 1e3, 4),
+                   "unfused_step_ms": round(t_unf * 1e3, 4),
+                   "attribution_step_ms": round(t_attr * 1e3, 4),
+                   "attribution_gemm_ms": round(gemm_ms, 4),
+                   "gemms": [{"op": a["op"], "M": a["M"], "N": a["N"], "K": a["K"],
+                              "calls": a["calls"], "ms": round(a["ms"], 4),
+                              "tflops": round(a["tflops"], 1), "kernel": a["kernel"]}
+                             for a in recs]},
+        "roofline": {"bound": "mfma", "achieved": round(achieved, 2), "peak": PEAK_BF16_TFLOPS,
+                     "unit": "TFLOP/s", "frac": round(achieved / PEAK_BF16_TFLOPS, 4),
+                     "traffic": None,
+                     "traffic_note": "no per-launch traffic summary for the chunked call",
+                     "kernel": dom["kernel"],
+                     "gemms": [f"{dom['op']} {dom['M']}x{dom['N']}x{dom['K']}"],
+                     "avg_launch_ms": round(dom["ms"] / dom["calls"], 4)},
     }
     if not args.no_cpu:
         out["cpu_baseline"] = cpu_lm_head_baseline()
@@ -1026,6 +1143,9 @@ def main():
         return
     if args.workload == "lm_head":
         lm_head_main(args)
+        return
+    if args.workload == "lm_head_chunked":
+        lm_head_chunked_main(args)
         return
     if args.workload == "norm":
         norm_main(args)

@@ -274,6 +274,40 @@ int mi_cross_entropy(void* stream, const void* logits, int32_t logits_dtype, int
                      int64_t ld_grad);
 
 /*
+ * LM head + softmax cross-entropy without the [rows, vocab] logits: the logits
+ * are made one vocabulary chunk of `chunk` columns at a time into the
+ * workspace, and never exist whole.  X [rows, ldx] is the final hidden state and
+ * W the output projection, both MI_BF16: w_layout 0 is W [hidden, ldw] (the
+ * reference's output_projection_, logits = X W), w_layout 1 is W [vocab, ldw]
+ * (a tied embedding table, logits = X W^T).  Per row r with y = targets[r] the
+ * results are those of mi_cross_entropy on the bf16 logits (same definitions
+ * of row_loss, loss_out, scale and a target outside [0, vocab)), and then
+ *   dX = G W^T (layout 0) or G W (layout 1)              (if dX is not NULL)
+ *   dW = dw_beta dW + X^T G (layout 0) or G^T X (layout 1) (if dW is not NULL)
+ * with G = scale * (softmax - onehot) rounded to bf16.  Pass 1 runs the logits
+ * GEMM of each chunk and merges its (max, sum exp) into per-row running values;
+ * pass 2, when dX or dW is requested, visits the chunks last first, recomputes
+ * each chunk's logits (the last chunk's are still in the workspace), overwrites
+ * them with G and runs the dX and dW GEMMs of the chunk (dX accumulated in
+ * fp32, in the workspace when dX is MI_BF16).  dX is MI_BF16 or MI_F32
+ * [rows, lddx]; dW is MI_BF16 or MI_F32 with W's shape.  chunk <= 0 or >= vocab
+ * means one chunk (no recomputation).  workspace (device memory, not overlapping
+ * any argument) holds at least mi_lm_head_xent_workspace_size bytes; bytes
+ * beyond that are split-K workspace for the GEMMs.  Deterministic.  Replaces the
+ * output projection and loss of the reference's step: final_h.matmul(
+ * output_projection_) (Transformer.cpp:193-194), CrossEntropyLoss::forward /
+ * backward (Loss.cpp:43-195), accumulate_output_projection_grads and
+ * gemm_proj_trans_b for grad_final_h (Transformer.cpp:600-616).
+ */
+size_t mi_lm_head_xent_workspace_size(int64_t rows, int64_t hidden, int64_t vocab, int64_t chunk,
+                                      int32_t dx_dtype);
+int mi_lm_head_xent(void* stream, const void* X, int64_t ldx, const void* W, int32_t w_layout, int64_t ldw,
+                    const uint32_t* targets, int64_t rows, int64_t hidden, int64_t vocab, float scale,
+                    float* row_loss, float* loss_out, void* dX, int32_t dx_dtype, int64_t lddx, void* dW,
+                    int32_t dw_dtype, int64_t lddw, float dw_beta, int64_t chunk, void* workspace,
+                    size_t workspace_bytes);
+
+/*
  * RMSNorm forward over rows of dims values: with residual != NULL, first
  * x += residual (x updated in place, in its own dtype), then
  *   y = x / sqrt(sum(x^2)/dims + eps) * weight

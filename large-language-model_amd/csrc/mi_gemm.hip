@@ -1314,6 +1314,161 @@ int mi_cross_entropy(void* stream, const void* logits, int32_t logits_dtype, int
   return e == hipSuccess ? MI_OK : fail(MI_ERR_HIP, "cross_entropy launch: %s", hipGetErrorString(e));
 }
 
+}  // extern "C"
+
+namespace {
+
+// Workspace carve of mi_lm_head_xent: the bf16 logits chunk [rows][lm_chunk_ld], three fp32
+// row arrays (running max, running sum then scale / sum, target logit), and an fp32
+// [rows][hidden] accumulator of dX when dX is bf16; each part 256-byte aligned, plus 256
+// bytes for aligning the base.  What is left over is split-K workspace for the GEMMs.
+int64_t lm_chunk_ld(int64_t chunk) { return (chunk + 7) / 8 * 8; }
+size_t align256(size_t b) { return (b + 255) / 256 * 256; }
+size_t lm_fixed_bytes(int64_t rows, int64_t hidden, int64_t chunk, bool dx_acc) {
+  return 256 + align256((size_t)rows * (size_t)lm_chunk_ld(chunk) * 2) + 3 * align256((size_t)rows * 4) +
+         (dx_acc ? align256((size_t)rows * (size_t)hidden * 4) : 0);
+}
+
+int lm_gemm(hipStream_t st, int tA, int tB, int64_t M, int64_t N, int64_t K, const void* A, int64_t lda,
+            const void* B, int64_t ldb, float beta, void* C, int64_t ldc, int32_t dtype_c, void* ws,
+            size_t ws_bytes) {
+  Problem P;
+  P.transA = tA; P.transB = tB;
+  P.M = M; P.N = N; P.K = K;
+  P.alpha = 1.0f; P.beta = beta;
+  P.A = A; P.B = B; P.lda = lda; P.ldb = ldb;
+  P.dtype_in = MI_BF16;
+  P.C = C; P.ldc = ldc; P.dtype_c = dtype_c;
+  P.bt = single_batch();
+  std::memset(&P.ep, 0, sizeof(P.ep));
+  P.ws = ws;
+  P.ws_bytes = ws_bytes;
+  return run(P, st);
+}
+
+}  // namespace
+
+extern "C" {
+
+size_t mi_lm_head_xent_workspace_size(int64_t rows, int64_t hidden, int64_t vocab, int64_t chunk,
+                                      int32_t dx_dtype) {
+  if (rows <= 0 || hidden <= 0 || vocab <= 0) return 0;
+  if (chunk <= 0 || chunk > vocab) chunk = vocab;
+  return lm_fixed_bytes(rows, hidden, chunk, dx_dtype == MI_BF16);
+}
+
+int mi_lm_head_xent(void* stream, const void* X, int64_t ldx, const void* W, int32_t w_layout, int64_t ldw,
+                    const uint32_t* targets, int64_t rows, int64_t hidden, int64_t vocab, float scale,
+                    float* row_loss, float* loss_out, void* dX, int32_t dx_dtype, int64_t lddx, void* dW,
+                    int32_t dw_dtype, int64_t lddw, float dw_beta, int64_t chunk, void* workspace,
+                    size_t workspace_bytes) {
+  if (rows < 0 || hidden < 0 || vocab < 0) return fail(MI_ERR_SHAPE, "negative size");
+  if (rows == 0 || vocab == 0) return MI_OK;
+  if (hidden == 0) return fail(MI_ERR_SHAPE, "hidden = 0");
+  if (rows > INT32_MAX || hidden > INT32_MAX || vocab > INT32_MAX)
+    return fail(MI_ERR_SHAPE, "size exceeds 2^31-1");
+  if (w_layout != 0 && w_layout != 1) return fail(MI_ERR_UNSUPPORTED, "w_layout %d (0 or 1)", w_layout);
+  if (!X || !W || !targets || !row_loss) return fail(MI_ERR_NULL, "X, W, targets or row_loss is NULL");
+  if (ldx < hidden) return fail(MI_ERR_LD, "ldx=%lld < hidden=%lld", (long long)ldx, (long long)hidden);
+  const int64_t w_row = w_layout == 0 ? vocab : hidden;
+  if (ldw < w_row) return fail(MI_ERR_LD, "ldw=%lld < %lld", (long long)ldw, (long long)w_row);
+  if (dX) {
+    if (dx_dtype != MI_F32 && dx_dtype != MI_BF16) return fail(MI_ERR_DTYPE, "dX dtype %d", dx_dtype);
+    if (lddx < hidden) return fail(MI_ERR_LD, "lddx=%lld < hidden=%lld", (long long)lddx, (long long)hidden);
+  }
+  if (dW) {
+    if (dw_dtype != MI_F32 && dw_dtype != MI_BF16) return fail(MI_ERR_DTYPE, "dW dtype %d", dw_dtype);
+    if (lddw < w_row) return fail(MI_ERR_LD, "lddw=%lld < %lld", (long long)lddw, (long long)w_row);
+  }
+  if (((uintptr_t)X & 1u) || ((uintptr_t)W & 1u) || ((uintptr_t)targets & 3u) || ((uintptr_t)row_loss & 3u) ||
+      ((uintptr_t)loss_out & 3u))
+    return fail(MI_ERR_UNSUPPORTED, "pointers must be aligned to their element size");
+  if (chunk <= 0 || chunk > vocab) chunk = vocab;
+  const bool dx_acc = dX && dx_dtype == MI_BF16;
+  const size_t need = lm_fixed_bytes(rows, hidden, chunk, dx_acc);
+  if (!workspace || workspace_bytes < need)
+    return fail(MI_ERR_WORKSPACE, "workspace of %zu bytes < %zu (mi_lm_head_xent_workspace_size)",
+                workspace_bytes, need);
+  const int st0 = init_devices();
+  if (st0 != MI_OK) return st0;
+  hipStream_t st = (hipStream_t)stream;
+  // carve the workspace
+  char* base = (char*)(((uintptr_t)workspace + 255) & ~(uintptr_t)255);
+  const int64_t ldl = lm_chunk_ld(chunk);
+  uint16_t* L = (uint16_t*)base;
+  base += align256((size_t)rows * (size_t)ldl * 2);
+  float* run_m = (float*)base;
+  base += align256((size_t)rows * 4);
+  float* run_s = (float*)base;
+  base += align256((size_t)rows * 4);
+  float* xy = (float*)base;
+  base += align256((size_t)rows * 4);
+  float* acc = nullptr;
+  if (dx_acc) {
+    acc = (float*)base;
+    base += align256((size_t)rows * (size_t)hidden * 4);
+  }
+  void* gws = base;
+  const size_t gws_bytes = workspace_bytes - (size_t)(base - (char*)workspace);
+  const uint16_t* w16 = (const uint16_t*)W;
+  const int64_t nchunks = (vocab + chunk - 1) / chunk;
+  // logits of chunk c: L[rows][n] = X Wc, Wc = W[:, c0:c0+n] (layout 0) or W[c0:c0+n, :]^T (layout 1)
+  auto logits = [&](int64_t c0, int64_t n) {
+    return w_layout == 0 ? lm_gemm(st, 0, 0, rows, n, hidden, X, ldx, w16 + c0, ldw, 0.0f, L, ldl, MI_BF16, gws,
+                                   gws_bytes)
+                         : lm_gemm(st, 0, 1, rows, n, hidden, X, ldx, w16 + c0 * ldw, ldw, 0.0f, L, ldl, MI_BF16,
+                                   gws, gws_bytes);
+  };
+  auto herr = [](hipError_t e) {
+    return e == hipSuccess ? MI_OK : fail(MI_ERR_HIP, "lm_head_xent launch: %s", hipGetErrorString(e));
+  };
+  // pass 1: running (max, sum) over the chunks in order, then the row losses
+  for (int64_t c = 0; c < nchunks; ++c) {
+    const int64_t c0 = c * chunk, n = std::min(chunk, vocab - c0);
+    int r = logits(c0, n);
+    if (r != MI_OK) return r;
+    r = herr(launch_xent_chunk_stats(L, ldl, (int)rows, (int)n, (int)c0, targets, run_m, run_s, xy, c == 0, st));
+    if (r != MI_OK) return r;
+  }
+  int r = herr(launch_xent_chunk_finish((int)rows, (int)vocab, targets, run_m, run_s, xy, scale, row_loss, st));
+  if (r == MI_OK && loss_out) r = herr(launch_xent_mean(row_loss, (int)rows, scale, loss_out, st));
+  if (r != MI_OK || (!dX && !dW)) return r;
+  // pass 2, last chunk first: its logits are still in L; every other chunk is recomputed
+  void* dx_c = dx_acc ? (void*)acc : dX;
+  const int64_t dx_ld = dx_acc ? hidden : lddx;
+  const int32_t dx_t = dx_acc ? MI_F32 : dx_dtype;
+  const int64_t esw = dw_dtype == MI_BF16 ? 2 : 4;
+  for (int64_t c = nchunks - 1; c >= 0; --c) {
+    const int64_t c0 = c * chunk, n = std::min(chunk, vocab - c0);
+    if (c != nchunks - 1 && (r = logits(c0, n)) != MI_OK) return r;
+    r = herr(launch_xent_chunk_grad(L, ldl, (int)rows, (int)n, (int)c0, targets, run_m, run_s, scale, st));
+    if (r != MI_OK) return r;
+    const float bx = c == nchunks - 1 ? 0.0f : 1.0f;
+    if (dX) {  // dX (+)= dL_c Wc^T
+      r = w_layout == 0 ? lm_gemm(st, 0, 1, rows, hidden, n, L, ldl, w16 + c0, ldw, bx, dx_c, dx_ld, dx_t, gws,
+                                  gws_bytes)
+                        : lm_gemm(st, 0, 0, rows, hidden, n, L, ldl, w16 + c0 * ldw, ldw, bx, dx_c, dx_ld, dx_t,
+                                  gws, gws_bytes);
+      if (r != MI_OK) return r;
+    }
+    if (dW) {  // dW's chunk = dw_beta dW's chunk + X^T dL_c (layout 0) or dL_c^T X (layout 1)
+      r = w_layout == 0 ? lm_gemm(st, 1, 0, hidden, n, rows, X, ldx, L, ldl, dw_beta,
+                                  (char*)dW + c0 * esw, lddw, dw_dtype, gws, gws_bytes)
+                        : lm_gemm(st, 1, 0, n, hidden, rows, L, ldl, X, ldx, dw_beta,
+                                  (char*)dW + c0 * lddw * esw, lddw, dw_dtype, gws, gws_bytes);
+      if (r != MI_OK) return r;
+    }
+  }
+  if (dx_acc) {
+    ConvParams cp{};
+    cp.src = acc; cp.dst = dX; cp.src_ld = hidden; cp.dst_ld = lddx;
+    cp.row0 = 0; cp.rows = rows; cp.cols = hidden;
+    cp.src_dtype = MI_F32; cp.dst_dtype = MI_BF16;
+    r = herr(launch_convert(cp, false, current_cus(), st));
+  }
+  return r;
+}
+
 int mi_gemm_describe(int transA, int transB, int64_t M, int64_t N, int64_t K, int32_t dtype_in,
                      int64_t batch, int32_t epi_mode, size_t workspace_bytes, char* buf,
                      size_t buf_len) {

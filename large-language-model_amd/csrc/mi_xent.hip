@@ -203,7 +203,7 @@ __global__ void __launch_bounds__(XENT_THREADS) xent_stream_kernel(XentParams p)
   for (int v = tid; v < p.vocab; v += XENT_THREADS) {
     const float x = load_elem<IN_BF16>(lrow, v);
     if (x > m) {
-      s = (m == -INFINITY ? 0.0f : s * __builtin_amdgcn_exp2f((m - x) * XENT_L2E)) + 1.0f;
+      s = (m == -INFINITY ? s * 0.0f : s * __builtin_amdgcn_exp2f((m - x) * XENT_L2E)) + 1.0f;  // keeps a NaN
       m = x;
     } else if (x != -INFINITY) {
       s += __builtin_amdgcn_exp2f((x - m) * XENT_L2E);  // NaN x propagates
@@ -261,6 +261,124 @@ __global__ void __launch_bounds__(1024) xent_mean_kernel(const float* row_loss, 
   }
 }
 
+// ---- vocabulary chunks ---------------------------------------------------------
+// The LM head without a full logits buffer: chunk c holds columns [c0, c0 + n) of
+// every row in L[rows][ldl] (bf16).  Pass 1 merges each chunk's (max, sum exp) into
+// the row's running (m, s) in chunk order and records the target's logit when it
+// lies in the chunk; the finish kernel turns (m, s, x_y) into the row loss and keeps
+// m and scale/s; pass 2 overwrites each recomputed chunk with its gradient
+// scale * (softmax - onehot).  Every merge runs in a fixed order (deterministic).
+__global__ void __launch_bounds__(256) xent_chunk_stats_kernel(const uint16_t* L, int64_t ldl, int n, int c0,
+                                                               const uint32_t* targets, float* run_m,
+                                                               float* run_s, float* xy, int first) {
+  const int row = blockIdx.x;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const uint16_t* lrow = L + (int64_t)row * ldl;
+  float m = -INFINITY, s = 0.0f;
+  if ((n & 7) == 0 && (ldl & 7) == 0) {  // 16-byte vectors of 8 logits, one rescale per vector
+    for (int v = tid * 8; v < n; v += 256 * 8) {
+      const xu32x4_t q = *(const xu32x4_t*)(lrow + v);
+      float x[8], mx = -INFINITY;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        x[e] = elem_of<true>(q, e);
+        mx = fmaxf(mx, x[e]);
+      }
+      if (mx > m) {
+        s = m == -INFINITY ? s * 0.0f : s * __builtin_amdgcn_exp2f((m - mx) * XENT_L2E);  // keeps a NaN
+        m = mx;
+      }
+      if (m != -INFINITY) {
+        const float mneg = -m * XENT_L2E;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) s += __builtin_amdgcn_exp2f(__builtin_fmaf(x[e], XENT_L2E, mneg));
+      } else {  // every logit so far is -inf or NaN (fmaxf skips NaN): add the NaNs
+#pragma unroll
+        for (int e = 0; e < 8; ++e) s += x[e] == -INFINITY ? 0.0f : x[e];
+      }
+    }
+  } else {
+    for (int v = tid; v < n; v += 256) {
+      const float x = bf16_bits_to_f32(lrow[v]);
+      if (x > m) {
+        s = (m == -INFINITY ? s * 0.0f : s * __builtin_amdgcn_exp2f((m - x) * XENT_L2E)) + 1.0f;  // keeps a NaN
+        m = x;
+      } else if (x != -INFINITY) {
+        s += __builtin_amdgcn_exp2f((x - m) * XENT_L2E);  // NaN x propagates
+      }
+    }
+  }
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) {
+    const float m2 = __shfl_xor(m, o, 64), s2 = __shfl_xor(s, o, 64);
+    merge_ms(m, s, m2, s2);
+  }
+  __shared__ float red_m[4], red_s[4];
+  if (lane == 0) {
+    red_m[wave] = m;
+    red_s[wave] = s;
+  }
+  __syncthreads();
+  if (tid == 0) {
+    float M = red_m[0], S = red_s[0];
+#pragma unroll
+    for (int w = 1; w < 4; ++w) merge_ms(M, S, red_m[w], red_s[w]);
+    if (!first) {  // the running part (earlier chunks) first, then this chunk
+      float M0 = run_m[row], S0 = run_s[row];
+      merge_ms(M0, S0, M, S);
+      M = M0;
+      S = S0;
+    }
+    run_m[row] = M;
+    run_s[row] = S;
+    const uint32_t y = targets[row];
+    if (y - (uint32_t)c0 < (uint32_t)n) xy[row] = bf16_bits_to_f32(lrow[y - (uint32_t)c0]);
+  }
+}
+
+// Row loss from the merged (m, s) and the target's logit; run_s becomes scale / s.
+__global__ void __launch_bounds__(256) xent_chunk_finish_kernel(int rows, int vocab, const uint32_t* targets,
+                                                                const float* run_m, float* run_s,
+                                                                const float* xy, float scale, float* row_loss) {
+  const int r = blockIdx.x * 256 + threadIdx.x;
+  if (r >= rows) return;
+  const float M = run_m[r], S = run_s[r];
+  float loss = __builtin_nanf("");
+  if (targets[r] < (uint32_t)vocab) loss = clamp_loss((log2f(S) - (xy[r] - M) * XENT_L2E) * XENT_LN2);
+  row_loss[r] = loss;
+  run_s[r] = scale / S;
+}
+
+// Gradient of one chunk in place: L[r][v] = scale * (exp(x - m) / s - [c0 + v == y]).
+__global__ void __launch_bounds__(256) xent_chunk_grad_kernel(uint16_t* L, int64_t ldl, int n, int c0,
+                                                              const uint32_t* targets, const float* run_m,
+                                                              const float* run_inv, float scale) {
+  const int row = blockIdx.x;
+  uint16_t* lrow = L + (int64_t)row * ldl;
+  const float mneg = -run_m[row] * XENT_L2E, inv = run_inv[row];
+  const uint32_t yc = targets[row] - (uint32_t)c0;  // the target's column in the chunk (or past n)
+  const bool vec = (n & 7) == 0 && (ldl & 7) == 0;  // 16-byte rows of 8 logits
+  if (vec) {
+    for (int v = threadIdx.x * 8; v < n; v += 256 * 8) {
+      xu32x4_t q = *(const xu32x4_t*)(lrow + v);
+      float g[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        g[e] = __builtin_amdgcn_exp2f(__builtin_fmaf(elem_of<true>(q, e), XENT_L2E, mneg)) * inv;
+        if ((uint32_t)(v + e) == yc) g[e] -= scale;
+      }
+      *(xu32x4_t*)(lrow + v) = xu32x4_t{pack_bf16x2(g[0], g[1]), pack_bf16x2(g[2], g[3]),
+                                        pack_bf16x2(g[4], g[5]), pack_bf16x2(g[6], g[7])};
+    }
+  } else {
+    for (int v = threadIdx.x; v < n; v += 256) {
+      float g = __builtin_amdgcn_exp2f(__builtin_fmaf(bf16_bits_to_f32(lrow[v]), XENT_L2E, mneg)) * inv;
+      if ((uint32_t)v == yc) g -= scale;
+      lrow[v] = (uint16_t)f32_to_bf16_rne(g);
+    }
+  }
+}
+
 template <bool IN_BF16, bool OUT_BF16>
 hipError_t launch_vec(const XentParams& p, int nv, hipStream_t st) {
   const dim3 grid((unsigned)p.rows), block(XENT_THREADS);
@@ -296,6 +414,29 @@ hipError_t launch_xent(const XentParams& p, bool in_bf16, bool out_bf16, bool ve
                     : launch_one<true, false>(p, vector_path, stream);
   return out_bf16 ? launch_one<false, true>(p, vector_path, stream)
                   : launch_one<false, false>(p, vector_path, stream);
+}
+
+hipError_t launch_xent_chunk_stats(const void* L, int64_t ldl, int rows, int n, int c0,
+                                   const uint32_t* targets, float* run_m, float* run_s, float* xy, bool first,
+                                   hipStream_t stream) {
+  hipLaunchKernelGGL(xent_chunk_stats_kernel, dim3((unsigned)rows), dim3(256), 0, stream, (const uint16_t*)L,
+                     ldl, n, c0, targets, run_m, run_s, xy, first ? 1 : 0);
+  return hipGetLastError();
+}
+
+hipError_t launch_xent_chunk_finish(int rows, int vocab, const uint32_t* targets, const float* run_m,
+                                    float* run_s, const float* xy, float scale, float* row_loss,
+                                    hipStream_t stream) {
+  hipLaunchKernelGGL(xent_chunk_finish_kernel, dim3((unsigned)((rows + 255) / 256)), dim3(256), 0, stream, rows,
+                     vocab, targets, run_m, run_s, xy, scale, row_loss);
+  return hipGetLastError();
+}
+
+hipError_t launch_xent_chunk_grad(void* L, int64_t ldl, int rows, int n, int c0, const uint32_t* targets,
+                                  const float* run_m, const float* run_inv, float scale, hipStream_t stream) {
+  hipLaunchKernelGGL(xent_chunk_grad_kernel, dim3((unsigned)rows), dim3(256), 0, stream, (uint16_t*)L, ldl, n,
+                     c0, targets, run_m, run_inv, scale);
+  return hipGetLastError();
 }
 
 hipError_t launch_xent_mean(const float* row_loss, int rows, float scale, float* loss_out,

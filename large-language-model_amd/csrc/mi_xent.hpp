@@ -30,4 +30,17 @@ hipError_t launch_xent(const XentParams& p, bool in_bf16, bool out_bf16, bool ve
 hipError_t launch_xent_mean(const float* row_loss, int rows, float scale, float* loss_out,
                             hipStream_t stream);
 
+// Vocabulary chunks (bf16 logits of columns [c0, c0 + n) in L[rows][ldl]): pass 1
+// merges each chunk into the running (run_m, run_s) and records the target's logit in
+// xy; finish writes the row losses and turns run_s into scale / s; pass 2 overwrites a
+// recomputed chunk with its gradient.
+hipError_t launch_xent_chunk_stats(const void* L, int64_t ldl, int rows, int n, int c0,
+                                   const uint32_t* targets, float* run_m, float* run_s, float* xy, bool first,
+                                   hipStream_t stream);
+hipError_t launch_xent_chunk_finish(int rows, int vocab, const uint32_t* targets, const float* run_m,
+                                    float* run_s, const float* xy, float scale, float* row_loss,
+                                    hipStream_t stream);
+hipError_t launch_xent_chunk_grad(void* L, int64_t ldl, int rows, int n, int c0, const uint32_t* targets,
+                                  const float* run_m, const float* run_inv, float scale, hipStream_t stream);
+
 }  // namespace mig

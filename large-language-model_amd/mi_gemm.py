@@ -38,7 +38,8 @@ C_SYMBOLS = (
     "mi_convert_matrix", "mi_flash_attn_bwd_workspace_size", "mi_profiler_enable",
     "mi_profiler_begin_step", "mi_profiler_count", "mi_profiler_record", "mi_profiler_totals",
     "mi_profiler_reset", "mi_gemm_noalloc", "mi_flash_attn_fwd_scaled", "mi_flash_attn_bwd_scaled",
-    "mi_convert_matrices", "mi_rmsnorm_fold_weight",
+    "mi_convert_matrices", "mi_rmsnorm_fold_weight", "mi_lm_head_xent",
+    "mi_lm_head_xent_workspace_size",
 )
 MI_ATTN_O_BHTD, MI_ATTN_O_BTHD = 0, 1
 
@@ -151,6 +152,11 @@ def load_library():
     L.mi_cross_entropy.restype = ctypes.c_int
     L.mi_cross_entropy.argtypes = [vp, vp, i32, i64, vp, i64, i64, ctypes.c_float, vp, vp, vp,
                                    i32, i64]
+    L.mi_lm_head_xent_workspace_size.restype = ctypes.c_size_t
+    L.mi_lm_head_xent_workspace_size.argtypes = [i64, i64, i64, i64, i32]
+    L.mi_lm_head_xent.restype = ctypes.c_int
+    L.mi_lm_head_xent.argtypes = [vp, vp, i64, vp, i32, i64, vp, i64, i64, i64, ctypes.c_float, vp, vp,
+                                  vp, i32, i64, vp, i32, i64, ctypes.c_float, i64, vp, ctypes.c_size_t]
     L.mi_rmsnorm_fwd.restype = ctypes.c_int
     L.mi_rmsnorm_fwd.argtypes = [vp, vp, vp, vp, i32, vp, vp, i64, i64, i64, i32, ctypes.c_float]
     L.mi_rmsnorm_bwd_workspace_size.restype = ctypes.c_size_t
@@ -780,6 +786,69 @@ def cross_entropy(logits, targets, grad="new", grad_dtype=None, scale=None, sync
     else:
         _check("mi_cross_entropy", st)
     return loss, row_loss, g
+
+
+def lm_head_xent_workspace_size(rows, hidden, vocab, chunk=8192, dx_dtype=None) -> int:
+    """Bytes of workspace lm_head_xent needs (mi_lm_head_xent_workspace_size)."""
+    torch = _torch()
+    dt = MI_F32 if dx_dtype == torch.float32 else MI_BF16
+    return int(load_library().mi_lm_head_xent_workspace_size(rows, hidden, vocab, chunk, dt))
+
+
+def lm_head_xent(X, W, targets, w_layout=0, chunk=8192, scale=None, dX="new", dx_dtype=None,
+                 dW=None, dw_beta=0.0, row_loss=None, loss=None, workspace=None, sync=None):
+    """LM head + cross-entropy over vocabulary chunks, no [rows, vocab] logits
+    (mi_lm_head_xent; the reference's final_h.matmul(output_projection_), Transformer.cpp:
+    193-194, CrossEntropyLoss, Loss.cpp:43-195, and the output projection backward,
+    Transformer.cpp:600-616).
+
+    X [rows, hidden] bf16; W bf16, [hidden, vocab] for w_layout 0 (logits = X W, the
+    reference's output_projection_) or [vocab, hidden] for w_layout 1 (logits = X W^T).
+    Returns (loss, row_loss, dX): dX = G W^T or G W with G = scale * (softmax - onehot);
+    dX "new" allocates it in dx_dtype (default bf16), None skips it, or a tensor to write
+    into. dW, if given (W's shape, bf16 or fp32), becomes dw_beta * dW + X^T G (or G^T X).
+    scale defaults to 1 / rows. workspace: a device tensor of at least
+    lm_head_xent_workspace_size bytes (allocated when None)."""
+    torch = _torch()
+    rows, hidden = X.shape
+    vocab = W.shape[1] if w_layout == 0 else W.shape[0]
+    if (W.shape[0] if w_layout == 0 else W.shape[1]) != hidden:
+        raise ValueError(f"W {tuple(W.shape)} does not match hidden={hidden} for w_layout {w_layout}")
+    for name, t in (("X", X), ("W", W)):
+        if t.dtype != torch.bfloat16 or t.stride(-1) != 1:
+            raise ValueError(f"{name} must be bf16 with a contiguous last dimension")
+    tg = targets.reshape(-1).to(torch.int32).contiguous()
+    if tg.numel() != rows:
+        raise ValueError(f"targets has {tg.numel()} entries for {rows} rows")
+    if scale is None:
+        scale = 1.0 / rows if rows else 0.0
+    dev = X.device
+    if row_loss is None:
+        row_loss = torch.empty((rows,), dtype=torch.float32, device=dev)
+    if loss is None:
+        loss = torch.empty((1,), dtype=torch.float32, device=dev)
+    if isinstance(dX, str) and dX == "new":
+        dX = torch.empty((rows, hidden), dtype=dx_dtype or torch.bfloat16, device=dev)
+    if dX is not None and (dX.shape != X.shape or dX.stride(-1) != 1):
+        raise ValueError("dX must match X's shape with a contiguous last dimension")
+    if dW is not None and (dW.shape != W.shape or dW.stride(-1) != 1):
+        raise ValueError("dW must match W's shape with a contiguous last dimension")
+    dxt = _dt(dX) if dX is not None else MI_BF16
+    need = int(load_library().mi_lm_head_xent_workspace_size(rows, hidden, vocab, chunk, dxt))
+    if workspace is None:
+        workspace = torch.empty((max(need, 1),), dtype=torch.uint8, device=dev)
+    wsb = workspace.numel() * workspace.element_size()
+    ld = lambda t: t.stride(0) if t.shape[0] > 1 else t.shape[1]  # noqa: E731
+    st = load_library().mi_lm_head_xent(
+        _stream(), _ptr(X), ld(X), _ptr(W), int(w_layout), ld(W), _ptr(tg), rows, hidden, vocab,
+        float(scale), _ptr(row_loss), _ptr(loss), _ptr(dX), dxt, ld(dX) if dX is not None else 0,
+        _ptr(dW), _dt(dW) if dW is not None else MI_F32, ld(dW) if dW is not None else 0,
+        float(dw_beta), int(chunk), _ptr(workspace), wsb)
+    if sync is None:
+        _finish("mi_lm_head_xent", st)
+    else:
+        _check("mi_lm_head_xent", st)
+    return loss, row_loss, dX
 
 
 class CrossEntropyLoss:

@@ -270,6 +270,43 @@ def test_cross_entropy_validation(mi):
     assert st == 5 and "aligned" in msg
 
 
+def test_lm_head_xent_validation(mi):
+    """mi_lm_head_xent's workspace size and argument checks (no device needed)."""
+    lib = mi.load_library()
+    vp = ctypes.c_void_p
+    a256 = lambda b: (b + 255) // 256 * 256  # noqa: E731
+    ws = lib.mi_lm_head_xent_workspace_size
+    # bf16 logits chunk (rows x chunk rounded up to 8), 3 fp32 row arrays, fp32 dX accumulator
+    assert ws(8192, 2048, 32000, 8192, mi.MI_BF16) == \
+        256 + a256(8192 * 8192 * 2) + 3 * a256(8192 * 4) + a256(8192 * 2048 * 4)
+    assert ws(100, 64, 777, 100, mi.MI_F32) == 256 + a256(100 * 104 * 2) + 3 * a256(400)
+    assert ws(100, 64, 777, 0, mi.MI_F32) == ws(100, 64, 777, 5000, mi.MI_F32) == \
+        256 + a256(100 * 784 * 2) + 3 * a256(400)                   # one chunk of the vocab
+    assert ws(0, 64, 777, 100, mi.MI_F32) == 0
+
+    def call(rows=4, hidden=64, vocab=100, ldx=64, layout=0, ldw=100, X=4096, W=8192, T=16384,
+             RL=20480, dX=None, dxt=1, lddx=64, dW=None, dwt=0, lddw=100, wsb=1 << 20):
+        st = lib.mi_lm_head_xent(None, vp(X) if X else None, ldx, vp(W) if W else None, layout, ldw,
+                                 vp(T) if T else None, rows, hidden, vocab, 0.25,
+                                 vp(RL) if RL else None, None, vp(dX) if dX else None, dxt, lddx,
+                                 vp(dW) if dW else None, dwt, lddw, 1.0, 64, vp(1 << 24), wsb)
+        return st, lib.mi_last_error().decode()
+
+    assert call(rows=0)[0] == 0 and call(vocab=0)[0] == 0
+    assert call(rows=-1)[0] == 1 and call(hidden=0)[0] == 1
+    assert call(layout=2)[0] == 5
+    assert call(X=0)[0] == 3 and call(W=0)[0] == 3 and call(T=0)[0] == 3 and call(RL=0)[0] == 3
+    st, msg = call(ldx=10)
+    assert st == 2 and "ldx" in msg
+    assert call(ldw=99)[0] == 2                       # layout 0: W [hidden, ldw >= vocab]
+    assert call(layout=1, ldw=63)[0] == 2             # layout 1: W [vocab, ldw >= hidden]
+    assert call(dX=65536, dxt=7)[0] == 4 and call(dX=65536, lddx=10)[0] == 2
+    assert call(dW=65536, dwt=3)[0] == 4 and call(dW=65536, lddw=50)[0] == 2
+    assert call(X=4097)[0] == 5
+    st, msg = call(wsb=1000)
+    assert st == 6 and "workspace" in msg             # MI_ERR_WORKSPACE
+
+
 def test_rmsnorm_validation(mi):
     # mi_rmsnorm_fwd / _bwd reject bad arguments before any device work.
     lib = mi.load_library()
