@@ -435,10 +435,20 @@ int validate(const Problem& P) {
 // for each XCD's resident tiles (its first round: 32 CUs x workgroups per CU)
 // and takes the group height in {1, 2, 4, 8, 16} whose XCDs fill the fewest panel
 // bytes, sum over XCDs of (distinct row panels x BM + distinct column panels x BN)
-// per K row; ties keep 8.  Configuration 3's 2048 x 5632 weight gradients (240
-// tiles of 256 x 192, 30 per XCD) get 4 (4 row panels x 7.5 column panels:
-// 2464 panel columns per K row against 2768 for 8 x 3.75); block set with
-// per-XCD K rotation 1110-1114 -> 1126-1128 TFLOP/s on one box (gate dW
+// per K row.  For bf16 C, ties go to the height whose resident tiles span more
+// column panels, then to 8 (fp32 C: to 8): the C tiles an XCD stores at once then
+// cover a wider window of each output row.  With a row pitch that is a multiple of
+// 4 KB (N = 2048 bf16), a window of 4 of the 8 column tiles (height 8) puts every
+// row's stores in the same half of each 4 KB period, where the memory channels
+// interleave; the full width (height 4, the same panel bytes) measured 1092 -> 1146
+// TFLOP/s (o projection, 8192 x 2048 x 2048 forward), 1111 -> 1180 (its dX), 1210
+// -> 1264 (QKV dX) and 1325 -> 1361 (down forward), alternating on one box; a
+// padded C pitch (+128 bytes) gave the same gains with height 8.  The fp32 weight
+// gradients do not gain: the o projection's (2048 x 2048, 128 x 128 tiles) lost
+// 3.6 % in the block set with the wider window.  Configuration 3's 2048 x 5632
+// weight gradients (240 tiles of 256 x 192, 30 per XCD) get 4 (4 row panels x 7.5
+// column panels: 2464 panel columns per K row against 2768 for 8 x 3.75); block
+// set with per-XCD K rotation 1110-1114 -> 1126-1128 TFLOP/s on one box (gate dW
 // 917-926 -> 1022-1036).
 int group_rows(const Problem& P, const Plan& plan) {
   const mi_batch& b = P.bt;
@@ -450,10 +460,10 @@ int group_rows(const Problem& P, const Plan& plan) {
   const int64_t resident = std::max<int64_t>(1, (int64_t)current_cus() / 8 * per_cu);
   const int64_t q = tiles / 8, rem = tiles % 8;
   int best = MI_GROUP_M;
-  int64_t best_cost = INT64_MAX;
+  int64_t best_cost = INT64_MAX, best_cols = 0;
   std::vector<char> seen_m((size_t)tm), seen_n((size_t)tn);
   for (int g : {8, 16, 4, 2, 1}) {
-    int64_t cost = 0;
+    int64_t cost = 0, cols = 0;
     for (int64_t x = 0; x < 8; ++x) {
       const int64_t first = x * q + std::min<int64_t>(x, rem);
       const int64_t count = std::min<int64_t>(q + (x < rem ? 1 : 0), resident);
@@ -469,8 +479,10 @@ int group_rows(const Problem& P, const Plan& plan) {
         if (!seen_n[(size_t)n]) seen_n[(size_t)n] = 1, ++dn;
       }
       cost += dm * ts.bm + dn * ts.bn;
+      cols += dn;
     }
-    if (cost < best_cost) best_cost = cost, best = g;
+    const bool wider = P.dtype_c == MI_BF16 && cols > best_cols;
+    if (cost < best_cost || (cost == best_cost && wider)) best_cost = cost, best_cols = cols, best = g;
   }
   return best;
 }
