@@ -276,9 +276,10 @@ def test_lm_head_xent_validation(mi):
     vp = ctypes.c_void_p
     a256 = lambda b: (b + 255) // 256 * 256  # noqa: E731
     ws = lib.mi_lm_head_xent_workspace_size
-    # bf16 logits chunk (rows x chunk rounded up to 8), 3 fp32 row arrays, fp32 dX accumulator
+    # bf16 logits chunk (rows x chunk rounded up to 8, + 128 when a multiple of 1024), 3 fp32
+    # row arrays, fp32 dX accumulator
     assert ws(8192, 2048, 32000, 8192, mi.MI_BF16) == \
-        256 + a256(8192 * 8192 * 2) + 3 * a256(8192 * 4) + a256(8192 * 2048 * 4)
+        256 + a256(8192 * 8320 * 2) + 3 * a256(8192 * 4) + a256(8192 * 2048 * 4)
     assert ws(100, 64, 777, 100, mi.MI_F32) == 256 + a256(100 * 104 * 2) + 3 * a256(400)
     assert ws(100, 64, 777, 0, mi.MI_F32) == ws(100, 64, 777, 5000, mi.MI_F32) == \
         256 + a256(100 * 784 * 2) + 3 * a256(400)                   # one chunk of the vocab
