@@ -220,8 +220,9 @@ int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
 //   * when even S tiles leave half the CUs idle, K is split over S tiles, given
 //     a workspace -- also for S tiles chosen by the fill rule and for the
 //     register-staged loader (unaligned operands);
-//   * fp32 (both configurations 128x128): fewer tiles than 5/8 of the CUs split
-//     K over L tiles, given a workspace (the rule at the fp32 branch).
+//   * fp32: 64x128 tiles with K split to about three units per CU (buffer-load
+//     loader), 128x128 tiles split below 5/8 of a wave (element-granular
+//     loader); the rules at the fp32 branch.
 // Every split fits the workspace: splits * M * N * batch <= ws_limit_elems.
 Plan make_plan(int dtype_in, int64_t M, int64_t N, int64_t Ktot, int64_t batch, int mode,
                bool allow_split, int64_t ws_limit_elems, int cus, bool fast) {
@@ -283,27 +284,49 @@ Plan make_plan(int dtype_in, int64_t M, int64_t N, int64_t Ktot, int64_t batch, 
     }
     return plan_for(CFG_S, split_of(tilesS, 32));
   }
-  // fp32: L and S are the same 128x128 tile; only S has the element-granular loader.
-  // Below 5/8 of a wave, K is split so that the units (tiles x splits, at most two
-  // per CU) leave the fewest K tiles on the busiest CU: ceil(units / cus) / splits,
-  // ties to more splits; a split keeps >= 8 K tiles of 32, or >= 4 when the units
-  // fit one per CU.  Fitted to a forced-split sweep of configurations 1 and 2 (96
+  // fp32 with the buffer-load loader: 64x128 tiles (V; four waves of 32x64, several
+  // workgroups per CU).  K is split so that the units (tiles x splits, at most three
+  // per CU) leave the fewest K tiles on the busiest CU, ceil(units / cus) / splits,
+  // ties to more splits, each split keeping at least 512 of K (128 while the units fit
+  // one per CU: configuration 1, 48 tiles at K = 768, splits 5).  Fitted to a forced-
+  // plan sweep of configuration 2's 12 distinct GEMMs over tiles 128x128, 64x64,
+  // 64x128, 128x64 and splits 1..8 (hot loop): this rule's picks sum to 0.94 ms
+  // against 0.936 for the best plan of every GEMM and 1.034 for 128x128 tiles with
+  // the split rule below (qkv forward 2048x2304x768: 86 vs 63 TFLOP/s, o forward
+  // 2048x768x768 66 vs 55, qkv dX 101 vs 85, gate forward 104 vs 99).
+  // The element-granular loader (any alignment) runs 128x128 tiles (S): below 5/8
+  // of a wave, K is split by the same score with units at most two per CU and each
+  // split keeping >= 8 K tiles of 32, or >= 4 when the units fit one per CU (96
   // tiles at K = 2048: splits 1..8 ran 43 71 59 74 83 66 69 76 TFLOP/s; 108 tiles:
-  // 47 78 67 83 65 73 76 71; 36 tiles: 16 28 37 44 49 52 54 41; 24 tiles at K = 768:
-  // 10 15 19 21 21 22 21 21; 96 tiles at K = 768: 37 49 43 46 49 41 41 43).
-  const int cfg = fast ? CFG_L : CFG_S;
-  if (tilesL * 8 >= (int64_t)cus * 5 || !allow_split) return plan_for(cfg, 1);
+  // 47 78 67 83 65 73 76 71; 36 tiles: 16 28 37 44 49 52 54 41).
+  if (fast) {
+    const CfgShape V = shape_of(dtype_in, CFG_V);
+    const int64_t tilesV = cdiv(M, V.bm) * cdiv(N, V.bn) * batch;
+    int best = 1;
+    double best_score = (double)cdiv(tilesV, cus);
+    if (allow_split) {
+      for (int sp = 2; sp <= 8; ++sp) {
+        const int64_t units = tilesV * sp;
+        if (units > 3 * (int64_t)cus || (int64_t)sp * M * N * batch > ws_limit_elems) continue;
+        if (Ktot < (units > cus ? 512 : 128) * (int64_t)sp) continue;
+        const double score = (double)cdiv(units, cus) / sp;
+        if (score <= best_score) best = sp, best_score = score;
+      }
+    }
+    return plan_for(CFG_V, best);
+  }
+  if (tilesS * 8 >= (int64_t)cus * 5 || !allow_split) return plan_for(CFG_S, 1);
   const int64_t kts = cdiv(Ktot, 32);
   int best = 1;
   double best_score = 1.0;
   for (int sp = 2; sp <= 8; ++sp) {
-    const int64_t units = tilesL * sp;
+    const int64_t units = tilesS * sp;
     if (units > 2 * (int64_t)cus || (int64_t)sp * M * N * batch > ws_limit_elems) continue;
     if (cdiv(kts, sp) < (units <= cus ? 4 : 8)) continue;
     const double score = (double)cdiv(units, cus) / sp;
     if (score <= best_score) best = sp, best_score = score;
   }
-  return plan_for(cfg, best);
+  return plan_for(CFG_S, best);
 }
 
 bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
