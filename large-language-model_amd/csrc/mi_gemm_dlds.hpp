@@ -735,14 +735,17 @@ __global__ void __launch_bounds__(64 * WGM * WGN * KG)
                 v[2] += beta * bf16_bits_to_f32(o[1] & 0xffffu);
                 v[3] += beta * bf16_bits_to_f32(o[1] >> 16);
               }
-              *(u32x2_t*)((uint16_t*)Cz + ci) = u32x2_t{pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3])};
+              // non-temporal: C streams out instead of filling the XCD's L2 with dirty lines
+              // (configuration-3 set 1133-1134 -> 1141-1144 TFLOP/s, down forward +4 %, one box)
+              __builtin_nontemporal_store(u32x2_t{pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3])},
+                                          (u32x2_t*)((uint16_t*)Cz + ci));
             } else {
               if constexpr (BETA) {
                 const f32x4_t o = old[i & 1][j][st];
                 v[0] += beta * o[0]; v[1] += beta * o[1];
                 v[2] += beta * o[2]; v[3] += beta * o[3];
               }
-              *(f32x4_t*)((float*)Cz + ci) = v;
+              __builtin_nontemporal_store(v, (f32x4_t*)((float*)Cz + ci));
             }
           }
           __builtin_amdgcn_sched_barrier(0);
