@@ -696,8 +696,10 @@ __global__ void __launch_bounds__(64 * WGM * WGN * KG)
 #pragma unroll
           for (int st = 0; st < 4; ++st) {
             const int64_t ci = (row_of(i) + 8 * st) * p.ldc + col_of(j);
-            if constexpr (BF) dst[j][st] = *(const u32x2_t*)((const uint16_t*)Cz + ci);
-            else dst[j][st] = *(const f32x4_t*)((const float*)Cz + ci);
+            // non-temporal: the old C is read once (configuration-3 set with its fp32 beta = 1
+            // weight gradients 1144-1146 -> 1163-1164 TFLOP/s, one box)
+            if constexpr (BF) dst[j][st] = __builtin_nontemporal_load((const u32x2_t*)((const uint16_t*)Cz + ci));
+            else dst[j][st] = __builtin_nontemporal_load((const f32x4_t*)((const float*)Cz + ci));
           }
         }
       };
