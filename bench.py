@@ -73,6 +73,8 @@ TRAFFIC_FILES = {   # per workload: the rocprofv3 --pmc summary that bench.py re
     "block_fp32": os.path.join(PROFILES, "gemm_block_set_f32_m2048_hbm_bytes.md"),
     "attention": os.path.join(PROFILES, "flash_attention_gqa_b8_t1024_hbm_bytes.md"),
     "lm_head": os.path.join(PROFILES, "lm_head_xent_m8192_v32000_hbm_bytes.md"),
+    "norm": os.path.join(PROFILES, "rmsnorm_add_norm_m8192_d2048_hbm_bytes.md"),
+    "convert": os.path.join(PROFILES, "checkpoint_convert_layer_lmhead_hbm_bytes.md"),
 }
 CSRC = "large-language-model_amd/csrc/"
 _GEMM_SRC = [CSRC + f for f in ("mi_gemm_dlds.hpp", "mi_gemm_device.hpp", "mi_gemm_inst.hip",
@@ -82,7 +84,11 @@ KERNEL_SOURCES = {  # the sources whose kernels (and launch plans) a workload's 
     "block_fp32": _GEMM_SRC,
     "attention": _GEMM_SRC + [CSRC + "mi_attn.hip", CSRC + "mi_attn.hpp"],
     "lm_head": _GEMM_SRC + [CSRC + "mi_xent.hip", CSRC + "mi_xent.hpp"],
+    "norm": [CSRC + "mi_norm.hip", CSRC + "mi_norm.hpp", CSRC + "mi_gemm.hip"],
+    "convert": [CSRC + "mi_convert.hip", CSRC + "mi_convert.hpp", CSRC + "mi_gemm.hip"],
 }
+# norm workload: the traffic row of one backward call (both of its kernels)
+NORM_BWD_KEY = "backward (norm_bwd_vec + norm_dw_reduce of one call)"
 
 
 def sources_sha16(workload: str) -> str:
@@ -671,6 +677,10 @@ def norm_main(args):
     dom_ms, dom_bytes, dom = max((ms_f, fwd_bytes, "norm_fwd_vec (residual add + RMSNorm)"),
                                  (ms_b, bwd_bytes, "norm_bwd_vec + norm_dw_reduce"))
     achieved = dom_bytes / (dom_ms / 1e3) / 1e9
+    traffic, traffic_note = hbm_bytes_per_launch(
+        "norm_fwd_vec" if dom.startswith("norm_fwd") else NORM_BWD_KEY, "norm")
+    if args.copy_calibration:
+        copy_calibration()
     out = {
         "metric": "RMSNorm HBM throughput GB/s (configuration 3 norms: fused add + norm fwd, bwd with dw)",
         "value": round(value, 1), "unit": "GB/s", "n_gpus": 1, "steps": args.steps,
@@ -684,7 +694,8 @@ def norm_main(args):
                    "fwd_GBs": round(fwd_bytes / (ms_f / 1e3) / 1e9, 1),
                    "bwd_GBs": round(bwd_bytes / (ms_b / 1e3) / 1e9, 1)},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": PEAK_HBM_GBS,
-                     "unit": "GB/s", "frac": round(achieved / PEAK_HBM_GBS, 4), "traffic": None,
+                     "unit": "GB/s", "frac": round(achieved / PEAK_HBM_GBS, 4), "traffic": traffic,
+                     **({"traffic_note": traffic_note} if traffic_note else {}),
                      "kernel": dom, "avg_launch_ms": round(dom_ms, 4)},
     }
     if not args.no_cpu:
@@ -905,6 +916,9 @@ def convert_main(args):
     out_bytes = 2 * 2 * V * H
     value = nbytes * args.steps / elapsed / 1e9
     achieved = nbytes / (ms_launch / 1e3) / 1e9
+    traffic, traffic_note = hbm_bytes_per_launch("convert_batch_kernel", "convert")
+    if args.copy_calibration:
+        copy_calibration()
     out = {
         "metric": "checkpoint conversion GB/s (Python/MLX layout -> engine layout, one "
                   "configuration-3 layer + LM head, bf16)",
@@ -920,7 +934,8 @@ def convert_main(args):
                    "lm_head_transpose_GBs": round(out_bytes / (ms_out / 1e3) / 1e9, 1),
                    "copy_GBs": round(out_bytes / (ms_copy / 1e3) / 1e9, 1)},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": PEAK_HBM_GBS,
-                     "unit": "GB/s", "frac": round(achieved / PEAK_HBM_GBS, 4), "traffic": None,
+                     "unit": "GB/s", "frac": round(achieved / PEAK_HBM_GBS, 4), "traffic": traffic,
+                     **({"traffic_note": traffic_note} if traffic_note else {}),
                      "kernel": "convert_batch_kernel (the nine conversions, one launch)",
                      "avg_launch_ms": round(ms_launch, 4)},
     }
@@ -972,7 +987,9 @@ def traffic_table_main(args):
     title = {"block": "config-3 decoder-block GEMM set, bf16, M=8192",
              "block_fp32": "config-2 decoder-block GEMM set, fp32, M=2048",
              "attention": "fused GQA flash attention, configuration 4",
-             "lm_head": "LM head + cross-entropy, configuration 5"}[w]
+             "lm_head": "LM head + cross-entropy, configuration 5",
+             "norm": "residual add + RMSNorm forward and backward, configuration 3 (8192 x 2048)",
+             "convert": "checkpoint conversion, one configuration-3 layer + LM head"}[w]
     lines.append(f"# HBM bytes per launch: {title}\n")
     lines.append("Source: two `rocprofv3 --pmc` runs of `bench.py` on one MI355X ($R = repository "
                  "root), then this summary from their output:\n")
@@ -1078,6 +1095,33 @@ def traffic_table_main(args):
         lines.append(row(ATT_BWD_KEY, ", ".join(k for k, _ in bwd), steps, fk, wk, alg_bwd))
         for k, (n, f_, w_) in names.items():
             lines.append(row(k, k, n, f_ / n, w_ / n, alg_fwd if "flash_fwd" in k else 0))
+    elif w in ("norm", "convert"):
+        # per kernel (template arguments dropped), averaged over the run's launches
+        names = {}
+        for (n, fv), (_, wv) in zip(fetch, write):
+            e = names.setdefault(short(n).split("<")[0], [0, 0.0, 0.0])
+            e[0] += 1
+            e[1] += fv * fs
+            e[2] += wv * ws_
+        rows_, dims = M_TOKENS, 2048
+        act = rows_ * dims * 2
+        lines.append("Every launch of the run (warm-up, timing passes, timed steps), averaged per kernel. "
+                     "`algorithmic`: " + ("forward: h, a read and h, y written once (bf16); backward "
+                                          "call: dy, h, the residual gradient read and dx written once, "
+                                          "the fp32 weight gradient read and written once."
+                                          if w == "norm" else "every converted element read and "
+                                          "written once (bf16).") + "\n")
+        lines.append(hdr)
+        lines.append(sep)
+        if w == "norm":
+            nb = names.get("norm_bwd_vec", [0, 0.0, 0.0])
+            nr = names.get("norm_dw_reduce", [0, 0.0, 0.0])
+            if nb[0] and nb[0] == nr[0]:
+                lines.append(row(NORM_BWD_KEY, "norm_bwd_vec, norm_dw_reduce", nb[0], (nb[1] + nr[1]) / nb[0],
+                                 (nb[2] + nr[2]) / nb[0], 4 * act + 2 * dims * 4))
+        for k, (n, f_, w_) in names.items():
+            alg = 4 * act if k == "norm_fwd_vec" else 0
+            lines.append(row(k, k, n, f_ / n, w_ / n, alg))
     elif w == "lm_head":
         M, H, V = LMH["M"], LMH["H"], LMH["V"]
         import mi_gemm as mi

@@ -131,3 +131,38 @@ def test_traffic_table_rejects_misaligned_runs(bench, tmp_path):
         sys.argv = sys_argv
     with pytest.raises(SystemExit):
         bench.traffic_table_main(args)
+
+
+def test_traffic_table_per_kernel(bench, tmp_path, capsys):
+    """The per-kernel summary of the norm workload: each kernel averaged over its launches
+    (template arguments dropped), and one backward call's row summing its two kernels."""
+    fetch, write = [], []
+    for i in range(3):
+        fetch += [("void mig::(anonymous namespace)::norm_fwd_vec<true, false, 4>(mig::NormParams)", 100.0 + i),
+                  ("void mig::(anonymous namespace)::norm_bwd_vec<true, false, 4, true>(mig::NormParams)", 200.0),
+                  ("void mig::(anonymous namespace)::norm_dw_reduce<false>(mig::NormParams)", 10.0)]
+        write += [("x", 50.0), ("x", 60.0), ("x", 1.0)]
+    fetch.append(("__amd_rocclr_copyBuffer", float(1 << 20)))
+    write.append(("__amd_rocclr_copyBuffer", float(1 << 20)))
+    write = [(f[0], w[1]) for f, w in zip(fetch, write)]
+    fd, wd = str(tmp_path / "f"), str(tmp_path / "w")
+    _write_counters(fd, "FETCH_SIZE", fetch)
+    _write_counters(wd, "WRITE_SIZE", write)
+    sys_argv = sys.argv
+    try:
+        sys.argv = ["bench.py", "--workload", "norm", "--steps", "2", "--warmup", "1",
+                    "--traffic-table", fd, wd]
+        args = bench.parse()
+    finally:
+        sys.argv = sys_argv
+    bench.traffic_table_main(args)
+    out = capsys.readouterr().out
+    rows = {}
+    for line in out.splitlines():
+        cells = [c.strip() for c in line.strip().strip("|").split("|")]
+        if len(cells) == 8 and cells[2].isdigit():
+            rows[cells[0]] = cells
+    assert int(rows["norm_fwd_vec"][2]) == 3
+    assert int(rows["norm_fwd_vec"][5]) == int(round((101.0 + 50.0) * 1024))  # mean FETCH 101
+    assert int(rows[bench.NORM_BWD_KEY][5]) == (210 + 61) * 1024
+    assert bench.NORM_BWD_KEY in out and "norm_dw_reduce" in rows
