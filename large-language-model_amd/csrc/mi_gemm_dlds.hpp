@@ -675,6 +675,11 @@ __global__ void __launch_bounds__(64 * WGM * WGN * KG)
     // BF: bf16 C; BETA: beta*C is added.  Both uniform, hoisted out of the tile.
     auto store_tile = [&](auto BF_c, auto BETA_c) __attribute__((always_inline)) {
       constexpr bool BF = decltype(BF_c)::value, BETA = decltype(BETA_c)::value;
+      // WIDE: patches of 32 x 64 (pitch 68 floats), lane -> row lane / 16, 4 columns
+      constexpr int PPW = 68;
+      constexpr bool WIDE = BF && !BETA && TN % 2 == 0 && KG == 1 && NWAVE * 32 * PPW * 4 <= LDS_BYTES;
+      float* patchw = reinterpret_cast<float*>(smem) + wave * (32 * PPW);
+      const int rw_out = lane >> 4, cw_out = (lane & 15) * 4;
       using OldT = std::conditional_t<BF, u32x2_t, f32x4_t>;
       auto col_of = [&](int j) __attribute__((always_inline)) { return n0 + wn * WTN + j * 32 + c_out; };
       auto row_of = [&](int i) __attribute__((always_inline)) {
@@ -713,6 +718,37 @@ __global__ void __launch_bounds__(64 * WGM * WGN * KG)
           if (i + 1 < TM && valid(i + 1)) load_old(i + 1, old[(i + 1) & 1]);
         }
         if (!valid(i)) continue;
+        if constexpr (WIDE) {
+          // bf16 without beta: two 32x32 blocks per patch, read back as 4 rows of 64
+          // columns, so every store instruction writes whole 128-byte rows (configuration-3
+          // set 1171-1173 -> 1181-1183 TFLOP/s, LM head 1203 -> 1222, one box)
+#pragma unroll
+          for (int jp = 0; jp < TN; jp += 2) {
+            if (!inside(jp)) continue;
+#pragma unroll
+            for (int h = 0; h < 2; ++h)
+#pragma unroll
+              for (int q = 0; q < 4; ++q) {
+                f32x4_t v;
+#pragma unroll
+                for (int e = 0; e < 4; ++e) v[e] = value(i, jp + h, q, e) * rsv[i];
+                *reinterpret_cast<f32x4_t*>(patchw + r_in * PPW + 32 * h + 8 * q + 4 * h_in) = v;
+              }
+            const int colw = n0 + wn * WTN + jp * 32 + cw_out;
+            const bool ok = cw_out < 32 || inside(jp + 1);  // the second block may lie past N
+            const int64_t roww = m0 + wm * WTM + i * 32 + rw_out;
+#pragma unroll
+            for (int st = 0; st < 8; ++st) {
+              const f32x4_t v = *reinterpret_cast<const f32x4_t*>(patchw + (rw_out + 4 * st) * PPW + cw_out);
+              const int64_t ci = (roww + 4 * st) * p.ldc + colw;
+              if (ok)
+                __builtin_nontemporal_store(u32x2_t{pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3])},
+                                            (u32x2_t*)((uint16_t*)Cz + ci));
+            }
+            __builtin_amdgcn_sched_barrier(0);
+          }
+          continue;
+        }
         const int64_t row0 = row_of(i);
 #pragma unroll
         for (int j = 0; j < TN; ++j) {
