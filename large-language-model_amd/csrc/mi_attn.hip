@@ -404,7 +404,8 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2)))
     if (orow_i < T) {
       uint16_t* orow = (uint16_t*)p.O + (p.o_bthd ? ((int64_t)(b * T + orow_i) * p.nH + h) * D
                                                   : ((int64_t)bh * T + orow_i) * D);
-      *(u32x4_t*)(orow + 8 * oj) = v;
+      // non-temporal: O is read again only by the backward (forward 64-66 -> 62-63 us, one box)
+      __builtin_nontemporal_store(v, (u32x4_t*)(orow + 8 * oj));
     }
   }
   if (row < T && p.lse && h32 == 0)
