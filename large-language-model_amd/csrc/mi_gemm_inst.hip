@@ -117,9 +117,7 @@ KernelFn MI_PICK_NAME(MI_DTN, MI_TA, MI_TB)(int cfg, bool fast, bool ktail, bool
       case CFG_L: return gemm_kernel<elem_t, LM, LN, 2, 2, AK, BK, MODE_PLAIN, true>;
       case CFG_S: return gemm_kernel<elem_t, SM, SN, 2, 2, AK, BK, MODE_PLAIN, true>;
 #if !MI_DT_BF16
-      case CFG_W: return gemm_kernel<elem_t, 64, 64, 2, 2, AK, BK, MODE_PLAIN, true>;
       case CFG_V: return gemm_kernel<elem_t, 64, 128, 2, 2, AK, BK, MODE_PLAIN, true>;
-      case CFG_M: return gemm_kernel<elem_t, 128, 64, 2, 2, AK, BK, MODE_PLAIN, true>;
 #endif
       case CFG_DUAL: return gemm_kernel<elem_t, DM, DN, 2, 2, AK, BK, MODE_DUAL, true>;
       case CFG_PRO:

@@ -38,11 +38,9 @@ inline CfgShape cfg_shape(bool bf16, int cfg) {
          : cfg == CFG_V ? CfgShape{128, 192, 512}
          : cfg == CFG_DUAL ? CfgShape{256, 128}
                            : CfgShape{256, 256};
-  // fp32: register-staged kernel, four waves; W, V and M name the smaller tiles
+  // fp32: register-staged kernel, four waves; V names the 64x128 tile
   return cfg == CFG_DUAL ? CfgShape{128, 64}
-       : cfg == CFG_W    ? CfgShape{64, 64}
        : cfg == CFG_V    ? CfgShape{64, 128}
-       : cfg == CFG_M    ? CfgShape{128, 64}
                          : CfgShape{128, 128};
 }
 
