@@ -59,6 +59,9 @@ CASES = [
     (130, 64, 4096, 0, 1, "bf16", None, 0.0),      # one chunk: no recomputation; no dW
     (50, 96, 3000, 1024, 1, None, "f32", 1.0),     # dW only
     (33, 128, 2000, 512, 0, None, None, 0.0),      # loss only (pass 1 alone)
+    (256, 256, 4096, 1024, 0, "bf16", "f32", 1.0),  # whole 64-column slices everywhere
+    (320, 128, 3040, 960, 1, "f32", "bf16", 0.0),   # tail chunk of 160 columns
+    (256, 128, 2048, 0, 1, None, None, 0.0),        # one chunk, loss only
 ]
 
 
