@@ -111,7 +111,7 @@ int current_cus() {
 // ---- kernel table ------------------------------------------------------------
 
 KernelFn pick_kernel(int dtype_in, int transA, int transB, int cfg, bool fast, bool ktail,
-                     bool fast_epi) {
+                     int fast_epi) {
   const int lay = (transA ? 2 : 0) | (transB ? 1 : 0);
   if (dtype_in == MI_BF16) {
     switch (lay) {
@@ -620,7 +620,13 @@ int run(const Problem& P, hipStream_t stream) {
   const bool fast_epi = plan.splits == 1 && !P.ep.bias && !P.ep.residual && cvec &&
                         b.causal != MI_CAUSAL_OUT_LOWER && P.M % 32 == 0 && P.N % 32 == 0;
   const int64_t kstep = plan.cfg == CFG_W || plan.cfg == CFG_V ? MI_W_BK : 64;
-  KernelFn fn = pick_kernel(P.dtype_in, P.transA, P.transB, plan.cfg, fast, P.K % kstep != 0, fast_epi);
+  // with a row scale the direct epilogue has a variant of its own (A K-contiguous on the
+  // 256x256, 256x192 and 128x128 tiles); elsewhere the general epilogue applies it
+  int epi_kind = fast_epi ? 1 : 0;
+  if (P.ep.row_scale && fast_epi)
+    epi_kind = (P.dtype_in == MI_BF16 && fast && !P.transA && P.K % kstep == 0 &&
+                (plan.cfg == CFG_L || plan.cfg == CFG_M || plan.cfg == CFG_S)) ? 2 : 0;
+  KernelFn fn = pick_kernel(P.dtype_in, P.transA, P.transB, plan.cfg, fast, P.K % kstep != 0, epi_kind);
   if (!fn) return fail(MI_ERR_UNSUPPORTED, "no kernel for this layout / mode");
 
   Params p;

@@ -73,6 +73,21 @@ typedef float elem_t;
 // 166; 2048x5632x8192 TN 170 vs 180; bit-identical results).
 template <bool AK, bool BK, int V>
 KernelFn dlds_kernel(int cfg) {
+  if constexpr ((V & DLDS_ROWSCALE) != 0) {
+    // the row-scale epilogue (a folded RMSNorm) exists where the norm's GEMMs run: a
+    // K-contiguous A on the 256x256, 256x192 and 128x128 tiles
+    if constexpr (AK) {
+      switch (cfg) {
+        case CFG_L:
+          return gemm_dlds_kernel<256, 256, MI_L_BK(AK, BK), MI_L_STAGES(AK, BK), AK, BK, MODE_PLAIN, V, 2, 4, 1>;
+        case CFG_M:
+          return gemm_dlds_kernel<256, 192, MI_M_BK(AK, BK), MI_M_STAGES(AK, BK), AK, BK, MODE_PLAIN, V, 4, 2, 1>;
+        case CFG_S: return gemm_dlds_kernel<128, 128, MI_S_BK(AK), MI_S_STAGES(AK), AK, BK, MODE_PLAIN, V>;
+        default: return nullptr;
+      }
+    }
+    return nullptr;
+  }
   switch (cfg) {
     case CFG_L:
       return gemm_dlds_kernel<256, 256, MI_L_BK(AK, BK), MI_L_STAGES(AK, BK), AK, BK, MODE_PLAIN, V, 2, 4, 1>;
@@ -89,7 +104,7 @@ KernelFn dlds_kernel(int cfg) {
 }
 #endif
 
-KernelFn MI_PICK_NAME(MI_DTN, MI_TA, MI_TB)(int cfg, bool fast, bool ktail, bool fast_epi) {
+KernelFn MI_PICK_NAME(MI_DTN, MI_TA, MI_TB)(int cfg, bool fast, bool ktail, int fast_epi) {
   constexpr bool AK = (MI_TA == 0);  // A is K-contiguous when not transposed
   constexpr bool BK = (MI_TB == 1);  // B is K-contiguous when transposed
 #if MI_DT_BF16
@@ -105,6 +120,7 @@ KernelFn MI_PICK_NAME(MI_DTN, MI_TA, MI_TB)(int cfg, bool fast, bool ktail, bool
       if constexpr (AK || BK) {
         if (ktail) return dlds_kernel<AK, BK, DLDS_KTAIL>(cfg);
       }
+      if (fast_epi == 2) return dlds_kernel<AK, BK, DLDS_FAST_EPI | DLDS_ROWSCALE>(cfg);
       return fast_epi ? dlds_kernel<AK, BK, DLDS_FAST_EPI>(cfg) : dlds_kernel<AK, BK, 0>(cfg);
     }
     switch (cfg) {

@@ -48,11 +48,11 @@ inline CfgShape cfg_shape(bool bf16, int cfg) {
 // the fast (buffer-load) or the element-granular loader, or nullptr when the
 // combination does not exist (prologue with transA = 1).  The element-granular
 // variant of the plain configurations exists only for CFG_S.  ktail: the K
-// extent is not a multiple of 64; fast_epi: every tile is full and the
+// extent is not a multiple of 64; fast_epi (1, or 2 with the row scale): every tile is full and the
 // epilogue is alpha (SiLU gate), beta*C and the output conversion only, with
 // no split-K.
 #define MI_DECL_PICK(dt, ta, tb) \
-  KernelFn pick_##dt##_##ta##tb(int cfg, bool fast, bool ktail, bool fast_epi);
+  KernelFn pick_##dt##_##ta##tb(int cfg, bool fast, bool ktail, int fast_epi);
 MI_DECL_PICK(bf16, 0, 0)
 MI_DECL_PICK(bf16, 0, 1)
 MI_DECL_PICK(bf16, 1, 0)
