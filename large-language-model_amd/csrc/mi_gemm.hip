@@ -284,36 +284,44 @@ Plan make_plan(int dtype_in, int64_t M, int64_t N, int64_t Ktot, int64_t batch, 
     }
     return plan_for(CFG_S, split_of(tilesS, 32));
   }
-  // fp32 with the buffer-load loader: 64x128 tiles (V; four waves of 32x64, several
-  // workgroups per CU).  K is split so that the units (tiles x splits, at most three
-  // per CU) leave the fewest K tiles on the busiest CU, ceil(units / cus) / splits,
-  // ties to more splits, each split keeping at least 512 of K (128 while the units fit
-  // one per CU: configuration 1, 48 tiles at K = 768, splits 5).  Fitted to a forced-
-  // plan sweep of configuration 2's 12 distinct GEMMs over tiles 128x128, 64x64,
-  // 64x128, 128x64 and splits 1..8 (hot loop): this rule's picks sum to 0.94 ms
-  // against 0.936 for the best plan of every GEMM and 1.034 for 128x128 tiles with
-  // the split rule below (qkv forward 2048x2304x768: 86 vs 63 TFLOP/s, o forward
-  // 2048x768x768 66 vs 55, qkv dX 101 vs 85, gate forward 104 vs 99).
+  // fp32 with the direct-to-LDS kernel: 64x128 tiles (V; four waves of 32x64) or 64x64
+  // tiles (M; four waves of 32x32), several workgroups per CU.  Score of a plan: the
+  // busiest CU's share of the work, ceil(units / cus) x tile area / splits (units =
+  // tiles x splits, at most three per CU once split, each split keeping at least 512 of
+  // K, or 128 while the units fit one per CU: configuration 1, 48 tiles at K = 768,
+  // splits 5).  Lowest score; ties to fewer splits, then to 64x128 tiles when K < 1024
+  // and 64x64 tiles otherwise.  Fitted to a forced-plan sweep of configuration 2's 12
+  // distinct GEMMs over these tiles, 128x128, and splits 1..8 (hot loop, TFLOP/s):
+  // qkv forward 2048x2304x768 64x64 115 vs 64x128 92; 2048x768x2048 (gate / qkv dX,
+  // down forward, down / gate dW) 64x64 split 2 113-117 vs 64x128 split 4 104-109;
+  // qkv dW 768x2304x2048 64x64 113 vs 64x128 102; o forward 2048x768x768 64x128 93 vs
+  // 64x64 87; gate forward 2048x2048x768 64x128 127 vs 64x64 122.  The rule picks the
+  // best plan of every one of the 12, or one within 2 %.
   // The element-granular loader (any alignment) runs 128x128 tiles (S): below 5/8
   // of a wave, K is split by the same score with units at most two per CU and each
   // split keeping >= 8 K tiles of 32, or >= 4 when the units fit one per CU (96
   // tiles at K = 2048: splits 1..8 ran 43 71 59 74 83 66 69 76 TFLOP/s; 108 tiles:
   // 47 78 67 83 65 73 76 71; 36 tiles: 16 28 37 44 49 52 54 41).
   if (fast) {
-    const CfgShape V = shape_of(dtype_in, CFG_V);
-    const int64_t tilesV = cdiv(M, V.bm) * cdiv(N, V.bn) * batch;
-    int best = 1;
-    double best_score = (double)cdiv(tilesV, cus);
-    if (allow_split) {
-      for (int sp = 2; sp <= 8; ++sp) {
-        const int64_t units = tilesV * sp;
-        if (units > 3 * (int64_t)cus || (int64_t)sp * M * N * batch > ws_limit_elems) continue;
-        if (Ktot < (units > cus ? 512 : 128) * (int64_t)sp) continue;
-        const double score = (double)cdiv(units, cus) / sp;
-        if (score <= best_score) best = sp, best_score = score;
+    int best_cfg = CFG_V, best_sp = 1;
+    double best_score = 1e300;
+    for (int cfg : {CFG_V, CFG_M}) {
+      const CfgShape t = shape_of(dtype_in, cfg);
+      const int64_t tiles = cdiv(M, t.bm) * cdiv(N, t.bn) * batch;
+      for (int sp = 1; sp <= (allow_split ? 8 : 1); ++sp) {
+        const int64_t units = tiles * sp;
+        if (sp > 1) {
+          if (units > 3 * (int64_t)cus || (int64_t)sp * M * N * batch > ws_limit_elems) continue;
+          if (Ktot < (units > cus ? 512 : 128) * (int64_t)sp) continue;
+        }
+        const double score = (double)cdiv(units, cus) * t.bm * t.bn / sp;
+        const bool wins = score < best_score ||
+                          (score == best_score &&
+                           (sp < best_sp || (sp == best_sp && cfg == (Ktot < 1024 ? CFG_V : CFG_M))));
+        if (wins) best_cfg = cfg, best_sp = sp, best_score = score;
       }
     }
-    return plan_for(CFG_V, best);
+    return plan_for(best_cfg, best_sp);
   }
   if (tilesS * 8 >= (int64_t)cus * 5 || !allow_split) return plan_for(CFG_S, 1);
   const int64_t kts = cdiv(Ktot, 32);
@@ -337,7 +345,8 @@ void describe_plan(char* buf, size_t len, int dtype_in, bool fast, const Plan& p
   const CfgShape sh = shape_of(dtype_in, pl.cfg);
   const char* kind = (dtype_in == MI_BF16 && fast && pl.cfg != CFG_PRO)
                          ? (pl.cfg == CFG_W || pl.cfg == CFG_V ? "dlds-kg2" : "dlds")
-                         : "regstage";
+                     : (dtype_in != MI_BF16 && fast && (pl.cfg == CFG_V || pl.cfg == CFG_M)) ? "dlds"
+                                                                                           : "regstage";
   std::snprintf(buf, len, "%s %s %dx%d %s%s split%d tiles%lld", kind,
                 dtype_in == MI_BF16 ? "bf16" : "f32", sh.bm, sh.bn, transA ? "T" : "N",
                 transB ? "T" : "N", pl.splits, (long long)pl.tiles_m * pl.tiles_n * batch);
@@ -619,7 +628,7 @@ int run(const Problem& P, hipStream_t stream) {
   // the direct epilogue works in whole 32x32 blocks (an edge tile skips those past M, N)
   const bool fast_epi = plan.splits == 1 && !P.ep.bias && !P.ep.residual && cvec &&
                         b.causal != MI_CAUSAL_OUT_LOWER && P.M % 32 == 0 && P.N % 32 == 0;
-  const int64_t kstep = plan.cfg == CFG_W || plan.cfg == CFG_V ? MI_W_BK : 64;
+  const int64_t kstep = P.dtype_in != MI_BF16 ? 32 : plan.cfg == CFG_W || plan.cfg == CFG_V ? MI_W_BK : 64;
   // with a row scale the direct epilogue has a variant of its own (A K-contiguous on the
   // 256x256, 256x192 and 128x128 tiles); elsewhere the general epilogue applies it
   int epi_kind = fast_epi ? 1 : 0;

@@ -74,6 +74,12 @@ __device__ __forceinline__ int mc_unswz(int kr, int p) {
   return p ^ ((kr & 3) << 2);
 }
 
+// fp32 row-contiguous tiles: chunk q of k-row kr sits at q ^ 8 on k-rows 4..7 (mod
+// 8).  A fragment read takes 32 consecutive columns (8 chunks, 128 bytes) of k-row
+// kr in lanes 0-31 and of k-row kr + 4 in lanes 32-63: the two halves of the
+// 256-byte bank window.  Self-inverse.
+__device__ __forceinline__ int mc_swz32(int kr, int q) { return q ^ (((kr >> 2) & 1) << 3); }
+
 // Row-contiguous tiles whose row is not a power of two (192 columns) are stored
 // in 128-byte granules, column block by column block: granule G holds k-row
 // G % BK of the 64-column block G / BK, so consecutive k-rows of one column block
@@ -110,28 +116,33 @@ __device__ __forceinline__ void static_for(F&& f) {
 }
 
 // One operand of the direct-to-LDS pipeline.  R: tile rows (M or N extent),
-// BK: K extent of a stage, KC: K-contiguous in memory, WT: rows of the wave
-// tile (fragments of 32 rows each), NW: waves sharing the DMA, NSUBW: K substeps
-// of 16 one wave computes per stage (BK/16, or half of it when two wave groups
-// split each stage's K range).
-template <int R, int BK, bool KC, int STAGES, int WT, int NW = 4, int NSUBW = BK / 16>
+// BK: K extent of a stage (elements), KC: K-contiguous in memory, WT: rows of the
+// wave tile (fragments of 32 rows each), NW: waves sharing the DMA, NSUBW: K
+// substeps one wave computes per stage (all of them, or half when two wave groups
+// split each stage's K range), ES: element bytes (2: bf16, 4: fp32).  A substep
+// covers 32 bytes of every row: 16 bf16 (one 32x32x16 MFMA) or 8 fp32 (four
+// 32x32x2 MFMAs).
+template <int R, int BK, bool KC, int STAGES, int WT, int NW = 4, int NSUBW = BK / 16, int ES = 2>
 struct DldsOperand {
-  static constexpr int NCH = BK / 8;                  // KC: 16-byte chunks per row
-  static constexpr int CPR = R / 8;                   // !KC: 16-byte chunks per k-row
+  static constexpr int EPC = 16 / ES;                 // elements per 16-byte chunk
+  static constexpr int NCH = BK / EPC;                // KC: 16-byte chunks per row
+  static constexpr int CPR = R / EPC;                 // !KC: 16-byte chunks per k-row
   static constexpr bool GRAN = !KC && (CPR & (CPR - 1)) != 0;  // 128-byte granule layout
-  static constexpr int KRB = GRAN ? 128 : R * 2;      // !KC: LDS bytes between k-rows
+  static constexpr int KRB = GRAN ? 128 : R * ES;     // !KC: LDS bytes between k-rows
   static_assert(!GRAN || R % 64 == 0, "granule layout needs 64-column blocks");
-  static constexpr int BYTES = R * BK * 2;            // one stage of this operand
+  static_assert(ES == 2 || (!GRAN && (KC || CPR >= 16)), "fp32 k-rows: 2^n >= 16 chunks");
+  static constexpr int BYTES = R * BK * ES;           // one stage of this operand
   static constexpr int NBLK = BYTES / 1024;           // 1 KB DMA blocks per stage
   static constexpr int NU = NBLK / NW;                // DMA instructions per wave
-  static constexpr int NSUB = BK / 16;
+  static constexpr int NSUB = BK * ES / 32;
   static constexpr int NF = WT / 32;                  // fragments per wave
   static constexpr int NRB = KC ? 2 * NSUBW : NF;     // read base registers
   static_assert(BYTES % 1024 == 0 && NBLK % NW == 0, "tile must split into whole DMA blocks per wave");
   static_assert(NSUB % NSUBW == 0, "wave groups split the stage's substeps evenly");
   // largest immediate offset added to a read base must fit the 16-bit DS offset
-  static constexpr int MAX_IMM = KC ? ((NF - 1) / 2) * 64 * BK * 2 + (STAGES - 1) * BYTES
-                                    : (16 * (NSUBW - 1) + 4) * KRB + (STAGES - 1) * BYTES;
+  static constexpr int MAX_IMM = KC ? ((NF - 1) / 2) * 64 * BK * ES + (STAGES - 1) * BYTES
+                                 : ES == 2 ? (16 * (NSUBW - 1) + 4) * KRB + (STAGES - 1) * BYTES
+                                           : (8 * (NSUBW - 1) + 3) * KRB + (STAGES - 1) * BYTES;
   static_assert(MAX_IMM < 65536, "LDS read offsets exceed the DS immediate");
 
   uint32_t voff[NU];  // byte offset of unit u from the tile's first K (kBufOOB: row outside)
@@ -143,7 +154,7 @@ struct DldsOperand {
   // first tile row, kseg: K extent of a segment.
   __device__ __forceinline__ void init_dma(int64_t ld, int rows, int row0, int kseg) {
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const int ldb = (int)ld * 2;
+    const int ldb = (int)ld * ES;
 #pragma unroll
     for (int u = 0; u < NU; ++u) {
       const int b = wave * NU + u;
@@ -151,7 +162,7 @@ struct DldsOperand {
         const int row = b * (64 / NCH) + lane / NCH;
         const int c = kc_swz<NCH>(row, lane % NCH);
         voff[u] = (uint32_t)((row0 + row) * ldb + c * 16);  // rows >= M lie past the extent
-        klim[u] = kseg - c * 8;
+        klim[u] = kseg - c * EPC;
       } else if constexpr (GRAN) {
         // LDS chunk qi: granule qi / 8 = k-row kr of 64-column block qi / 8 / BK
         const int qi = b * 64 + lane;
@@ -164,9 +175,9 @@ struct DldsOperand {
         // chunk q of the stage lands at LDS chunk q: k-row q / CPR, position q % CPR
         const int qi = b * 64 + lane;
         const int kr = qi / CPR;
-        const int q = mc_unswz<CPR>(kr, qi - kr * CPR);
-        const int grow = row0 + q * 8;
-        voff[u] = grow < rows ? (uint32_t)(kr * ldb + grow * 2) : kBufOOB;
+        const int q = ES == 2 ? mc_unswz<CPR>(kr, qi - kr * CPR) : mc_swz32(kr, qi - kr * CPR);
+        const int grow = row0 + q * EPC;
+        voff[u] = grow < rows ? (uint32_t)(kr * ldb + grow * ES) : kBufOOB;
         klim[u] = 0;
       }
     }
@@ -185,8 +196,17 @@ struct DldsOperand {
         for (int par = 0; par < 2; ++par) {
           const int r = w0 + 32 * par + (lane & 31);
           const int c = 2 * (ks0 + s) + (lane >> 5);
-          rb[2 * s + par] = region + (uint32_t)(r * (BK * 2) + 16 * kc_swz<NCH>(r, c));
+          rb[2 * s + par] = region + (uint32_t)(r * (BK * ES) + 16 * kc_swz<NCH>(r, c));
         }
+    } else if constexpr (ES == 4) {
+      // lane: column n of fragment f, k-rows 4h .. 4h+3 of each 8-k substep (h = lane / 32)
+      const int h = lane >> 5;
+#pragma unroll
+      for (int f = 0; f < NF; ++f) {
+        const int n = w0 + 32 * f + (lane & 31);
+        const int kr = 8 * ks0 + 4 * h;
+        rb[f] = region + (uint32_t)(kr * KRB + 16 * mc_swz32(kr, n >> 2) + 4 * (n & 3));
+      }
     } else {
       const int g = lane >> 4, j = lane & 15;
 #pragma unroll
@@ -220,8 +240,16 @@ struct DldsOperand {
   template <int S, int J>
   __device__ __forceinline__ u32x4_t frag(int f) const {
     if constexpr (KC) {
-      const uint32_t a = rb[2 * S + (f & 1)] + (uint32_t)((f >> 1) * 64 * BK * 2 + J * BYTES);
+      const uint32_t a = rb[2 * S + (f & 1)] + (uint32_t)((f >> 1) * 64 * BK * ES + J * BYTES);
       return *(const lds_u32x4_t*)(uintptr_t)a;
+    } else if constexpr (ES == 4) {
+      // fp32 k-rows 8S + 4h + t, t = 0..3: value t feeds the substep's MFMA t
+      typedef __attribute__((address_space(3))) const uint32_t lds_u32_t;
+      u32x4_t out;
+#pragma unroll
+      for (int t = 0; t < 4; ++t)
+        out[t] = *(lds_u32_t*)(uintptr_t)(rb[f] + (uint32_t)((8 * S + t) * KRB + J * BYTES));
+      return out;
     } else {
       u32x4_t out = {0u, 0u, 0u, 0u};
 #pragma unroll
@@ -258,7 +286,7 @@ enum { DLDS_KTAIL = 1, DLDS_FAST_EPI = 2, DLDS_ROWSCALE = 4 };
 // output tile; the groups' accumulators are summed through LDS before the
 // epilogue, each group then storing half of the tile.
 template <int BM, int BN, int BK, int STAGES, bool AK, bool BKC, int MODE, int VAR, int WGM = 2,
-          int WGN = 2, int KG = 1>
+          int WGN = 2, int KG = 1, int ES = 2>
 __global__ void __launch_bounds__(64 * WGM * WGN * KG)
     __attribute__((amdgpu_waves_per_eu(WGM * WGN * KG / 4)))
     gemm_dlds_kernel(Params p) {
@@ -274,15 +302,19 @@ __global__ void __launch_bounds__(64 * WGM * WGN * KG)
   constexpr int TM = WTM / 32, TN = WTN / 32;
   constexpr bool DUAL = (MODE == MODE_DUAL);
   constexpr int NB = DUAL ? 2 * TN : TN;
-  constexpr int NSUBT = BK / 16;          // K substeps of a stage
+  constexpr int NSUBT = BK * ES / 32;     // K substeps of a stage (32 bytes of every row)
   constexpr int NSUB = NSUBT / KG;        // K substeps one wave computes per stage
   static_assert(MODE != MODE_PROLOGUE, "the SiLU-gate prologue needs register staging");
   static_assert(KG == 1 || KG == 2, "one or two K groups");
   static_assert(KG == 1 || (MODE == MODE_PLAIN && TM == 2), "split-K groups: plain mode, two row blocks");
   static_assert(NSUB == 2 || NSUB == 4, "each wave computes 2 or 4 substeps per stage");
   static_assert(STAGES >= 2 && STAGES <= 4, "2..4 stages");
-  using OpA = DldsOperand<BM, BK, AK, STAGES, WTM, NWAVE, NSUB>;
-  using OpB = DldsOperand<BN, BK, BKC, STAGES, WTN, NWAVE, NSUB>;
+  static_assert(ES == 2 || (ES == 4 && !DUAL), "bf16, or fp32 without the dual B");
+  // TRR: fragments of a row-contiguous bf16 operand come from transpose reads issued
+  // as inline asm, whose completion the code waits for itself
+  constexpr bool TRR = ES == 2 && (!AK || !BKC);
+  using OpA = DldsOperand<BM, BK, AK, STAGES, WTM, NWAVE, NSUB, ES>;
+  using OpB = DldsOperand<BN, BK, BKC, STAGES, WTN, NWAVE, NSUB, ES>;
   constexpr int A_REG = 0;                                   // LDS regions (bytes)
   constexpr int B_REG = A_REG + STAGES * OpA::BYTES;
   constexpr int B2_REG = B_REG + STAGES * OpB::BYTES;
@@ -299,10 +331,10 @@ __global__ void __launch_bounds__(64 * WGM * WGN * KG)
   const int m0 = uniform(tc.tm * BM), n0 = uniform(tc.tn * BN);
   const int zo = uniform(tc.z / p.heads), zi = uniform(tc.z - (tc.z / p.heads) * p.heads);
   const int ziA = uniform(zi / p.gA), ziB = uniform(zi / p.gB), ziC = uniform(zi / p.gC);
-  const __bf16* Ab = uniform((const __bf16*)p.A + (int64_t)zo * p.aO + (int64_t)ziA * p.aI);
-  const __bf16* Bb = uniform((const __bf16*)p.B + (int64_t)zo * p.bO + (int64_t)ziB * p.bI);
-  const __bf16* B2b = DUAL ? uniform((const __bf16*)p.B2 + (int64_t)zo * p.bO + (int64_t)ziB * p.bI)
-                           : nullptr;
+  const char* Ab = uniform((const char*)p.A + ((int64_t)zo * p.aO + (int64_t)ziA * p.aI) * ES);
+  const char* Bb = uniform((const char*)p.B + ((int64_t)zo * p.bO + (int64_t)ziB * p.bI) * ES);
+  const char* B2b = DUAL ? uniform((const char*)p.B2 + ((int64_t)zo * p.bO + (int64_t)ziB * p.bI) * ES)
+                         : nullptr;
   const int64_t coff = (int64_t)zo * p.cO + (int64_t)ziC * p.cI;
   void* Cz = (char*)p.C + coff * (p.c_bf16 ? 2 : 4);
   const void* Rz = p.R ? (const char*)p.R + ((int64_t)zo * p.rO + (int64_t)zi * p.rI) * (p.r_bf16 ? 2 : 4)
@@ -363,8 +395,8 @@ __global__ void __launch_bounds__(64 * WGM * WGN * KG)
   // extent reduced by the same amount) and step by one K tile; crossing into
   // the next K segment re-seats them at that segment's first tile.  A tile past
   // it1 gets an empty extent and loads zeros.
-  const uint32_t a_step = (uint32_t)BK * (AK ? 2u : (uint32_t)p.lda * 2u);  // bytes per K tile
-  const uint32_t b_step = (uint32_t)BK * (BKC ? 2u : (uint32_t)p.ldb * 2u);
+  const uint32_t a_step = (uint32_t)BK * (AK ? (uint32_t)ES : (uint32_t)p.lda * ES);  // bytes per K tile
+  const uint32_t b_step = (uint32_t)BK * (BKC ? (uint32_t)ES : (uint32_t)p.ldb * ES);
   // K rotation (krot; one problem, one K segment, no split, no causal skipping):
   // the workgroups of XCD x (hardware dispatch: block id mod 8) walk the K tiles
   // starting at tile x*per_seg/8 and wrap around (the segment-crossing step below
@@ -379,9 +411,9 @@ __global__ void __launch_bounds__(64 * WGM * WGN * KG)
   int d_it = it0;
   int d_seg = uniform(per_seg > 0 ? it0 / per_seg : 0);
   int d_kt = uniform(it0 - d_seg * per_seg + rot);
-  const char* a_ptr = (const char*)(Ab + (int64_t)d_seg * p.segA) + (uint32_t)(klo + d_kt) * a_step;
-  const char* b_ptr = (const char*)(Bb + (int64_t)d_seg * p.segB) + (uint32_t)(klo + d_kt) * b_step;
-  const char* b2_ptr = DUAL ? (const char*)(B2b + (int64_t)d_seg * p.segB) + (uint32_t)(klo + d_kt) * b_step
+  const char* a_ptr = Ab + (int64_t)d_seg * p.segA * ES + (uint32_t)(klo + d_kt) * a_step;
+  const char* b_ptr = Bb + (int64_t)d_seg * p.segB * ES + (uint32_t)(klo + d_kt) * b_step;
+  const char* b2_ptr = DUAL ? B2b + (int64_t)d_seg * p.segB * ES + (uint32_t)(klo + d_kt) * b_step
                             : nullptr;
   uint32_t a_ext = p.extA - (uint32_t)(klo + d_kt) * a_step;
   uint32_t b_ext = p.extB - (uint32_t)(klo + d_kt) * b_step;
@@ -404,9 +436,9 @@ __global__ void __launch_bounds__(64 * WGM * WGN * KG)
     b_ext -= b_step;
     if (++d_kt == per_seg) {  // next K segment
       d_kt = 0;
-      a_ptr += (int64_t)p.segA * 2 - (int64_t)per_seg * a_step;
-      b_ptr += (int64_t)p.segB * 2 - (int64_t)per_seg * b_step;
-      if constexpr (DUAL) b2_ptr += (int64_t)p.segB * 2 - (int64_t)per_seg * b_step;
+      a_ptr += (int64_t)p.segA * ES - (int64_t)per_seg * a_step;
+      b_ptr += (int64_t)p.segB * ES - (int64_t)per_seg * b_step;
+      if constexpr (DUAL) b2_ptr += (int64_t)p.segB * ES - (int64_t)per_seg * b_step;
       a_ext += per_seg * a_step;
       b_ext += per_seg * b_step;
     }
@@ -438,9 +470,18 @@ __global__ void __launch_bounds__(64 * WGM * WGN * KG)
     }
   };
   auto mfma_op = [&](int set, int i, int j) __attribute__((always_inline)) {
-    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, fb[set][j]),
-                                                        __builtin_bit_cast(bf16x8_t, fa[set][i]),
-                                                        acc[i][j], 0, 0, 0);
+    if constexpr (ES == 2) {
+      acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, fb[set][j]),
+                                                          __builtin_bit_cast(bf16x8_t, fa[set][i]),
+                                                          acc[i][j], 0, 0, 0);
+    } else {
+      // fp32: value t of both fragments is k = 8S + t (lanes 0-31) and 8S + 4 + t
+      // (lanes 32-63), the two k of one 32x32x2 MFMA
+#pragma unroll
+      for (int t = 0; t < 4; ++t)
+        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(__uint_as_float(fb[set][j][t]),
+                                                         __uint_as_float(fa[set][i][t]), acc[i][j], 0, 0, 0);
+    }
   };
 
   // One substep = TM*NB MFMA slots.  The fragment reads of the next substep go
@@ -458,7 +499,18 @@ __global__ void __launch_bounds__(64 * WGM * WGN * KG)
   constexpr bool SPREAD = STAGES >= 3;
   // SPREAD: DMA instructions issued before the last substep of a K tile.
   constexpr int DMA_EARLY = (NL * (NSUB - 1) * NS + TOT - 1) / TOT;
-  static_assert(NREAD <= NS, "one fragment read per MFMA slot at most");
+  // at most one fragment read per MFMA slot (an fp32 slot is four MFMAs and may take more)
+  static_assert(NREAD <= NS || ES == 4, "one fragment read per MFMA slot at most");
+  // fragment reads of slot q: one each in the first NREAD slots, or spread evenly
+  auto slot_reads = [&](int q, auto JR_c, auto RS_c, int set) __attribute__((always_inline)) {
+    if constexpr (NREAD <= NS) {
+      if (q < NREAD) read_op(q, JR_c, RS_c, set);
+    } else {
+#pragma unroll
+      for (int o = (q * NREAD + NS - 1) / NS; o < ((q + 1) * NREAD + NS - 1) / NS; ++o)
+        read_op(o, JR_c, RS_c, set);
+    }
+  };
   // S: substep index within the tile (fragment set S & 1).  RS / JR: substep
   // and stage whose fragments are read into the other set.  DMA: 0 none, 1 the
   // whole DMA of tile t spread over this substep, 2 the share of slots
@@ -468,7 +520,7 @@ __global__ void __launch_bounds__(64 * WGM * WGN * KG)
     constexpr int S = decltype(S_c)::value;
     constexpr int DMA = decltype(DMA_c)::value;
     constexpr int set = S & 1;
-    if constexpr (!AK || !BKC) {
+    if constexpr (TRR) {
       // fragments of this set issued by transpose-read asm are complete only
       // after lgkmcnt(0); nothing may be scheduled above this point
       __builtin_amdgcn_s_waitcnt(0xC07F);
@@ -477,7 +529,7 @@ __global__ void __launch_bounds__(64 * WGM * WGN * KG)
 #pragma unroll
     for (int q = 0; q < NS; ++q) {
       mfma_op(set, q / NB, q % NB);
-      if (q < NREAD) read_op(q, JR_c, RS_c, set ^ 1);
+      slot_reads(q, JR_c, RS_c, set ^ 1);
       if constexpr (DMA == 1) {
 #pragma unroll
         for (int o = (q * NL + NS - 1) / NS; o < ((q + 1) * NL + NS - 1) / NS; ++o) dma(o, t, JF_c);
@@ -504,7 +556,7 @@ __global__ void __launch_bounds__(64 * WGM * WGN * KG)
     // first half NL/2 instructions, second half the rest (NL may be odd)
     constexpr int H0 = DPART == 2 ? NL / 2 : 0;
     constexpr int HN = DPART == 1 ? NL / 2 : DPART == 2 ? NL - NL / 2 : 0;
-    if constexpr (!AK || !BKC) {
+    if constexpr (TRR) {
       // set S was read two substeps ago; the previous substep's LDS reads (one
       // set, READ_OPS instructions) may stay in flight: LDS returns in order
       __builtin_amdgcn_s_waitcnt(0xC07F | (LGKM_KEEP << 8));
@@ -513,7 +565,7 @@ __global__ void __launch_bounds__(64 * WGM * WGN * KG)
 #pragma unroll
     for (int q = 0; q < NS; ++q) {
       mfma_op(S, q / NB, q % NB);
-      if (q < NREAD) read_op(q, JR_c, RS_c, RSET);
+      slot_reads(q, JR_c, RS_c, RSET);
 #pragma unroll
       for (int o = H0 + (q * HN + NS - 1) / NS; o < H0 + ((q + 1) * HN + NS - 1) / NS; ++o)
         dma(o, t, JF_c);
@@ -597,7 +649,7 @@ __global__ void __launch_bounds__(64 * WGM * WGN * KG)
     for (int it = it0; it < it1; it += STAGES) static_for<STAGES>(iteration);
   }
 
-  if constexpr (!AK || !BKC) {
+  if constexpr (TRR) {
     // The last substep issued transpose reads (asm) for a K tile that does not
     // exist.  Their registers count as dead to the compiler while the reads are
     // still in flight: wait for them, and keep the registers allocated until

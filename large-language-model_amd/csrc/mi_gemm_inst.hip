@@ -104,6 +104,22 @@ KernelFn dlds_kernel(int cfg) {
 }
 #endif
 
+#if !MI_DT_BF16
+// fp32 direct-to-LDS kernels: K tile 32 (128-byte rows, the bytes of a bf16 K tile
+// of 64), four 32x32x2 MFMAs per fragment pair and substep; 64x128 (four waves of
+// 32x64) and 64x64 (four waves of 32x32).  The 64x128 tile replaced the register-
+// staged kernel of that tile (configuration 2's set 89-91 -> 104-107 TFLOP/s, same
+// box, two runs each).
+template <bool AK, bool BK, int V>
+KernelFn dlds32_kernel(int cfg) {
+  switch (cfg) {
+    case CFG_V: return gemm_dlds_kernel<64, 128, 32, 2, AK, BK, MODE_PLAIN, V, 2, 2, 1, 4>;
+    case CFG_M: return gemm_dlds_kernel<64, 64, 32, 2, AK, BK, MODE_PLAIN, V, 2, 2, 1, 4>;
+    default: return nullptr;
+  }
+}
+#endif
+
 KernelFn MI_PICK_NAME(MI_DTN, MI_TA, MI_TB)(int cfg, bool fast, bool ktail, int fast_epi) {
   constexpr bool AK = (MI_TA == 0);  // A is K-contiguous when not transposed
   constexpr bool BK = (MI_TB == 1);  // B is K-contiguous when transposed
@@ -129,12 +145,17 @@ KernelFn MI_PICK_NAME(MI_DTN, MI_TA, MI_TB)(int cfg, bool fast, bool ktail, int 
         return nullptr;
     }
 #endif
+#if !MI_DT_BF16
+    if (cfg == CFG_V || cfg == CFG_M) {
+      if constexpr (AK || BK) {
+        if (ktail) return dlds32_kernel<AK, BK, DLDS_KTAIL>(cfg);
+      }
+      return fast_epi ? dlds32_kernel<AK, BK, DLDS_FAST_EPI>(cfg) : dlds32_kernel<AK, BK, 0>(cfg);
+    }
+#endif
     switch (cfg) {
       case CFG_L: return gemm_kernel<elem_t, LM, LN, 2, 2, AK, BK, MODE_PLAIN, true>;
       case CFG_S: return gemm_kernel<elem_t, SM, SN, 2, 2, AK, BK, MODE_PLAIN, true>;
-#if !MI_DT_BF16
-      case CFG_V: return gemm_kernel<elem_t, 64, 128, 2, 2, AK, BK, MODE_PLAIN, true>;
-#endif
       case CFG_DUAL: return gemm_kernel<elem_t, DM, DN, 2, 2, AK, BK, MODE_DUAL, true>;
       case CFG_PRO:
         if constexpr (AK) return gemm_kernel<elem_t, PM, PN, 2, 2, AK, BK, MODE_PROLOGUE, true>;

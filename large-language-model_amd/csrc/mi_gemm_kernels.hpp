@@ -15,7 +15,8 @@ typedef void (*KernelFn)(Params);
 //         64x64, each over half of every K tile, summed through LDS),
 //         M 256x192 (8 waves of 64x96), V 128x192 with wave-level split-K (two
 //         groups of 4 waves of 64x96).
-//   fp32: L = S = W 128x128, DUAL 128x64, PRO 128x128.
+//   fp32: V 64x128 and M 64x64 direct-to-LDS (four waves); register-staged
+//         L = S = W 128x128, DUAL 128x64, PRO 128x128.
 enum Cfg { CFG_L = 0, CFG_S = 1, CFG_DUAL = 2, CFG_PRO = 3, CFG_W = 4, CFG_M = 5, CFG_V = 6, NCFG = 7 };
 
 struct CfgShape {
@@ -38,9 +39,11 @@ inline CfgShape cfg_shape(bool bf16, int cfg) {
          : cfg == CFG_V ? CfgShape{128, 192, 512}
          : cfg == CFG_DUAL ? CfgShape{256, 128}
                            : CfgShape{256, 256};
-  // fp32: register-staged kernel, four waves; V names the 64x128 tile
+  // fp32: V and M name the direct-to-LDS 64x128 and 64x64 tiles (four waves), the
+  // others the register-staged kernel (four waves)
   return cfg == CFG_DUAL ? CfgShape{128, 64}
        : cfg == CFG_V    ? CfgShape{64, 128}
+       : cfg == CFG_M    ? CfgShape{64, 64}
                          : CfgShape{128, 128};
 }
 
