@@ -1,4 +1,4 @@
-// mi_gemm_dlds.hpp -- bf16 GEMM main loop with direct-to-LDS loads (gfx950).
+// mi_gemm_dlds.hpp -- bf16 and fp32 GEMM main loop with direct-to-LDS loads (gfx950).
 //
 // Operand tiles move global -> LDS with buffer_load_dwordx4 ... lds: each lane's
 // 16 bytes land at M0 + 16*lane, so the LDS layout (and its bank swizzle) is set
@@ -21,7 +21,8 @@
 //   row-contiguous operand [BK k-rows][R]  (R/8 chunks per k-row, chunk index
 //       XOR-swizzled by the k-row); MFMA fragments are two ds_read_b64_tr_b16,
 //       whose 16-lane groups turn a 4 (k) x 16 (row) block into 16 lanes x 4 k.
-// Both read patterns are bank-conflict free on the 64-bank LDS.
+//       fp32: four ds_read_b32 per fragment (mc_swz32).
+// The read patterns are bank-conflict free on the 64-bank LDS.
 #pragma once
 #include "mi_gemm_device.hpp"
 
@@ -279,7 +280,8 @@ struct DldsOperand {
 // both epilogues would need the accumulators in two places at once.
 enum { DLDS_KTAIL = 1, DLDS_FAST_EPI = 2, DLDS_ROWSCALE = 4 };
 
-// bf16 GEMM of WGM x WGN waves, wave tile (BM/WGM) x (BN/WGN) of 32x32x16 MFMAs.
+// GEMM of WGM x WGN waves, wave tile (BM/WGM) x (BN/WGN) of 32x32 MFMA blocks: bf16
+// (ES = 2, one 32x32x16 MFMA per block and substep) or fp32 (ES = 4, four 32x32x2).
 // KG = 2 (wave-level split-K): a second group of WGM x WGN waves computes the
 // same output tile over the other half of every LDS stage's K range (both
 // groups share the stage's DMA), so a workgroup keeps two waves per SIMD on one
