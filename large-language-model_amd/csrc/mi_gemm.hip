@@ -220,9 +220,10 @@ int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
 //   * when even S tiles leave half the CUs idle, K is split over S tiles, given
 //     a workspace -- also for S tiles chosen by the fill rule and for the
 //     register-staged loader (unaligned operands);
-//   * fp32: 64x128 tiles with K split to about three units per CU (buffer-load
-//     loader), 128x128 tiles split below 5/8 of a wave (element-granular
-//     loader); the rules at the fp32 branch.
+//   * fp32: 64x128 or 64x64 direct-to-LDS tiles with K split to about three
+//     units per CU (16-byte-aligned operands), 128x128 register-staged tiles
+//     split below 5/8 of a wave (element-granular loader); the rules at the fp32
+//     branch.
 // Every split fits the workspace: splits * M * N * batch <= ws_limit_elems.
 Plan make_plan(int dtype_in, int64_t M, int64_t N, int64_t Ktot, int64_t batch, int mode,
                bool allow_split, int64_t ws_limit_elems, int cus, bool fast) {
