@@ -325,6 +325,41 @@ def test_fp32_direct_to_lds(mi, dev, oracle, tA, tB):
         assert np.array_equal(C.cpu().numpy(), a.astype(np.int64) @ b.astype(np.int64)), (M, N, K)
 
 
+@pytest.mark.parametrize("bf16", [True, False], ids=["bf16", "f32"])
+@pytest.mark.parametrize("tA,tB", [(0, 0), (0, 1), (1, 0), (1, 1)], ids=["NN", "NT", "TN", "TT"])
+def test_batched_head_groups(mi, dev, oracle, bf16, tA, tB):
+    """mi_gemm_batched with a head map (batch x heads problems, B shared by groups of 2
+    heads, as GQA's K/V) and with two K segments (C = sum over segments of A_s B_s), on
+    the direct-to-LDS kernels (16-byte-aligned operands), against the oracle per problem."""
+    import torch
+
+    nb, heads, grp, M, N, K = 2, 4, 2, 130, 196, 132
+    tol = _tol(bf16)
+    a = inputs(oracle, (nb, heads, M, K), 61, 1.0, bf16)
+    b = inputs(oracle, (nb, heads // grp, K, N), 62, 0.02, bf16)
+    A = np.stack([np.stack([layout(a[i, h], tA) for h in range(heads)]) for i in range(nb)])
+    B = np.stack([np.stack([layout(b[i, h], tB) for h in range(heads // grp)]) for i in range(nb)])
+    C = torch.zeros((nb, heads, M, N), dtype=torch.float32, device=dev)
+    bt = mi.make_batch(nb * heads, heads, a=(heads * M * K, M * K, 1),
+                       b=((heads // grp) * K * N, K * N, grp), c=(heads * M * N, M * N, 1))
+    assert mi.describe(tA, tB, M, N, K, mi.MI_BF16 if bf16 else mi.MI_F32,
+                       batch=nb * heads).split()[0].startswith("dlds")
+    mi.gemm_batched(to_dev(A, dev, bf16), to_dev(B, dev, bf16), C, M, N, K, bt, transA=tA, transB=tB)
+    got = host(C)
+    for i in range(nb):
+        for h in range(heads):
+            check(got[i, h], oracle.gemm(0, 0, M, N, K, a[i, h], b[i, h // grp]), tol,
+                  f"problem ({i}, {h}) tA={tA} tB={tB}")
+    # two K segments of one problem: C = A_0 B_0 + A_1 B_1 (segment strides in elements)
+    C2 = torch.zeros((M, N), dtype=torch.float32, device=dev)
+    seg_a, seg_b = M * K, K * N
+    bt2 = mi.make_batch(1, 1, k_segments=2, seg_a=seg_a, seg_b=seg_b)
+    mi.gemm_batched(to_dev(A[0, :2], dev, bf16), to_dev(B[0], dev, bf16), C2, M, N, K, bt2,
+                    transA=tA, transB=tB)
+    ref = oracle.gemm(0, 0, M, N, K, a[0, 0], b[0, 0]) + oracle.gemm(0, 0, M, N, K, a[0, 1], b[0, 1])
+    check(host(C2), ref, tol, f"two K segments tA={tA} tB={tB}")
+
+
 @pytest.mark.parametrize("tA,tB", [(0, 0), (0, 1), (1, 0), (1, 1)], ids=["NN", "NT", "TN", "TT"])
 def test_tile_256x192(mi, dev, oracle, tA, tB):
     """256x192 tiles (8 waves of 64x96; a row-contiguous B stored in 128-byte granules
