@@ -405,8 +405,9 @@ int mi_convert_matrices(void* stream, const mi_convert_job* jobs, int64_t n);
 
 /*
  * Describe the kernel mi_gemm_batched would launch for this problem (tile,
- * loader, split-K factor) as text into buf (always NUL-terminated).  For
- * measurement and logging; no reference counterpart.  epi_mode: 0 plain,
+ * loader, split-K factor) as text into buf (always NUL-terminated), for packed
+ * operands (leading dimension = contiguous extent) at 16-byte-aligned addresses.
+ * For measurement and logging; no reference counterpart.  epi_mode: 0 plain,
  * 1 dual-B, 2 SiLU-gate prologue.
  */
 int mi_gemm_describe(int transA, int transB, int64_t M, int64_t N, int64_t K, int32_t dtype_in,

@@ -1538,8 +1538,13 @@ int mi_gemm_describe(int transA, int transB, int64_t M, int64_t N, int64_t K, in
   if (init_devices() == MI_OK) cus = current_cus();
   const int mode = epi_mode == 1 ? MODE_DUAL : (epi_mode == 2 ? MODE_PROLOGUE : MODE_PLAIN);
   const int64_t ws = (int64_t)(workspace_bytes / sizeof(float));
-  const Plan pl = make_plan(dtype_in, M, N, K, batch, mode, ws > 0, ws, cus, true);
-  describe_plan(buf, buf_len, dtype_in, true, pl, transA, transB, batch);
+  // packed operands (leading dimension = contiguous extent), 16-byte-aligned bases: the
+  // 16-byte loaders need the contiguous extents in whole 16-byte chunks, as run() checks
+  const int64_t ch = dtype_in == MI_BF16 ? 8 : 4;
+  const int64_t a_contig = transA ? M : K, b_contig = transB ? K : N;
+  const bool fast = K == 0 || (a_contig % ch == 0 && b_contig % ch == 0);
+  const Plan pl = make_plan(dtype_in, M, N, K, batch, mode, ws > 0, ws, cus, fast);
+  describe_plan(buf, buf_len, dtype_in, fast, pl, transA, transB, batch);
   return MI_OK;
 }
 
