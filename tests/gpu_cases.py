@@ -48,3 +48,44 @@ def sample_rows(M, n=8, seed=0):
     rows = set(rng.choice(M, size=min(n, M), replace=False).tolist())
     rows |= {0, M - 1}
     return np.array(sorted(rows), dtype=np.int64)
+
+
+def dense_attention(q, k, v, causal):
+    """float64 softmax(Q K^T / sqrt(d)) V and the row log-sum-exp, [B,nH,T,d] layouts
+    (the closed form; the causal case is also checked against the oracle)."""
+    Bn, nH, T, d = q.shape
+    g = nH // k.shape[1]
+    kk = np.repeat(k.astype(np.float64), g, axis=1)
+    vv = np.repeat(v.astype(np.float64), g, axis=1)
+    s = np.einsum("bhqc,bhkc->bhqk", q.astype(np.float64), kk) / np.sqrt(d)
+    if causal:
+        s = np.where(np.tril(np.ones((T, T), bool)), s, -np.inf)
+    mx = s.max(axis=-1, keepdims=True)
+    e = np.exp(s - mx)
+    lse = (np.log(e.sum(axis=-1)) + mx[..., 0])
+    o = np.einsum("bhqk,bhkc->bhqc", e / e.sum(axis=-1, keepdims=True), vv)
+    return o, lse
+
+
+def dense_attention_bwd(q, k, v, do, causal):
+    """float64 closed form of the backward: dV = P^T dO, dS = P (dO V^T - rowsum(dO O)),
+    dQ = dS K / sqrt(d), dK = dS^T Q / sqrt(d), dK and dV summed over a KV head's query
+    heads.  do is [B, T, nH*d]."""
+    Bn, nH, T, d = q.shape
+    nKV = k.shape[1]
+    g = nH // nKV
+    qq = q.astype(np.float64)
+    kk = np.repeat(k.astype(np.float64), g, axis=1)
+    vv = np.repeat(v.astype(np.float64), g, axis=1)
+    s = np.matmul(qq, kk.transpose(0, 1, 3, 2)) / np.sqrt(d)
+    if causal:
+        s = np.where(np.tril(np.ones((T, T), bool)), s, -np.inf)
+    p = np.exp(s - s.max(axis=-1, keepdims=True))
+    p /= p.sum(axis=-1, keepdims=True)
+    o = np.matmul(p, vv)
+    g4 = do.astype(np.float64).reshape(Bn, T, nH, d).transpose(0, 2, 1, 3)
+    ds = p * (np.matmul(g4, vv.transpose(0, 1, 3, 2)) - (g4 * o).sum(axis=-1, keepdims=True))
+    dq = np.matmul(ds, kk) / np.sqrt(d)
+    dk = (np.matmul(ds.transpose(0, 1, 3, 2), qq) / np.sqrt(d)).reshape(Bn, nKV, g, T, d).sum(2)
+    dv = np.matmul(p.transpose(0, 1, 3, 2), g4).reshape(Bn, nKV, g, T, d).sum(2)
+    return dq, dk, dv

@@ -8,7 +8,7 @@ of a KV group = the KV-group reduction), dP = dO V^T (NT), dQ = dS K (NN).
 import numpy as np
 import pytest
 
-from gpu_cases import TOL_BF16, check, host, inputs, layout, to_dev
+from gpu_cases import TOL_BF16, check, dense_attention, dense_attention_bwd, host, inputs, layout, to_dev
 
 pytestmark = pytest.mark.gpu
 
@@ -101,23 +101,6 @@ def test_causal_modes(mi, dev, oracle, bf16):
 
 # ---- fused flash-attention forward ------------------------------------------------
 
-def _dense_attention(q, k, v, causal):
-    """float64 softmax(Q K^T / sqrt(d)) V and the row log-sum-exp, [B,nH,T,d] layouts
-    (the closed form; the causal case is also checked against the oracle)."""
-    Bn, nH, T, d = q.shape
-    g = nH // k.shape[1]
-    kk = np.repeat(k.astype(np.float64), g, axis=1)
-    vv = np.repeat(v.astype(np.float64), g, axis=1)
-    s = np.einsum("bhqc,bhkc->bhqk", q.astype(np.float64), kk) / np.sqrt(d)
-    if causal:
-        s = np.where(np.tril(np.ones((T, T), bool)), s, -np.inf)
-    mx = s.max(axis=-1, keepdims=True)
-    e = np.exp(s - mx)
-    lse = (np.log(e.sum(axis=-1)) + mx[..., 0])
-    o = np.einsum("bhqk,bhkc->bhqc", e / e.sum(axis=-1, keepdims=True), vv)
-    return o, lse
-
-
 @pytest.mark.parametrize("d", [128, 64])
 @pytest.mark.parametrize("Bn,nH,nKV,T", [(2, 16, 4, 256), (1, 4, 2, 300), (1, 2, 1, 64),
                                          (1, 4, 4, 520)])
@@ -135,7 +118,7 @@ def test_flash_forward(mi, dev, oracle, Bn, nH, nKV, T, d):
     O_ref = oracle.attention_fwd(q, k, v)
     check(host(O), O_ref, TOL_BF16, "O [B,T,nH*d]")
     check(host(O2).transpose(0, 2, 1, 3).reshape(Bn, T, nH * d), O_ref, TOL_BF16, "O [B,nH,T,d]")
-    _, lse_ref = _dense_attention(q, k, v, True)
+    _, lse_ref = dense_attention(q, k, v, True)
     err = np.abs(host(lse) - lse_ref).max()
     assert err < 1e-3, f"lse max abs err {err:.3e}"
 
@@ -147,7 +130,7 @@ def test_flash_forward_noncausal(mi, dev, oracle, d):
     q, k, v, _ = _qkv(oracle, Bn, nH, nKV, T, d, 1700)
     Q, K, V = (to_dev(x, dev, True) for x in (q, k, v))
     O = mi.flash_attn_fwd(Q, K, V, causal=False, layout="bhtd")
-    o_ref, _ = _dense_attention(q, k, v, False)
+    o_ref, _ = dense_attention(q, k, v, False)
     check(host(O), o_ref, TOL_BF16, "non-causal O")
 
 
@@ -189,30 +172,6 @@ def test_flash_backward(mi, dev, oracle, Bn, nH, nKV, T, ws, d):
     check(host(dQ), dQ_ref, TOL_BF16, "dQ")
 
 
-def _dense_attention_bwd(q, k, v, do, causal):
-    """float64 closed form of the backward: dV = P^T dO, dS = P (dO V^T - rowsum(dO O)),
-    dQ = dS K / sqrt(d), dK = dS^T Q / sqrt(d), dK and dV summed over a KV head's query
-    heads.  do is [B, T, nH*d]."""
-    Bn, nH, T, d = q.shape
-    nKV = k.shape[1]
-    g = nH // nKV
-    qq = q.astype(np.float64)
-    kk = np.repeat(k.astype(np.float64), g, axis=1)
-    vv = np.repeat(v.astype(np.float64), g, axis=1)
-    s = np.matmul(qq, kk.transpose(0, 1, 3, 2)) / np.sqrt(d)
-    if causal:
-        s = np.where(np.tril(np.ones((T, T), bool)), s, -np.inf)
-    p = np.exp(s - s.max(axis=-1, keepdims=True))
-    p /= p.sum(axis=-1, keepdims=True)
-    o = np.matmul(p, vv)
-    g4 = do.astype(np.float64).reshape(Bn, T, nH, d).transpose(0, 2, 1, 3)
-    ds = p * (np.matmul(g4, vv.transpose(0, 1, 3, 2)) - (g4 * o).sum(axis=-1, keepdims=True))
-    dq = np.matmul(ds, kk) / np.sqrt(d)
-    dk = (np.matmul(ds.transpose(0, 1, 3, 2), qq) / np.sqrt(d)).reshape(Bn, nKV, g, T, d).sum(2)
-    dv = np.matmul(p.transpose(0, 1, 3, 2), g4).reshape(Bn, nKV, g, T, d).sum(2)
-    return dq, dk, dv
-
-
 @pytest.mark.parametrize("d", [128, 64])
 @pytest.mark.parametrize("ws", ["auto", None])
 def test_flash_backward_noncausal(mi, dev, oracle, ws, d):
@@ -222,14 +181,14 @@ def test_flash_backward_noncausal(mi, dev, oracle, ws, d):
 
     Bn, nH, nKV, T = 1, 4, 2, 200
     q, k, v, do = _qkv(oracle, Bn, nH, nKV, T, d, 2300)
-    for ref, got in zip(_dense_attention_bwd(q, k, v, do, True), oracle.attention_bwd(q, k, v, do)):
+    for ref, got in zip(dense_attention_bwd(q, k, v, do, True), oracle.attention_bwd(q, k, v, do)):
         assert np.abs(ref - got).max() <= 1e-9 * max(1.0, np.abs(got).max())
     Q, K, V, dO = (to_dev(x, dev, True) for x in (q, k, v, do))
     lse = torch.empty((Bn, nH, T), dtype=torch.float32, device=dev)
     O = mi.flash_attn_fwd(Q, K, V, causal=False, lse=lse)
     print(f"flash backward non-causal T={T} workspace={ws}", flush=True)
     dQ, dK, dV = mi.flash_attn_bwd(Q, K, V, O, dO, lse, causal=False, workspace=ws)
-    dq_ref, dk_ref, dv_ref = _dense_attention_bwd(q, k, v, do, False)
+    dq_ref, dk_ref, dv_ref = dense_attention_bwd(q, k, v, do, False)
     check(host(dV), dv_ref, TOL_BF16, "dV")
     check(host(dK), dk_ref, TOL_BF16, "dK")
     check(host(dQ), dq_ref, TOL_BF16, "dQ")
@@ -308,7 +267,7 @@ def test_flash_head_dim_padded(mi, dev, oracle, d, layout):
     O_ref = oracle.attention_fwd(q, k, v)
     got = host(O) if layout == "bthd" else host(O).transpose(0, 2, 1, 3).reshape(Bn, T, nH * d)
     check(got, O_ref, TOL_BF16, f"O d={d}")
-    _, lse_ref = _dense_attention(q, k, v, True)
+    _, lse_ref = dense_attention(q, k, v, True)
     err = np.abs(host(lse) - lse_ref).max()
     assert err < 1e-3, f"lse max abs err {err:.3e}"
     dO_l = dO if layout == "bthd" else dO.reshape(Bn, T, nH, d).permute(0, 2, 1, 3).contiguous()
