@@ -25,6 +25,8 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <functional>
+#include <queue>
 #include <vector>
 
 #include "mi_attn.hpp"
@@ -1092,11 +1094,47 @@ __global__ void __launch_bounds__(256) flash_bwd_dkdv_reduce_kernel(FbParams p) 
 // last, and one workgroup per key block leaves the CUs of the short ones idle while
 // the long ones run (configuration 4: 64 iterations for key block 0, 8 for key block
 // 7, 56 % of the CU time used).  Each key block is cut into units of at most W
-// iterations, W = the total over all (batch, KV head) pairs / the CU count, and the
-// units launch largest first, so the hardware's in-order dispatch to the CU that
-// frees up first packs them (longest-processing-time-first).  When the partials of
-// the cut blocks do not fit the room given, W grows by half until they do; when the
-// tables do not fit the kernel arguments, n_units stays 0.
+// iterations and the units launch largest first, so the hardware's in-order dispatch
+// to the CU that frees up first packs them (longest-processing-time-first).  A unit
+// costs its iterations plus a fixed FB_UNIT_COST (the K/V load before its first tile,
+// the halves' exchange and the dK/dV stores after its last; the dK/dV kernel holds a
+// CU alone, so none of it overlaps another unit): W is the cut, from the even share
+// W0 = total iterations / CUs up to 1.5 W0, whose simulated dispatch ends earliest
+// (ties to the larger W: fewer partials to sum).  When the partials of the cut
+// blocks do not fit the room given, W grows by half until they do; when the tables
+// do not fit the kernel arguments, n_units stays 0.
+constexpr int FB_UNIT_COST = 7;
+
+// Unit lengths of a key block of `w` iterations cut at W: at most 8 units of
+// max(W, ceil(w / 8)) iterations, the last one the remainder.
+void cut_units(int w, int64_t W, std::vector<int>& out) {
+  if (w <= W) {
+    out.push_back(w);
+    return;
+  }
+  const int c = (int)std::max<int64_t>(W, (w + 7) / 8);
+  for (int j = 0; j * c < w; ++j) out.push_back(std::min(w, (j + 1) * c) - j * c);
+}
+
+// End of the busiest CU when the units (the same list for every one of the BKV
+// (batch, KV head) pairs, largest first, dispatched unit-major as the kernel maps
+// workgroups) go in order to the CU that frees up first, each costing its
+// iterations + FB_UNIT_COST.
+int64_t dkdv_makespan(std::vector<int> lens, int64_t BKV, int cus) {
+  std::sort(lens.begin(), lens.end(), std::greater<int>());
+  std::priority_queue<int64_t, std::vector<int64_t>, std::greater<int64_t>> free_at;
+  for (int c = 0; c < cus; ++c) free_at.push(0);
+  int64_t end = 0;
+  for (const int len : lens)
+    for (int64_t i = 0; i < BKV; ++i) {
+      const int64_t t = free_at.top() + len + FB_UNIT_COST;
+      free_at.pop();
+      free_at.push(t);
+      end = std::max(end, t);
+    }
+  return end;
+}
+
 void plan_dkdv_schedule(FbParams& p, int head_dim) {
   p.n_units = p.n_slots = p.n_split = 0;
   if (!p.dsT || !p.part || p.cus <= 0) return;
@@ -1111,10 +1149,38 @@ void plan_dkdv_schedule(FbParams& p, int head_dim) {
     if (w[k] >= 65536) return;
     sum += w[k];
   }
+  // The cut: simulated over W0 .. 1.5 W0 (configuration 4, W0 = 36: backward 171-173 us
+  // at W = 36, 168-169 at 38, 167 at 39, 163-166 at 40, 166-170 at 42, 173-178 at 46;
+  // the simulation picks 40).  The last choice is kept per thread for repeated calls.
+  const int64_t W0 = std::max<int64_t>(1, (sum * BKV + p.cus - 1) / p.cus);
+  struct CutCache { int64_t bkv, T, W; int nkb, group, causal, cus; };
+  thread_local CutCache cache = {-1, -1, 0, 0, 0, 0, 0};
+  int64_t Wbest = W0;
+  if (cache.bkv == BKV && cache.T == p.T && cache.nkb == NKB && cache.group == p.group &&
+      cache.causal == p.causal && cache.cus == p.cus) {
+    Wbest = cache.W;
+  } else {
+    // at most 25 candidates, and no search when one simulation would dispatch over
+    // 20 K workgroups (the host cost stays under a millisecond)
+    const int64_t step = std::max<int64_t>(1, W0 / 48);
+    int64_t best = -1;
+    std::vector<int> lens;
+    for (int64_t W = W0; W <= W0 + W0 / 2; W += step) {
+      lens.clear();
+      for (int k = 0; k < NKB; ++k) cut_units(w[k], W, lens);
+      if ((int64_t)lens.size() * BKV > 20000) break;
+      const int64_t m = dkdv_makespan(lens, BKV, p.cus);
+      if (best < 0 || m <= best) {
+        best = m;
+        Wbest = W;
+      }
+    }
+    cache = {BKV, p.T, Wbest, NKB, p.group, p.causal, p.cus};
+  }
   struct Unit { int kbi, ib, ie, slot; };
   std::vector<Unit> units;
   int slots = 0, nsplit = 0;
-  for (int64_t W = std::max<int64_t>(1, (sum * BKV + p.cus - 1) / p.cus);; W += (W + 1) / 2) {
+  for (int64_t W = Wbest;; W += (W + 1) / 2) {
     units.clear();
     slots = nsplit = 0;
     bool fits = true;
